@@ -1,0 +1,299 @@
+/*
+ * kvm_hotpath.h -- C ABI of the MI355X (gfx950) KVMem retrieval + attention hot path.
+ *
+ * Plain C: pointers, sizes and status codes only.  Every entry point names the
+ * reference interface it replaces (paths relative to the reference repository).
+ * All device pointers are HIP device addresses on the state's device; "host"
+ * pointers must be pinned (hipHostMalloc) so kernels can read them over PCIe.
+ *
+ * Return convention: KVM_OK (0) on success, a negative KVM_E* code otherwise;
+ * the message is available from kvm_state_last_error().  This replaces the
+ * reference's `bool` + stderr convention (src/adapter/llama-kvmem-stagein.cu:93-99):
+ * a failed call leaves the window unchanged where the reference caller would
+ * fall back (src/adapter/llama-memory-kvmem.cpp:4032-4038).
+ *
+ * Threading: a kvm_state is one execution domain (src/adapter/llama-kvmem-hooks.h:46-55);
+ * it must not be used from two threads at once.  All GPU work of a state is
+ * enqueued in order on its stream.
+ */
+#ifndef KVM_HOTPATH_H
+#define KVM_HOTPATH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVM_ABI_VERSION 1
+
+enum kvm_status {
+    KVM_OK = 0,
+    KVM_EINVAL = -1,       /* bad argument or shape */
+    KVM_EHIP = -2,         /* HIP runtime error */
+    KVM_ENOMEM = -3,       /* allocation failed */
+    KVM_ERANGE = -4,       /* size beyond a documented maximum */
+    KVM_EUNSUPPORTED = -5  /* type combination not implemented */
+};
+
+/* ggml type ids (ggml.h enum ggml_type) for the types this path handles. */
+enum kvm_type {
+    KVM_TYPE_F32 = 0,
+    KVM_TYPE_F16 = 1,
+    KVM_TYPE_Q4_0 = 2,
+    KVM_TYPE_Q8_0 = 8,
+    KVM_TYPE_BF16 = 30
+};
+
+/* Cells per window tile: the window is stored in tiles of 64 cells per kv head. */
+#define KVM_TILE_CELLS 64u
+/* Largest block count one top-k selection handles (1 M tokens at 128-token blocks). */
+#define KVM_MAX_TOPK_BLOCKS 8192u
+
+/* ------------------------------------------------------------------------ */
+/* Execution state                                                           */
+/* ------------------------------------------------------------------------ */
+typedef struct kvm_state kvm_state;
+
+/* Replaces kvmem_gpu_state_create / kvmem_gpu_state_free
+ * (src/adapter/llama-kvmem-stagein.h:12-15).  Creates a non-blocking stream of
+ * default priority on `device`.  NULL on failure. */
+kvm_state *kvm_state_create(int device);
+void kvm_state_free(kvm_state *st);
+/* Run subsequent work on `hip_stream` (a hipStream_t; NULL restores the state's
+ * own stream).  Replaces the per-execution stream (llama-kvmem-stagein.cu:334-343). */
+int kvm_state_set_stream(kvm_state *st, void *hip_stream);
+void *kvm_state_stream(kvm_state *st);
+/* Replaces kvmem_stagein_sync (src/adapter/llama-kvmem-stagein.h:31). */
+int kvm_state_sync(kvm_state *st);
+const char *kvm_state_last_error(const kvm_state *st);
+int kvm_abi_version(void);
+/* Pinned, device-mapped host memory for histories and staging buffers
+ * (hipHostMalloc); kernels read it directly over PCIe.  NULL on failure. */
+void *kvm_host_alloc(size_t bytes);
+void kvm_host_free(void *p);
+
+/* ------------------------------------------------------------------------ */
+/* Window: the bounded GPU slot pool of one attention layer                 */
+/* (llama-memory-kvmem.cpp:611-779 sizing, 1720-1741 slots).                  */
+/* Cell c belongs to slot c / block_tokens.  K and V are kept in a tiled      */
+/* layout private to this library (64-cell tiles, per kv head, laid out in    */
+/* the order the attention kernel's matrix-core operands consume them);      */
+/* kvm_window_import_rows / kvm_window_export_rows convert from / to ggml    */
+/* cache rows ([cell][n_head_kv * row(head_dim)]).                            */
+/* ------------------------------------------------------------------------ */
+typedef struct kvm_window {
+    uint32_t n_cells;       /* multiple of KVM_TILE_CELLS and of block_tokens */
+    uint32_t n_head_kv;
+    uint32_t head_dim;      /* 128 or 256 */
+    uint32_t block_tokens;  /* cells per slot (llama_kvmem_params.block_tokens) */
+    int32_t k_type;         /* KVM_TYPE_Q8_0 (with v_type Q4_0) or KVM_TYPE_F16 (with F16) */
+    int32_t v_type;
+    void *k;                /* device, kvm_window_k_bytes() */
+    void *v;                /* device, kvm_window_v_bytes() */
+    int32_t *cell_pos;      /* device [n_cells]: position of the cell's token, -1 = empty */
+    uint32_t *slot_block;   /* device [n_slots]: block id held by the slot, 0xffffffff = none */
+    int32_t *slot_base;     /* device [n_slots]: position the slot's first cell is baked at */
+} kvm_window;
+
+size_t kvm_window_k_bytes(const kvm_window *w);
+size_t kvm_window_v_bytes(const kvm_window *w);
+/* Checks geometry; KVM_OK when the window is usable. */
+int kvm_window_check(const kvm_window *w);
+/* Empties every cell and slot (reset_slots + seq_rm of the pool,
+ * llama-memory-kvmem.cpp:1018-1024). */
+int kvm_window_reset(kvm_state *st, const kvm_window *w);
+/* Copies ggml cache rows for cells [cell0, cell0+n) into the tiled window and
+ * sets their positions (pos: device int32[n], NULL = leave cell_pos alone).
+ * k_rows / v_rows: device (or pinned host) rows of w->k_type / w->v_type.
+ * This is the cpy of new K/V rows into cache cells (llama-kvmem-batch.cpp:42-50). */
+int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
+                           const void *k_rows, const void *v_rows, const int32_t *pos);
+/* Inverse of import: ggml rows of cells [cell0, cell0+n).  Used by stage-out
+ * (src/adapter/llama-kvmem-stagein.h:48-54) and by byte-exact checks. */
+int kvm_window_export_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
+                           void *k_rows, void *v_rows);
+
+/* ------------------------------------------------------------------------ */
+/* Row codecs (src/adapter/llama-kvmem-stagein.cu:133-234, ggml quantizers)  */
+/* ------------------------------------------------------------------------ */
+/* n_rows x n_per_row fp32 (device) -> ggml rows of type (Q8_0, Q4_0 or F16). */
+int kvm_quantize_rows(kvm_state *st, int type, const float *src, void *dst, int64_t n_rows,
+                      int64_t n_per_row);
+/* ggml rows -> fp32 (Q8_0, Q4_0, F16). */
+int kvm_dequantize_rows(kvm_state *st, int type, const void *src, float *dst, int64_t n_rows,
+                        int64_t n_per_row);
+
+/* ------------------------------------------------------------------------ */
+/* Capture-side index upkeep (the GPU half of the attn-qk-capture hook,      */
+/* patches/0002-attn-qk-capture-hook.patch:33-60, harvest_pending             */
+/* llama-memory-kvmem.cpp:3194).                                              */
+/* ------------------------------------------------------------------------ */
+/* Query accumulator q_sum_ / q_count_ (llama-memory-kvmem.cpp:3300-3315 reset,
+ * 3417-3433 / 3470-3483 add). */
+typedef struct kvm_query_acc {
+    uint32_t n_layer;
+    uint32_t n_head;        /* query heads */
+    uint32_t head_dim;
+    float *q_sum;           /* device [n_layer][n_head * head_dim] */
+    uint32_t *q_count;      /* device [n_layer] */
+} kvm_query_acc;
+
+int kvm_query_reset(kvm_state *st, const kvm_query_acc *acc);
+/* q_sum[il] += each of the n_rows pre-RoPE query rows in order; q_count[il] += n_rows.
+ * q_rows: device fp32 [n_rows][n_head * head_dim]. */
+int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const float *q_rows,
+                  uint32_t n_rows);
+
+/* Mean-K index: per (layer, block) the ordered fp32 sum of pre-RoPE K rows and
+ * its token count (RawKvStore k_sum / mean_tokens, raw_kv_store.cpp:215-234). */
+typedef struct kvm_meank_index {
+    uint32_t n_layer;
+    uint32_t n_blocks;      /* capacity in blocks */
+    uint32_t n_head_kv;
+    uint32_t head_dim;
+    uint32_t block_tokens;
+    float *k_sum;           /* device [n_layer][n_head_kv * head_dim][n_blocks]: embedding-major,
+                             * blocks fastest, so scoring lanes (one block each) read coalesced */
+    uint32_t *mean_tokens;  /* device [n_layer][n_blocks] */
+    uint8_t *present;       /* device [n_blocks] (RawKvStore::has_block), or NULL = all */
+} kvm_meank_index;
+
+/* RawKvStore::write_layer_mean_k (raw_kv_store.cpp:685-705): add n token rows of
+ * layer il starting at original position pos0.  k_rows: device fp32
+ * [n][n_head_kv * head_dim].  Also the decode running sum meank_add_f32
+ * (llama-kvmem-stagein.cu:270-286). */
+int kvm_meank_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
+                  uint32_t n, const float *k_rows);
+
+/* ------------------------------------------------------------------------ */
+/* Retrieval: scoring + top-k + chronological window layout                 */
+/* ------------------------------------------------------------------------ */
+typedef struct kvm_select_params {
+    uint32_t n_blocks;          /* blocks in the store (<= index capacity) */
+    uint32_t budget_blocks;     /* KvMemStore::budget_blocks() */
+    uint32_t sink_blocks;       /* always-kept prefix */
+    uint32_t recent_blocks;     /* always-kept suffix */
+    const uint32_t *mandatory;  /* device [n_mandatory], caller order (newest last), or NULL */
+    uint32_t n_mandatory;
+    const uint32_t *n_tokens;   /* device [n_blocks] tokens per block */
+} kvm_select_params;
+
+/* Device outputs of one retrieval.  info[0] = selected blocks, info[1] = total
+ * window tokens, info[2] = slots that need stage-in, info[3] = status (0 ok). */
+typedef struct kvm_selection {
+    uint32_t cap;               /* capacity of ids / to_base / stage_slots */
+    double *scores;             /* device [n_blocks] (score_retrieval output) */
+    uint32_t *ids;              /* device [cap], ascending block ids */
+    int32_t *to_base;           /* device [cap], window position of each block */
+    uint32_t *stage_slots;      /* device [cap], slots whose contents must be (re)staged */
+    uint32_t *info;             /* device [4] */
+} kvm_selection;
+
+/* score_retrieval (llama-memory-kvmem.cpp:4149-4196) + pick_topk_blocks
+ * (kvmem/src/host/kvmem_store.cpp:357-359, 482-623, TopK policy, no media ranges)
+ * + the window remap of set_selection (kvmem_store.cpp:758-882) with the
+ * chronological slot order of layout_gpu_slots_by_orig_pos
+ * (llama-memory-kvmem.cpp:1958-1993): slot k holds the k-th selected block at
+ * window position to_base[k].  When `w` is given, stage_slots lists the slots
+ * whose current (block, base) differs from the new layout.  Scores are
+ * bit-identical to the reference's host loop; ids are chosen by the strict
+ * order (score desc, block id desc).  n_blocks <= KVM_MAX_TOPK_BLOCKS. */
+int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
+                   const kvm_select_params *p, const kvm_window *w, const kvm_selection *out);
+
+/* Top-k + layout on caller-provided scores (KvMemStore::set_retrieval_scores,
+ * kvmem_store.cpp:242-248, then pick_topk_blocks as above): `scores` is a device
+ * double [p->n_blocks]; out->scores is not written. */
+int kvm_select_topk(kvm_state *st, const double *scores, const kvm_select_params *p,
+                    const kvm_window *w, const kvm_selection *out);
+
+/* ------------------------------------------------------------------------ */
+/* Stage-in: host history -> window, re-applying RoPE at the window position */
+/* ------------------------------------------------------------------------ */
+/* NeoX RoPE on the first n_rot dims, theta_i = freq_base^(-2i/n_rot) * freq_scale
+ * (kvmem/src/host/rope.cpp:8-45); hadamard_nrot > 0 applies the normalised
+ * Walsh-Hadamard transform in hadamard_nrot-wide chunks after RoPE
+ * (llama-kvmem-quant.h:22-36; 0 = off, -1 = the attn_rot default for the K type). */
+typedef struct kvm_rope_params {
+    uint32_t n_rot;
+    float freq_base;
+    float freq_scale;
+    int32_t hadamard_nrot;
+} kvm_rope_params;
+
+/* Host-resident (pinned) packed history of one layer: the raw (unrotated,
+ * pre-RoPE) K rows and the V rows in cache format, as RawKvStore keeps them
+ * (copy_k_gpu / copy_v_gpu, raw_kv_store.cpp:930-985). */
+typedef struct kvm_history {
+    const void *k_raw;          /* [n_tokens][n_head_kv * row(head_dim)] of window k_type */
+    const void *v;              /* [n_tokens][n_head_kv * row(head_dim)] of window v_type */
+    uint32_t n_tokens;
+} kvm_history;
+
+/* Stages every slot listed by kvm_score_topk's stage_slots: reads the block's
+ * raw K and V rows straight from pinned host memory, dequantises K, applies
+ * RoPE at to_base + t, the Walsh-Hadamard rotation and q8_0 requantisation
+ * (llama-kvmem-stagein.cu:731-786 order) and writes the tiled window; V bytes
+ * are moved unchanged (stagein.cu:733-744).  Updates cell_pos, slot_block and
+ * slot_base.  Replaces write_block_to_gpu + kvmem_stagein_flush
+ * (llama-memory-kvmem.cpp:4000-4071, stagein.cu:669-790) for one retrieval. */
+int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
+                          const kvm_selection *sel, const kvm_rope_params *rope);
+
+/* Item-at-a-time form with the reference's arguments
+ * (src/adapter/llama-kvmem-stagein.h:36-46).  `dst` is (window, first cell)
+ * instead of a raw cache pointer; packed rows are copied into the state's
+ * pinned slab, so the host buffer is free on return (stagein.h:23).  flush
+ * runs one fused launch over all queued items. */
+int kvm_stagein_enqueue_k(kvm_state *st, int type, const void *packed, size_t nbytes,
+                          const kvm_window *w, uint32_t cell0, int64_t nt, int64_t n_embd,
+                          int nrot, int n_head, int n_embd_head, int n_rot_rope, int32_t pos0,
+                          const float *theta, int n_theta);
+int kvm_stagein_enqueue_v(kvm_state *st, const void *packed, size_t nbytes,
+                          const kvm_window *w, uint32_t cell0, int64_t nt);
+int kvm_stagein_flush(kvm_state *st);
+
+/* ------------------------------------------------------------------------ */
+/* Flash attention over the window (ggml_flash_attn_ext as called by          */
+/* build_attn, patches/0002-attn-qk-capture-hook.patch:225,256)              */
+/* ------------------------------------------------------------------------ */
+/* q: device [n_tokens][n_head][head_dim] (KVM_TYPE_F32 or KVM_TYPE_BF16);
+ * q_pos: device int32 [n_tokens]; out: device fp32 [n_tokens][n_head][head_dim].
+ * Cell c is visible to token t iff 0 <= cell_pos[c] <= q_pos[t]
+ * (patches/0003-kv-cache-skip-hole-purge.patch:78-90).  Query head h reads kv
+ * head h / (n_head / n_head_kv).  A token with no visible cell outputs zeros.
+ * Decode form: n_tokens * (n_head / n_head_kv) <= 32 (MTP verify widths). */
+int kvm_fa_decode(kvm_state *st, const kvm_window *w, const void *q, int q_type,
+                  const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                  float *out);
+
+/* Several independent conversations in one launch sequence (multi-lane
+ * decode, docs/multi-lane-conversations.md:1-20). */
+typedef struct kvm_lane {
+    const kvm_window *w;
+    const void *q;
+    const int32_t *q_pos;
+    float *out;
+    uint32_t n_tokens;
+} kvm_lane;
+int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
+                        uint32_t n_head, float scale);
+
+/* Chunked prefill / long MTP verify: any n_tokens; same visibility rule. */
+int kvm_fa_prefill(kvm_state *st, const kvm_window *w, const void *q, int q_type,
+                   const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                   float *out);
+
+/* ------------------------------------------------------------------------ */
+/* Batched device copies (kvmem_d2d_batched, llama-kvmem-stagein.h:55-56).   */
+/* src/dst/nbytes: host arrays of n entries.                                  */
+/* ------------------------------------------------------------------------ */
+int kvm_d2d_batched(kvm_state *st, const void *const *src, void *const *dst,
+                    const size_t *nbytes, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KVM_HOTPATH_H */

@@ -1,0 +1,185 @@
+// kvm_internal.h -- shared definitions of the gfx950 hot-path library:
+// state object, error plumbing, the tiled window layout and small device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/kvm_hotpath.h"
+
+// ---------------------------------------------------------------------------
+// Execution state (one per execution domain; replaces kvmem_gpu_state,
+// src/adapter/llama-kvmem-stagein.cu:324-354).
+// ---------------------------------------------------------------------------
+struct kvm_stage_item {          // one queued enqueue_k / enqueue_v
+    uint32_t kind;               // 0 = K (re-RoPE chain), 1 = V (byte move)
+    uint32_t cell0;              // first window cell
+    uint32_t nt;                 // tokens
+    int32_t pos0;                // RoPE position of the first token (K)
+    uint64_t off;                // byte offset of the packed rows in the slab
+    kvm_window w;                // destination window
+    uint32_t n_rot;              // RoPE dims (K)
+    int32_t nrot;                // Hadamard width, 0 = off (K)
+};
+
+struct kvm_state {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string err;
+    // growable device workspace (attention partials, top-k scratch, tables)
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    // RoPE cos/sin table: [n_pos][n_rot/2] float2, generated on the host
+    float2 *rope_tab = nullptr;
+    size_t rope_tab_bytes = 0;
+    uint32_t rope_n_pos = 0, rope_n_half = 0;
+    std::vector<float> rope_theta;  // theta_i the current table was built from
+    // pinned slab for the enqueue/flush API (32 MiB like the reference's slab)
+    uint8_t *slab = nullptr;
+    size_t slab_bytes = 0, slab_used = 0;
+    bool slab_busy = false;      // a flush's kernels may still read the slab
+    std::vector<kvm_stage_item> items;
+    std::vector<float> theta;    // theta of the queued K items
+    // small device buffer for item descriptors / lane tables
+    void *desc = nullptr;
+    size_t desc_bytes = 0;
+    hipEvent_t ev = nullptr;
+};
+
+// error helpers ----------------------------------------------------------------
+int kvm_fail(kvm_state *st, int code, const char *fmt, ...);
+#define KVM_HIP(st, expr)                                                          \
+    do {                                                                           \
+        hipError_t e__ = (expr);                                                   \
+        if (e__ != hipSuccess)                                                     \
+            return kvm_fail((st), KVM_EHIP, "%s: %s", #expr, hipGetErrorString(e__)); \
+    } while (0)
+#define KVM_LAUNCH_CHECK(st, what)                                                 \
+    do {                                                                           \
+        hipError_t e__ = hipGetLastError();                                        \
+        if (e__ != hipSuccess)                                                     \
+            return kvm_fail((st), KVM_EHIP, "%s launch: %s", (what), hipGetErrorString(e__)); \
+    } while (0)
+
+// Ensures the state's workspace holds at least `bytes`; returns it or nullptr.
+void *kvm_workspace(kvm_state *st, size_t bytes);
+// Ensures a device copy of `bytes` of descriptor data; returns the device pointer.
+void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes);
+// theta_i = powf(base, -2i/n_rot) * scale for i < n_rot/2 (kvmem/src/host/rope.cpp:19-22)
+std::vector<float> kvm_rope_theta(float freq_base, float freq_scale, uint32_t n_rot);
+// Ensures the (cos, sin) table for `theta` covers positions [0, n_pos).
+int kvm_rope_table(kvm_state *st, const float *theta, uint32_t n_half, uint32_t n_pos);
+
+// ---------------------------------------------------------------------------
+// Tiled window layout.  Per kv head, cells are grouped in tiles of 64; the K
+// and V of one (head, tile) are contiguous and ordered as the attention
+// kernel's matrix-core operands are loaded, so every wave load is a fully
+// coalesced 16-byte-per-lane access.
+//
+// q8_0 K tile (head_dim D, NB = D/32 blocks):
+//   quants  64*D bytes: [sub 4][pair NB/2][lane 64][16 B]; lane l = 16g + m
+//           holds key 16*sub + m, dims 32*(2p)+8g..+7 then 32*(2p+1)+8g..+7
+//   scales  64*NB fp16: [sub 4][g 4][block NB][i 4] = key 16*sub + 4g + i
+// q4_0 V tile:
+//   nibbles D*32 bytes: [dim D][64 nibbles] with key c = 32ks + 8g + j stored at
+//           nibble 8*(2g+ks)+j (byte /2, low nibble when even)
+//   scales  NB*64 fp16: [block NB][ks 2][g 4][j 8]
+// f16 K tile: [sub 4][kstep D/32][lane 64][8 halves] = key 16*sub+m, dims 32ks+8g..+7
+// f16 V tile: [dim D][64 halves] in the same key order as the q4_0 nibbles.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline uint32_t kvm_ktile_bytes(int ktype, uint32_t D) {
+    return ktype == KVM_TYPE_Q8_0 ? 64u * D + 64u * (D / 32u) * 2u : 64u * D * 2u;
+}
+__host__ __device__ inline uint32_t kvm_vtile_bytes(int vtype, uint32_t D) {
+    return vtype == KVM_TYPE_Q4_0 ? D * 32u + (D / 32u) * 64u * 2u : 64u * D * 2u;
+}
+// byte offset, inside a q8_0 K tile, of quant (cell c in [0,64), dim d)
+__host__ __device__ inline uint32_t kvm_kq_off(uint32_t D, uint32_t c, uint32_t d) {
+    const uint32_t s = c >> 4, m = c & 15u, b = d >> 5, g = (d & 31u) >> 3, j = d & 7u;
+    const uint32_t l = 16u * g + m;
+    return (((s * (D / 64u) + (b >> 1)) * 64u + l) << 4) + (b & 1u) * 8u + j;
+}
+// byte offset of the fp16 scale of (cell c, block b) inside a q8_0 K tile
+__host__ __device__ inline uint32_t kvm_kd_off(uint32_t D, uint32_t c, uint32_t b) {
+    const uint32_t s = c >> 4, g = (c & 15u) >> 2, i = c & 3u;
+    return 64u * D + ((((s * 4u + g) * (D / 32u) + b) * 4u + i) << 1);
+}
+// nibble position (0..63) of cell c inside a V dim row
+__host__ __device__ inline uint32_t kvm_vkey_pos(uint32_t c) {
+    const uint32_t ks = c >> 5, g = (c & 31u) >> 3, j = c & 7u;
+    return 8u * (2u * g + ks) + j;
+}
+__host__ __device__ inline uint32_t kvm_vd_off(uint32_t D, uint32_t c, uint32_t b) {
+    const uint32_t ks = c >> 5, g = (c & 31u) >> 3, j = c & 7u;
+    return D * 32u + ((((b * 2u + ks) * 4u + g) * 8u + j) << 1);
+}
+// f16 K tile: half index of (cell c, dim d)
+__host__ __device__ inline uint32_t kvm_kh_idx(uint32_t D, uint32_t c, uint32_t d) {
+    const uint32_t s = c >> 4, m = c & 15u, ks = d >> 5, g = (d & 31u) >> 3, j = d & 7u;
+    return ((s * (D / 32u) + ks) * 64u + 16u * g + m) * 8u + j;
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef int32_t kvm_i32x4 __attribute__((ext_vector_type(4)));
+typedef float kvm_f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 kvm_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 kvm_f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 kvm_f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ inline float kvm_h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+// IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode)
+__device__ inline uint16_t kvm_f2h(float f) {
+    _Float16 v = (_Float16)f;
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+__device__ inline float kvm_bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// q8_0 / q4_0 block quantisers with the reference kernels' exact arithmetic
+// (llama-kvmem-stagein.cu:181-234): fp32 amax, d = amax/127 (q8) or vmax/-8
+// (q4), id = d ? 1/d : 0, fp16 d with RNE, roundf (ties away) / (int)(x*id+8.5).
+// Division and reciprocal are correctly rounded (__fdiv_rn) to match host IEEE.
+__device__ inline void kvm_quant_block_q8_0(const float *x, uint16_t *d_out, int8_t *q) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    *d_out = kvm_f2h(d);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) q[j] = (int8_t)roundf(__fmul_rn(x[j], id));
+}
+__device__ inline void kvm_quant_block_q4_0(const float *x, uint16_t *d_out, uint8_t *q) {
+    float amax = 0.0f, vmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const float a = fabsf(x[j]);
+        if (amax < a) { amax = a; vmax = x[j]; }
+    }
+    const float d = __fdiv_rn(vmax, -8.0f);
+    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    *d_out = kvm_f2h(d);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        int x0 = (int)__fadd_rn(__fmul_rn(x[j], id), 8.5f);
+        int x1 = (int)__fadd_rn(__fmul_rn(x[j + 16], id), 8.5f);
+        x0 = x0 > 15 ? 15 : x0;
+        x1 = x1 > 15 ? 15 : x1;
+        q[j] = (uint8_t)((x0 & 15) | ((x1 & 15) << 4));
+    }
+}
+
+inline uint32_t kvm_cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }

@@ -1,0 +1,433 @@
+// kvm_window.hip -- window geometry, ggml-row <-> tiled-window conversion,
+// row codecs and batched device copies.
+#include "kvm_internal.h"
+
+#include <algorithm>
+
+// ---------------------------------------------------------------------------
+// geometry
+// ---------------------------------------------------------------------------
+extern "C" int kvm_window_check(const kvm_window *w) {
+    if (!w) return KVM_EINVAL;
+    if (w->n_cells == 0 || w->n_cells % KVM_TILE_CELLS) return KVM_EINVAL;
+    if (w->head_dim != 128 && w->head_dim != 256) return KVM_EUNSUPPORTED;
+    if (w->n_head_kv == 0 || w->block_tokens == 0 || w->n_cells % w->block_tokens) return KVM_EINVAL;
+    const bool q = w->k_type == KVM_TYPE_Q8_0 && w->v_type == KVM_TYPE_Q4_0;
+    const bool h = w->k_type == KVM_TYPE_F16 && w->v_type == KVM_TYPE_F16;
+    if (!q && !h) return KVM_EUNSUPPORTED;
+    if (!w->k || !w->v || !w->cell_pos) return KVM_EINVAL;
+    return KVM_OK;
+}
+
+extern "C" size_t kvm_window_k_bytes(const kvm_window *w) {
+    if (!w || w->n_cells % KVM_TILE_CELLS) return 0;
+    return (size_t)w->n_head_kv * (w->n_cells / KVM_TILE_CELLS) * kvm_ktile_bytes(w->k_type, w->head_dim);
+}
+
+extern "C" size_t kvm_window_v_bytes(const kvm_window *w) {
+    if (!w || w->n_cells % KVM_TILE_CELLS) return 0;
+    return (size_t)w->n_head_kv * (w->n_cells / KVM_TILE_CELLS) * kvm_vtile_bytes(w->v_type, w->head_dim);
+}
+
+__global__ void k_fill_i32(int32_t *p, int32_t v, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+extern "C" int kvm_window_reset(kvm_state *st, const kvm_window *w) {
+    if (!st) return KVM_EINVAL;
+    int rc = kvm_window_check(w);
+    if (rc) return kvm_fail(st, rc, "window_reset: bad window");
+    KVM_HIP(st, hipSetDevice(st->device));
+    hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(w->n_cells, 256)), dim3(256), 0, st->stream,
+                       w->cell_pos, -1, w->n_cells);
+    const uint32_t n_slots = w->n_cells / w->block_tokens;
+    if (w->slot_block)
+        hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
+                           (int32_t *)w->slot_block, -1, n_slots);
+    if (w->slot_base)
+        hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
+                           w->slot_base, -1, n_slots);
+    KVM_LAUNCH_CHECK(st, "window_reset");
+    return KVM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// ggml rows -> tiled window
+// ---------------------------------------------------------------------------
+struct win_geo {
+    uint8_t *k, *v;
+    uint32_t H, D, n_tiles, ktile, vtile;
+};
+
+static win_geo geo_of(const kvm_window *w) {
+    win_geo g;
+    g.k = (uint8_t *)w->k;
+    g.v = (uint8_t *)w->v;
+    g.H = w->n_head_kv;
+    g.D = w->head_dim;
+    g.n_tiles = w->n_cells / KVM_TILE_CELLS;
+    g.ktile = kvm_ktile_bytes(w->k_type, w->head_dim);
+    g.vtile = kvm_vtile_bytes(w->v_type, w->head_dim);
+    return g;
+}
+
+// one thread per (cell, head, 32-dim block) of q8_0 K rows
+__global__ void k_import_k_q8(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    const uint8_t *src = rows + ((uint64_t)t * g.H + h) * NB * 34 + (uint64_t)b * 34;
+    uint8_t *dst = g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile;
+#pragma unroll
+    for (uint32_t gg = 0; gg < 4; ++gg) {
+        uint8_t *q = dst + kvm_kq_off(g.D, c, 32 * b + 8 * gg);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = src[2 + 8 * gg + j];
+    }
+    uint8_t *sd = dst + kvm_kd_off(g.D, c, b);
+    sd[0] = src[0];
+    sd[1] = src[1];
+}
+
+// f16 K rows: one thread per (cell, head, dim)
+__global__ void k_import_k_f16(win_geo g, uint32_t cell0, uint32_t n, const uint16_t *rows) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * g.D) return;
+    const uint32_t d = i % g.D, h = (i / g.D) % g.H, t = (uint32_t)(i / ((uint64_t)g.D * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    uint16_t *dst = (uint16_t *)(g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile);
+    dst[kvm_kh_idx(g.D, c, d)] = rows[((uint64_t)t * g.H + h) * g.D + d];
+}
+
+// q4_0 V nibbles: one thread per destination byte (head, tile, dim, byte) so the
+// two cells sharing a byte are written by one thread; cells outside
+// [cell0, cell0+n) keep their nibble.
+__global__ void k_import_v_q4(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint32_t t0 = cell0 / 64, t1 = (cell0 + n + 63) / 64;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)(t1 - t0) * g.H * g.D * 32) return;
+    const uint32_t kbyte = i % 32, d = (i / 32) % g.D, h = (i / (32ull * g.D)) % g.H;
+    const uint32_t tile = t0 + (uint32_t)(i / (32ull * g.D * g.H));
+    uint8_t *dst = g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile + d * 32 + kbyte;
+    uint8_t byte = *dst;
+    const uint32_t b = d / 32, e = d % 32;
+#pragma unroll
+    for (uint32_t half = 0; half < 2; ++half) {
+        const uint32_t pos = 2 * kbyte + half, q = pos / 8;
+        const uint32_t c = 32 * (q & 1) + 8 * (q >> 1) + (pos & 7);
+        const uint32_t cell = tile * 64 + c;
+        if (cell < cell0 || cell >= cell0 + n) continue;
+        const uint8_t *blk = rows + ((uint64_t)(cell - cell0) * g.H + h) * NB * 18 + (uint64_t)b * 18;
+        const uint8_t nib = e < 16 ? (blk[2 + e] & 15) : (blk[2 + e - 16] >> 4);
+        byte = half ? (uint8_t)((byte & 0x0f) | (nib << 4)) : (uint8_t)((byte & 0xf0) | nib);
+    }
+    *dst = byte;
+}
+
+__global__ void k_import_v_q4_scales(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    const uint8_t *blk = rows + ((uint64_t)t * g.H + h) * NB * 18 + (uint64_t)b * 18;
+    uint8_t *dst = g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile + kvm_vd_off(g.D, c, b);
+    dst[0] = blk[0];
+    dst[1] = blk[1];
+}
+
+__global__ void k_import_v_f16(win_geo g, uint32_t cell0, uint32_t n, const uint16_t *rows) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * g.D) return;
+    const uint32_t d = i % g.D, h = (i / g.D) % g.H, t = (uint32_t)(i / ((uint64_t)g.D * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    uint16_t *dst = (uint16_t *)(g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile);
+    dst[d * 64 + kvm_vkey_pos(c)] = rows[((uint64_t)t * g.H + h) * g.D + d];
+}
+
+__global__ void k_copy_i32(int32_t *dst, const int32_t *src, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0,
+                                      uint32_t n, const void *k_rows, const void *v_rows,
+                                      const int32_t *pos) {
+    if (!st) return KVM_EINVAL;
+    int rc = kvm_window_check(w);
+    if (rc) return kvm_fail(st, rc, "import_rows: bad window");
+    if ((uint64_t)cell0 + n > w->n_cells) return kvm_fail(st, KVM_ERANGE, "import_rows: cells past window");
+    if (n == 0) return KVM_OK;
+    KVM_HIP(st, hipSetDevice(st->device));
+    const win_geo g = geo_of(w);
+    const uint32_t NB = g.D / 32;
+    if (k_rows) {
+        if (w->k_type == KVM_TYPE_Q8_0) {
+            const uint64_t nt = (uint64_t)n * g.H * NB;
+            hipLaunchKernelGGL(k_import_k_q8, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (const uint8_t *)k_rows);
+        } else {
+            const uint64_t nt = (uint64_t)n * g.H * g.D;
+            hipLaunchKernelGGL(k_import_k_f16, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (const uint16_t *)k_rows);
+        }
+    }
+    if (v_rows) {
+        if (w->v_type == KVM_TYPE_Q4_0) {
+            const uint32_t t0 = cell0 / 64, t1 = (cell0 + n + 63) / 64;
+            const uint64_t nb = (uint64_t)(t1 - t0) * g.H * g.D * 32;
+            hipLaunchKernelGGL(k_import_v_q4, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (const uint8_t *)v_rows);
+            const uint64_t ns = (uint64_t)n * g.H * NB;
+            hipLaunchKernelGGL(k_import_v_q4_scales, dim3(kvm_cdiv(ns, 256)), dim3(256), 0, st->stream, g,
+                               cell0, n, (const uint8_t *)v_rows);
+        } else {
+            const uint64_t nt = (uint64_t)n * g.H * g.D;
+            hipLaunchKernelGGL(k_import_v_f16, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (const uint16_t *)v_rows);
+        }
+    }
+    if (pos)
+        hipLaunchKernelGGL(k_copy_i32, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream,
+                           w->cell_pos + cell0, pos, n);
+    KVM_LAUNCH_CHECK(st, "import_rows");
+    return KVM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// tiled window -> ggml rows
+// ---------------------------------------------------------------------------
+__global__ void k_export_k_q8(win_geo g, uint32_t cell0, uint32_t n, uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    uint8_t *dst = rows + ((uint64_t)t * g.H + h) * NB * 34 + (uint64_t)b * 34;
+    const uint8_t *src = g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile;
+    const uint8_t *sd = src + kvm_kd_off(g.D, c, b);
+    dst[0] = sd[0];
+    dst[1] = sd[1];
+#pragma unroll
+    for (uint32_t gg = 0; gg < 4; ++gg) {
+        const uint8_t *q = src + kvm_kq_off(g.D, c, 32 * b + 8 * gg);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[2 + 8 * gg + j] = q[j];
+    }
+}
+
+__global__ void k_export_v_q4(win_geo g, uint32_t cell0, uint32_t n, uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    uint8_t *dst = rows + ((uint64_t)t * g.H + h) * NB * 18 + (uint64_t)b * 18;
+    const uint8_t *src = g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile;
+    const uint8_t *sd = src + kvm_vd_off(g.D, c, b);
+    dst[0] = sd[0];
+    dst[1] = sd[1];
+    const uint32_t pos = kvm_vkey_pos(c);
+    for (uint32_t e = 0; e < 16; ++e) {
+        const uint8_t lo = src[(32 * b + e) * 32 + pos / 2];
+        const uint8_t hi = src[(32 * b + e + 16) * 32 + pos / 2];
+        const uint8_t n0 = (pos & 1) ? (lo >> 4) : (lo & 15);
+        const uint8_t n1 = (pos & 1) ? (hi >> 4) : (hi & 15);
+        dst[2 + e] = (uint8_t)(n0 | (n1 << 4));
+    }
+}
+
+__global__ void k_export_f16(win_geo g, uint32_t cell0, uint32_t n, uint16_t *krows, uint16_t *vrows) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * g.D) return;
+    const uint32_t d = i % g.D, h = (i / g.D) % g.H, t = (uint32_t)(i / ((uint64_t)g.D * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    if (krows) {
+        const uint16_t *src = (const uint16_t *)(g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile);
+        krows[((uint64_t)t * g.H + h) * g.D + d] = src[kvm_kh_idx(g.D, c, d)];
+    }
+    if (vrows) {
+        const uint16_t *src = (const uint16_t *)(g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile);
+        vrows[((uint64_t)t * g.H + h) * g.D + d] = src[d * 64 + kvm_vkey_pos(c)];
+    }
+}
+
+extern "C" int kvm_window_export_rows(kvm_state *st, const kvm_window *w, uint32_t cell0,
+                                      uint32_t n, void *k_rows, void *v_rows) {
+    if (!st) return KVM_EINVAL;
+    int rc = kvm_window_check(w);
+    if (rc) return kvm_fail(st, rc, "export_rows: bad window");
+    if ((uint64_t)cell0 + n > w->n_cells) return kvm_fail(st, KVM_ERANGE, "export_rows: cells past window");
+    if (n == 0) return KVM_OK;
+    KVM_HIP(st, hipSetDevice(st->device));
+    const win_geo g = geo_of(w);
+    const uint32_t NB = g.D / 32;
+    if (w->k_type == KVM_TYPE_Q8_0) {
+        const uint64_t nt = (uint64_t)n * g.H * NB;
+        if (k_rows)
+            hipLaunchKernelGGL(k_export_k_q8, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (uint8_t *)k_rows);
+        if (v_rows)
+            hipLaunchKernelGGL(k_export_v_q4, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (uint8_t *)v_rows);
+    } else {
+        const uint64_t nt = (uint64_t)n * g.H * g.D;
+        hipLaunchKernelGGL(k_export_f16, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                           (uint16_t *)k_rows, (uint16_t *)v_rows);
+    }
+    KVM_LAUNCH_CHECK(st, "export_rows");
+    return KVM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// row codecs: one thread per 32-value block
+// ---------------------------------------------------------------------------
+__global__ void k_quant_q8(const float *x, uint8_t *y, uint64_t nblk) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = x[i * 32 + j];
+    uint16_t d;
+    int8_t q[32];
+    kvm_quant_block_q8_0(v, &d, q);
+    uint8_t *o = y + i * 34;
+    o[0] = (uint8_t)d;
+    o[1] = (uint8_t)(d >> 8);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)q[j];
+}
+
+__global__ void k_quant_q4(const float *x, uint8_t *y, uint64_t nblk) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = x[i * 32 + j];
+    uint16_t d;
+    uint8_t q[16];
+    kvm_quant_block_q4_0(v, &d, q);
+    uint8_t *o = y + i * 18;
+    o[0] = (uint8_t)d;
+    o[1] = (uint8_t)(d >> 8);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[2 + j] = q[j];
+}
+
+__global__ void k_quant_f16(const float *x, uint16_t *y, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = kvm_f2h(x[i]);
+}
+
+__global__ void k_dequant_q8(const uint8_t *x, float *y, uint64_t nblk) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint8_t *b = x + i * 34;
+    const float d = kvm_h2f((uint16_t)(b[0] | (b[1] << 8)));
+#pragma unroll
+    for (int j = 0; j < 32; ++j) y[i * 32 + j] = (float)(int8_t)b[2 + j] * d;
+}
+
+__global__ void k_dequant_q4(const uint8_t *x, float *y, uint64_t nblk) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint8_t *b = x + i * 18;
+    const float d = kvm_h2f((uint16_t)(b[0] | (b[1] << 8)));
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        y[i * 32 + j] = (float)((b[2 + j] & 15) - 8) * d;
+        y[i * 32 + j + 16] = (float)((b[2 + j] >> 4) - 8) * d;
+    }
+}
+
+__global__ void k_dequant_f16(const uint16_t *x, float *y, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = kvm_h2f(x[i]);
+}
+
+extern "C" int kvm_quantize_rows(kvm_state *st, int type, const float *src, void *dst,
+                                 int64_t n_rows, int64_t n_per_row) {
+    if (!st || !src || !dst || n_rows < 0 || n_per_row <= 0) return kvm_fail(st, KVM_EINVAL, "quantize_rows: args");
+    if (n_rows == 0) return KVM_OK;
+    KVM_HIP(st, hipSetDevice(st->device));
+    const uint64_t n = (uint64_t)n_rows * (uint64_t)n_per_row;
+    if (type == KVM_TYPE_Q8_0 || type == KVM_TYPE_Q4_0) {
+        if (n_per_row % 32) return kvm_fail(st, KVM_EINVAL, "quantize_rows: row not a multiple of 32");
+        const uint64_t nb = n / 32;
+        if (type == KVM_TYPE_Q8_0)
+            hipLaunchKernelGGL(k_quant_q8, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, src, (uint8_t *)dst, nb);
+        else
+            hipLaunchKernelGGL(k_quant_q4, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, src, (uint8_t *)dst, nb);
+    } else if (type == KVM_TYPE_F16) {
+        hipLaunchKernelGGL(k_quant_f16, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream, src, (uint16_t *)dst, n);
+    } else {
+        return kvm_fail(st, KVM_EUNSUPPORTED, "quantize_rows: type %d", type);
+    }
+    KVM_LAUNCH_CHECK(st, "quantize_rows");
+    return KVM_OK;
+}
+
+extern "C" int kvm_dequantize_rows(kvm_state *st, int type, const void *src, float *dst,
+                                   int64_t n_rows, int64_t n_per_row) {
+    if (!st || !src || !dst || n_rows < 0 || n_per_row <= 0) return kvm_fail(st, KVM_EINVAL, "dequantize_rows: args");
+    if (n_rows == 0) return KVM_OK;
+    KVM_HIP(st, hipSetDevice(st->device));
+    const uint64_t n = (uint64_t)n_rows * (uint64_t)n_per_row;
+    if (type == KVM_TYPE_Q8_0 || type == KVM_TYPE_Q4_0) {
+        if (n_per_row % 32) return kvm_fail(st, KVM_EINVAL, "dequantize_rows: row not a multiple of 32");
+        const uint64_t nb = n / 32;
+        if (type == KVM_TYPE_Q8_0)
+            hipLaunchKernelGGL(k_dequant_q8, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, (const uint8_t *)src, dst, nb);
+        else
+            hipLaunchKernelGGL(k_dequant_q4, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, (const uint8_t *)src, dst, nb);
+    } else if (type == KVM_TYPE_F16) {
+        hipLaunchKernelGGL(k_dequant_f16, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream, (const uint16_t *)src, dst, n);
+    } else {
+        return kvm_fail(st, KVM_EUNSUPPORTED, "dequantize_rows: type %d", type);
+    }
+    KVM_LAUNCH_CHECK(st, "dequantize_rows");
+    return KVM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// batched device copies (kvmem_d2d_batched / copy_bytes, stagein.cu:236-261)
+// ---------------------------------------------------------------------------
+struct kvm_copy_op {
+    const uint8_t *src;
+    uint8_t *dst;
+    uint64_t nbytes;
+};
+
+__global__ void k_copy_ops(const kvm_copy_op *ops, int n) {
+    const int i = blockIdx.x;
+    if (i >= n) return;
+    const kvm_copy_op op = ops[i];
+    if (!op.src || !op.dst || op.nbytes == 0) return;
+    const uintptr_t a = (uintptr_t)op.src | (uintptr_t)op.dst;
+    if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
+        const uint4 *s = (const uint4 *)op.src;
+        uint4 *d = (uint4 *)op.dst;
+        for (uint64_t j = threadIdx.x; j < op.nbytes / 16; j += blockDim.x) d[j] = s[j];
+        return;
+    }
+    for (uint64_t j = threadIdx.x; j < op.nbytes; j += blockDim.x) op.dst[j] = op.src[j];
+}
+
+extern "C" int kvm_d2d_batched(kvm_state *st, const void *const *src, void *const *dst,
+                               const size_t *nbytes, int n) {
+    if (!st || n < 0 || (n > 0 && (!src || !dst || !nbytes))) return kvm_fail(st, KVM_EINVAL, "d2d_batched: args");
+    if (n == 0) return KVM_OK;
+    if (n > 65535) return kvm_fail(st, KVM_ERANGE, "d2d_batched: %d ops > 65535", n);
+    KVM_HIP(st, hipSetDevice(st->device));
+    std::vector<kvm_copy_op> ops((size_t)n);
+    for (int i = 0; i < n; ++i) ops[i] = {(const uint8_t *)src[i], (uint8_t *)dst[i], (uint64_t)nbytes[i]};
+    void *d = kvm_upload_desc(st, ops.data(), ops.size() * sizeof(kvm_copy_op));
+    if (!d) return kvm_fail(st, KVM_ENOMEM, "d2d_batched: descriptor upload");
+    hipLaunchKernelGGL(k_copy_ops, dim3(n), dim3(256), 0, st->stream, (const kvm_copy_op *)d, n);
+    KVM_LAUNCH_CHECK(st, "d2d_batched");
+    return KVM_OK;
+}

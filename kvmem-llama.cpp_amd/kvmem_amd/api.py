@@ -1,0 +1,293 @@
+"""Host-side mirror of the KVMem hot-path interface over libkvm_hotpath.so.
+
+PyTorch is used only for device memory and the stream; every computation is a
+kernel of libkvm_hotpath.so.  Names follow the reference's domain: a window is
+the bounded GPU slot pool of one attention layer (llama-memory-kvmem.cpp:611-779),
+the mean-K index is RawKvStore's per-block K sums (raw_kv_store.cpp:215-234),
+the query accumulator is the adapter's q_sum_/q_count_ (llama-memory-kvmem.cpp:3300-3315).
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+class State:
+    """One execution domain (kvmem_gpu_state, llama-kvmem-stagein.h:12-15)."""
+
+    def __init__(self, device=0, stream=None):
+        self.lib = L.load()
+        self.device = device
+        self.h = self.lib.kvm_state_create(device)
+        if not self.h:
+            raise L.KvmError(L.KVM_EHIP, f"kvm_state_create({device}) failed")
+        s = stream if stream is not None else torch.cuda.current_stream(device).cuda_stream
+        self.check(self.lib.kvm_state_set_stream(self.h, C.c_void_p(s)))
+
+    def check(self, rc):
+        if rc != L.KVM_OK:
+            raise L.KvmError(rc, self.lib.kvm_state_last_error(self.h).decode())
+        return rc
+
+    def sync(self):
+        self.check(self.lib.kvm_state_sync(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.kvm_state_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HostBuffer:
+    """Pinned, device-mapped host memory (kvm_host_alloc) viewed as numpy."""
+
+    def __init__(self, nbytes):
+        self.lib = L.load()
+        self.nbytes = int(nbytes)
+        self.ptr = self.lib.kvm_host_alloc(self.nbytes)
+        if not self.ptr:
+            raise L.KvmError(L.KVM_ENOMEM, f"kvm_host_alloc({nbytes}) failed")
+        self.u8 = np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.ptr))
+
+    def close(self):
+        if self.ptr:
+            self.lib.kvm_host_free(C.c_void_p(self.ptr))
+            self.ptr = None
+            self.u8 = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def row_bytes(ty, n):
+    return {L.T_F32: 4 * n, L.T_F16: 2 * n, L.T_Q8_0: n // 32 * 34, L.T_Q4_0: n // 32 * 18}[ty]
+
+
+class KVWindow:
+    """Bounded GPU window of one attention layer in the library's tiled layout."""
+
+    def __init__(self, st, n_cells, n_head_kv, head_dim, block_tokens=128,
+                 k_type=L.T_Q8_0, v_type=L.T_Q4_0):
+        self.st = st
+        dev = torch.device("cuda", st.device)
+        self.c = L.Window(n_cells, n_head_kv, head_dim, block_tokens, k_type, v_type)
+        kb = st.lib.kvm_window_k_bytes(C.byref(self.c))
+        vb = st.lib.kvm_window_v_bytes(C.byref(self.c))
+        if kb == 0 or vb == 0:
+            raise L.KvmError(L.KVM_EINVAL, "bad window geometry")
+        self.k = torch.zeros(kb, dtype=torch.uint8, device=dev)
+        self.v = torch.zeros(vb, dtype=torch.uint8, device=dev)
+        self.cell_pos = torch.full((n_cells,), -1, dtype=torch.int32, device=dev)
+        n_slots = n_cells // block_tokens
+        self.slot_block = torch.full((n_slots,), -1, dtype=torch.int32, device=dev)
+        self.slot_base = torch.full((n_slots,), -1, dtype=torch.int32, device=dev)
+        self.c.k, self.c.v = self.k.data_ptr(), self.v.data_ptr()
+        self.c.cell_pos = self.cell_pos.data_ptr()
+        self.c.slot_block = self.slot_block.data_ptr()
+        self.c.slot_base = self.slot_base.data_ptr()
+        st.check(st.lib.kvm_window_check(C.byref(self.c)))
+        self.n_cells, self.n_head_kv, self.head_dim = n_cells, n_head_kv, head_dim
+        self.block_tokens, self.k_type, self.v_type = block_tokens, k_type, v_type
+
+    @property
+    def bytes(self):
+        return self.k.numel() + self.v.numel()
+
+    def k_row_bytes(self):
+        return self.n_head_kv * row_bytes(self.k_type, self.head_dim)
+
+    def v_row_bytes(self):
+        return self.n_head_kv * row_bytes(self.v_type, self.head_dim)
+
+    def reset(self):
+        self.st.check(self.st.lib.kvm_window_reset(self.st.h, C.byref(self.c)))
+
+    def import_rows(self, cell0, k_rows, v_rows, pos=None):
+        """k_rows / v_rows: uint8 device tensors of ggml rows ([n][row bytes])."""
+        n = (k_rows if k_rows is not None else v_rows).shape[0]
+        self.st.check(self.st.lib.kvm_window_import_rows(
+            self.st.h, C.byref(self.c), cell0, n, _ptr(k_rows), _ptr(v_rows), _ptr(pos)))
+
+    def export_rows(self, cell0, n):
+        dev = self.k.device
+        kr = torch.empty((n, self.k_row_bytes()), dtype=torch.uint8, device=dev)
+        vr = torch.empty((n, self.v_row_bytes()), dtype=torch.uint8, device=dev)
+        self.st.check(self.st.lib.kvm_window_export_rows(
+            self.st.h, C.byref(self.c), cell0, n, _ptr(kr), _ptr(vr)))
+        return kr, vr
+
+
+class MeanKIndex:
+    """Device mean-K index: ordered fp32 K sums + token counts per (layer, block)."""
+
+    def __init__(self, st, n_layer, n_blocks, n_head_kv, head_dim, block_tokens=128):
+        dev = torch.device("cuda", st.device)
+        self.st = st
+        self.k_sum = torch.zeros((n_layer, n_head_kv * head_dim, n_blocks), dtype=torch.float32, device=dev)
+        self.mean_tokens = torch.zeros((n_layer, n_blocks), dtype=torch.int32, device=dev)
+        self.present = torch.zeros((n_blocks,), dtype=torch.uint8, device=dev)
+        self.c = L.MeanKIndex(n_layer, n_blocks, n_head_kv, head_dim, block_tokens,
+                              self.k_sum.data_ptr(), self.mean_tokens.data_ptr(), self.present.data_ptr())
+
+    def add(self, il, pos0, k_rows):
+        """k_rows: device fp32 [n][n_head_kv*head_dim] of pre-RoPE K at positions pos0.."""
+        k_rows = k_rows.contiguous()
+        self.st.check(self.st.lib.kvm_meank_add(self.st.h, C.byref(self.c), il, pos0,
+                                                k_rows.shape[0], _ptr(k_rows)))
+
+
+class QueryAcc:
+    def __init__(self, st, n_layer, n_head, head_dim):
+        dev = torch.device("cuda", st.device)
+        self.st = st
+        self.q_sum = torch.zeros((n_layer, n_head * head_dim), dtype=torch.float32, device=dev)
+        self.q_count = torch.zeros((n_layer,), dtype=torch.int32, device=dev)
+        self.c = L.QueryAcc(n_layer, n_head, head_dim, self.q_sum.data_ptr(), self.q_count.data_ptr())
+
+    def reset(self):
+        self.st.check(self.st.lib.kvm_query_reset(self.st.h, C.byref(self.c)))
+
+    def add(self, il, q_rows):
+        q_rows = q_rows.contiguous()
+        self.st.check(self.st.lib.kvm_query_add(self.st.h, C.byref(self.c), il, _ptr(q_rows),
+                                                q_rows.shape[0]))
+
+
+class SelectionBuffers:
+    """Device outputs of one retrieval (scores, ascending ids, window layout, staging list)."""
+
+    def __init__(self, st, n_blocks, cap):
+        dev = torch.device("cuda", st.device)
+        self.scores = torch.zeros((max(n_blocks, 1),), dtype=torch.float64, device=dev)
+        self.ids = torch.zeros((cap,), dtype=torch.int32, device=dev)
+        self.to_base = torch.zeros((cap,), dtype=torch.int32, device=dev)
+        self.stage_slots = torch.zeros((cap,), dtype=torch.int32, device=dev)
+        self.info = torch.zeros((4,), dtype=torch.int32, device=dev)
+        self.c = L.Selection(cap, self.scores.data_ptr(), self.ids.data_ptr(), self.to_base.data_ptr(),
+                             self.stage_slots.data_ptr(), self.info.data_ptr())
+
+    def result(self):
+        info = self.info.cpu().numpy().astype(np.int64)
+        n = int(info[0])
+        return {"ids": self.ids[:n].cpu().numpy().astype(np.int64),
+                "to_base": self.to_base[:n].cpu().numpy().astype(np.int64),
+                "total": int(info[1]), "stage_slots": self.stage_slots[:int(info[2])].cpu().numpy(),
+                "status": int(info[3])}
+
+
+def score_topk(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks=1, recent_blocks=0,
+               mandatory=None, window=None, sel=None):
+    """n_tokens: device int32 [n_blocks]; mandatory: device int32 tensor or None."""
+    if sel is None:
+        cap = min(n_blocks, budget_blocks) if budget_blocks else n_blocks
+        sel = SelectionBuffers(st, n_blocks, max(cap, 1))
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks,
+                       None if mandatory is None else mandatory.data_ptr(),
+                       0 if mandatory is None else mandatory.numel(), n_tokens.data_ptr())
+    st.check(st.lib.kvm_score_topk(st.h, C.byref(index.c), C.byref(query.c), C.byref(p),
+                                   None if window is None else C.byref(window.c), C.byref(sel.c)))
+    return sel
+
+
+def select_topk(st, scores, n_tokens, budget_blocks, sink_blocks=1, recent_blocks=0, mandatory=None,
+                window=None, sel=None):
+    """Top-k + layout on given scores (device float64 [n_blocks])."""
+    n_blocks = scores.numel()
+    if sel is None:
+        cap = min(n_blocks, budget_blocks) if budget_blocks else n_blocks
+        sel = SelectionBuffers(st, n_blocks, max(cap, 1))
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks,
+                       None if mandatory is None else mandatory.data_ptr(),
+                       0 if mandatory is None else mandatory.numel(), n_tokens.data_ptr())
+    st.check(st.lib.kvm_select_topk(st.h, C.c_void_p(scores.data_ptr()), C.byref(p),
+                                    None if window is None else C.byref(window.c), C.byref(sel.c)))
+    return sel
+
+
+def stagein_selection(st, history, window, sel, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    st.check(st.lib.kvm_stagein_selection(st.h, C.byref(history.c), C.byref(window.c), C.byref(sel.c),
+                                          C.byref(r)))
+
+
+class History:
+    """Pinned host history of one layer: raw (pre-RoPE) K rows and V rows in cache format."""
+
+    def __init__(self, k_rows_np, v_rows_np):
+        n = k_rows_np.shape[0]
+        self.kbuf = HostBuffer(k_rows_np.nbytes)
+        self.vbuf = HostBuffer(v_rows_np.nbytes)
+        self.kbuf.u8[:] = np.ascontiguousarray(k_rows_np).reshape(-1).view(np.uint8)
+        self.vbuf.u8[:] = np.ascontiguousarray(v_rows_np).reshape(-1).view(np.uint8)
+        self.c = L.History(self.kbuf.ptr, self.vbuf.ptr, n)
+        self.n_tokens = n
+
+
+def fa_decode(st, window, q, q_pos, n_head, scale, out=None):
+    """q: device [n_tokens][n_head][head_dim] fp32 or bf16; q_pos: device int32 [n_tokens]."""
+    q = q.contiguous()
+    n_tokens = q.shape[0]
+    if out is None:
+        out = torch.empty((n_tokens, n_head, window.head_dim), dtype=torch.float32, device=q.device)
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    st.check(st.lib.kvm_fa_decode(st.h, C.byref(window.c), _ptr(q), qt, _ptr(q_pos), n_tokens, n_head,
+                                  float(scale), _ptr(out)))
+    return out
+
+
+def fa_prefill(st, window, q, q_pos, n_head, scale, out=None):
+    q = q.contiguous()
+    n_tokens = q.shape[0]
+    if out is None:
+        out = torch.empty((n_tokens, n_head, window.head_dim), dtype=torch.float32, device=q.device)
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    st.check(st.lib.kvm_fa_prefill(st.h, C.byref(window.c), _ptr(q), qt, _ptr(q_pos), n_tokens, n_head,
+                                   float(scale), _ptr(out)))
+    return out
+
+
+def fa_decode_lanes(st, windows, qs, q_poss, n_head, scale, outs=None):
+    n = len(windows)
+    if outs is None:
+        outs = [torch.empty((q.shape[0], n_head, w.head_dim), dtype=torch.float32, device=q.device)
+                for w, q in zip(windows, qs)]
+    lanes = (L.Lane * n)()
+    keep = []
+    for i, (w, q, qp, o) in enumerate(zip(windows, qs, q_poss, outs)):
+        q = q.contiguous()
+        keep.append(q)
+        lanes[i] = L.Lane(C.pointer(w.c), q.data_ptr(), qp.data_ptr(), o.data_ptr(), q.shape[0])
+    qt = L.T_BF16 if qs[0].dtype == torch.bfloat16 else L.T_F32
+    st.check(st.lib.kvm_fa_decode_lanes(st.h, lanes, n, qt, n_head, float(scale)))
+    return outs
+
+
+def quantize_rows(st, ty, x):
+    """x: device fp32 [n_rows][n_per_row] -> uint8 ggml rows."""
+    x = x.contiguous()
+    n_rows, n = x.shape
+    out = torch.empty((n_rows, row_bytes(ty, n)), dtype=torch.uint8, device=x.device)
+    st.check(st.lib.kvm_quantize_rows(st.h, ty, _ptr(x), _ptr(out), n_rows, n))
+    return out
+
+
+def dequantize_rows(st, ty, rows, n_per_row):
+    n_rows = rows.shape[0]
+    out = torch.empty((n_rows, n_per_row), dtype=torch.float32, device=rows.device)
+    st.check(st.lib.kvm_dequantize_rows(st.h, ty, _ptr(rows), _ptr(out), n_rows, n_per_row))
+    return out

@@ -1,0 +1,36 @@
+"""Shared helpers of the GPU parity tests (inputs are built on the CPU and the
+oracle computes the expected results)."""
+import numpy as np
+import torch
+
+import oracle as O
+from kvmem_amd import api, _lib as L
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def rand_rows(rng, n_cells, n_head_kv, d, kt, vt, scale=1.0):
+    """Random K / V rows in ggml cache format (and their fp32 sources)."""
+    k = (rng.standard_normal((n_cells, n_head_kv * d)) * scale).astype(np.float32)
+    v = rng.standard_normal((n_cells, n_head_kv * d)).astype(np.float32)
+
+    def enc(ty, x):
+        if ty == L.T_F16:
+            return x.astype(np.float16).view(np.uint8).reshape(n_cells, -1)
+        return O.quant(ty, x.reshape(-1)).reshape(n_cells, -1)
+    return enc(kt, k), enc(vt, v)
+
+
+def check_attention(out, ref, atol=2e-3, rtol=1e-3):
+    """max |out - ref| <= atol and <= rtol * max |ref|."""
+    err = float(np.abs(out - ref).max())
+    scale = float(np.abs(ref).max())
+    assert err <= atol, (err, scale)
+    assert err <= rtol * scale, (err, scale)
+    return err, scale

@@ -1,0 +1,110 @@
+"""GPU flash attention over the window against the ggml-semantics oracle
+(tolerance 2e-3 max-abs and 1e-3 relative to max |ref|) and the float64 anchor."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import check_attention, dev, host, rand_rows
+from kvmem_amd import api, _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _window(st, rng, n_cells, H, D, kt, vt, live=None, holes=0, kscale=1.0):
+    w = api.KVWindow(st, n_cells, H, D, 128, kt, vt)
+    kr, vr = rand_rows(rng, n_cells, H, D, kt, vt, kscale)
+    cp = np.arange(n_cells, dtype=np.int32)
+    if live is not None:
+        cp[live:] = -1
+    if holes:
+        cp[rng.choice(n_cells, holes, replace=False)] = -1
+    w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    return w, kr, vr, cp
+
+
+CASES = [
+    # n_cells, H, G, D, tokens, kt, vt, kscale
+    (4096, 4, 6, 256, 4, L.T_Q8_0, L.T_Q4_0, 1.0),      # MTP3 verify, 24 rows per kv head
+    (4096, 4, 6, 256, 1, L.T_Q8_0, L.T_Q4_0, 1.0),      # single decode token
+    (2048, 2, 4, 128, 1, L.T_F16, L.T_F16, 1.0),        # fp16 cache, head_dim 128
+    (2048, 2, 4, 128, 3, L.T_Q8_0, L.T_Q4_0, 3.0),      # peaked softmax
+    (1024, 4, 8, 256, 4, L.T_F16, L.T_F16, 2.0),        # 32 rows per kv head
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("qdt", ["f32", "bf16"])
+def test_fa_decode_parity(kvm_state, case, qdt):
+    n_cells, H, G, D, T, kt, vt, ks = CASES[case]
+    rng = np.random.default_rng(case)
+    w, kr, vr, cp = _window(kvm_state, rng, n_cells, H, D, kt, vt, live=n_cells - 100, holes=50, kscale=ks)
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    if qdt == "bf16":
+        qt = torch.from_numpy(q).to(torch.bfloat16)
+        q = qt.float().numpy()
+        qd = qt.cuda()
+    else:
+        qd = dev(q)
+    qp = np.arange(n_cells - 100 - T, n_cells - 100, dtype=np.int32)
+    scale = 1.0 / np.sqrt(D)
+    out = host(api.fa_decode(kvm_state, w, qd, dev(qp), H * G, scale))
+    ref = O.fa_ggml(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
+    check_attention(out, ref)
+    f64 = O.fa_f64(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
+    assert np.abs(out - f64).max() <= 3e-2 * np.abs(f64).max()
+
+
+def test_fa_decode_masks_and_empty_rows(kvm_state):
+    rng = np.random.default_rng(7)
+    H, G, D, n = 4, 6, 256, 1024
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, L.T_Q8_0, L.T_Q4_0)
+    q = rng.standard_normal((4, H * G, D)).astype(np.float32)
+    qp = np.array([-1, 0, 500, 1023], np.int32)          # token 0 sees nothing, token 1 sees cell 0
+    out = host(api.fa_decode(kvm_state, w, dev(q), dev(qp), H * G, 0.0625))
+    assert np.all(out[0] == 0)
+    V = O.dequant(O.T_Q4_0, vr[0].reshape(-1), H * D).reshape(H, D)
+    for h in range(H * G):
+        np.testing.assert_allclose(out[1, h], V[h // G], rtol=2e-3, atol=2e-3)
+    ref = O.fa_ggml(L.T_Q8_0, L.T_Q4_0, q, kr, vr, cp, qp, H * G, H, D, 0.0625)
+    check_attention(out, ref)
+
+
+def test_fa_decode_lanes_match_single_lane(kvm_state):
+    rng = np.random.default_rng(8)
+    H, G, D = 4, 6, 256
+    ws, qs, qps, refs = [], [], [], []
+    for i, n in enumerate((1024, 2048, 3072, 4096)):
+        w, kr, vr, cp = _window(kvm_state, rng, n, H, D, L.T_Q8_0, L.T_Q4_0)
+        q = rng.standard_normal((1, H * G, D)).astype(np.float32)
+        qp = np.array([n - 1], np.int32)
+        ws.append(w)
+        qs.append(dev(q))
+        qps.append(dev(qp))
+        refs.append(host(api.fa_decode(kvm_state, w, dev(q), dev(qp), H * G, 0.0625)))
+    outs = api.fa_decode_lanes(kvm_state, ws, qs, qps, H * G, 0.0625)
+    for o, r in zip(outs, refs):
+        assert np.array_equal(host(o), r)
+
+
+def test_fa_prefill_chunked_causal(kvm_state):
+    rng = np.random.default_rng(9)
+    H, G, D, n_win, T = 4, 6, 256, 2048, 40
+    w, kr, vr, cp = _window(kvm_state, rng, n_win + 64, H, D, L.T_Q8_0, L.T_Q4_0, live=n_win)
+    kc, vc = rand_rows(rng, T, H, D, L.T_Q8_0, L.T_Q4_0)
+    pos = np.arange(n_win, n_win + T, dtype=np.int32)
+    w.import_rows(n_win, dev(kc), dev(vc), dev(pos))           # the chunk's own K/V
+    kr[n_win:n_win + T], vr[n_win:n_win + T] = kc, vc
+    cp[n_win:n_win + T] = pos
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    out = host(api.fa_prefill(kvm_state, w, dev(q), dev(pos), H * G, 0.0625))
+    ref = O.fa_ggml(L.T_Q8_0, L.T_Q4_0, q, kr, vr, cp, pos, H * G, H, D, 0.0625)
+    check_attention(out, ref)
+
+
+def test_fa_decode_rejects_wide_batches(kvm_state):
+    rng = np.random.default_rng(10)
+    w, *_ = _window(kvm_state, rng, 256, 4, 256, L.T_Q8_0, L.T_Q4_0)
+    q = dev(np.zeros((6, 24, 256), np.float32))
+    with pytest.raises(L.KvmError):
+        api.fa_decode(kvm_state, w, q, dev(np.zeros(6, np.int32)), 24, 0.0625)

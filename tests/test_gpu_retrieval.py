@@ -1,0 +1,151 @@
+"""GPU retrieval: query accumulator, mean-K sums, scoring (bit-exact), top-k and
+window layout against the oracle and the reference's top-k known answers."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import dev, host
+from kvmem_amd import api, _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def test_query_add_bit_exact(kvm_state):
+    rng = np.random.default_rng(1)
+    qa = api.QueryAcc(kvm_state, 2, 24, 256)
+    qa.reset()
+    rows0 = rng.standard_normal((4, 24 * 256)).astype(np.float32)
+    rows1 = (rng.standard_normal((3, 24 * 256)) * 1e4).astype(np.float32)
+    qa.add(0, dev(rows0))
+    qa.add(1, dev(rows1[:1]))
+    qa.add(1, dev(rows1[1:]))
+    want0 = np.zeros(24 * 256, np.float32)
+    for r in rows0:
+        want0 = (want0 + r).astype(np.float32)
+    want1 = np.zeros(24 * 256, np.float32)
+    for r in rows1:
+        want1 = (want1 + r).astype(np.float32)
+    got = host(qa.q_sum)
+    assert np.array_equal(got[0].view(np.uint32), want0.view(np.uint32))
+    assert np.array_equal(got[1].view(np.uint32), want1.view(np.uint32))
+    assert list(host(qa.q_count)) == [4, 3]
+
+
+def test_meank_add_bit_exact(kvm_state):
+    rng = np.random.default_rng(2)
+    n, e, bt = 700, 512, 128
+    k = rng.standard_normal((n, e)).astype(np.float32)
+    k[::7] *= 1e6
+    ix = api.MeanKIndex(kvm_state, 1, 8, 2, 256, bt)
+    pos = 0
+    for chunk in (5, 200, 11, 300, 184):
+        ix.add(0, pos, dev(k[pos:pos + chunk]))
+        pos += chunk
+    sums, mt = O.meank_sums(k, bt, chunk=None)
+    got = host(ix.k_sum)[0].T                        # [blocks][e]
+    assert np.array_equal(got[:6].view(np.uint32), sums.view(np.uint32))
+    assert list(host(ix.mean_tokens)[0][:6]) == list(mt)
+    assert list(host(ix.present)[:7]) == [1, 1, 1, 1, 1, 1, 0]
+
+
+def _build_index(st, k_sum, mt, n_blocks_cap, H, D, bt=128):
+    L_, nb, e = k_sum.shape
+    ix = api.MeanKIndex(st, L_, n_blocks_cap, H, D, bt)
+    ix.k_sum[:, :, :nb] = dev(np.ascontiguousarray(k_sum.transpose(0, 2, 1)))
+    ix.mean_tokens[:, :nb] = dev(mt.astype(np.int32))
+    ix.present[:nb] = 1
+    return ix
+
+
+def _case(seed, n_blocks, n_layer=1, n_head=24, H=4, D=256, planted=16):
+    rng = np.random.default_rng(seed)
+    k_sum = (rng.standard_normal((n_layer, n_blocks, H * D)) * 128).astype(np.float32)
+    mt = np.full((n_layer, n_blocks), 128, np.uint32)
+    mt[:, -1] = 77
+    ids = rng.choice(np.arange(1, n_blocks), planted, replace=False)
+    g = n_head // H
+    q = np.zeros((n_layer, n_head * D), np.float32)
+    inv = np.float32(1.0) / mt.astype(np.float32)
+    for il in range(n_layer):
+        for b in ids:
+            mean = k_sum[il, b] * inv[il, b]
+            for h in range(n_head):
+                q[il, h * D:(h + 1) * D] += mean[(h // g) * D:(h // g + 1) * D]
+    q += (rng.standard_normal(q.shape) * 0.1).astype(np.float32)
+    return q, np.full(n_layer, 4, np.uint32), k_sum, mt, ids
+
+
+@pytest.mark.parametrize("n_blocks,n_layer,n_head,H,D", [(2048, 1, 24, 4, 256), (128, 1, 8, 2, 128),
+                                                       (300, 3, 24, 4, 256), (5000, 1, 24, 4, 256)])
+def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
+    q, qc, k_sum, mt, planted = _case(n_blocks + n_layer, n_blocks, n_layer, n_head, H, D)
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 5, H, D)
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D)
+    qa.q_sum.copy_(dev(q))
+    qa.q_count.copy_(dev(qc.astype(np.int32)))
+    n_tokens = np.full(n_blocks, 128, np.int32)
+    n_tokens[-1] = 77
+    budget = 128 if n_blocks > 128 else 32
+    sel = api.score_topk(kvm_state, ix, qa, n_blocks, dev(n_tokens), budget, sink_blocks=1)
+    res = sel.result()
+    want_scores = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
+    got_scores = host(sel.scores)[:n_blocks]
+    assert np.array_equal(got_scores.view(np.uint64), want_scores.view(np.uint64))
+    want_ids = O.pick_topk(want_scores, budget, 1, 0)
+    assert np.array_equal(res["ids"], want_ids)
+    assert set(planted) <= set(res["ids"])
+    to_base, _, total = O.window_layout(want_ids, n_tokens.astype(np.uint32), 128, len(want_ids))
+    assert np.array_equal(res["to_base"], to_base) and res["total"] == total and res["status"] == 0
+
+
+KATS = [
+    # (scores, budget, sink, recent, mandatory, expected) -- kvmem_store_test.cpp
+    ({5: 100.0, 6: 90.0, 3: 10.0}, 4, 1, 1, [], [0, 5, 6, 9]),
+    ({3: 80.0, 5: 100.0, 6: 90.0, 9: -100.0}, 4, 1, 0, [], [0, 3, 5, 6]),
+    ({2: 100.0, 3: 90.0, 4: 80.0, 8: -10.0, 9: -20.0}, 4, 1, 0, [8, 9], [0, 2, 8, 9]),
+    ({}, 4, 2, 3, [0, 0, 5], [0, 1, 5, 9]),
+    ({}, 4, 1, 2, [1, 2, 3, 4], [0, 2, 3, 4]),
+    ({}, 4, 1, 0, [], [0, 7, 8, 9]),
+    ({}, 100, 1, 0, [], list(range(10))),
+]
+
+
+@pytest.mark.parametrize("kat", range(len(KATS)))
+def test_select_topk_reference_kats(kvm_state, kat):
+    sc, budget, sink, recent, mand, want = KATS[kat]
+    s = np.zeros(10)
+    for i, v in sc.items():
+        s[i] = v
+    nt = dev(np.full(10, 128, np.int32))
+    m = dev(np.array(mand, np.int32)) if mand else None
+    res = api.select_topk(kvm_state, dev(s), nt, budget, sink, recent, m).result()
+    assert list(res["ids"]) == want
+
+
+def test_select_topk_random_vs_oracle(kvm_state):
+    rng = np.random.default_rng(3)
+    for trial in range(40):
+        n = int(rng.integers(1, 8192))
+        budget = int(rng.integers(0, min(n + 3, 600)))
+        sink, recent = int(rng.integers(0, 4)), int(rng.integers(0, 4))
+        s = rng.integers(-3, 4, n).astype(np.float64) if trial % 2 else rng.standard_normal(n)
+        mand = rng.integers(0, n, int(rng.integers(0, 6))).astype(np.int32)
+        nt = np.full(n, 128, np.int32)
+        res = api.select_topk(kvm_state, dev(s), dev(nt), budget, sink, recent,
+                              dev(mand) if mand.size else None).result()
+        want = O.pick_topk(s, budget, sink, recent, list(mand))
+        assert np.array_equal(res["ids"], want), trial
+
+
+def test_stage_plan_against_slot_map(kvm_state):
+    w = api.KVWindow(kvm_state, 1024, 4, 256, 128)           # 8 slots
+    s = np.zeros(20)
+    s[[4, 9, 13]] = [3.0, 2.0, 1.0]
+    nt = dev(np.full(20, 128, np.int32))
+    # slots hold (block, base): slot 0 = (0, 0) matches, slot 1 = (4, 999) wrong base
+    w.slot_block[:2] = dev(np.array([0, 4], np.int32))
+    w.slot_base[:2] = dev(np.array([0, 999], np.int32))
+    res = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w).result()
+    assert list(res["ids"]) == [0, 4, 9, 13]
+    assert list(res["stage_slots"]) == [1, 2, 3]

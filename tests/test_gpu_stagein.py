@@ -1,0 +1,117 @@
+"""GPU stage-in (pinned host history -> tiled window with RoPE re-applied at the
+window position, Walsh-Hadamard and q8_0 requantisation) against the oracle,
+byte for byte."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import dev, host, rand_rows
+from kvmem_amd import api, _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+def _history(seed, n_tokens, H=4, D=256):
+    rng = np.random.default_rng(seed)
+    kr, vr = rand_rows(rng, n_tokens, H, D, L.T_Q8_0, L.T_Q4_0)
+    return api.History(kr, vr), kr, vr
+
+
+@pytest.mark.parametrize("n_rot,hadamard,freq_base", [(64, -1, 1e7), (64, 0, 1e7), (128, 128, 1e4)])
+def test_stagein_selection_bytes(kvm_state, n_rot, hadamard, freq_base):
+    H, D, bt = 4, 256, 128
+    n_blocks = 40
+    n_hist = n_blocks * bt - 50                     # last block is partial (78 tokens)
+    hist, kr, vr = _history(n_rot + hadamard, n_hist, H, D)
+    w = api.KVWindow(kvm_state, 16 * bt, H, D, bt)
+    rng = np.random.default_rng(5)
+    s = rng.standard_normal(n_blocks)
+    s[n_blocks - 1] = 10.0                          # select the partial block too
+    nt = np.array([min(bt, n_hist - b * bt) for b in range(n_blocks)], np.int32)
+    sel = api.select_topk(kvm_state, dev(s), dev(nt), 12, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, n_rot, freq_base, 1.0, hadamard)
+    res = sel.result()
+    assert res["status"] == 0 and len(res["ids"]) == 12 and list(res["stage_slots"]) == list(range(12))
+    nrot = 256 if hadamard == -1 else hadamard
+    theta = O.rope_theta(freq_base, 1.0, n_rot)
+    ek, ev = w.export_rows(0, 12 * bt)
+    ek, ev = host(ek), host(ev)
+    cp = host(w.cell_pos)
+    for k, (bid, base) in enumerate(zip(res["ids"], res["to_base"])):
+        n = int(nt[bid])
+        packed = kr[bid * bt:bid * bt + n]
+        want = O.stagein_k(packed.reshape(-1), n, H, D, n_rot, nrot, int(base), theta).reshape(n, -1)
+        assert np.array_equal(ek[k * bt:k * bt + n], want), (k, bid)
+        assert np.array_equal(ev[k * bt:k * bt + n], vr[bid * bt:bid * bt + n])
+        assert np.array_equal(cp[k * bt:k * bt + n], np.arange(base, base + n))
+        assert np.all(cp[k * bt + n:(k + 1) * bt] == -1)
+    assert list(host(w.slot_block)[:12]) == list(res["ids"])
+    assert list(host(w.slot_base)[:12]) == list(res["to_base"])
+    # the same retrieval again stages nothing
+    sel2 = api.select_topk(kvm_state, dev(s), dev(nt), 12, 1, 0, None, window=w)
+    assert len(sel2.result()["stage_slots"]) == 0
+
+
+def test_stagein_reselect_moves_only_changed_slots(kvm_state):
+    H, D, bt, n_blocks = 4, 256, 128, 30
+    hist, kr, vr = _history(9, n_blocks * bt, H, D)
+    w = api.KVWindow(kvm_state, 8 * bt, H, D, bt)
+    nt = dev(np.full(n_blocks, bt, np.int32))
+    s = np.zeros(n_blocks)
+    s[[3, 7, 20]] = [3, 2, 1]
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    s[25] = 5                                        # block 25 replaces block 3; later slots shift
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    res = sel.result()
+    assert list(res["ids"]) == [0, 7, 20, 25]
+    assert list(res["stage_slots"]) == [1, 2, 3]     # slot 0 (sink at base 0) stays
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    ek, _ = w.export_rows(0, 4 * bt)
+    theta = O.rope_theta(1e7, 1.0, 64)
+    for k, bid in enumerate(res["ids"]):
+        want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, k * bt, theta)
+        assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want)
+
+
+def test_enqueue_flush_api(kvm_state):
+    """Reference-shaped item API (llama-kvmem-stagein.h:36-46) at arbitrary cells."""
+    H, D = 4, 256
+    rng = np.random.default_rng(10)
+    w = api.KVWindow(kvm_state, 512, H, D, 128)
+    kr, vr = rand_rows(rng, 100, H, D, L.T_Q8_0, L.T_Q4_0)
+    theta = O.rope_theta(1e7, 1.0, 64)
+    lib = kvm_state.lib
+    items = [(0, 30, 500), (30, 70, 7)]             # (row0, n, pos0)
+    cells = [3, 200]
+    for (r0, n, pos0), c0 in zip(items, cells):
+        kb = np.ascontiguousarray(kr[r0:r0 + n])
+        vb = np.ascontiguousarray(vr[r0:r0 + n])
+        kvm_state.check(lib.kvm_stagein_enqueue_k(kvm_state.h, L.T_Q8_0, kb.ctypes.data_as(C.c_void_p), kb.nbytes,
+                                                  C.byref(w.c), c0, n, H * D, 256, H, D, 64, pos0,
+                                                  theta.ctypes.data_as(C.c_void_p), 32))
+        kvm_state.check(lib.kvm_stagein_enqueue_v(kvm_state.h, vb.ctypes.data_as(C.c_void_p), vb.nbytes,
+                                                  C.byref(w.c), c0, n))
+    kvm_state.check(lib.kvm_stagein_flush(kvm_state.h))
+    ek, ev = w.export_rows(0, 512)
+    ek, ev = host(ek), host(ev)
+    cp = host(w.cell_pos)
+    for (r0, n, pos0), c0 in zip(items, cells):
+        want = O.stagein_k(kr[r0:r0 + n].reshape(-1), n, H, D, 64, 256, pos0, theta).reshape(n, -1)
+        assert np.array_equal(ek[c0:c0 + n], want)
+        assert np.array_equal(ev[c0:c0 + n], vr[r0:r0 + n])
+        assert np.array_equal(cp[c0:c0 + n], np.arange(pos0, pos0 + n))
+
+
+def test_stagein_rejects_bad_arguments(kvm_state):
+    w = api.KVWindow(kvm_state, 256, 4, 256, 128)
+    hist, _, _ = _history(11, 256)
+    sel = api.SelectionBuffers(kvm_state, 2, 2)
+    with pytest.raises(L.KvmError):
+        api.stagein_selection(kvm_state, hist, w, sel, 7, 1e7)      # n_rot not a multiple of 8
+    wf = api.KVWindow(kvm_state, 256, 4, 128, 128, L.T_F16, L.T_F16)
+    with pytest.raises(L.KvmError):
+        api.stagein_selection(kvm_state, hist, wf, sel, 64, 1e7)    # re-RoPE stage-in needs q8_0 K
