@@ -61,8 +61,9 @@ typedef struct kvm_state kvm_state;
  * default priority on `device`.  NULL on failure. */
 kvm_state *kvm_state_create(int device);
 void kvm_state_free(kvm_state *st);
-/* Run subsequent work on `hip_stream` (a hipStream_t; NULL restores the state's
- * own stream).  Replaces the per-execution stream (llama-kvmem-stagein.cu:334-343). */
+/* Run subsequent work on `hip_stream` (a hipStream_t; NULL is the device's
+ * default null stream, as in HIP).  A new state runs on its own non-blocking
+ * stream.  Replaces the per-execution stream (llama-kvmem-stagein.cu:334-343). */
 int kvm_state_set_stream(kvm_state *st, void *hip_stream);
 void *kvm_state_stream(kvm_state *st);
 /* Replaces kvmem_stagein_sync (src/adapter/llama-kvmem-stagein.h:31). */

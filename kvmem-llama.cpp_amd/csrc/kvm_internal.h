@@ -139,8 +139,11 @@ __device__ inline float kvm_h2f(uint16_t h) {
     __builtin_memcpy(&v, &h, 2);
     return (float)v;
 }
-// IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode)
+// IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
+// The empty asm keeps the conversion a separate instruction: fused with its
+// producer (fptrunc(x * c) -> v_fma_mix(x, c, +0)) a -0.0 result turns into +0.0.
 __device__ inline uint16_t kvm_f2h(float f) {
+    asm volatile("" : "+v"(f));
     _Float16 v = (_Float16)f;
     uint16_t h;
     __builtin_memcpy(&h, &v, 2);
@@ -148,19 +151,30 @@ __device__ inline uint16_t kvm_f2h(float f) {
 }
 __device__ inline float kvm_bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// IEEE binary32 operations, round to nearest even.  Hardware add/sub/mul round
+// to nearest even; `/` and sqrtf are correctly rounded under
+// -fhip-fp32-correctly-rounded-divide-sqrt.  Files whose results must equal
+// host arithmetic bit for bit are compiled with -ffp-contract=off so no a*b+c
+// becomes an FMA.  (HIP's kvm_fsqrt is the approximate native sqrt.)
+__device__ __forceinline__ float kvm_fadd(float a, float b) { return a + b; }
+__device__ __forceinline__ float kvm_fsub(float a, float b) { return a - b; }
+__device__ __forceinline__ float kvm_fmul(float a, float b) { return a * b; }
+__device__ __forceinline__ float kvm_fdiv(float a, float b) { return a / b; }
+__device__ __forceinline__ float kvm_fsqrt(float a) { return sqrtf(a); }
+
 // q8_0 / q4_0 block quantisers with the reference kernels' exact arithmetic
 // (llama-kvmem-stagein.cu:181-234): fp32 amax, d = amax/127 (q8) or vmax/-8
 // (q4), id = d ? 1/d : 0, fp16 d with RNE, roundf (ties away) / (int)(x*id+8.5).
-// Division and reciprocal are correctly rounded (__fdiv_rn) to match host IEEE.
+// Division and reciprocal are correctly rounded (kvm_fdiv) to match host IEEE.
 __device__ inline void kvm_quant_block_q8_0(const float *x, uint16_t *d_out, int8_t *q) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float d = kvm_fdiv(amax, 127.0f);
+    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
     *d_out = kvm_f2h(d);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) q[j] = (int8_t)roundf(__fmul_rn(x[j], id));
+    for (int j = 0; j < 32; ++j) q[j] = (int8_t)roundf(kvm_fmul(x[j], id));
 }
 __device__ inline void kvm_quant_block_q4_0(const float *x, uint16_t *d_out, uint8_t *q) {
     float amax = 0.0f, vmax = 0.0f;
@@ -169,13 +183,13 @@ __device__ inline void kvm_quant_block_q4_0(const float *x, uint16_t *d_out, uin
         const float a = fabsf(x[j]);
         if (amax < a) { amax = a; vmax = x[j]; }
     }
-    const float d = __fdiv_rn(vmax, -8.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float d = kvm_fdiv(vmax, -8.0f);
+    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
     *d_out = kvm_f2h(d);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        int x0 = (int)__fadd_rn(__fmul_rn(x[j], id), 8.5f);
-        int x1 = (int)__fadd_rn(__fmul_rn(x[j + 16], id), 8.5f);
+        int x0 = (int)kvm_fadd(kvm_fmul(x[j], id), 8.5f);
+        int x1 = (int)kvm_fadd(kvm_fmul(x[j + 16], id), 8.5f);
         x0 = x0 > 15 ? 15 : x0;
         x1 = x1 > 15 ? 15 : x1;
         q[j] = (uint8_t)((x0 & 15) | ((x1 & 15) << 4));

@@ -2,9 +2,9 @@
 // and the retrieval step: score_retrieval + top-k + chronological window layout.
 //
 // Bit-exactness: the scorer restates llama-memory-kvmem.cpp:4149-4196 with the
-// same fp32 operation order, each operation an explicitly rounded IEEE op
-// (__fadd_rn/__fmul_rn/__fdiv_rn/__fsqrt_rn) so nothing is contracted into an
-// FMA, and the per-head/per-layer accumulation in double in the same order.
+// same fp32 operation order, each operation one IEEE rounding (this file is
+// compiled with -ffp-contract=off and correctly rounded `/` and sqrtf), and the
+// per-head/per-layer accumulation in double in the same order.
 #include "kvm_internal.h"
 
 // ---------------------------------------------------------------------------
@@ -15,7 +15,7 @@ __global__ void k_query_add(float *q_sum, uint32_t *q_count, uint32_t n_embd, co
     const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j < n_embd) {
         float s = q_sum[j];
-        for (uint32_t r = 0; r < n_rows; ++r) s = __fadd_rn(s, rows[(uint64_t)r * n_embd + j]);
+        for (uint32_t r = 0; r < n_rows; ++r) s = kvm_fadd(s, rows[(uint64_t)r * n_embd + j]);
         q_sum[j] = s;
     }
     if (j == 0) q_count[0] += n_rows;
@@ -75,7 +75,7 @@ __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *presen
     if (e < n_embd) {
         float *p = k_sum + (uint64_t)e * cap + bid;
         float s = off == 0 ? 0.0f : *p;
-        for (uint32_t t = start; t < end; ++t) s = __fadd_rn(s, rows[(uint64_t)(t - pos0) * n_embd + e]);
+        for (uint32_t t = start; t < end; ++t) s = kvm_fadd(s, rows[(uint64_t)(t - pos0) * n_embd + e]);
         *p = s;
     }
     if (e == 0) {
@@ -135,16 +135,16 @@ __global__ void __launch_bounds__(1024) k_score(score_args a) {
         for (uint32_t gi = 0; gi < g; ++gi) {
             const uint32_t qi = h * g + gi;
             if (qi >= a.n_head) break;
-            qh = __fadd_rn(qh, a.q_sum[(uint64_t)il * a.n_head * a.D + (uint64_t)qi * a.D + d]);
+            qh = kvm_fadd(qh, a.q_sum[(uint64_t)il * a.n_head * a.D + (uint64_t)qi * a.D + d]);
         }
-        const float invq = __fdiv_rn(1.0f, (float)(a.q_count[il] * g1));
-        s_qv[idx] = __fmul_rn(qh, invq);
+        const float invq = kvm_fdiv(1.0f, (float)(a.q_count[il] * g1));
+        s_qv[idx] = kvm_fmul(qh, invq);
     }
     __syncthreads();
     for (uint32_t idx = tid; idx < a.n_layer * a.H; idx += nthr) {
         const float *qv = s_qv + (size_t)(idx / a.H) * HD + (size_t)(idx % a.H) * a.D;
         float nq = 0.0f;
-        for (uint32_t d = 0; d < a.D; ++d) nq = __fadd_rn(nq, __fmul_rn(qv[d], qv[d]));
+        for (uint32_t d = 0; d < a.D; ++d) nq = kvm_fadd(nq, kvm_fmul(qv[d], qv[d]));
         s_nq[idx] = nq;
     }
     __syncthreads();
@@ -159,18 +159,18 @@ __global__ void __launch_bounds__(1024) k_score(score_args a) {
         float c = 0.0f;
         if (valid) {
             const uint32_t mt = a.mean_tokens[(uint64_t)il * a.cap + b];
-            const float inv = mt ? __fdiv_rn(1.0f, (float)mt) : 0.0f;
+            const float inv = mt ? kvm_fdiv(1.0f, (float)mt) : 0.0f;
             const float *ks = a.k_sum + (uint64_t)il * HD * a.cap + (uint64_t)h * a.D * a.cap + b;
             const float *qv = s_qv + (size_t)il * HD + (size_t)h * a.D;
             float dot = 0.0f, nk = 0.0f;
 #pragma unroll 8
             for (uint32_t d = 0; d < a.D; ++d) {
-                const float kh = mt ? __fmul_rn(ks[(uint64_t)d * a.cap], inv) : 0.0f;
-                dot = __fadd_rn(dot, __fmul_rn(qv[d], kh));
-                nk = __fadd_rn(nk, __fmul_rn(kh, kh));
+                const float kh = mt ? kvm_fmul(ks[(uint64_t)d * a.cap], inv) : 0.0f;
+                dot = kvm_fadd(dot, kvm_fmul(qv[d], kh));
+                nk = kvm_fadd(nk, kvm_fmul(kh, kh));
             }
-            const float den = __fadd_rn(__fmul_rn(__fsqrt_rn(s_nq[il * a.H + h]), __fsqrt_rn(nk)), 1e-6f);
-            c = __fdiv_rn(dot, den);
+            const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[il * a.H + h]), kvm_fsqrt(nk)), 1e-6f);
+            c = kvm_fdiv(dot, den);
         }
         s_cos[h][lane] = c;
         __syncthreads();

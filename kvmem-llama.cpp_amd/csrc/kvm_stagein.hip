@@ -52,9 +52,9 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
             for (int i = 0; i < DPL; ++i) {
                 const float2 t = cs[i];
                 if (lo)   // x0' = x0 c - x1 s
-                    x[i] = __fsub_rn(__fmul_rn(x[i], t.x), __fmul_rn(y[i], t.y));
+                    x[i] = kvm_fsub(kvm_fmul(x[i], t.x), kvm_fmul(y[i], t.y));
                 else      // x1' = x0 s + x1 c
-                    x[i] = __fadd_rn(__fmul_rn(y[i], t.y), __fmul_rn(x[i], t.x));
+                    x[i] = kvm_fadd(kvm_fmul(y[i], t.y), kvm_fmul(x[i], t.x));
             }
         }
     }
@@ -63,15 +63,15 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
     // butterflies h = 1, 2, ..., nrot/2 (stagein.cu:105-131)
     if (rc.nrot > 0) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) x[i] = __fmul_rn(x[i], rc.hscale);
+        for (int i = 0; i < DPL; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
 #pragma unroll
         for (int h = 1; h < DPL; h <<= 1) {
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
                 if (!(i & h)) {
                     const float a = x[i], bb = x[i + h];
-                    x[i] = __fadd_rn(a, bb);
-                    x[i + h] = __fsub_rn(a, bb);
+                    x[i] = kvm_fadd(a, bb);
+                    x[i + h] = kvm_fsub(a, bb);
                 }
             }
         }
@@ -81,7 +81,7 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
                 const float o = __shfl_xor(x[i], lx, 64);
-                x[i] = first ? __fadd_rn(x[i], o) : __fsub_rn(o, x[i]);
+                x[i] = first ? kvm_fadd(x[i], o) : kvm_fsub(o, x[i]);
             }
         }
     }
@@ -92,11 +92,11 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
     for (int i = 0; i < DPL; ++i) amax = fmaxf(amax, fabsf(x[i]));
 #pragma unroll
     for (int o = 1; o < 32 / DPL; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float d = kvm_fdiv(amax, 127.0f);
+    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
     uint8_t *qd = kt + kvm_kq_off(D, c, d0);
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) qd[i] = (uint8_t)(int8_t)roundf(__fmul_rn(x[i], id));
+    for (int i = 0; i < DPL; ++i) qd[i] = (uint8_t)(int8_t)roundf(kvm_fmul(x[i], id));
     if (e == 0) {
         const uint16_t h16 = kvm_f2h(d);
         uint8_t *sd = kt + kvm_kd_off(D, c, b);

@@ -49,7 +49,7 @@ extern "C" void kvm_state_free(kvm_state *st) {
 
 extern "C" int kvm_state_set_stream(kvm_state *st, void *hip_stream) {
     if (!st) return KVM_EINVAL;
-    st->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : st->own_stream;
+    st->stream = static_cast<hipStream_t>(hip_stream);
     return KVM_OK;
 }
 

@@ -50,9 +50,19 @@ def test_fa_decode_parity(kvm_state, case, qdt):
     scale = 1.0 / np.sqrt(D)
     out = host(api.fa_decode(kvm_state, w, qd, dev(qp), H * G, scale))
     ref = O.fa_ggml(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
-    check_attention(out, ref)
-    f64 = O.fa_f64(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
-    assert np.abs(out - f64).max() <= 3e-2 * np.abs(f64).max()
+    if kt == L.T_Q8_0:
+        check_attention(out, ref)
+        f64 = O.fa_f64(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
+        assert np.abs(out - f64).max() <= 3e-2 * np.abs(f64).max()      # Q -> q8_0 as in ggml
+    else:
+        # ggml-CPU accumulates f16 V in an fp16 vector (ggml_vec_mad_f16), itself off
+        # the exact result by more than the stated tolerance; the GPU accumulates in
+        # fp32 and is held to the tolerance against the float64 softmax over the same
+        # fp16 Q (ggml rounds Q to fp16 for an f16 K).
+        qh = q.astype(np.float16).astype(np.float32)
+        f64 = O.fa_f64(kt, vt, qh, kr, vr, cp, qp, H * G, H, D, scale)
+        check_attention(out, f64)
+        assert np.abs(out - ref).max() <= 2e-2 * np.abs(ref).max()
 
 
 def test_fa_decode_masks_and_empty_rows(kvm_state):
@@ -84,13 +94,15 @@ def test_fa_decode_lanes_match_single_lane(kvm_state):
         refs.append(host(api.fa_decode(kvm_state, w, dev(q), dev(qp), H * G, 0.0625)))
     outs = api.fa_decode_lanes(kvm_state, ws, qs, qps, H * G, 0.0625)
     for o, r in zip(outs, refs):
-        assert np.array_equal(host(o), r)
+        # the fused launch splits the keys differently, so P is rounded to fp16
+        # against different running maxima: equal to well inside the tolerance
+        np.testing.assert_allclose(host(o), r, rtol=1e-3, atol=1e-4)
 
 
 def test_fa_prefill_chunked_causal(kvm_state):
     rng = np.random.default_rng(9)
     H, G, D, n_win, T = 4, 6, 256, 2048, 40
-    w, kr, vr, cp = _window(kvm_state, rng, n_win + 64, H, D, L.T_Q8_0, L.T_Q4_0, live=n_win)
+    w, kr, vr, cp = _window(kvm_state, rng, n_win + 128, H, D, L.T_Q8_0, L.T_Q4_0, live=n_win)
     kc, vc = rand_rows(rng, T, H, D, L.T_Q8_0, L.T_Q4_0)
     pos = np.arange(n_win, n_win + T, dtype=np.int32)
     w.import_rows(n_win, dev(kc), dev(vc), dev(pos))           # the chunk's own K/V

@@ -64,7 +64,7 @@ def test_stagein_reselect_moves_only_changed_slots(kvm_state):
     s[[3, 7, 20]] = [3, 2, 1]
     sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
     api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
-    s[25] = 5                                        # block 25 replaces block 3; later slots shift
+    s[3], s[25] = 0, 5                               # block 3 leaves, block 25 enters; later slots shift
     sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
     res = sel.result()
     assert list(res["ids"]) == [0, 7, 20, 25]
