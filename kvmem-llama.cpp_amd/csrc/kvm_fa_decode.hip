@@ -311,39 +311,78 @@ __global__ void __launch_bounds__(256) k_fa_decode(fa_args a) {
             }
 }
 
-// Merge the splits of one (lane, kv head, row): thread = output dim.
+// Merge the splits of one (lane, kv head, row): thread = output dim.  The split
+// maxima / sums are reduced first; then every thread issues its loads of 32
+// splits at once, so the merge streams the partials instead of paying one
+// memory latency per split.
+#define KVM_MAX_SPLITS 512
 template <int D>
 __global__ void __launch_bounds__(D) k_fa_combine(fa_args a, int rmax) {
+    __shared__ float s_w[KVM_MAX_SPLITS];
+    __shared__ float s_red[D / 64];
     const fa_lane ln = a.lanes[blockIdx.z];
     const uint32_t h = blockIdx.y, row = blockIdx.x;
     const uint32_t R = ln.n_tokens * a.G;
     if (row >= R) return;
-    const uint32_t d = threadIdx.x;
-    const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < a.n_splits; ++s) M = fmaxf(M, a.ws_ml[((p0 + s) * rmax + row) * 2]);
-    float L = 0.0f, acc = 0.0f;
-    if (M != -INFINITY) {
-        for (uint32_t s = 0; s < a.n_splits; ++s) {
-            const float ms = a.ws_ml[((p0 + s) * rmax + row) * 2];
-            if (ms == -INFINITY) continue;
-            const float f = exp2f(ms - M);
-            L += a.ws_ml[((p0 + s) * rmax + row) * 2 + 1] * f;
-            acc += a.ws[((p0 + s) * rmax + row) * D + d] * f;
-        }
+    const uint32_t d = threadIdx.x, S = a.n_splits;
+    const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
+    const float *ml = a.ws_ml + (p0 * rmax + row) * 2;
+    const uint64_t mstride = (uint64_t)rmax * 2;
+    float mloc = -INFINITY;
+    for (uint32_t s = d; s < S; s += D) {
+        const float m = ml[s * mstride];
+        s_w[s] = m;
+        mloc = fmaxf(mloc, m);
     }
+    for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+    if ((d & 63) == 0) s_red[d >> 6] = mloc;
+    __syncthreads();
+    float M = s_red[0];
+#pragma unroll
+    for (int w = 1; w < D / 64; ++w) M = fmaxf(M, s_red[w]);
     const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
-    ln.out[((uint64_t)t * a.n_head + qh) * D + d] = L > 0.0f ? acc / L : 0.0f;
+    float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
+    if (M == -INFINITY) {                     // no visible cell for this row
+        *out = 0.0f;
+        return;
+    }
+    float lloc = 0.0f;
+    for (uint32_t s = d; s < S; s += D) {
+        const float m = s_w[s];
+        const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
+        s_w[s] = wgt;
+        lloc += ml[s * mstride + 1] * wgt;
+    }
+    for (int o = 32; o > 0; o >>= 1) lloc += __shfl_xor(lloc, o, 64);
+    __syncthreads();
+    if ((d & 63) == 0) s_red[d >> 6] = lloc;
+    __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < D / 64; ++w) L += s_red[w];
+    const float *po = a.ws + (p0 * rmax + row) * D + d;
+    const uint64_t ostride = (uint64_t)rmax * D;
+    float acc = 0.0f;
+    for (uint32_t s0 = 0; s0 < S; s0 += 32) {
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = s0 + j < S ? po[(s0 + j) * ostride] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc += s0 + j < S ? v[j] * s_w[s0 + j] : 0.0f;
+    }
+    *out = L > 0.0f ? acc / L : 0.0f;
 }
 
 static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
     if (const char *e = getenv("KVM_FA_SPLITS")) {
-        const int v = atoi(e);
-        if (v > 0) return (uint32_t)v < n_tiles ? (uint32_t)v : n_tiles;
+        uint32_t v = (uint32_t)atoi(e);
+        if (v > KVM_MAX_SPLITS) v = KVM_MAX_SPLITS;
+        if (v > 0) return v < n_tiles ? v : n_tiles;
     }
     // about 2 workgroups per CU on a 256-CU device
     uint32_t s = (512 + n_lanes * H - 1) / (n_lanes * H);
     if (s < 1) s = 1;
+    if (s > KVM_MAX_SPLITS) s = KVM_MAX_SPLITS;
     return s < n_tiles ? s : n_tiles;
 }
 

@@ -118,33 +118,34 @@ struct score_args {
     const uint32_t *mean_tokens;
     const uint8_t *present;
     double *scores;
-    uint32_t n_blocks, cap, n_layer, n_head, H, D;
+    uint32_t n_blocks, cap, n_layer, n_head, H;
 };
 
-__global__ void __launch_bounds__(1024) k_score(score_args a) {
+template <int D, int CH, int MAXT>
+__global__ void __launch_bounds__(MAXT) k_score(score_args a) {
     extern __shared__ float s_qv[];                  // [n_layer][H*D] then nq[n_layer][H]
-    const uint32_t HD = a.H * a.D;
+    const uint32_t HD = a.H * D;
     float *s_nq = s_qv + (size_t)a.n_layer * HD;
     __shared__ float s_cos[16][64];
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t g = a.H == 0 ? 1u : a.n_head / a.H;
     const uint32_t g1 = g > 1u ? g : 1u;
     for (uint32_t idx = tid; idx < a.n_layer * HD; idx += nthr) {
-        const uint32_t il = idx / HD, h = (idx % HD) / a.D, d = idx % a.D;
+        const uint32_t il = idx / HD, h = (idx % HD) / D, d = idx % D;
         float qh = 0.0f;
         for (uint32_t gi = 0; gi < g; ++gi) {
             const uint32_t qi = h * g + gi;
             if (qi >= a.n_head) break;
-            qh = kvm_fadd(qh, a.q_sum[(uint64_t)il * a.n_head * a.D + (uint64_t)qi * a.D + d]);
+            qh = kvm_fadd(qh, a.q_sum[(uint64_t)il * a.n_head * D + (uint64_t)qi * D + d]);
         }
         const float invq = kvm_fdiv(1.0f, (float)(a.q_count[il] * g1));
         s_qv[idx] = kvm_fmul(qh, invq);
     }
     __syncthreads();
     for (uint32_t idx = tid; idx < a.n_layer * a.H; idx += nthr) {
-        const float *qv = s_qv + (size_t)(idx / a.H) * HD + (size_t)(idx % a.H) * a.D;
+        const float *qv = s_qv + (size_t)(idx / a.H) * HD + (size_t)(idx % a.H) * D;
         float nq = 0.0f;
-        for (uint32_t d = 0; d < a.D; ++d) nq = kvm_fadd(nq, kvm_fmul(qv[d], qv[d]));
+        for (uint32_t d = 0; d < D; ++d) nq = kvm_fadd(nq, kvm_fmul(qv[d], qv[d]));
         s_nq[idx] = nq;
     }
     __syncthreads();
@@ -160,14 +161,23 @@ __global__ void __launch_bounds__(1024) k_score(score_args a) {
         if (valid) {
             const uint32_t mt = a.mean_tokens[(uint64_t)il * a.cap + b];
             const float inv = mt ? kvm_fdiv(1.0f, (float)mt) : 0.0f;
-            const float *ks = a.k_sum + (uint64_t)il * HD * a.cap + (uint64_t)h * a.D * a.cap + b;
-            const float *qv = s_qv + (size_t)il * HD + (size_t)h * a.D;
+            const float *ks = a.k_sum + (uint64_t)il * HD * a.cap + (uint64_t)h * D * a.cap + b;
+            // Issue CH dims of the column at once (one coalesced 256-byte access
+            // per dim across the wave) before the sequential fp32 chain over them,
+            // so the index streams with CH loads in flight per lane.
+            const float *qv = s_qv + (size_t)il * HD + (size_t)h * D;
             float dot = 0.0f, nk = 0.0f;
-#pragma unroll 8
-            for (uint32_t d = 0; d < a.D; ++d) {
-                const float kh = mt ? kvm_fmul(ks[(uint64_t)d * a.cap], inv) : 0.0f;
-                dot = kvm_fadd(dot, kvm_fmul(qv[d], kh));
-                nk = kvm_fadd(nk, kvm_fmul(kh, kh));
+            for (uint32_t c0 = 0; c0 < (uint32_t)D; c0 += CH) {
+                float kraw[CH];
+#pragma unroll
+                for (uint32_t d = 0; d < (uint32_t)CH; ++d)
+                    kraw[d] = __builtin_nontemporal_load(ks + (uint64_t)(c0 + d) * a.cap);
+#pragma unroll
+                for (uint32_t d = 0; d < (uint32_t)CH; ++d) {
+                    const float kh = mt ? kvm_fmul(kraw[d], inv) : 0.0f;
+                    dot = kvm_fadd(dot, kvm_fmul(qv[c0 + d], kh));
+                    nk = kvm_fadd(nk, kvm_fmul(kh, kh));
+                }
             }
             const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[il * a.H + h]), kvm_fsqrt(nk)), 1e-6f);
             c = kvm_fdiv(dot, den);
@@ -240,12 +250,17 @@ __device__ uint32_t block_scan(uint32_t v, uint32_t *s_tmp, uint32_t *total) {
     return res;
 }
 
+// Selection of the `need` best candidates under the strict order
+// (score desc, block id desc): an 8-pass MSB-first radix select over the
+// order-preserving 64-bit keys finds the need-th largest key T; keys above T
+// are taken, and among keys equal to T the highest block ids.
 __global__ void __launch_bounds__(1024) k_topk(topk_args a) {
     __shared__ uint64_t s_key[KVM_MAX_TOPK_BLOCKS];
-    __shared__ uint16_t s_id[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
+    __shared__ uint32_t s_hist[256];
     __shared__ uint32_t s_tmp[32];
-    __shared__ uint32_t s_count;
+    __shared__ uint32_t s_count, s_k;
+    __shared__ uint64_t s_prefix;
     const uint32_t tid = threadIdx.x, nthr = blockDim.x, n = a.n;
     const bool all = a.budget == 0 || n <= a.budget;
     for (uint32_t i = tid; i < n; i += nthr) s_kept[i] = all ? 1 : 0;
@@ -270,39 +285,67 @@ __global__ void __launch_bounds__(1024) k_topk(topk_args a) {
         __syncthreads();
         const uint32_t count = s_count;
         if (count < a.budget) {
-            uint32_t np = 64;
-            while (np < n) np <<= 1;
-            // candidates sort first by (score desc, id desc); others last
-            uint32_t ncand_local = 0;
-            for (uint32_t i = tid; i < np; i += nthr) {
-                const bool cand = i < n && !s_kept[i];
-                s_key[i] = cand ? ~ord_key(a.scores[i]) : ~0ull;
-                s_id[i] = (uint16_t)(cand ? (0xffffu - i) : 0xffffu);
-                ncand_local += cand;
+            uint32_t nc_local = 0;
+            for (uint32_t i = tid; i < n; i += nthr) {
+                s_key[i] = ord_key(a.scores[i]);
+                nc_local += !s_kept[i];
             }
             uint32_t ncand;
-            (void)block_scan(ncand_local, s_tmp, &ncand);
-            // bitonic sort ascending on (key, ~id)
-            for (uint32_t k = 2; k <= np; k <<= 1) {
-                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-                    for (uint32_t i = tid; i < np; i += nthr) {
-                        const uint32_t l = i ^ j;
-                        if (l > i) {
-                            const uint64_t ki = s_key[i], kl = s_key[l];
-                            const uint16_t ii = s_id[i], il = s_id[l];
-                            const bool gt = ki > kl || (ki == kl && ii > il);
-                            const bool up = (i & k) == 0;
-                            if (gt == up) {
-                                s_key[i] = kl; s_key[l] = ki;
-                                s_id[i] = il; s_id[l] = ii;
-                            }
-                        }
+            (void)block_scan(nc_local, s_tmp, &ncand);
+            const uint32_t need = a.budget - count < ncand ? a.budget - count : ncand;
+            if (tid == 0) { s_prefix = 0; s_k = need; }
+            uint64_t mask = 0;
+            for (int shift = 56; shift >= 0 && need; shift -= 8) {
+                if (tid < 256) s_hist[tid] = 0;
+                __syncthreads();
+                const uint64_t prefix = s_prefix;
+                for (uint32_t i = tid; i < n; i += nthr)
+                    if (!s_kept[i] && (s_key[i] & mask) == prefix)
+                        atomicAdd(&s_hist[(uint32_t)(s_key[i] >> shift) & 255u], 1u);
+                __syncthreads();
+                if (tid < 64) {
+                    // lane l owns bins 255-4l .. 252-4l (descending)
+                    uint32_t c[4], tot = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) { c[j] = s_hist[255 - 4 * tid - j]; tot += c[j]; }
+                    uint32_t incl = tot;
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const uint32_t y = __shfl_up(incl, o, 64);
+                        if (tid >= (uint32_t)o) incl += y;
                     }
-                    __syncthreads();
+                    uint32_t run = incl - tot;           // keys in higher bins
+                    const uint32_t k = s_k;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (run < k && k <= run + c[j]) {
+                            s_prefix = prefix | ((uint64_t)(255 - 4 * tid - j) << shift);
+                            s_k = k - run;
+                        }
+                        run += c[j];
+                    }
+                }
+                mask |= (uint64_t)0xff << shift;
+                __syncthreads();
+            }
+            // keys above T are selected; among keys equal to T the s_k highest ids
+            const uint64_t T = s_prefix;
+            const uint32_t ktie = s_k;
+            const uint32_t per = (n + nthr - 1) / nthr;
+            const uint32_t i0 = tid * per, i1 = i0 + per < n ? i0 + per : n;
+            uint32_t ties = 0;
+            for (uint32_t i = i0; i < i1; ++i) ties += !s_kept[i] && s_key[i] == T;
+            uint32_t n_ties;
+            uint32_t before = block_scan(ties, s_tmp, &n_ties);
+            for (uint32_t i = i0; i < i1 && need; ++i) {
+                if (s_kept[i]) continue;
+                if (s_key[i] > T) {
+                    s_kept[i] = 2;
+                } else if (s_key[i] == T) {
+                    if (n_ties - 1 - before < ktie) s_kept[i] = 2;     // rank by descending id
+                    ++before;
                 }
             }
-            const uint32_t need = a.budget - count < ncand ? a.budget - count : ncand;
-            for (uint32_t r = tid; r < need; r += nthr) s_kept[0xffffu - s_id[r]] = 1;
             __syncthreads();
         }
     }
@@ -310,7 +353,7 @@ __global__ void __launch_bounds__(1024) k_topk(topk_args a) {
     const uint32_t per = (n + nthr - 1) / nthr;
     const uint32_t i0 = tid * per, i1 = i0 + per < n ? i0 + per : n;
     uint32_t local = 0;
-    for (uint32_t i = i0; i < i1; ++i) local += s_kept[i];
+    for (uint32_t i = i0; i < i1; ++i) local += s_kept[i] != 0;
     uint32_t n_sel;
     uint32_t rank = block_scan(local, s_tmp, &n_sel);
     const bool fits = n_sel <= a.cap;
@@ -396,6 +439,7 @@ extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kv
         return kvm_fail(st, KVM_EINVAL, "score_topk: null buffer");
     if (p->n_blocks > ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "score_topk: n_blocks %u > index capacity %u", p->n_blocks, ix->n_blocks);
     if (q->n_layer != ix->n_layer || q->head_dim != ix->head_dim) return kvm_fail(st, KVM_EINVAL, "score_topk: query/index shape mismatch");
+    if (ix->head_dim != 128 && ix->head_dim != 256) return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: head_dim %u", ix->head_dim);
     if (ix->n_head_kv == 0 || ix->n_head_kv > 16 || q->n_head % ix->n_head_kv)
         return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: n_head %u / n_head_kv %u", q->n_head, ix->n_head_kv);
     const size_t lds = ((size_t)ix->n_layer * ix->n_head_kv * ix->head_dim + (size_t)ix->n_layer * ix->n_head_kv) * 4;
@@ -403,10 +447,22 @@ extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kv
     KVM_HIP(st, hipSetDevice(st->device));
     if (p->n_blocks) {
         score_args sa{q->q_sum, q->q_count, ix->k_sum, ix->mean_tokens, ix->present, out->scores,
-                      p->n_blocks, ix->n_blocks, ix->n_layer, q->n_head, ix->n_head_kv, ix->head_dim};
+                      p->n_blocks, ix->n_blocks, ix->n_layer, q->n_head, ix->n_head_kv};
+        // up to 4 kv heads: 256 threads, 128 dims in flight per lane; more heads
+        // (up to 16 waves) keep 32 in flight within the smaller register budget
+        const bool small = ix->n_head_kv <= 4;
+        const void *fn = ix->head_dim == 256 ? (small ? (const void *)k_score<256, 128, 256> : (const void *)k_score<256, 32, 1024>)
+                                              : (small ? (const void *)k_score<128, 128, 256> : (const void *)k_score<128, 32, 1024>);
         if (lds > 64 * 1024)
-            KVM_HIP(st, hipFuncSetAttribute((const void *)k_score, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(k_score, dim3(kvm_cdiv(p->n_blocks, 64)), dim3(64 * ix->n_head_kv), lds, st->stream, sa);
+            KVM_HIP(st, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        const dim3 grid(kvm_cdiv(p->n_blocks, 64)), block(64 * ix->n_head_kv);
+        if (ix->head_dim == 256) {
+            if (small) hipLaunchKernelGGL((k_score<256, 128, 256>), grid, block, lds, st->stream, sa);
+            else hipLaunchKernelGGL((k_score<256, 32, 1024>), grid, block, lds, st->stream, sa);
+        } else {
+            if (small) hipLaunchKernelGGL((k_score<128, 128, 256>), grid, block, lds, st->stream, sa);
+            else hipLaunchKernelGGL((k_score<128, 32, 1024>), grid, block, lds, st->stream, sa);
+        }
         KVM_LAUNCH_CHECK(st, "score");
     }
     return launch_topk(st, out->scores, p, w, out);
