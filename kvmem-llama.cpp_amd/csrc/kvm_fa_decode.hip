@@ -9,13 +9,16 @@
 // f16/f16 cache Q is rounded to fp16 and Q.K is an fp16 dot with fp32
 // accumulation.
 //
-// Work split (gfx950, wave64, 4 waves per workgroup; one workgroup per
-// (lane, kv head, key split)):
-//   phase 1: wave w scores keys 16w..16w+15 of the 64-cell tile against all
-//            rows with v_mfma_i32_16x16x32_i8 (one MFMA per 32-dim block and
-//            16-row tile, then the per-block scale), masks by cell position
-//            and reduces the row max; the four waves exchange maxima in LDS.
-//   phase 2: wave w accumulates O[:, dims of quarter w] += P V with
+// Work split (gfx950, wave64; one workgroup per (lane, kv head, key split) with
+// 4 waves per 16 padded query rows, i.e. 4 or 8 waves):
+//   tiles:   each wave loads its own operands of a 64-cell tile straight from
+//            HBM into registers (three buffers, two tiles in flight);
+//   phase 1: wave (kq, rt) scores keys 16kq..16kq+15 of the tile against the
+//            16 rows of row tile rt with v_mfma_i32_16x16x32_i8 (one MFMA per
+//            32-dim block; the d_k*d_q products of four blocks come from one
+//            v_mfma_f32_16x16x1_4b_f32 outer product), masks by cell position
+//            and reduces the row max; maxima are exchanged in LDS;
+//   phase 2: wave w accumulates O[:, dims D/W*w ..] += P V for all rows with
 //            v_mfma_f32_16x16x32_f16; the q4_0 block scale of V is folded
 //            into P so V enters the MFMA as exact integers (nibble - 8).
 // Partial (m, l, O) of each split go to a workspace and k_fa_combine merges them.
@@ -50,15 +53,17 @@ __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
     return bf16 ? kvm_bf2f(((const uint16_t *)q)[i]) : ((const float *)q)[i];
 }
 
-// 8 q4_0 nibbles (keys j = 0..7, low nibble first) -> 8 fp16 values nibble - 8.
-// (0x6400 | n) is the fp16 1024 + n; subtracting 1032 is exact.
+// 8 q4_0 nibbles of one word (key j in byte j%4, high nibble for j >= 4) ->
+// 8 fp16 values nibble - 8 in key order.  Each v_perm packs two nibble bytes
+// under an 0x64 high byte, giving the fp16 1024 + n; subtracting 1032 is exact.
 __device__ inline kvm_f16x8 nib8_to_f16(uint32_t w) {
     const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+    const uint32_t c64 = 0x64646464u;
     uint32_t r[4];
-    r[0] = __builtin_amdgcn_perm(hi, lo, 0x0c040c00u) | 0x64006400u;
-    r[1] = __builtin_amdgcn_perm(hi, lo, 0x0c050c01u) | 0x64006400u;
-    r[2] = __builtin_amdgcn_perm(hi, lo, 0x0c060c02u) | 0x64006400u;
-    r[3] = __builtin_amdgcn_perm(hi, lo, 0x0c070c03u) | 0x64006400u;
+    r[0] = __builtin_amdgcn_perm(c64, lo, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(c64, lo, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(c64, hi, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(c64, hi, 0x04030402u);
     kvm_f16x8 v;
     __builtin_memcpy(&v, r, 16);
     const kvm_f16x8 off = {(_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f,
@@ -66,239 +71,372 @@ __device__ inline kvm_f16x8 nib8_to_f16(uint32_t w) {
     return v - off;
 }
 
+typedef uint32_t kvm_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t kvm_u32x2 __attribute__((ext_vector_type(2)));
+typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
+
+// Workgroup barrier that orders LDS traffic only: it waits for this wave's LDS
+// operations but not for its outstanding global loads (a __syncthreads fence
+// would drain the tile prefetch and serialise the pipeline).
+#define KVM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+// A row's running maximum moves only when a tile raises it by more than
+// 2^KVM_LAZY_MAX (log2 domain), so most tiles skip rescaling O; probabilities
+// stay below 2^KVM_LAZY_MAX, well inside fp16.
+#define KVM_LAZY_MAX 8.0f
+
+// One wave's operands of one 64-cell tile, loaded straight from HBM in MFMA
+// operand order (the window's tile layout is built for this):
+//   phase 1 (key quarter kq): K quants of keys 16kq+m (lane l = 16g+m holds
+//            dims 32b+8g..+7 of every block b), the fp16 scales of key 16kq+m
+//            for blocks 4gi+g (q8_0), positions of keys 16kq+4g..+3;
+//   phase 2 (dim slice w): q4_0 nibble words of dims DW*w+16nt+m for keys
+//            32ks+8g..+7, and the V scales of those keys for each dim block.
+template <int D, bool QUANT, int NT, int NBW>
+struct fa_tile_regs {
+    static constexpr int NB = D / 32;
+    kvm_u32x4 k[QUANT ? NB / 2 : NB];     // q8_0: 2 blocks per 16 B; f16: one k-step
+    uint32_t dk[QUANT ? NB / 4 : 1];      // fp16 scale (low half)
+    kvm_u32x4 cp;                          // 4 cell positions
+    kvm_u32x2 vq[QUANT ? NT : 1];          // both ks nibble words
+    kvm_u32x4 vs[QUANT ? NBW : 1][2];      // V scales [block][ks]
+    kvm_u32x4 vh[QUANT ? 1 : NT][2];       // f16 V [ks]
+};
+
 template <int D, int NRT, bool QUANT>
-__global__ void __launch_bounds__(256) k_fa_decode(fa_args a) {
+__global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
+    constexpr int WAVES = 4 * NRT;
     constexpr int NB = D / 32;          // 32-dim blocks per row
+    constexpr int NG = QUANT ? NB / 4 : 1;   // 4-block scale groups
     constexpr int RMAX = 16 * NRT;      // padded query rows
-    constexpr int DW = D / 4;           // output dims per wave
+    constexpr int DW = D / WAVES;       // output dims per wave (phase 2)
     constexpr int NT = DW / 16;         // 16-dim output tiles per wave
+    constexpr int NBW = DW >= 32 ? DW / 32 : 1;   // V scale blocks per wave
+    constexpr int NTB = NT / NBW;       // output tiles per V scale block
     constexpr uint32_t KTILE = QUANT ? 64u * D + 64u * NB * 2u : 64u * D * 2u;
     constexpr uint32_t VTILE = QUANT ? D * 32u + NB * 64u * 2u : 64u * D * 2u;
+    constexpr int QT = RMAX * NB / (WAVES * 16);  // query quantisation tasks per lane
     constexpr int PSTR = 64 + 8;        // padded fp16 row stride of P in LDS
+    static_assert(NT >= 1 && NT % NBW == 0, "phase-2 dim split");
+    static_assert(QT >= 1 && QT * WAVES * 16 == RMAX * NB, "query task split");
+    using Regs = fa_tile_regs<D, QUANT, NT, NBW>;
 
     const fa_lane ln = a.lanes[blockIdx.z];
     const uint32_t h = blockIdx.y, split = blockIdx.x;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, m = l & 15;
+    const int tid = threadIdx.x, l = tid & 63, g = l >> 4, m = l & 15;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kq = w & 3, rq = w >> 2;  // phase 1: key quarter, row tile
     const int R = (int)(ln.n_tokens * a.G);
     const uint32_t tps = (ln.n_tiles + a.n_splits - 1) / a.n_splits;
     const uint32_t t_begin = split * tps;
     const uint32_t t_end = t_begin + tps < ln.n_tiles ? t_begin + tps : ln.n_tiles;
+    const uint32_t n_t = t_end > t_begin ? t_end - t_begin : 0;
 
     __shared__ __align__(16) int8_t s_qq[QUANT ? RMAX : 1][D];
     __shared__ __align__(16) _Float16 s_qh[QUANT ? 1 : RMAX][D];
     __shared__ float s_dq[RMAX][NB];
-    __shared__ int32_t s_qpos[RMAX];
     __shared__ float s_max[4][RMAX];
     __shared__ float s_alpha[RMAX];
+    __shared__ int32_t s_rescale[NRT];
     __shared__ float s_l[4][RMAX];
     __shared__ __align__(16) _Float16 s_p[RMAX][PSTR];
 
-    // ---- query rows of this kv head: row r = token r/G, query head h*G + r%G
-    for (int idx = tid; idx < RMAX * NB; idx += 256) {
-        const int r = idx / NB, b = idx % NB;
-        float x[32];
-        if (r < R) {
-            const uint64_t base = ((uint64_t)(r / a.G) * a.n_head + h * a.G + r % a.G) * D + 32 * b;
+    // ---- query rows (row r = token r/G, query head h*G + r%G): task (t, lane)
+    // covers dims 32b + 8q4 .. +7 of row r.  The raw rows are loaded first,
+    // unconditionally (rows past R re-read row 0, zeroed later; a bf16 row
+    // loads its 16 bytes twice), so that the tile prologue can be issued
+    // behind them and the quantisation waits for the query only.
+    if (R == 0) return;                  // lane without query rows: no partials
+    const int myrow = 16 * rq + m;
+    const int32_t qp = myrow < R ? ln.q_pos[myrow / a.G] : -1;
+    kvm_u32x4 qraw[QT][2];
+    {
+        const uint32_t esz = a.q_bf16 ? 2u : 4u;
 #pragma unroll
-            for (int j = 0; j < 32; ++j) x[j] = load_q(ln.q, base + j, a.q_bf16);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) x[j] = 0.0f;
-        }
-        if constexpr (QUANT) {
-            uint16_t d16;
-            kvm_quant_block_q8_0(x, &d16, &s_qq[r][32 * b]);
-            s_dq[r][b] = kvm_h2f(d16);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 32; ++j) s_qh[r][32 * b + j] = (_Float16)x[j];
+        for (int t = 0; t < QT; ++t) {
+            const int item = (t * WAVES + w) * 16 + m, rr = item / NB, b = item % NB;
+            const int r = rr < R ? rr : 0;
+            const uint64_t e0 = ((uint64_t)(r / a.G) * a.n_head + h * a.G + r % a.G) * D + 32 * b + 8 * g;
+            const uint8_t *qb = (const uint8_t *)ln.q + e0 * esz;
+            qraw[t][0] = *(const kvm_u32x4 *)qb;
+            qraw[t][1] = *(const kvm_u32x4 *)(qb + (esz == 4u ? 16u : 0u));
         }
     }
-    if (tid < RMAX) s_qpos[tid] = tid < R ? ln.q_pos[tid / a.G] : -1;
-    __syncthreads();
+    asm volatile("" ::: "memory");       // keep the query loads ahead of the tile loads
 
-    // B operands (Q^T): lane (row m of row-tile rt, k-group g)
-    long qop_i[QUANT ? NRT : 1][QUANT ? NB : 1];
-    kvm_f16x8 qop_h[QUANT ? 1 : NRT][QUANT ? 1 : NB];
-    float dqv[QUANT ? NRT : 1][QUANT ? NB : 1];
-    int32_t qp[NRT];
+    // ---- per-lane tile addressing (the tile index is wave-uniform)
+    const uint8_t *kbase = ln.wk + (uint64_t)h * ln.n_tiles * KTILE;
+    const uint8_t *vbase = ln.wv + (uint64_t)h * ln.n_tiles * VTILE;
+    const uint32_t k_off = QUANT ? (uint32_t)((kq * (NB / 2) * 64 + l) << 4) : (uint32_t)((kq * NB * 64 + l) << 4);
+    const uint32_t dk_off = 64u * D + (uint32_t)(((kq * NB + g) * 16 + m) << 1);
+    const uint32_t cp_off = (uint32_t)(16 * kq + 4 * g) * 4u;
+    const uint32_t vq_off = kvm_vq_word((uint32_t)(DW * w + m), (uint32_t)g, 0);
+    const uint32_t vs_off = D * 32u + (uint32_t)(((((DW * w) / 32) * 2) * 4 + g) * 8 * 2);
+    const uint32_t vh_off = kvm_vh_idx((uint32_t)(8 * g), (uint32_t)(DW * w + m)) << 1;
+    // loads of one tile in three parts (K; scales and positions; V), so that
+    // a step can spread them over its phases instead of stalling on the
+    // address queue all at once
+    // tile to load for step i: past the split's last tile the loads re-read it,
+    // and an empty split reads tile 0 (every window has one), so every step
+    // issues the same loads and the prologue needs no branch
+    auto tile_index = [&](uint32_t i) { return n_t == 0 ? 0u : t_begin + (i < n_t ? i : n_t - 1); };
+    auto load_k = [&](Regs &rg, uint32_t T) {
+        const uint8_t *kt = kbase + (uint64_t)T * KTILE;
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-        qp[rt] = s_qpos[16 * rt + m];
+        for (int p = 0; p < (QUANT ? NB / 2 : NB); ++p) rg.k[p] = *(const kvm_u32x4 *)(kt + k_off + 1024u * p);
+    };
+    auto load_s = [&](Regs &rg, uint32_t T) {
+        const uint8_t *kt = kbase + (uint64_t)T * KTILE;
+        if constexpr (QUANT) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if constexpr (QUANT) {
-                __builtin_memcpy(&qop_i[rt][b], &s_qq[16 * rt + m][32 * b + 8 * g], 8);
-                dqv[rt][b] = s_dq[16 * rt + m][b];
-            } else {
-                __builtin_memcpy(&qop_h[rt][b], &s_qh[16 * rt + m][32 * b + 8 * g], 16);
+            for (int gi = 0; gi < NG; ++gi) rg.dk[gi] = *(const uint16_t *)(kt + dk_off + 128u * gi);
+        }
+        rg.cp = *(const kvm_u32x4 *)((const uint8_t *)(ln.cell_pos + (uint64_t)T * 64) + cp_off);
+    };
+    auto load_v = [&](Regs &rg, uint32_t T) {
+        const uint8_t *vt = vbase + (uint64_t)T * VTILE;
+        if constexpr (QUANT) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) rg.vq[nt] = *(const kvm_u32x2 *)(vt + vq_off + 512u * nt);
+#pragma unroll
+            for (int bw = 0; bw < NBW; ++bw)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) rg.vs[bw][ks] = *(const kvm_u32x4 *)(vt + vs_off + 128u * bw + 64u * ks);
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) rg.vh[nt][ks] = *(const kvm_u32x4 *)(vt + vh_off + 2048u * nt + 16u * ks);
+        }
+    };
+    auto load_tile = [&](Regs &rg, uint32_t i) {
+        const uint32_t T = tile_index(i);
+        load_k(rg, T);
+        load_s(rg, T);
+        load_v(rg, T);
+    };
+    Regs b0, b1, b2;
+    load_tile(b0, 0);
+    load_tile(b1, 1);
+    asm volatile("" ::: "memory");       // ... and the tile prologue ahead of the query's use
+
+    // ---- quantise the query rows (q8_0 per 32 dims, as ggml's vec_dot path)
+    // or round them to fp16; four lanes share a 32-dim block
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+        const int item = (t * WAVES + w) * 16 + m, r = item / NB, b = item % NB;
+        float qx[8];
+        if (r >= R) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qx[j] = 0.0f;
+        } else if (a.q_bf16) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qx[2 * j] = __uint_as_float(qraw[t][0][j] << 16);
+                qx[2 * j + 1] = __uint_as_float(qraw[t][0][j] & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qx[j] = __uint_as_float(qraw[t][0][j]);
+                qx[4 + j] = __uint_as_float(qraw[t][1][j]);
             }
         }
+        if constexpr (QUANT) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qx[j]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+            const float d = kvm_fdiv(amax, 127.0f);
+            const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+            uint32_t q01[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                q01[j >> 2] |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(qx[j], id)) << (8 * (j & 3));
+            *(kvm_u32x2 *)&s_qq[r][32 * b + 8 * g] = kvm_u32x2{q01[0], q01[1]};
+            if (g == 0) s_dq[r][b] = kvm_h2f(kvm_f2h(d));
+        } else {
+            kvm_f16x8 hv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) hv[j] = (_Float16)qx[j];
+            *(kvm_f16x8 *)&s_qh[r][32 * b + 8 * g] = hv;
+        }
     }
+    KVM_LDS_BARRIER();
+    // B operands (Q^T) of this wave's row tile: lane (row m, k-group g)
+    long qop_i[QUANT ? NB : 1];
+    kvm_f16x8 qop_h[QUANT ? 1 : NB];
+    float dqo[NG];                       // scale MFMA B operand: dq of (row m, block 4gi+g)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if constexpr (QUANT) __builtin_memcpy(&qop_i[b], &s_qq[myrow][32 * b + 8 * g], 8);
+        else qop_h[b] = *(const kvm_f16x8 *)&s_qh[myrow][32 * b + 8 * g];
+    }
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) dqo[gi] = QUANT ? s_dq[myrow][4 * gi + g] : 0.0f;
 
     kvm_f32x4 O[NRT][NT];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
-    float m_run[NRT], l_run[NRT];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) { m_run[rt] = -INFINITY; l_run[rt] = 0.0f; }
+    float m_run = -INFINITY, l_run = 0.0f;   // row myrow over this wave's keys
 
-    for (uint32_t T = t_begin; T < t_end; ++T) {
-        const uint8_t *kt = ln.wk + ((uint64_t)h * ln.n_tiles + T) * KTILE;
-        const uint8_t *vt = ln.wv + ((uint64_t)h * ln.n_tiles + T) * VTILE;
-        // ---------------- phase 1: scores of keys 16w + 4g + i -----------------
-        const int4 cp = *(const int4 *)(ln.cell_pos + (uint64_t)T * 64 + 16 * w + 4 * g);
-        float s[NRT][4];
+    auto compute_tile = [&](const Regs &rg, Regs &nx, uint32_t inext) {
+        const uint32_t Tn = tile_index(inext);
+        load_k(nx, Tn);
+        // ---------------- phase 1: scores of keys 16kq + 4g + i, row myrow -----
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (QUANT) {
-            uint4 ka[NB / 2];
+            // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
+            kvm_f32x16 dd[NG];
 #pragma unroll
-            for (int p = 0; p < NB / 2; ++p)
-                ka[p] = *(const uint4 *)(kt + (((w * (NB / 2) + p) * 64 + l) << 4));
-            uint2 dkr[NB];
-            const uint8_t *kd = kt + 64u * D + (((w * 4 + g) * NB) << 3);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) dkr[b] = *(const uint2 *)(kd + 8 * b);
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+            for (int gi = 0; gi < NG; ++gi)
+                dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[gi],
+                                                               kvm_f32x16{}, 0, 0, 0);
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                long av;
-                const uint32_t *kw = (const uint32_t *)&ka[b >> 1];
+                const kvm_u32x4 kw = rg.k[b >> 1];
                 const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
-                av = (long)(lo32 | (hi32 << 32));
-                float dk[4];
-                dk[0] = kvm_h2f((uint16_t)(dkr[b].x & 0xffffu));
-                dk[1] = kvm_h2f((uint16_t)(dkr[b].x >> 16));
-                dk[2] = kvm_h2f((uint16_t)(dkr[b].y & 0xffffu));
-                dk[3] = kvm_h2f((uint16_t)(dkr[b].y >> 16));
+                const long av = (long)(lo32 | (hi32 << 32));
+                const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) {
-                    const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b],
-                                                                             kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) s[rt][i] += (float)c[i] * (dk[i] * dqv[rt][b]);
-                }
+                for (int i = 0; i < 4; ++i) s[i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[i]);
             }
         } else {
-            kvm_f32x4 acc[NRT];
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) acc[rt] = {0.f, 0.f, 0.f, 0.f};
+            kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < NB; ++ks) {
                 kvm_f16x8 av;
-                __builtin_memcpy(&av, kt + (((w * NB + ks) * 64 + l) << 4), 16);
-#pragma unroll
-                for (int rt = 0; rt < NRT; ++rt)
-                    acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[rt][ks], acc[rt], 0, 0, 0);
+                __builtin_memcpy(&av, &rg.k[ks], 16);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[ks], acc, 0, 0, 0);
             }
 #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[rt][i] = acc[rt][i];
+            for (int i = 0; i < 4; ++i) s[i] = acc[i];
         }
-        const int32_t cpos[4] = {cp.x, cp.y, cp.z, cp.w};
-        float mx[NRT];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            mx[rt] = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool vis = cpos[i] >= 0 && cpos[i] <= qp[rt];
-                s[rt][i] = vis ? s[rt][i] * a.scale_log2 : -INFINITY;
-                mx[rt] = fmaxf(mx[rt], s[rt][i]);
-            }
-            mx[rt] = fmaxf(mx[rt], __shfl_xor(mx[rt], 16, 64));
-            mx[rt] = fmaxf(mx[rt], __shfl_xor(mx[rt], 32, 64));
-            if (g == 0) s_max[w][16 * rt + m] = mx[rt];
+        for (int i = 0; i < 4; ++i) {
+            const int32_t cpos = (int32_t)rg.cp[i];
+            const bool vis = cpos >= 0 && cpos <= qp;
+            s[i] = vis ? s[i] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, s[i]);
         }
-        __syncthreads();
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const int row = 16 * rt + m;
-            const float tm = fmaxf(fmaxf(s_max[0][row], s_max[1][row]), fmaxf(s_max[2][row], s_max[3][row]));
-            const float mn = fmaxf(m_run[rt], tm);
-            const float alpha = mn == -INFINITY ? 1.0f : exp2f(m_run[rt] - mn);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (g == 0) s_max[kq][myrow] = mx;
+        load_s(nx, Tn);
+        KVM_LDS_BARRIER();
+        // ---------------- softmax of the tile (lazy running maximum) ----------
+        {
+            const float tm = fmaxf(fmaxf(s_max[0][myrow], s_max[1][myrow]), fmaxf(s_max[2][myrow], s_max[3][myrow]));
+            const bool up = tm > m_run + KVM_LAZY_MAX;
+            const float mn = up ? tm : m_run;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
             float psum = 0.0f;
             _Float16 ph[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = mn == -INFINITY ? 0.0f : exp2f(s[rt][i] - mn);
+                const float p = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
                 const _Float16 p16 = (_Float16)p;
                 ph[i] = p16;
                 psum += (float)p16;
             }
-            l_run[rt] = l_run[rt] * alpha + psum;
-            m_run[rt] = mn;
-            __builtin_memcpy(&s_p[row][16 * w + 4 * g], ph, 8);
-            if (w == 0 && g == 0) s_alpha[row] = alpha;
+            l_run = l_run * alpha + psum;
+            m_run = mn;
+            __builtin_memcpy(&s_p[myrow][16 * kq + 4 * g], ph, 8);
+            if (kq == 0) {
+                if (g == 0) s_alpha[myrow] = alpha;
+                const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
+                if (l == 0) s_rescale[rq] = any;
+            }
         }
-        __syncthreads();
-        // ---------------- phase 2: O[:, quarter w] += P V ----------------------
+        load_v(nx, Tn);
+        KVM_LDS_BARRIER();
+        // ---------------- phase 2: O[:, dims of wave w] += P V ----------------
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
-            float ar[4];
+            if (s_rescale[rt]) {
+                float ar[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
+                for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+                for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
+                    for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
+            }
         }
+        kvm_f16x8 pa[2][NRT];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            kvm_f16x8 pa[NRT];
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt)
-                __builtin_memcpy(&pa[rt], &s_p[16 * rt + m][32 * ks + 8 * g], 16);
+            for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[16 * rt + m][32 * ks + 8 * g];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int n = DW * w + 16 * nt + m;
-                kvm_f16x8 vb;
-                if constexpr (QUANT) {
-                    const uint32_t nib = *(const uint32_t *)(vt + n * 32 + 4 * (2 * g + ks));
-                    vb = nib8_to_f16(nib);
-                    const int b = (DW * w + 16 * nt) / 32;
+        for (int bw = 0; bw < NBW; ++bw) {
+            kvm_f16x8 pp[2][NRT];
+            if constexpr (QUANT) {
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
                     kvm_f16x8 dv;
-                    __builtin_memcpy(&dv, vt + D * 32 + ((((b * 2 + ks) * 4 + g) * 8) << 1), 16);
+                    __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
 #pragma unroll
-                    for (int rt = 0; rt < NRT; ++rt) {
-                        const kvm_f16x8 pp = pa[rt] * dv;
-                        O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp, vb, O[rt][nt], 0, 0, 0);
+                    for (int rt = 0; rt < NRT; ++rt) pp[ks][rt] = pa[ks][rt] * dv;
+                }
+            }
+#pragma unroll
+            for (int ntb = 0; ntb < NTB; ++ntb) {
+                const int nt = bw * NTB + ntb;
+                if constexpr (QUANT) {
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const kvm_f16x8 vb = nib8_to_f16(rg.vq[nt][ks]);
+#pragma unroll
+                        for (int rt = 0; rt < NRT; ++rt)
+                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], vb, O[rt][nt], 0, 0, 0);
                     }
                 } else {
-                    __builtin_memcpy(&vb, vt + ((n * 64 + 8 * (2 * g + ks)) << 1), 16);
 #pragma unroll
-                    for (int rt = 0; rt < NRT; ++rt)
-                        O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[rt], vb, O[rt][nt], 0, 0, 0);
+                    for (int ks = 0; ks < 2; ++ks) {
+                        kvm_f16x8 vb;
+                        __builtin_memcpy(&vb, &rg.vh[nt][ks], 16);
+#pragma unroll
+                        for (int rt = 0; rt < NRT; ++rt)
+                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ks][rt], vb, O[rt][nt], 0, 0, 0);
+                    }
                 }
             }
         }
+    };
+
+    // three register buffers, two tiles in flight.  The loop body is straight
+    // line so the compiler's wait counts see the same loads in flight on every
+    // trip (a conditional step would make it wait for all of them); the last
+    // one or two tiles are handled after the loop.
+    uint32_t it = 0;
+    for (; it + 3 <= n_t; it += 3) {
+        compute_tile(b0, b2, it + 2);
+        compute_tile(b1, b0, it + 3);
+        compute_tile(b2, b1, it + 4);
+    }
+    if (it < n_t) {
+        compute_tile(b0, b2, it + 2);
+        if (it + 1 < n_t) compute_tile(b1, b0, it + 3);
     }
 
     // ---- partial results of this split
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-        float lr = l_run[rt];
+    {
+        float lr = l_run;
         lr += __shfl_xor(lr, 16, 64);
         lr += __shfl_xor(lr, 32, 64);
-        if (g == 0) s_l[w][16 * rt + m] = lr;
+        if (g == 0) s_l[kq][myrow] = lr;
     }
     __syncthreads();
     const uint64_t pidx = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits + split;
     float *po = a.ws + pidx * RMAX * D;
-    if (w == 0 && g == 0) {
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const int row = 16 * rt + m;
-            if (row < R) {
-                a.ws_ml[(pidx * RMAX + row) * 2 + 0] = m_run[rt];
-                a.ws_ml[(pidx * RMAX + row) * 2 + 1] = s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row];
-            }
-        }
+    if (kq == 0 && g == 0 && myrow < R) {
+        a.ws_ml[(pidx * RMAX + myrow) * 2 + 0] = m_run;
+        a.ws_ml[(pidx * RMAX + myrow) * 2 + 1] = s_l[0][myrow] + s_l[1][myrow] + s_l[2][myrow] + s_l[3][myrow];
     }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
@@ -311,55 +449,39 @@ __global__ void __launch_bounds__(256) k_fa_decode(fa_args a) {
             }
 }
 
-// Merge the splits of one (lane, kv head, row): thread = output dim.  The split
-// maxima / sums are reduced first; then every thread issues its loads of 32
-// splits at once, so the merge streams the partials instead of paying one
-// memory latency per split.
+// Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
+// output dim.  Split maxima and sums are reduced across the wave; then each
+// lane issues its loads of 32 splits at once so the merge streams the partials.
 #define KVM_MAX_SPLITS 512
 template <int D>
-__global__ void __launch_bounds__(D) k_fa_combine(fa_args a, int rmax) {
+__global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     __shared__ float s_w[KVM_MAX_SPLITS];
-    __shared__ float s_red[D / 64];
     const fa_lane ln = a.lanes[blockIdx.z];
-    const uint32_t h = blockIdx.y, row = blockIdx.x;
+    const uint32_t h = blockIdx.y, row = blockIdx.x / (D / 64);
     const uint32_t R = ln.n_tokens * a.G;
     if (row >= R) return;
-    const uint32_t d = threadIdx.x, S = a.n_splits;
+    const uint32_t l = threadIdx.x, d = (blockIdx.x % (D / 64)) * 64 + l, S = a.n_splits;
     const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
     const float *ml = a.ws_ml + (p0 * rmax + row) * 2;
     const uint64_t mstride = (uint64_t)rmax * 2;
-    float mloc = -INFINITY;
-    for (uint32_t s = d; s < S; s += D) {
-        const float m = ml[s * mstride];
-        s_w[s] = m;
-        mloc = fmaxf(mloc, m);
-    }
-    for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
-    if ((d & 63) == 0) s_red[d >> 6] = mloc;
-    __syncthreads();
-    float M = s_red[0];
-#pragma unroll
-    for (int w = 1; w < D / 64; ++w) M = fmaxf(M, s_red[w]);
+    float M = -INFINITY;
+    for (uint32_t s = l; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
     const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
     float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
     if (M == -INFINITY) {                     // no visible cell for this row
         *out = 0.0f;
         return;
     }
-    float lloc = 0.0f;
-    for (uint32_t s = d; s < S; s += D) {
-        const float m = s_w[s];
+    float L = 0.0f;
+    for (uint32_t s = l; s < S; s += 64) {
+        const float m = ml[s * mstride];
         const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
         s_w[s] = wgt;
-        lloc += ml[s * mstride + 1] * wgt;
+        L += ml[s * mstride + 1] * wgt;
     }
-    for (int o = 32; o > 0; o >>= 1) lloc += __shfl_xor(lloc, o, 64);
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     __syncthreads();
-    if ((d & 63) == 0) s_red[d >> 6] = lloc;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < D / 64; ++w) L += s_red[w];
     const float *po = a.ws + (p0 * rmax + row) * D + d;
     const uint64_t ostride = (uint64_t)rmax * D;
     float acc = 0.0f;
@@ -379,8 +501,8 @@ static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
         if (v > KVM_MAX_SPLITS) v = KVM_MAX_SPLITS;
         if (v > 0) return v < n_tiles ? v : n_tiles;
     }
-    // about 2 workgroups per CU on a 256-CU device
-    uint32_t s = (512 + n_lanes * H - 1) / (n_lanes * H);
+    // about one workgroup per CU on a 256-CU device
+    uint32_t s = (256 + n_lanes * H - 1) / (n_lanes * H);
     if (s < 1) s = 1;
     if (s > KVM_MAX_SPLITS) s = KVM_MAX_SPLITS;
     return s < n_tiles ? s : n_tiles;
@@ -388,7 +510,7 @@ static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
 
 template <int D, int NRT, bool QUANT>
 static void launch_decode(const fa_args &a, uint32_t n_lanes, hipStream_t stream) {
-    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT>), dim3(a.n_splits, a.H, n_lanes), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT>), dim3(a.n_splits, a.H, n_lanes), dim3(256 * NRT), 0, stream, a);
 }
 
 static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
@@ -441,9 +563,9 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     }
     KVM_LAUNCH_CHECK(st, "fa_decode");
     if (D == 256)
-        hipLaunchKernelGGL(k_fa_combine<256>, dim3(rmax, H, n_lanes), dim3(256), 0, st->stream, a, (int)rmax);
+        hipLaunchKernelGGL(k_fa_combine<256>, dim3(rmax * 4, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
     else
-        hipLaunchKernelGGL(k_fa_combine<128>, dim3(rmax, H, n_lanes), dim3(128), 0, st->stream, a, (int)rmax);
+        hipLaunchKernelGGL(k_fa_combine<128>, dim3(rmax * 2, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
     KVM_LAUNCH_CHECK(st, "fa_combine");
     return KVM_OK;
 }

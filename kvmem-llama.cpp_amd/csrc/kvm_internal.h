@@ -85,13 +85,18 @@ int kvm_rope_table(kvm_state *st, const float *theta, uint32_t n_half, uint32_t 
 // q8_0 K tile (head_dim D, NB = D/32 blocks):
 //   quants  64*D bytes: [sub 4][pair NB/2][lane 64][16 B]; lane l = 16g + m
 //           holds key 16*sub + m, dims 32*(2p)+8g..+7 then 32*(2p+1)+8g..+7
-//   scales  64*NB fp16: [sub 4][g 4][block NB][i 4] = key 16*sub + 4g + i
+//   scales  64*NB fp16: [sub 4][block NB][m 16] = key 16*sub + m (a lane of
+//           the 4-block scale MFMA reads 128 contiguous bytes per 4 blocks)
 // q4_0 V tile:
-//   nibbles D*32 bytes: [dim D][64 nibbles] with key c = 32ks + 8g + j stored at
-//           nibble 8*(2g+ks)+j (byte /2, low nibble when even)
+//   nibbles D*32 bytes: for dim d, key c = 32ks + 8g + j: 4-byte word
+//           ((d/16)*64 + 16g + d%16)*8 + 4ks holds keys j = 0..7 of (d, g, ks),
+//           key j in byte j%4, low nibble for j < 4 and high nibble for
+//           j >= 4 (so masking the low / shifted high nibbles gives keys 0..3 /
+//           4..7 in byte order); a lane (dim d%16, key group g) reads both ks
+//           words as one 8-byte access
 //   scales  NB*64 fp16: [block NB][ks 2][g 4][j 8]
 // f16 K tile: [sub 4][kstep D/32][lane 64][8 halves] = key 16*sub+m, dims 32ks+8g..+7
-// f16 V tile: [dim D][64 halves] in the same key order as the q4_0 nibbles.
+// f16 V tile: halves ((d/16)*64 + 16g + d%16)*16 + 8ks + j (same key order as q4_0)
 // ---------------------------------------------------------------------------
 __host__ __device__ inline uint32_t kvm_ktile_bytes(int ktype, uint32_t D) {
     return ktype == KVM_TYPE_Q8_0 ? 64u * D + 64u * (D / 32u) * 2u : 64u * D * 2u;
@@ -107,14 +112,20 @@ __host__ __device__ inline uint32_t kvm_kq_off(uint32_t D, uint32_t c, uint32_t 
 }
 // byte offset of the fp16 scale of (cell c, block b) inside a q8_0 K tile
 __host__ __device__ inline uint32_t kvm_kd_off(uint32_t D, uint32_t c, uint32_t b) {
-    const uint32_t s = c >> 4, g = (c & 15u) >> 2, i = c & 3u;
-    return 64u * D + ((((s * 4u + g) * (D / 32u) + b) * 4u + i) << 1);
+    const uint32_t s = c >> 4, m = c & 15u;
+    return 64u * D + (((s * (D / 32u) + b) * 16u + m) << 1);
 }
-// nibble position (0..63) of cell c inside a V dim row
-__host__ __device__ inline uint32_t kvm_vkey_pos(uint32_t c) {
-    const uint32_t ks = c >> 5, g = (c & 31u) >> 3, j = c & 7u;
-    return 8u * (2u * g + ks) + j;
+// byte offset of the 4-byte nibble word holding keys 32ks+8g .. +7 of dim d
+__host__ __device__ inline uint32_t kvm_vq_word(uint32_t d, uint32_t g, uint32_t ks) {
+    return ((((d >> 4) * 64u + 16u * g + (d & 15u)) << 3) + (ks << 2));
 }
+// byte offset and nibble shift of (cell c, dim d) inside a q4_0 V tile
+__host__ __device__ inline uint32_t kvm_vq_byte(uint32_t c, uint32_t d) {
+    return kvm_vq_word(d, (c & 31u) >> 3, c >> 5) + (c & 3u);
+}
+__host__ __device__ inline uint32_t kvm_vq_shift(uint32_t c) { return c & 4u; }
+// bit position of key j (0..7) inside its 4-byte nibble word
+__host__ __device__ inline uint32_t kvm_vq_nib_shift(uint32_t j) { return ((j & 3u) << 3) | (j & 4u); }
 __host__ __device__ inline uint32_t kvm_vd_off(uint32_t D, uint32_t c, uint32_t b) {
     const uint32_t ks = c >> 5, g = (c & 31u) >> 3, j = c & 7u;
     return D * 32u + ((((b * 2u + ks) * 4u + g) * 8u + j) << 1);
@@ -123,6 +134,11 @@ __host__ __device__ inline uint32_t kvm_vd_off(uint32_t D, uint32_t c, uint32_t 
 __host__ __device__ inline uint32_t kvm_kh_idx(uint32_t D, uint32_t c, uint32_t d) {
     const uint32_t s = c >> 4, m = c & 15u, ks = d >> 5, g = (d & 31u) >> 3, j = d & 7u;
     return ((s * (D / 32u) + ks) * 64u + 16u * g + m) * 8u + j;
+}
+// f16 V tile: half index of (cell c, dim d)
+__host__ __device__ inline uint32_t kvm_vh_idx(uint32_t c, uint32_t d) {
+    const uint32_t ks = c >> 5, g = (c & 31u) >> 3, j = c & 7u;
+    return ((((d >> 4) * 64u + 16u * g + (d & 15u)) * 2u + ks) << 3) + j;
 }
 
 // ---------------------------------------------------------------------------
@@ -166,17 +182,25 @@ __device__ __forceinline__ float kvm_fsqrt(float a) { return sqrtf(a); }
 // (llama-kvmem-stagein.cu:181-234): fp32 amax, d = amax/127 (q8) or vmax/-8
 // (q4), id = d ? 1/d : 0, fp16 d with RNE, roundf (ties away) / (int)(x*id+8.5).
 // Division and reciprocal are correctly rounded (kvm_fdiv) to match host IEEE.
-__device__ inline void kvm_quant_block_q8_0(const float *x, uint16_t *d_out, int8_t *q) {
+__device__ __forceinline__ void kvm_quant_block_q8_0(const float (&x)[32], uint16_t *d_out, int8_t *q) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
     const float d = kvm_fdiv(amax, 127.0f);
     const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
     *d_out = kvm_f2h(d);
+    uint32_t packed[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) q[j] = (int8_t)roundf(kvm_fmul(x[j], id));
+    for (int j = 0; j < 8; ++j) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            wv |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(x[4 * j + k], id)) << (8 * k);
+        packed[j] = wv;
+    }
+    __builtin_memcpy(q, packed, 32);
 }
-__device__ inline void kvm_quant_block_q4_0(const float *x, uint16_t *d_out, uint8_t *q) {
+__device__ __forceinline__ void kvm_quant_block_q4_0(const float (&x)[32], uint16_t *d_out, uint8_t *q) {
     float amax = 0.0f, vmax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {

@@ -171,24 +171,25 @@ __global__ void __launch_bounds__(256) k_stagein(stage_args a) {
         uint8_t *kt = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
         stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, j, base + (int32_t)(t0 + j), a.rc);
     }
-    // V nibbles: destination-driven, one 32-bit word (4 bytes = 8 keys) per step
+    // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
     for (uint32_t wi = tid; wi < a.H * D * 8; wi += 256) {
-        const uint32_t h = wi / (D * 8), dd = (wi / 8) % D, kb0 = (wi % 8) * 4;
+        const uint32_t h = wi / (D * 8), r = wi % (D * 8);
+        const uint32_t X = r >> 1, ks = r & 1u;
+        const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
         const uint32_t b = dd / 32, e = dd % 32;
         uint32_t word = 0;
 #pragma unroll
-        for (uint32_t k = 0; k < 8; ++k) {
-            const uint32_t pos = 2 * kb0 + k, q = pos / 8;
-            const uint32_t cj = 32 * (q & 1) + 8 * (q >> 1) + (pos & 7);
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t cj = 32 * ks + 8 * gg + j;
             uint32_t nib = 0;
             if (cj < count) {
                 const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
                 nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
             }
-            word |= nib << (4 * k);
+            word |= nib << kvm_vq_nib_shift(j);
         }
-        *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + dd * 32 + kb0) = word;
+        *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
     }
     for (uint32_t si2 = tid; si2 < a.H * 64 * NB; si2 += 256) {
         const uint32_t h = si2 / (64 * NB), cj = (si2 / NB) % 64, b = si2 % NB;

@@ -102,30 +102,30 @@ __global__ void k_import_k_f16(win_geo g, uint32_t cell0, uint32_t n, const uint
     dst[kvm_kh_idx(g.D, c, d)] = rows[((uint64_t)t * g.H + h) * g.D + d];
 }
 
-// q4_0 V nibbles: one thread per destination byte (head, tile, dim, byte) so the
-// two cells sharing a byte are written by one thread; cells outside
+// q4_0 V nibbles: one thread per destination 32-bit word (8 keys of one dim),
+// so the cells sharing a byte are written by one thread; cells outside
 // [cell0, cell0+n) keep their nibble.
 __global__ void k_import_v_q4(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
     const uint32_t NB = g.D / 32;
     const uint32_t t0 = cell0 / 64, t1 = (cell0 + n + 63) / 64;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (uint64_t)(t1 - t0) * g.H * g.D * 32) return;
-    const uint32_t kbyte = i % 32, d = (i / 32) % g.D, h = (i / (32ull * g.D)) % g.H;
-    const uint32_t tile = t0 + (uint32_t)(i / (32ull * g.D * g.H));
-    uint8_t *dst = g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile + d * 32 + kbyte;
-    uint8_t byte = *dst;
+    if (i >= (uint64_t)(t1 - t0) * g.H * g.D * 8) return;
+    const uint32_t wi = i % (g.D * 8), h = (i / (8ull * g.D)) % g.H;
+    const uint32_t tile = t0 + (uint32_t)(i / (8ull * g.D * g.H));
+    const uint32_t X = wi >> 1, ks = wi & 1u;
+    const uint32_t d = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
+    uint32_t *dst = (uint32_t *)(g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile + kvm_vq_word(d, gg, ks));
+    uint32_t word = *dst;
     const uint32_t b = d / 32, e = d % 32;
 #pragma unroll
-    for (uint32_t half = 0; half < 2; ++half) {
-        const uint32_t pos = 2 * kbyte + half, q = pos / 8;
-        const uint32_t c = 32 * (q & 1) + 8 * (q >> 1) + (pos & 7);
-        const uint32_t cell = tile * 64 + c;
+    for (uint32_t j = 0; j < 8; ++j) {
+        const uint32_t cell = tile * 64 + 32 * ks + 8 * gg + j;
         if (cell < cell0 || cell >= cell0 + n) continue;
         const uint8_t *blk = rows + ((uint64_t)(cell - cell0) * g.H + h) * NB * 18 + (uint64_t)b * 18;
-        const uint8_t nib = e < 16 ? (blk[2 + e] & 15) : (blk[2 + e - 16] >> 4);
-        byte = half ? (uint8_t)((byte & 0x0f) | (nib << 4)) : (uint8_t)((byte & 0xf0) | nib);
+        const uint32_t nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
+        word = (word & ~(15u << kvm_vq_nib_shift(j))) | (nib << kvm_vq_nib_shift(j));
     }
-    *dst = byte;
+    *dst = word;
 }
 
 __global__ void k_import_v_q4_scales(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
@@ -146,7 +146,7 @@ __global__ void k_import_v_f16(win_geo g, uint32_t cell0, uint32_t n, const uint
     const uint32_t d = i % g.D, h = (i / g.D) % g.H, t = (uint32_t)(i / ((uint64_t)g.D * g.H));
     const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
     uint16_t *dst = (uint16_t *)(g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile);
-    dst[d * 64 + kvm_vkey_pos(c)] = rows[((uint64_t)t * g.H + h) * g.D + d];
+    dst[kvm_vh_idx(c, d)] = rows[((uint64_t)t * g.H + h) * g.D + d];
 }
 
 __global__ void k_copy_i32(int32_t *dst, const int32_t *src, uint32_t n) {
@@ -179,7 +179,7 @@ extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32
     if (v_rows) {
         if (w->v_type == KVM_TYPE_Q4_0) {
             const uint32_t t0 = cell0 / 64, t1 = (cell0 + n + 63) / 64;
-            const uint64_t nb = (uint64_t)(t1 - t0) * g.H * g.D * 32;
+            const uint64_t nb = (uint64_t)(t1 - t0) * g.H * g.D * 8;
             hipLaunchKernelGGL(k_import_v_q4, dim3(kvm_cdiv(nb, 256)), dim3(256), 0, st->stream, g, cell0, n,
                                (const uint8_t *)v_rows);
             const uint64_t ns = (uint64_t)n * g.H * NB;
@@ -231,12 +231,10 @@ __global__ void k_export_v_q4(win_geo g, uint32_t cell0, uint32_t n, uint8_t *ro
     const uint8_t *sd = src + kvm_vd_off(g.D, c, b);
     dst[0] = sd[0];
     dst[1] = sd[1];
-    const uint32_t pos = kvm_vkey_pos(c);
+    const uint32_t sh = kvm_vq_shift(c);
     for (uint32_t e = 0; e < 16; ++e) {
-        const uint8_t lo = src[(32 * b + e) * 32 + pos / 2];
-        const uint8_t hi = src[(32 * b + e + 16) * 32 + pos / 2];
-        const uint8_t n0 = (pos & 1) ? (lo >> 4) : (lo & 15);
-        const uint8_t n1 = (pos & 1) ? (hi >> 4) : (hi & 15);
+        const uint8_t n0 = (src[kvm_vq_byte(c, 32 * b + e)] >> sh) & 15;
+        const uint8_t n1 = (src[kvm_vq_byte(c, 32 * b + e + 16)] >> sh) & 15;
         dst[2 + e] = (uint8_t)(n0 | (n1 << 4));
     }
 }
@@ -252,7 +250,7 @@ __global__ void k_export_f16(win_geo g, uint32_t cell0, uint32_t n, uint16_t *kr
     }
     if (vrows) {
         const uint16_t *src = (const uint16_t *)(g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile);
-        vrows[((uint64_t)t * g.H + h) * g.D + d] = src[d * 64 + kvm_vkey_pos(c)];
+        vrows[((uint64_t)t * g.H + h) * g.D + d] = src[kvm_vh_idx(c, d)];
     }
 }
 

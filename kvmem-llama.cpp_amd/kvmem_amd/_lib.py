@@ -113,11 +113,15 @@ _lib = None
 
 
 def load(path=None):
-    """Load libkvm_hotpath.so (raises if it is missing) and bind every entry point."""
+    """Load libkvm_hotpath.so (raises if it is missing) and bind every entry point.
+
+    KVM_HOTPATH_LIB in the environment names another build of the library to
+    load in place of the in-tree one.
+    """
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = path or LIB_PATH
+    p = path or os.environ.get("KVM_HOTPATH_LIB") or LIB_PATH
     if not os.path.exists(p):
         raise RuntimeError(f"libkvm_hotpath.so is not built ({p}); run __graft_entry__.build()")
     lib = C.CDLL(p)
