@@ -72,7 +72,7 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02):
     hist.c = L.History(kbuf.ptr, vbuf.ptr, HIST_TOKENS)
     # query: 4 tokens whose pre-RoPE rows point at 16 planted blocks
     planted = W.distinct_ids(seed, 0, PLANTED, 1, n_blocks)
-    means = ix0.k_sum[0][:, torch.from_numpy(planted).to(dev)] / float(BT)      # [H*D, 16]
+    means = ix0.block_sums()[0][torch.from_numpy(planted).to(dev)].T / float(BT)   # [H*D, 16]
     qsum_kv = means.sum(1).view(H_KV, D)
     qrows = qsum_kv.repeat_interleave(G, 0).reshape(1, N_HEAD * D).repeat(MTP, 1)
     qrows = qrows + 0.1 * torch.randn(qrows.shape, generator=gen, device=dev)
@@ -139,7 +139,7 @@ def cpu_baseline(O, np, wl, out_gpu, budget_s=20.0):
     n_threads = min(16, os.cpu_count() or 1)
     ix, w, sel = wl["reps"][0]
     n_blocks = HIST_TOKENS // BT
-    k_sum = np.ascontiguousarray(ix.k_sum[0].cpu().numpy().T)[None]          # [1][blocks][e]
+    k_sum = ix.block_sums().cpu().numpy()                                   # [1][blocks][e]
     mt = ix.mean_tokens.cpu().numpy().astype(np.uint32)
     q_sum = wl["qa"].q_sum.cpu().numpy()
     q_cnt = wl["qa"].q_count.cpu().numpy().astype(np.uint32)

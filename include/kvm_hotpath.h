@@ -155,11 +155,16 @@ typedef struct kvm_meank_index {
     uint32_t n_head_kv;
     uint32_t head_dim;
     uint32_t block_tokens;
-    float *k_sum;           /* device [n_layer][n_head_kv * head_dim][n_blocks]: embedding-major,
-                             * blocks fastest, so scoring lanes (one block each) read coalesced */
+    float *k_sum;           /* device [n_layer][ceil(n_blocks/8)][n_head_kv * head_dim][8]:
+                             * 8-block tiles, embedding-major inside a tile, so one tile's
+                             * sums for every head are one contiguous slab for the scorer;
+                             * kvm_meank_k_sum_floats() gives the size */
     uint32_t *mean_tokens;  /* device [n_layer][n_blocks] */
     uint8_t *present;       /* device [n_blocks] (RawKvStore::has_block), or NULL = all */
 } kvm_meank_index;
+
+/* Number of floats k_sum must hold for the index geometry in *ix. */
+size_t kvm_meank_k_sum_floats(const kvm_meank_index *ix);
 
 /* RawKvStore::write_layer_mean_k (raw_kv_store.cpp:685-705): add n token rows of
  * layer il starting at original position pos0.  k_rows: device fp32

@@ -450,9 +450,11 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
 }
 
 // Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
-// output dim.  Split maxima and sums are reduced across the wave; then each
-// lane issues its loads of 32 splits at once so the merge streams the partials.
+// output dim.  Every load is issued before any use (split maxima and sums one
+// per lane, the partial outputs KVM_COMBINE_BATCH splits per lane), so the
+// merge costs one memory round trip for up to that many splits.
 #define KVM_MAX_SPLITS 512
+#define KVM_COMBINE_BATCH 64
 template <int D>
 __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     __shared__ float s_w[KVM_MAX_SPLITS];
@@ -464,8 +466,16 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
     const float *ml = a.ws_ml + (p0 * rmax + row) * 2;
     const uint64_t mstride = (uint64_t)rmax * 2;
-    float M = -INFINITY;
-    for (uint32_t s = l; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
+    const float *po = a.ws + (p0 * rmax + row) * D + d;
+    const uint64_t ostride = (uint64_t)rmax * D;
+    // first batch of partial outputs, and this lane's split (m, l), in flight together
+    float v[KVM_COMBINE_BATCH];
+#pragma unroll
+    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) v[j] = po[(uint64_t)(j < (int)S ? j : 0) * ostride];
+    const float m_l = l < S ? ml[l * mstride] : -INFINITY;
+    const float l_l = l < S ? ml[l * mstride + 1] : 0.0f;
+    float M = m_l;
+    for (uint32_t s = l + 64; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
     const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
     float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
@@ -475,22 +485,22 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     }
     float L = 0.0f;
     for (uint32_t s = l; s < S; s += 64) {
-        const float m = ml[s * mstride];
+        const float m = s == l ? m_l : ml[s * mstride];
         const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
         s_w[s] = wgt;
-        L += ml[s * mstride + 1] * wgt;
+        L += (s == l ? l_l : ml[s * mstride + 1]) * wgt;
     }
     for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
     __syncthreads();
-    const float *po = a.ws + (p0 * rmax + row) * D + d;
-    const uint64_t ostride = (uint64_t)rmax * D;
     float acc = 0.0f;
-    for (uint32_t s0 = 0; s0 < S; s0 += 32) {
-        float v[32];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = s0 + j < S ? po[(s0 + j) * ostride] : 0.0f;
+    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) acc += j < (int)S ? v[j] * s_w[j] : 0.0f;
+    for (uint32_t s0 = KVM_COMBINE_BATCH; s0 < S; s0 += 32) {
+        float u[32];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) acc += s0 + j < S ? v[j] * s_w[s0 + j] : 0.0f;
+        for (int j = 0; j < 32; ++j) u[j] = s0 + j < S ? po[(s0 + j) * ostride] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc += s0 + j < S ? u[j] * s_w[s0 + j] : 0.0f;
     }
     *out = L > 0.0f ? acc / L : 0.0f;
 }

@@ -155,6 +155,18 @@ __device__ inline float kvm_h2f(uint16_t h) {
     __builtin_memcpy(&v, &h, 2);
     return (float)v;
 }
+// Inclusive prefix sum over a wave64 with DPP: Kogge-Stone row shifts within
+// each 16-lane row, then row broadcasts of lane 15 (to rows 1, 3) and lane 31
+// (to rows 2, 3).
+__device__ inline uint32_t kvm_wave_incl_scan(uint32_t x) {
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
 // IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
 // The empty asm keeps the conversion a separate instruction: fused with its
 // producer (fptrunc(x * c) -> v_fma_mix(x, c, +0)) a -0.0 result turns into +0.0.

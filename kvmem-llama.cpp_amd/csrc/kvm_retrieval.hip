@@ -58,9 +58,22 @@ extern "C" int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t i
 // ---------------------------------------------------------------------------
 // Mean-K sums (RawKvStore::write_layer_mean_k / add_mean_f32,
 // raw_kv_store.cpp:215-234, 685-705).  Device layout of the index:
-// k_sum[il][e][block] (embedding-major, blocks fastest) so the scorer's lanes
-// (one block each) read consecutive addresses.
+// k_sum[il][tile][e][8] with tile = block / 8 (KVM_MEANK_TILE blocks, the
+// embedding index e fastest after the block-in-tile): a tile's sums for all
+// heads are one contiguous slab, which the scorer streams whole.
 // ---------------------------------------------------------------------------
+#define KVM_MEANK_TILE 8u
+
+__host__ __device__ inline uint64_t kvm_meank_off(uint32_t n_embd, uint32_t e, uint32_t b) {
+    return ((uint64_t)(b / KVM_MEANK_TILE) * n_embd + e) * KVM_MEANK_TILE + b % KVM_MEANK_TILE;
+}
+
+extern "C" size_t kvm_meank_k_sum_floats(const kvm_meank_index *ix) {
+    if (!ix) return 0;
+    const size_t tiles = (ix->n_blocks + KVM_MEANK_TILE - 1) / KVM_MEANK_TILE;
+    return (size_t)ix->n_layer * tiles * KVM_MEANK_TILE * ix->n_head_kv * ix->head_dim;
+}
+
 __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *present, uint32_t cap,
                             uint32_t n_embd, uint32_t bt, uint32_t pos0, uint32_t n,
                             const float *rows) {
@@ -73,7 +86,7 @@ __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *presen
     if (bid >= cap || start >= end) return;
     const uint32_t off = start - bid * bt, take = end - start;
     if (e < n_embd) {
-        float *p = k_sum + (uint64_t)e * cap + bid;
+        float *p = k_sum + kvm_meank_off(n_embd, e, bid);
         float s = off == 0 ? 0.0f : *p;
         for (uint32_t t = start; t < end; ++t) s = kvm_fadd(s, rows[(uint64_t)(t - pos0) * n_embd + e]);
         *p = s;
@@ -97,8 +110,9 @@ extern "C" int kvm_meank_add(kvm_state *st, const kvm_meank_index *ix, uint32_t 
     KVM_HIP(st, hipSetDevice(st->device));
     const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
     const uint32_t n_chunks = last - pos0 / bt + 1;
+    const uint64_t layer_floats = (uint64_t)kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE) * KVM_MEANK_TILE * n_embd;
     hipLaunchKernelGGL(k_meank_add, dim3(kvm_cdiv(n_embd, 256), n_chunks), dim3(256), 0, st->stream,
-                       ix->k_sum + (uint64_t)il * n_embd * ix->n_blocks,
+                       ix->k_sum + (uint64_t)il * layer_floats,
                        ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present, ix->n_blocks, n_embd,
                        bt, pos0, n, k_rows);
     KVM_LAUNCH_CHECK(st, "meank_add");
@@ -106,104 +120,206 @@ extern "C" int kvm_meank_add(kvm_state *st, const kvm_meank_index *ix, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
-// Scoring.  Workgroup = n_head_kv waves; wave h scores kv head h of 64
-// consecutive blocks (lane = block).  The per-(layer, head) query vector
-// qv = qh * invq and its sequential norm nq do not depend on the block and are
-// built once per workgroup in LDS with the reference's operation order.
+// Scoring.  Workgroup = (8-block tile t, layer il), four waves; chain lane
+// (hh, bi) = 8*hh + bi owns block 8t + bi under head 8c + hh of head chunk c
+// (up to 8 heads per chunk).  Per chunk:
+//   1. the tile's slab of mean-K sums (8 blocks x the chunk's heads x D,
+//      contiguous) is loaded in one round trip, turned into
+//      kh = k_sum * (1/mean_tokens) (+0.0 for a block without tokens, the
+//      reference's zeroed mean) and written to LDS as [dim][lane], while each
+//      wave builds qv = qh * invq of two of the chunk's heads;
+//   2. wave 0 runs the sequential fp32 dot chains, wave 1 the nk chains and
+//      wave 2 the block-independent nq chains (lane hh), in the reference's
+//      operation order;
+//   3. wave 0 forms the cosines.
+// Lanes bi of wave 0 then sum each block's cosines over the heads in double
+// in head order and write the layer's contribution layer/H to a workspace
+// [layer][block] that the top-k kernel averages over layers.
 // ---------------------------------------------------------------------------
 struct score_args {
     const float *q_sum;
     const uint32_t *q_count;
     const float *k_sum;
     const uint32_t *mean_tokens;
-    const uint8_t *present;
-    double *scores;
-    uint32_t n_blocks, cap, n_layer, n_head, H;
+    double *layer_score;    // [n_layer][cap]
+    uint32_t n_blocks, cap, n_tiles, n_layer, n_head, H;
 };
 
-template <int D, int CH, int MAXT>
-__global__ void __launch_bounds__(MAXT) k_score(score_args a) {
-    extern __shared__ float s_qv[];                  // [n_layer][H*D] then nq[n_layer][H]
-    const uint32_t HD = a.H * D;
-    float *s_nq = s_qv + (size_t)a.n_layer * HD;
-    __shared__ float s_cos[16][64];
-    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
-    const uint32_t g = a.H == 0 ? 1u : a.n_head / a.H;
-    const uint32_t g1 = g > 1u ? g : 1u;
-    for (uint32_t idx = tid; idx < a.n_layer * HD; idx += nthr) {
-        const uint32_t il = idx / HD, h = (idx % HD) / D, d = idx % D;
-        float qh = 0.0f;
-        for (uint32_t gi = 0; gi < g; ++gi) {
-            const uint32_t qi = h * g + gi;
-            if (qi >= a.n_head) break;
-            qh = kvm_fadd(qh, a.q_sum[(uint64_t)il * a.n_head * D + (uint64_t)qi * D + d]);
-        }
-        const float invq = kvm_fdiv(1.0f, (float)(a.q_count[il] * g1));
-        s_qv[idx] = kvm_fmul(qh, invq);
-    }
-    __syncthreads();
-    for (uint32_t idx = tid; idx < a.n_layer * a.H; idx += nthr) {
-        const float *qv = s_qv + (size_t)(idx / a.H) * HD + (size_t)(idx % a.H) * D;
-        float nq = 0.0f;
-        for (uint32_t d = 0; d < D; ++d) nq = kvm_fadd(nq, kvm_fmul(qv[d], qv[d]));
-        s_nq[idx] = nq;
-    }
-    __syncthreads();
+// Workgroup barrier for LDS traffic only (no wait for outstanding global
+// stores, which a __syncthreads fence would add).
+#define KVM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+#define KVM_SCORE_GMAX 16   // largest query group (n_head / n_head_kv)
+#define KVM_SCORE_HMAX 16   // largest n_head_kv
 
-    const uint32_t h = tid >> 6, lane = tid & 63;
-    const uint32_t b = blockIdx.x * 64 + lane;
-    const bool valid = b < a.n_blocks;
-    double acc = 0.0;
-    uint32_t nlay = 0;
-    for (uint32_t il = 0; il < a.n_layer; ++il) {
-        if (a.q_count[il] == 0) continue;             // uniform across the workgroup
-        float c = 0.0f;
-        if (valid) {
-            const uint32_t mt = a.mean_tokens[(uint64_t)il * a.cap + b];
-            const float inv = mt ? kvm_fdiv(1.0f, (float)mt) : 0.0f;
-            const float *ks = a.k_sum + (uint64_t)il * HD * a.cap + (uint64_t)h * D * a.cap + b;
-            // Issue CH dims of the column at once (one coalesced 256-byte access
-            // per dim across the wave) before the sequential fp32 chain over them,
-            // so the index streams with CH loads in flight per lane.
-            const float *qv = s_qv + (size_t)il * HD + (size_t)h * D;
-            float dot = 0.0f, nk = 0.0f;
-            for (uint32_t c0 = 0; c0 < (uint32_t)D; c0 += CH) {
-                float kraw[CH];
+// One head chunk of a tile (up to 8 heads): slab batches of 32 dims for all
+// the chunk's heads stream into LDS as kh while the chains advance batch by
+// batch.  UPB = 16-byte slab units per thread and batch (1 for <= 4 heads).
+template <int D, int UPB>
+__device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile, uint32_t c,
+                                            uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[64],
+                                            float (*s_qv)[D + 4], float *s_nq, float *s_nk,
+                                            float (*s_cos)[KVM_MEANK_TILE], float *dot_out) {
+    constexpr uint32_t TW = KVM_MEANK_TILE, HC = 64 / TW, NBAT = D / 32;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t HD = a.H * D;
+    // ---- all loads first: query gathers, token counts, slab batches
+    float qg[2][8][D / 64];
 #pragma unroll
-                for (uint32_t d = 0; d < (uint32_t)CH; ++d)
-                    kraw[d] = __builtin_nontemporal_load(ks + (uint64_t)(c0 + d) * a.cap);
+    for (int hs = 0; hs < 2; ++hs) {
+        const uint32_t hl = w + 4 * hs, h = c * HC + (hl < nh ? hl : 0u);
 #pragma unroll
-                for (uint32_t d = 0; d < (uint32_t)CH; ++d) {
-                    const float kh = mt ? kvm_fmul(kraw[d], inv) : 0.0f;
-                    dot = kvm_fadd(dot, kvm_fmul(qv[c0 + d], kh));
-                    nk = kvm_fadd(nk, kvm_fmul(kh, kh));
-                }
-            }
-            const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[il * a.H + h]), kvm_fsqrt(nk)), 1e-6f);
-            c = kvm_fdiv(dot, den);
+        for (int gi = 0; gi < 8; ++gi) {
+            const uint32_t gc = (uint32_t)gi < g ? (uint32_t)gi : 0u;
+#pragma unroll
+            for (int j = 0; j < D / 64; ++j)
+                qg[hs][gi][j] = a.q_sum[((uint64_t)il * a.n_head + h * g + gc) * D + lane + 64 * j];
         }
-        s_cos[h][lane] = c;
-        __syncthreads();
-        if (h == 0 && valid) {
-            double layer = 0.0;
-            for (uint32_t hh = 0; hh < a.H; ++hh) layer += (double)s_cos[hh][lane];
-            acc += layer / (double)(a.H > 1 ? a.H : 1);
-            nlay++;
-        }
-        __syncthreads();
     }
-    if (h == 0 && valid) {
-        double sc = nlay ? acc / (double)nlay : 0.0;
-        if (a.present && !a.present[b]) sc = 0.0;
-        a.scores[b] = sc;
+    const uint32_t quad = tid % (TW / 4);
+    uint32_t mt4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t b = tile * TW + 4 * quad + j;
+        mt4[j] = a.mean_tokens[(uint64_t)il * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
+    }
+    // unit t + 256*x of batch k: head hu = unit/64, dim 32k + (unit%64)/2, quad
+    const kvm_f32x4 *slab = (const kvm_f32x4 *)(a.k_sum + (((uint64_t)il * a.n_tiles + tile) * HD + (uint64_t)c * HC * D) * TW);
+    kvm_f32x4 kv[NBAT][UPB];
+#pragma unroll
+    for (uint32_t k = 0; k < NBAT; ++k)
+#pragma unroll
+        for (int x = 0; x < UPB; ++x) {
+            const uint32_t u = tid + 256u * x, hu = u / 64, r = (u % 64) / 2;
+            const uint32_t row = (hu < nh ? hu : 0u) * D + 32 * k + r;
+            kv[k][x] = __builtin_nontemporal_load(slab + row * (TW / 4) + quad);
+        }
+    if (qc == 0) return;                 // layer without queries: skipped by the reduction
+    // ---- qv of heads w, w + 4 (the group's q rows summed in order, scaled)
+    const float invq = kvm_fdiv(1.0f, (float)(qc * (g > 1u ? g : 1u)));
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs) {
+        const uint32_t hl = w + 4 * hs;
+        if (hl < nh) {
+            const uint32_t h = c * HC + hl;
+#pragma unroll
+            for (int j = 0; j < D / 64; ++j) {
+                float qh = 0.0f;
+#pragma unroll
+                for (int gi = 0; gi < 8; ++gi)
+                    if ((uint32_t)gi < g) qh = kvm_fadd(qh, qg[hs][gi][j]);
+                for (uint32_t g0 = 8; g0 < g; ++g0)              // groups above 8 (rare)
+                    qh = kvm_fadd(qh, a.q_sum[((uint64_t)il * a.n_head + h * g + g0) * D + lane + 64 * j]);
+                s_qv[hl][lane + 64 * j] = kvm_fmul(qh, invq);
+            }
+        }
+    }
+    float inv4[4];
+    uint32_t keep4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        inv4[j] = mt4[j] ? kvm_fdiv(1.0f, (float)mt4[j]) : 0.0f;
+        keep4[j] = mt4[j] ? 0xffffffffu : 0u;
+    }
+    // ---- batches: write kh, then the chains take 32 more dims
+    const uint32_t hh = lane / TW;
+    const float *qrow = s_qv[hh < nh ? hh : 0u];
+    const float *nqrow = s_qv[lane < nh ? lane : 0u];
+    float chain = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < NBAT; ++k) {
+#pragma unroll
+        for (int x = 0; x < UPB; ++x) {
+            const uint32_t u = tid + 256u * x, hu = u / 64, r = (u % 64) / 2;
+            if (hu < nh) {
+                float4 kh;
+                kh.x = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][0], inv4[0])) & keep4[0]);
+                kh.y = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][1], inv4[1])) & keep4[1]);
+                kh.z = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][2], inv4[2])) & keep4[2]);
+                kh.w = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][3], inv4[3])) & keep4[3]);
+                *(float4 *)&s_k[32 * k + r][hu * TW + 4 * quad] = kh;
+            }
+        }
+        KVM_LDS_BARRIER();
+        if (w == 0) {
+#pragma unroll
+            for (int d = 32 * k; d < (int)(32 * k + 32); d += 4) {
+                const float4 q4 = *(const float4 *)&qrow[d];
+                chain = kvm_fadd(chain, kvm_fmul(q4.x, s_k[d][lane]));
+                chain = kvm_fadd(chain, kvm_fmul(q4.y, s_k[d + 1][lane]));
+                chain = kvm_fadd(chain, kvm_fmul(q4.z, s_k[d + 2][lane]));
+                chain = kvm_fadd(chain, kvm_fmul(q4.w, s_k[d + 3][lane]));
+            }
+        } else if (w == 1) {
+#pragma unroll
+            for (int d = 32 * k; d < (int)(32 * k + 32); ++d) {
+                const float kh = s_k[d][lane];
+                chain = kvm_fadd(chain, kvm_fmul(kh, kh));
+            }
+        } else if (w == 2) {
+#pragma unroll
+            for (int d = 32 * k; d < (int)(32 * k + 32); d += 4) {
+                const float4 q4 = *(const float4 *)&nqrow[d];
+                chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
+                chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
+                chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
+                chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
+            }
+        }
+    }
+    if (w == 1) s_nk[lane] = chain;
+    if (w == 2 && lane < nh) s_nq[lane] = chain;
+    KVM_LDS_BARRIER();
+    // ---- cosines of the chunk
+    const uint32_t bi = lane % TW, b = tile * TW + bi;
+    if (w == 0 && hh < nh && b < a.n_blocks) {
+        const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[hh]), kvm_fsqrt(s_nk[lane])), 1e-6f);
+        s_cos[c * HC + hh][bi] = kvm_fdiv(chain, den);
+    }
+    *dot_out = chain;
+    KVM_LDS_BARRIER();                   // chunk c's LDS reads done before chunk c+1 writes
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) k_score(score_args a) {
+    constexpr uint32_t TW = KVM_MEANK_TILE;       // blocks per tile
+    constexpr uint32_t HC = 64 / TW;              // heads per chunk
+    __shared__ float s_k[D][64];                  // kh as [dim][lane]
+    __shared__ __align__(16) float s_qv[HC][D + 4];
+    __shared__ float s_nq[HC];
+    __shared__ float s_nk[64];
+    __shared__ float s_cos[KVM_SCORE_HMAX][TW];
+    const uint32_t tile = blockIdx.x, il = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t qc = a.q_count[il];
+    const uint32_t g = a.n_head / a.H;
+    for (uint32_t c = 0; c * HC < a.H; ++c) {
+        const uint32_t nh = a.H - c * HC < HC ? a.H - c * HC : HC;
+        float dot;
+        if (nh <= 4) score_chunk<D, 1>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
+        else score_chunk<D, 2>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
+        if (qc == 0) return;
+    }
+    if (w == 0 && lane < TW && tile * TW + lane < a.n_blocks) {
+        double layer = 0.0;
+        for (uint32_t h = 0; h < a.H; ++h) layer += (double)s_cos[h][lane];
+        a.layer_score[(uint64_t)il * a.cap + tile * TW + lane] = layer / (double)(a.H > 1 ? a.H : 1);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Top-k + layout: one workgroup of 1024 threads.
+// Top-k + layout: one workgroup of 1024 threads; thread t owns the blocks
+// t, t + 1024, ... for loading and the contiguous range [t*per, (t+1)*per)
+// for compaction.  Every global read is issued before any use; barriers
+// order LDS only.
 // ---------------------------------------------------------------------------
 struct topk_args {
-    const double *scores;
+    const double *scores_in;   // caller's scores (kvm_select_topk), or null
+    const double *layer_score; // per-layer contributions [layer][cap] (kvm_score_topk)
+    const uint32_t *q_count;
+    const uint8_t *present;
+    double *scores_out;        // scores reduced from the layer contributions
     const uint32_t *n_tokens;
     const uint32_t *mandatory;
     const uint32_t *slot_block;
@@ -212,8 +328,11 @@ struct topk_args {
     int32_t *to_base;
     uint32_t *stage_slots;
     uint32_t *info;
-    uint32_t n, budget, sink, recent, n_mand, n_slots, cap;
+    uint32_t n, budget, sink, recent, n_mand, n_slots, cap, n_layer, ls_cap;
 };
+
+#define KVM_TOPK_THREADS 1024
+#define KVM_TOPK_LOAD (KVM_MAX_TOPK_BLOCKS / KVM_TOPK_THREADS)
 
 // order-preserving map of a double to uint64 (-0.0 folded onto +0.0, so the
 // two compare equal as in the reference's `sa != sb` test)
@@ -223,48 +342,92 @@ __device__ inline uint64_t ord_key(double x) {
     return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
 }
 
-// exclusive prefix sum over the workgroup; returns the total through *total
-__device__ uint32_t block_scan(uint32_t v, uint32_t *s_tmp, uint32_t *total) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
-    uint32_t x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(x, o, 64);
-        if (lane >= (uint32_t)o) x += y;
-    }
-    if (lane == 63) s_tmp[wid] = x;
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t run = 0;
-        for (uint32_t w = 0; w < nw; ++w) {
-            const uint32_t t = s_tmp[w];
-            s_tmp[w] = run;
-            run += t;
-        }
-        s_tmp[nw] = run;
-    }
-    __syncthreads();
-    const uint32_t res = x - v + s_tmp[wid];
-    *total = s_tmp[nw];
-    __syncthreads();
-    return res;
+// exclusive prefix sums of two values over the workgroup (DPP wave scans,
+// one LDS exchange of the wave totals); totals through t1, t2
+__device__ void block_scan2(uint32_t v1, uint32_t v2, uint32_t *s_tmp, uint32_t &e1, uint32_t &e2,
+                            uint32_t &t1, uint32_t &t2) {
+    constexpr uint32_t NW = KVM_TOPK_THREADS / 64;
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint32_t x1 = kvm_wave_incl_scan(v1), x2 = kvm_wave_incl_scan(v2);
+    if (lane == 63) { s_tmp[wid] = x1; s_tmp[NW + wid] = x2; }
+    KVM_LDS_BARRIER();
+    const uint32_t w1 = lane < NW ? s_tmp[lane] : 0u, w2 = lane < NW ? s_tmp[NW + lane] : 0u;
+    const uint32_t i1 = kvm_wave_incl_scan(w1), i2 = kvm_wave_incl_scan(w2);
+    e1 = x1 - v1 + __builtin_amdgcn_readlane(i1 - w1, wid);
+    e2 = x2 - v2 + __builtin_amdgcn_readlane(i2 - w2, wid);
+    t1 = __builtin_amdgcn_readlane(i1, NW - 1);
+    t2 = __builtin_amdgcn_readlane(i2, NW - 1);
+    KVM_LDS_BARRIER();
+}
+
+// s_hist[bin] += 1 for every active lane, one atomic per distinct bin run:
+// the lanes sharing the first active lane's bin are counted with a ballot
+// (the skewed top digits put most keys in one bin), the rest individually.
+__device__ inline void hist_add(uint32_t *s_hist, uint32_t bin, bool active) {
+    const uint64_t act = __builtin_amdgcn_ballot_w64(active);
+    if (!act) return;
+    const uint32_t lead = (uint32_t)__builtin_ctzll(act);
+    const uint32_t lbin = __builtin_amdgcn_readlane(bin, lead);
+    const uint64_t same = __builtin_amdgcn_ballot_w64(active && bin == lbin);
+    if ((threadIdx.x & 63) == lead) atomicAdd(&s_hist[lbin], (uint32_t)__builtin_popcountll(same));
+    if (active && bin != lbin) atomicAdd(&s_hist[bin], 1u);
 }
 
 // Selection of the `need` best candidates under the strict order
-// (score desc, block id desc): an 8-pass MSB-first radix select over the
-// order-preserving 64-bit keys finds the need-th largest key T; keys above T
-// are taken, and among keys equal to T the highest block ids.
-__global__ void __launch_bounds__(1024) k_topk(topk_args a) {
+// (score desc, block id desc): an MSB-first radix select over the
+// order-preserving 64-bit keys narrows to the bin holding the need-th largest
+// key; it stops as soon as that bin is taken whole, otherwise ties on the full
+// key are broken by descending block id.
+__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_args a) {
     __shared__ uint64_t s_key[KVM_MAX_TOPK_BLOCKS];
+    __shared__ uint32_t s_ntok[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_tmp[32];
-    __shared__ uint32_t s_count, s_k;
+    __shared__ uint32_t s_hist[2][256];
+    __shared__ uint32_t s_tmp[2 * (KVM_TOPK_THREADS / 64)];
+    __shared__ uint32_t s_count, s_k, s_done, s_need;
     __shared__ uint64_t s_prefix;
-    const uint32_t tid = threadIdx.x, nthr = blockDim.x, n = a.n;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, n = a.n;
     const bool all = a.budget == 0 || n <= a.budget;
-    for (uint32_t i = tid; i < n; i += nthr) s_kept[i] = all ? 1 : 0;
-    __syncthreads();
+    // ---- phase A: scores, keys, token counts (all loads first)
+    const uint32_t kpt = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
+    double sv[KVM_TOPK_LOAD];
+    uint32_t nt[KVM_TOPK_LOAD];
+    uint32_t pr[KVM_TOPK_LOAD];
+    const uint32_t qc0 = a.layer_score ? a.q_count[0] : 0u;
+#pragma unroll
+    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
+        if (k < kpt) {
+            const uint32_t i = tid + k * KVM_TOPK_THREADS, ic = i < n ? i : n - 1;
+            sv[k] = a.layer_score ? a.layer_score[ic] : a.scores_in[ic];
+            nt[k] = a.n_tokens[ic];
+            pr[k] = a.layer_score && a.present ? a.present[ic] : 1u;
+        }
+    }
+    if (tid < 256) s_hist[0][tid] = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
+        const uint32_t i = tid + k * KVM_TOPK_THREADS;
+        if (k < kpt && i < n) {
+            double sc = sv[k];
+            if (a.layer_score) {
+                // average of the layers with queries, in layer order
+                double acc = 0.0;
+                uint32_t nlay = 0;
+                if (qc0) { acc += sc; nlay++; }
+                for (uint32_t il = 1; il < a.n_layer; ++il)
+                    if (a.q_count[il]) { acc += a.layer_score[(uint64_t)il * a.ls_cap + i]; nlay++; }
+                sc = nlay ? acc / (double)nlay : 0.0;
+                if (!pr[k]) sc = 0.0;
+                a.scores_out[i] = sc;
+            }
+            s_key[i] = ord_key(sc);
+            s_ntok[i] = nt[k];
+            s_kept[i] = all ? 1 : 0;
+        }
+    }
+    KVM_LDS_BARRIER();
+    const uint32_t per = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
+    const uint32_t i0 = tid * per < n ? tid * per : n, i1 = i0 + per < n ? i0 + per : n;
     if (!all) {
         // sink prefix, mandatory ids newest first, recent tail (kvmem_store.cpp:520-545)
         if (tid == 0) {
@@ -281,110 +444,120 @@ __global__ void __launch_bounds__(1024) k_topk(topk_args a) {
                 if (!s_kept[id]) { s_kept[id] = 1; ++count; }
             }
             s_count = count;
+            s_prefix = 0;
+            s_done = 0;
         }
-        __syncthreads();
+        KVM_LDS_BARRIER();
         const uint32_t count = s_count;
         if (count < a.budget) {
-            uint32_t nc_local = 0;
-            for (uint32_t i = tid; i < n; i += nthr) {
-                s_key[i] = ord_key(a.scores[i]);
-                nc_local += !s_kept[i];
-            }
-            uint32_t ncand;
-            (void)block_scan(nc_local, s_tmp, &ncand);
-            const uint32_t need = a.budget - count < ncand ? a.budget - count : ncand;
-            if (tid == 0) { s_prefix = 0; s_k = need; }
+            // radix passes: histogram into buffer p&1 -> barrier -> wave 0 picks
+            // the bin and clears the other buffer -> barrier
             uint64_t mask = 0;
-            for (int shift = 56; shift >= 0 && need; shift -= 8) {
-                if (tid < 256) s_hist[tid] = 0;
-                __syncthreads();
+            uint32_t need = 1;                       // known after the first pass
+            for (int shift = 56, p = 0; shift >= 0 && need; shift -= 8, ++p) {
+                uint32_t *hist = s_hist[p & 1];
                 const uint64_t prefix = s_prefix;
-                for (uint32_t i = tid; i < n; i += nthr)
-                    if (!s_kept[i] && (s_key[i] & mask) == prefix)
-                        atomicAdd(&s_hist[(uint32_t)(s_key[i] >> shift) & 255u], 1u);
-                __syncthreads();
+                for (uint32_t k = 0; k < per; ++k) {
+                    const uint32_t i = i0 + k;
+                    const bool act = i < i1 && !s_kept[i] && (s_key[i] & mask) == prefix;
+                    hist_add(hist, act ? (uint32_t)(s_key[i] >> shift) & 255u : 0u, act);
+                }
+                KVM_LDS_BARRIER();
                 if (tid < 64) {
                     // lane l owns bins 255-4l .. 252-4l (descending)
                     uint32_t c[4], tot = 0;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) { c[j] = s_hist[255 - 4 * tid - j]; tot += c[j]; }
-                    uint32_t incl = tot;
-#pragma unroll
-                    for (int o = 1; o < 64; o <<= 1) {
-                        const uint32_t y = __shfl_up(incl, o, 64);
-                        if (tid >= (uint32_t)o) incl += y;
+                    for (int j = 0; j < 4; ++j) { c[j] = hist[255 - 4 * lane - j]; tot += c[j]; }
+                    const uint32_t incl = kvm_wave_incl_scan(tot);
+                    uint32_t k;
+                    if (p == 0) {
+                        // candidates = keys in the first histogram
+                        const uint32_t ncand = __builtin_amdgcn_readlane(incl, 63);
+                        k = a.budget - count < ncand ? a.budget - count : ncand;
+                        if (lane == 0) s_need = k;
+                    } else {
+                        k = s_k;
                     }
                     uint32_t run = incl - tot;           // keys in higher bins
-                    const uint32_t k = s_k;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         if (run < k && k <= run + c[j]) {
-                            s_prefix = prefix | ((uint64_t)(255 - 4 * tid - j) << shift);
+                            s_prefix = prefix | ((uint64_t)(255 - 4 * lane - j) << shift);
                             s_k = k - run;
+                            s_done = k - run == c[j];    // the whole bin is taken
                         }
                         run += c[j];
                     }
+                    s_hist[(p + 1) & 1][4 * lane] = 0;
+                    s_hist[(p + 1) & 1][4 * lane + 1] = 0;
+                    s_hist[(p + 1) & 1][4 * lane + 2] = 0;
+                    s_hist[(p + 1) & 1][4 * lane + 3] = 0;
                 }
                 mask |= (uint64_t)0xff << shift;
-                __syncthreads();
+                KVM_LDS_BARRIER();
+                need = s_need;
+                if (s_done) break;
             }
-            // keys above T are selected; among keys equal to T the s_k highest ids
+            // keys above the bin are selected; a bin taken whole is selected;
+            // otherwise (full 64-bit ties) the s_k highest ids among equal keys
             const uint64_t T = s_prefix;
             const uint32_t ktie = s_k;
-            const uint32_t per = (n + nthr - 1) / nthr;
-            const uint32_t i0 = tid * per, i1 = i0 + per < n ? i0 + per : n;
+            const bool whole = s_done;
             uint32_t ties = 0;
-            for (uint32_t i = i0; i < i1; ++i) ties += !s_kept[i] && s_key[i] == T;
-            uint32_t n_ties;
-            uint32_t before = block_scan(ties, s_tmp, &n_ties);
+            if (!whole && need)
+                for (uint32_t i = i0; i < i1; ++i) ties += !s_kept[i] && (s_key[i] & mask) == T;
+            uint32_t before = 0, n_ties = 0, z0, z1;
+            if (!whole && need) block_scan2(ties, 0u, s_tmp, before, z0, n_ties, z1);
             for (uint32_t i = i0; i < i1 && need; ++i) {
                 if (s_kept[i]) continue;
-                if (s_key[i] > T) {
+                const uint64_t km = s_key[i] & mask;
+                if (km > T) {
                     s_kept[i] = 2;
-                } else if (s_key[i] == T) {
-                    if (n_ties - 1 - before < ktie) s_kept[i] = 2;     // rank by descending id
-                    ++before;
+                } else if (km == T) {
+                    if (whole || n_ties - 1 - before < ktie) s_kept[i] = 2;     // rank by descending id
+                    if (!whole) ++before;
                 }
             }
-            __syncthreads();
+            KVM_LDS_BARRIER();
         }
     }
-    // ascending compaction of the kept flags
-    const uint32_t per = (n + nthr - 1) / nthr;
-    const uint32_t i0 = tid * per, i1 = i0 + per < n ? i0 + per : n;
-    uint32_t local = 0;
-    for (uint32_t i = i0; i < i1; ++i) local += s_kept[i] != 0;
-    uint32_t n_sel;
-    uint32_t rank = block_scan(local, s_tmp, &n_sel);
+    // ---- ascending compaction with window positions: ranks and token
+    // offsets of this thread's blocks come from one scan
+    uint32_t local = 0, tok = 0;
+    for (uint32_t i = i0; i < i1; ++i)
+        if (s_kept[i]) { ++local; tok += s_ntok[i]; }
+    uint32_t rank0, base0, n_sel, total;
+    block_scan2(local, tok, s_tmp, rank0, base0, n_sel, total);
     const bool fits = n_sel <= a.cap;
-    if (fits)
-        for (uint32_t i = i0; i < i1; ++i)
-            if (s_kept[i]) a.ids[rank++] = i;
-    __syncthreads();
-    // window positions: to_base[k] = sum of n_tokens of the selected blocks before k
-    const uint32_t per2 = (n_sel + nthr - 1) / nthr;
-    const uint32_t k0 = tid * per2, k1 = fits ? (k0 + per2 < n_sel ? k0 + per2 : n_sel) : k0;
-    uint32_t tok = 0;
-    for (uint32_t k = k0; k < k1; ++k) tok += a.n_tokens[a.ids[k]];
-    uint32_t total;
-    uint32_t base = block_scan(tok, s_tmp, &total);
-    for (uint32_t k = k0; k < k1; ++k) {
-        a.to_base[k] = (int32_t)base;
-        base += a.n_tokens[a.ids[k]];
-    }
-    __syncthreads();
-    // slots whose (block, base) differ from the new layout
-    uint32_t need_local = 0;
     const uint32_t ns = fits ? (n_sel < a.n_slots ? n_sel : a.n_slots) : 0;
-    const uint32_t per3 = (ns + nthr - 1) / nthr;
-    const uint32_t s0 = tid * per3, s1 = s0 + per3 < ns ? s0 + per3 : ns;
-    for (uint32_t s = s0; s < s1; ++s)
-        need_local += !a.slot_block || a.slot_block[s] != a.ids[s] || a.slot_base[s] != a.to_base[s];
-    uint32_t n_stage;
-    uint32_t pos = block_scan(need_local, s_tmp, &n_stage);
-    for (uint32_t s = s0; s < s1; ++s)
-        if (!a.slot_block || a.slot_block[s] != a.ids[s] || a.slot_base[s] != a.to_base[s])
-            a.stage_slots[pos++] = s;
+    // slots whose (block, base) differ from the new layout
+    uint32_t need_mask = 0, need_local = 0;
+    if (fits) {
+        uint32_t rank = rank0, base = base0, k = 0;
+        for (uint32_t i = i0; i < i1; ++i) {
+            if (!s_kept[i]) continue;
+            a.ids[rank] = i;
+            a.to_base[rank] = (int32_t)base;
+            if (rank < ns && (!a.slot_block || a.slot_block[rank] != i || a.slot_base[rank] != (int32_t)base)) {
+                need_mask |= 1u << k;
+                ++need_local;
+            }
+            base += s_ntok[i];
+            ++rank;
+            ++k;
+        }
+    }
+    uint32_t pos, n_stage, z2, z3;
+    block_scan2(need_local, 0u, s_tmp, pos, z2, n_stage, z3);
+    if (need_mask) {
+        uint32_t rank = rank0, k = 0;
+        for (uint32_t i = i0; i < i1; ++i) {
+            if (!s_kept[i]) continue;
+            if (need_mask >> k & 1u) a.stage_slots[pos++] = rank;
+            ++rank;
+            ++k;
+        }
+    }
     if (tid == 0) {
         a.info[0] = n_sel;
         a.info[1] = total;
@@ -393,16 +566,19 @@ __global__ void __launch_bounds__(1024) k_topk(topk_args a) {
     }
 }
 
-static int launch_topk(kvm_state *st, const double *scores, const kvm_select_params *p,
+static int launch_topk(kvm_state *st, const double *scores, const double *layer_score,
+                       const kvm_meank_index *ix, const kvm_query_acc *q, const kvm_select_params *p,
                        const kvm_window *w, const kvm_selection *out) {
     if (w && (kvm_window_check(w) || !w->slot_block || !w->slot_base))
         return kvm_fail(st, KVM_EINVAL, "topk: bad window or window without slot map");
-    topk_args ta{scores, p->n_tokens, p->mandatory,
+    topk_args ta{scores, layer_score, q ? q->q_count : nullptr, ix ? ix->present : nullptr, out->scores,
+                 p->n_tokens, p->mandatory,
                  w ? w->slot_block : nullptr, w ? w->slot_base : nullptr,
                  out->ids, out->to_base, out->stage_slots, out->info,
                  p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
-                 w ? w->n_cells / w->block_tokens : 0u, out->cap};
-    hipLaunchKernelGGL(k_topk, dim3(1), dim3(1024), 0, st->stream, ta);
+                 w ? w->n_cells / w->block_tokens : 0u, out->cap,
+                 ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u};
+    hipLaunchKernelGGL(k_topk, dim3(1), dim3(KVM_TOPK_THREADS), 0, st->stream, ta);
     KVM_LAUNCH_CHECK(st, "topk");
     return KVM_OK;
 }
@@ -425,7 +601,7 @@ extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_se
     if (rc) return rc;
     if (p->n_blocks && !scores) return kvm_fail(st, KVM_EINVAL, "select_topk: null scores");
     KVM_HIP(st, hipSetDevice(st->device));
-    return launch_topk(st, scores, p, w, out);
+    return launch_topk(st, scores, nullptr, nullptr, nullptr, p, w, out);
 }
 
 extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
@@ -440,30 +616,22 @@ extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kv
     if (p->n_blocks > ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "score_topk: n_blocks %u > index capacity %u", p->n_blocks, ix->n_blocks);
     if (q->n_layer != ix->n_layer || q->head_dim != ix->head_dim) return kvm_fail(st, KVM_EINVAL, "score_topk: query/index shape mismatch");
     if (ix->head_dim != 128 && ix->head_dim != 256) return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: head_dim %u", ix->head_dim);
-    if (ix->n_head_kv == 0 || ix->n_head_kv > 16 || q->n_head % ix->n_head_kv)
-        return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: n_head %u / n_head_kv %u", q->n_head, ix->n_head_kv);
-    const size_t lds = ((size_t)ix->n_layer * ix->n_head_kv * ix->head_dim + (size_t)ix->n_layer * ix->n_head_kv) * 4;
-    if (lds > 120 * 1024) return kvm_fail(st, KVM_ERANGE, "score_topk: %u layers x %u heads x %u dims exceeds LDS", ix->n_layer, ix->n_head_kv, ix->head_dim);
+    if (ix->n_head_kv == 0 || ix->n_head_kv > KVM_SCORE_HMAX || q->n_head % ix->n_head_kv ||
+        q->n_head / ix->n_head_kv > KVM_SCORE_GMAX)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: n_head %u / n_head_kv %u (at most %d kv heads, groups of at most %d)",
+                        q->n_head, ix->n_head_kv, KVM_SCORE_HMAX, KVM_SCORE_GMAX);
     KVM_HIP(st, hipSetDevice(st->device));
-    if (p->n_blocks) {
-        score_args sa{q->q_sum, q->q_count, ix->k_sum, ix->mean_tokens, ix->present, out->scores,
-                      p->n_blocks, ix->n_blocks, ix->n_layer, q->n_head, ix->n_head_kv};
-        // up to 4 kv heads: 256 threads, 128 dims in flight per lane; more heads
-        // (up to 16 waves) keep 32 in flight within the smaller register budget
-        const bool small = ix->n_head_kv <= 4;
-        const void *fn = ix->head_dim == 256 ? (small ? (const void *)k_score<256, 128, 256> : (const void *)k_score<256, 32, 1024>)
-                                              : (small ? (const void *)k_score<128, 128, 256> : (const void *)k_score<128, 32, 1024>);
-        if (lds > 64 * 1024)
-            KVM_HIP(st, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        const dim3 grid(kvm_cdiv(p->n_blocks, 64)), block(64 * ix->n_head_kv);
-        if (ix->head_dim == 256) {
-            if (small) hipLaunchKernelGGL((k_score<256, 128, 256>), grid, block, lds, st->stream, sa);
-            else hipLaunchKernelGGL((k_score<256, 32, 1024>), grid, block, lds, st->stream, sa);
-        } else {
-            if (small) hipLaunchKernelGGL((k_score<128, 128, 256>), grid, block, lds, st->stream, sa);
-            else hipLaunchKernelGGL((k_score<128, 32, 1024>), grid, block, lds, st->stream, sa);
-        }
-        KVM_LAUNCH_CHECK(st, "score");
-    }
-    return launch_topk(st, out->scores, p, w, out);
+    if (p->n_blocks == 0) return launch_topk(st, out->scores, nullptr, nullptr, nullptr, p, w, out);
+    double *ls = (double *)kvm_workspace(st, (size_t)ix->n_layer * ix->n_blocks * sizeof(double));
+    if (!ls) return kvm_fail(st, KVM_ENOMEM, "score_topk: workspace");
+    const uint32_t n_tiles = kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE);
+    score_args sa{q->q_sum, q->q_count, ix->k_sum, ix->mean_tokens, ls,
+                  p->n_blocks, ix->n_blocks, n_tiles, ix->n_layer, q->n_head, ix->n_head_kv};
+    const dim3 grid(kvm_cdiv(p->n_blocks, KVM_MEANK_TILE), ix->n_layer), block(256);
+    if (ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sa);
+    else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sa);
+    KVM_LAUNCH_CHECK(st, "score");
+    return launch_topk(st, nullptr, ls, ix, q, p, w, out);
+
+
 }

@@ -93,6 +93,7 @@ SIGNATURES = {
     "kvm_dequantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_query_reset": (C.c_int, [_P, C.POINTER(QueryAcc)]),
     "kvm_query_add": (C.c_int, [_P, C.POINTER(QueryAcc), _u32, _P, _u32]),
+    "kvm_meank_k_sum_floats": (_sz, [C.POINTER(MeanKIndex)]),
     "kvm_meank_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32, _P]),
     "kvm_score_topk": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
                                  C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),

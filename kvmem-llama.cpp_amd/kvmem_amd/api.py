@@ -133,16 +133,38 @@ class KVWindow:
 
 
 class MeanKIndex:
-    """Device mean-K index: ordered fp32 K sums + token counts per (layer, block)."""
+    """Device mean-K index: ordered fp32 K sums + token counts per (layer, block).
+
+    k_sum is stored in 8-block tiles, [n_layer][tiles][n_head_kv*head_dim][8];
+    block_sums() / set_block_sums() convert to and from [n_layer][block][e].
+    """
+
+    TILE = 8
 
     def __init__(self, st, n_layer, n_blocks, n_head_kv, head_dim, block_tokens=128):
         dev = torch.device("cuda", st.device)
         self.st = st
-        self.k_sum = torch.zeros((n_layer, n_head_kv * head_dim, n_blocks), dtype=torch.float32, device=dev)
+        self.n_blocks = n_blocks
+        n_tiles = (n_blocks + self.TILE - 1) // self.TILE
+        self.k_sum = torch.zeros((n_layer, n_tiles, n_head_kv * head_dim, self.TILE), dtype=torch.float32, device=dev)
         self.mean_tokens = torch.zeros((n_layer, n_blocks), dtype=torch.int32, device=dev)
         self.present = torch.zeros((n_blocks,), dtype=torch.uint8, device=dev)
         self.c = L.MeanKIndex(n_layer, n_blocks, n_head_kv, head_dim, block_tokens,
                               self.k_sum.data_ptr(), self.mean_tokens.data_ptr(), self.present.data_ptr())
+        assert self.k_sum.numel() == st.lib.kvm_meank_k_sum_floats(C.byref(self.c))
+
+    def block_sums(self):
+        """K sums as [n_layer][n_blocks][n_head_kv*head_dim] (a copy)."""
+        Lr, T, E, W = self.k_sum.shape
+        return self.k_sum.permute(0, 1, 3, 2).reshape(Lr, T * W, E)[:, :self.n_blocks].contiguous()
+
+    def set_block_sums(self, sums, first=0):
+        """Store sums [n_layer][n][e] (device tensor) for blocks first .. first+n-1."""
+        Lr, T, E, W = self.k_sum.shape
+        n = sums.shape[1]
+        view = self.k_sum.permute(0, 1, 3, 2).reshape(Lr, T * W, E)
+        view[:, first:first + n] = sums
+        self.k_sum.copy_(view.reshape(Lr, T, W, E).permute(0, 1, 3, 2))
 
     def add(self, il, pos0, k_rows):
         """k_rows: device fp32 [n][n_head_kv*head_dim] of pre-RoPE K at positions pos0.."""

@@ -43,7 +43,7 @@ def test_meank_add_bit_exact(kvm_state):
         ix.add(0, pos, dev(k[pos:pos + chunk]))
         pos += chunk
     sums, mt = O.meank_sums(k, bt, chunk=None)
-    got = host(ix.k_sum)[0].T                        # [blocks][e]
+    got = host(ix.block_sums())[0]                   # [blocks][e]
     assert np.array_equal(got[:6].view(np.uint32), sums.view(np.uint32))
     assert list(host(ix.mean_tokens)[0][:6]) == list(mt)
     assert list(host(ix.present)[:7]) == [1, 1, 1, 1, 1, 1, 0]
@@ -52,7 +52,7 @@ def test_meank_add_bit_exact(kvm_state):
 def _build_index(st, k_sum, mt, n_blocks_cap, H, D, bt=128):
     L_, nb, e = k_sum.shape
     ix = api.MeanKIndex(st, L_, n_blocks_cap, H, D, bt)
-    ix.k_sum[:, :, :nb] = dev(np.ascontiguousarray(k_sum.transpose(0, 2, 1)))
+    ix.set_block_sums(dev(np.ascontiguousarray(k_sum)))
     ix.mean_tokens[:, :nb] = dev(mt.astype(np.int32))
     ix.present[:nb] = 1
     return ix
