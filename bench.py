@@ -48,6 +48,22 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "fa_decode_256k_32k_hbm_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per flash-attention launch (split + combine) from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02):
     from kvmem_amd import workload as W
     dev = torch.device("cuda", 0)
@@ -258,7 +274,8 @@ def main():
         "roofline_step_us": round(STEP_BYTES / (HBM_PEAK_GBPS * 1e9) * 1e6, 3),
         "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode (k_fa_decode split-K + k_fa_combine)",
                      "achieved": round(fa_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                     "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
                      "launch_us": round(fa_ms * 1e3, 3), "algorithmic_bytes": fa_bytes},
     }
     if not args.no_cpu_baseline:
