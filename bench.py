@@ -187,8 +187,104 @@ def cpu_baseline(O, np, wl, out_gpu, budget_s=20.0):
                       f"the full {WINDOW}-cell window ({t_att:.2f} s), scaled to one step"}
 
 
+# ---- chunked prefill over the window (2,048-token chunk, MFMA) ----------------
+PF_CHUNK = 2048
+PF_CELLS = WINDOW + PF_CHUNK
+# useful (query, key) pairs per query head: the whole window plus the causal chunk
+PF_PAIRS = PF_CHUNK * WINDOW + PF_CHUNK * (PF_CHUNK + 1) // 2          # 69,207,040
+PF_FLOP = 4 * D * PF_PAIRS * N_HEAD                                     # 1.7008 TFLOP
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def run_prefill(args, st, api, L, torch, np):
+    """Chunked prefill: a 2,048-token bf16 query chunk at positions 32768..34815,
+    causal, against a 32,768-cell q8_0/q4_0 window plus the chunk's own cells
+    (written quantised), 24 q heads / 4 kv heads / head_dim 256."""
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC0FFEE04)
+    reps = []
+    for r in range(args.replicas):
+        w = api.KVWindow(st, PF_CELLS, H_KV, D, BT)
+        for c0 in range(0, PF_CELLS, 8192):
+            n = min(8192, PF_CELLS - c0)
+            k = api.quantize_rows(st, L.T_Q8_0, torch.randn((n, H_KV * D), generator=gen, device=dev))
+            v = api.quantize_rows(st, L.T_Q4_0, torch.randn((n, H_KV * D), generator=gen, device=dev))
+            w.import_rows(c0, k, v, torch.arange(c0, c0 + n, dtype=torch.int32, device=dev))
+        reps.append(w)
+    q = torch.randn((PF_CHUNK, N_HEAD, D), generator=gen, device=dev).to(torch.bfloat16)
+    q_pos = torch.arange(WINDOW, WINDOW + PF_CHUNK, dtype=torch.int32, device=dev)
+    out = torch.empty((PF_CHUNK, N_HEAD, D), dtype=torch.float32, device=dev)
+    scale = D ** -0.5
+    for i in range(args.warmup):
+        api.fa_prefill(st, reps[i % len(reps)], q, q_pos, N_HEAD, scale, out)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        api.fa_prefill(st, reps[i % len(reps)], q, q_pos, N_HEAD, scale, out)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+    out_gpu = out.cpu().numpy()
+    # full-size check: sampled tokens (first, middle, last of the chunk), all heads,
+    # against the float64 softmax over the same fp16 operands
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    w = reps[(args.steps - 1) % len(reps)]
+    ek, ev = w.export_rows(0, PF_CELLS)
+    ek, ev = ek.cpu().numpy(), ev.cpu().numpy()
+    cp = w.cell_pos.cpu().numpy()
+    kh = O.dequant(O.T_Q8_0, ek.reshape(-1), PF_CELLS * H_KV * D).astype(np.float16).view(np.uint8).reshape(PF_CELLS, -1)
+    vh = O.dequant(O.T_Q4_0, ev.reshape(-1), PF_CELLS * H_KV * D).astype(np.float16).view(np.uint8).reshape(PF_CELLS, -1)
+    qf = q.float().cpu().numpy()
+    qp = q_pos.cpu().numpy()
+    toks = np.array([0, 1, PF_CHUNK // 2, PF_CHUNK - 1])
+    ref = O.fa_f64(O.T_F16, O.T_F16, qf[toks], kh, vh, cp, qp[toks], N_HEAD, H_KV, D, scale,
+                   n_threads=min(16, os.cpu_count() or 1))
+    err = float(np.abs(out_gpu[toks] - ref).max())
+    assert err <= 2e-3 and err <= 1e-3 * float(np.abs(ref).max()), err
+    log("prefill sampled-token check passed (max err %.2e)" % err)
+    tflops = PF_FLOP / (ms * 1e-3) / 1e12
+    rec = {
+        "metric": "chunked prefill attention TFLOP/s (2048-token chunk over a 32K q8_0/q4_0 window)",
+        "value": round(tflops, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16 MFMA (K/V dequantised to f16), bf16 Q, fp32 softmax/accumulate",
+        "data": "synthetic N(0,1), seed 0xC0FFEE04",
+        "config": {"workload": "chunked prefill: 2048 bf16 query tokens at positions 32768..34815, causal, "
+                               "over a 34816-cell q8_0/q4_0 window (32768 window cells + the chunk's own), "
+                               "24 q heads / 4 kv heads / head_dim 256",
+                   "useful_pairs_per_head": PF_PAIRS, "flop": PF_FLOP},
+        "roofline": {"bound": "mfma", "kernel": "kvm_fa_prefill (k_pf_stage + k_pf_attn + k_pf_combine)",
+                     "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "launch_us": round(ms * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        n_threads = min(16, os.cpu_count() or 1)
+        rows_done, t_att, t_i = 0, 0.0, 0
+        while t_att < 10.0 and t_i < PF_CHUNK:
+            tok = np.array([PF_CHUNK - 1 - t_i])
+            t1 = time.perf_counter()
+            O.fa_ggml(O.T_Q8_0, O.T_Q4_0, qf[tok], ek, ev, cp, qp[tok], N_HEAD, H_KV, D, scale, n_threads=n_threads)
+            t_att += time.perf_counter() - t1
+            rows_done += N_HEAD
+            t_i += 97
+        total = t_att * (PF_CHUNK * N_HEAD) / rows_done
+        rec["cpu_baseline"] = {
+            "value": round(PF_FLOP / total / 1e12, 4), "unit": "TFLOP/s", "cores": n_threads, "kind": "port",
+            "sample": f"oracle ggml-semantics C (OpenMP) attention for {rows_done} of {PF_CHUNK * N_HEAD} "
+                      f"query rows (tokens spread over the chunk) over the 34816-cell window ({t_att:.1f} s), "
+                      f"scaled to the whole chunk ({total:.0f} s)"}
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill"],
+                    help="decode: the headline decode step (default); prefill: chunked-prefill attention")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -206,6 +302,8 @@ def main():
     from kvmem_amd import api, _lib as L
 
     st = api.State(0)
+    if args.workload == "prefill":
+        return run_prefill(args, st, api, L, torch, np)
     log("building workload (256K history, 32K window, %d replicas)" % args.replicas)
     t0 = time.time()
     wl = build_workload(st, api, L, torch, np, args.replicas)

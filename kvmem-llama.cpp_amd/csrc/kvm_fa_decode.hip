@@ -71,8 +71,6 @@ __device__ inline kvm_f16x8 nib8_to_f16(uint32_t w) {
     return v - off;
 }
 
-typedef uint32_t kvm_u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t kvm_u32x2 __attribute__((ext_vector_type(2)));
 typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
 
 // Workgroup barrier that orders LDS traffic only: it waits for this wave's LDS

@@ -149,6 +149,8 @@ typedef float kvm_f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 kvm_f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 kvm_f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 kvm_f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t kvm_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t kvm_u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline float kvm_h2f(uint16_t h) {
     _Float16 v;

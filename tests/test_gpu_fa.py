@@ -99,6 +99,28 @@ def test_fa_decode_lanes_match_single_lane(kvm_state):
         np.testing.assert_allclose(host(o), r, rtol=1e-3, atol=1e-4)
 
 
+def _f16_rows(ty, rows, n_cells, H, D):
+    """Rows dequantised and rounded to fp16: the operands the prefill MFMA kernel
+    multiplies (ggml's GPU backends convert a quantised cache to f16 for
+    multi-token attention the same way)."""
+    x = O.dequant(ty, np.ascontiguousarray(rows).reshape(-1), n_cells * H * D) if ty != L.T_F16 else \
+        np.ascontiguousarray(rows).view(np.float16).astype(np.float32).reshape(-1)
+    return x.astype(np.float16).view(np.uint8).reshape(n_cells, -1)
+
+
+def _prefill_check(out, q, kr, vr, cp, pos, H, G, D, kt, vt, scale):
+    n = kr.shape[0]
+    qh = q.astype(np.float16).astype(np.float32)
+    ref16 = O.fa_f64(L.T_F16, L.T_F16, qh, _f16_rows(kt, kr, n, H, D), _f16_rows(vt, vr, n, H, D), cp, pos,
+                     H * G, H, D, scale)
+    err = check_attention(out, ref16)
+    if kt == L.T_Q8_0:
+        # ggml-CPU rounds Q to q8_0 for a q8_0 K: a coarser computation of the same op
+        ref = O.fa_ggml(kt, vt, q, kr, vr, cp, pos, H * G, H, D, scale)
+        assert np.abs(out - ref).max() <= 3e-2 * np.abs(ref).max()
+    return err
+
+
 def test_fa_prefill_chunked_causal(kvm_state):
     rng = np.random.default_rng(9)
     H, G, D, n_win, T = 4, 6, 256, 2048, 40
@@ -110,8 +132,76 @@ def test_fa_prefill_chunked_causal(kvm_state):
     cp[n_win:n_win + T] = pos
     q = rng.standard_normal((T, H * G, D)).astype(np.float32)
     out = host(api.fa_prefill(kvm_state, w, dev(q), dev(pos), H * G, 0.0625))
-    ref = O.fa_ggml(L.T_Q8_0, L.T_Q4_0, q, kr, vr, cp, pos, H * G, H, D, 0.0625)
-    check_attention(out, ref)
+    _prefill_check(out, q, kr, vr, cp, pos, H, G, D, L.T_Q8_0, L.T_Q4_0, 0.0625)
+
+
+PREFILL_CASES = [
+    # n_cells, H, G, D, tokens, kt, vt, holes, empty cell range, splits (None = auto), q dtype
+    (2048, 4, 6, 256, 48, L.T_Q8_0, L.T_Q4_0, 40, None, None, "bf16"),
+    (1024, 2, 4, 128, 64, L.T_F16, L.T_F16, 0, None, 1, "f32"),
+    (4096, 4, 6, 256, 30, L.T_Q8_0, L.T_Q4_0, 7, (1024, 2048), 3, "f32"),   # whole empty tiles
+    (2048, 1, 8, 256, 20, L.T_Q8_0, L.T_Q4_0, 0, None, 8, "bf16"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PREFILL_CASES)))
+def test_fa_prefill_mfma(kvm_state, case, monkeypatch):
+    n_cells, H, G, D, T, kt, vt, holes, empty, splits, qdt = PREFILL_CASES[case]
+    if splits is not None:
+        monkeypatch.setenv("KVM_PF_SPLITS", str(splits))
+    rng = np.random.default_rng(100 + case)
+    w, kr, vr, cp = _window(kvm_state, rng, n_cells, H, D, kt, vt, holes=holes)
+    if empty is not None:
+        cp[empty[0]:empty[1]] = -1
+        w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    # the chunk occupies the last T cells at positions n_cells - T .. n_cells - 1:
+    # causal inside the chunk, the whole earlier window visible
+    pos = np.arange(n_cells - T, n_cells, dtype=np.int32)
+    cp[n_cells - T:] = pos
+    w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    if qdt == "bf16":
+        qt = torch.from_numpy(q).to(torch.bfloat16)
+        q = qt.float().numpy()
+        qd = qt.cuda()
+    else:
+        qd = dev(q)
+    scale = 1.0 / np.sqrt(D)
+    out = host(api.fa_prefill(kvm_state, w, qd, dev(pos), H * G, scale))
+    _prefill_check(out, q, kr, vr, cp, pos, H, G, D, kt, vt, scale)
+
+
+def test_fa_prefill_blind_rows_and_single_key(kvm_state):
+    """A token that sees no cell gets zeros; a token that sees exactly one cell
+    gets that cell's V row."""
+    rng = np.random.default_rng(11)
+    H, G, D, n = 2, 6, 256, 1024
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, L.T_Q8_0, L.T_Q4_0)
+    T = 12
+    pos = np.full(T, 700, np.int32)
+    pos[0], pos[1] = -1, 0
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    out = host(api.fa_prefill(kvm_state, w, dev(q), dev(pos), H * G, 0.0625))
+    assert np.all(out[0] == 0)
+    V = _f16_rows(L.T_Q4_0, vr[:1], 1, H, D).view(np.float16).astype(np.float32).reshape(H, D)
+    for h in range(H * G):
+        np.testing.assert_allclose(out[1, h], V[h // G], rtol=1e-3, atol=1e-3)
+    _prefill_check(out, q, kr, vr, cp, pos, H, G, D, L.T_Q8_0, L.T_Q4_0, 0.0625)
+
+
+def test_fa_prefill_splits_agree(kvm_state, monkeypatch):
+    rng = np.random.default_rng(12)
+    H, G, D, n, T = 4, 6, 256, 4096, 64
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, L.T_Q8_0, L.T_Q4_0)
+    pos = np.arange(n - T, n, dtype=np.int32)
+    q = dev(rng.standard_normal((T, H * G, D)).astype(np.float32))
+    outs = []
+    for s in (1, 2, 5):
+        monkeypatch.setenv("KVM_PF_SPLITS", str(s))
+        outs.append(host(api.fa_prefill(kvm_state, w, q, dev(pos), H * G, 0.0625)))
+    for o in outs[1:]:
+        # P is rounded to fp16 against each split's own running maxima
+        np.testing.assert_allclose(o, outs[0], rtol=1e-3, atol=1e-4)
 
 
 def test_fa_decode_rejects_wide_batches(kvm_state):
