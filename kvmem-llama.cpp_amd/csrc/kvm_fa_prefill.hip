@@ -22,7 +22,7 @@
 //               cross-lane exchange.
 // Launch 2, k_pf_attn: one workgroup per (128 query rows, kv head, key split);
 // a row is (token, query head of the group), so the 6 query heads of a kv
-// head share every K/V tile.  4 waves x 32 rows.  K/V tiles are copied from
+// head share every K/V tile.  8 waves x 16 rows (two waves per SIMD).  K/V tiles are copied from
 // global memory straight into LDS (double buffered, one barrier per tile); the
 // tiles of the workgroup's key range that some row can see are listed in LDS
 // once at the start.  Q stays in registers as f16 B
@@ -163,15 +163,16 @@ struct pf_args {
     int q_bf16;
 };
 
-template <int D>
-__global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
+template <int D, int RT>
+__global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
+    constexpr int NW = 8 / RT;                            // waves; NW x RT x 16 = 128 rows
     constexpr int KS = D / 32, DT = D / 16;
     constexpr uint32_t TILE_H = 64u * D;                  // halves per K (or V) tile
     __shared__ __align__(16) _Float16 s_kv[2][2 * TILE_H];   // [buffer][K tile | V tile]
     __shared__ __align__(16) int32_t s_cp[2][64];           // the tiles' cell positions
     __shared__ uint16_t s_list[KVM_PF_LIST];
-    __shared__ int32_t s_mm[2][4];
-    __shared__ uint32_t s_wsum[4];
+    __shared__ int32_t s_mm[2][NW];
+    __shared__ uint32_t s_wsum[NW];
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, m = l & 15;
 
     // Workgroup -> (row tile, kv head, split).  Consecutive hardware workgroup
@@ -185,13 +186,13 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
     const uint32_t h = hs % a.H, split = hs / a.H;
     const uint32_t r0 = rt_i * KVM_PF_ROWS;
 
-    // ---- rows of this lane: r0 + 32w + 16rt + m
-    int32_t qpos[2];
-    uint32_t rows[2];
+    // ---- rows of this lane: r0 + 16 RT w + 16 rt + m
+    int32_t qpos[RT];
+    uint32_t rows[RT];
     int32_t mn = INT_MAX, mx = INT_MIN;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        rows[rt] = r0 + 32 * w + 16 * rt + m;
+    for (int rt = 0; rt < RT; ++rt) {
+        rows[rt] = r0 + 16 * RT * w + 16 * rt + m;
         const bool live = rows[rt] < a.n_rows;
         qpos[rt] = live ? a.q_pos[rows[rt] / a.G] : INT_MIN;
         if (live) {
@@ -210,9 +211,9 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
     }
 
     // ---- Q rows as f16 B operands: lane (g, m) holds Q[row m][32ks + 8g .. +7]
-    kvm_f16x8 qop[2][KS];
+    kvm_f16x8 qop[RT][KS];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
         const bool live = rows[rt] < a.n_rows;
         const uint32_t row = live ? rows[rt] : 0;
         const uint64_t base = ((uint64_t)(row / a.G) * a.n_head + h * a.G + row % a.G) * D + 8 * g;
@@ -240,8 +241,12 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
         }
     }
     __syncthreads();
-    const int32_t wg_min = min(min(s_mm[0][0], s_mm[0][1]), min(s_mm[0][2], s_mm[0][3]));
-    const int32_t wg_max = max(max(s_mm[1][0], s_mm[1][1]), max(s_mm[1][2], s_mm[1][3]));
+    int32_t wg_min = s_mm[0][0], wg_max = s_mm[1][0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+        wg_min = min(wg_min, s_mm[0][i]);
+        wg_max = max(wg_max, s_mm[1][i]);
+    }
 
     // ---- this split's tiles.  A list in LDS holds the tiles some row here can
     // see (tile - t_begin, bit 15 = every cell live and visible to every row,
@@ -250,7 +255,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
     const uint32_t t_begin = split * tps < a.n_tiles ? split * tps : a.n_tiles;
     const uint32_t t_end = t_begin + tps < a.n_tiles ? t_begin + tps : a.n_tiles;
     uint32_t n_live = 0;
-    for (uint32_t t0 = t_begin; t0 < t_end; t0 += 256) {
+    for (uint32_t t0 = t_begin; t0 < t_end; t0 += 64 * NW) {
         const uint32_t t = t0 + tid;
         uint32_t live = 0, full = 0;
         if (t < t_end) {
@@ -261,51 +266,64 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
         const uint32_t incl = kvm_wave_incl_scan(live);
         if (l == 63) s_wsum[w] = incl;
         __syncthreads();
-        uint32_t before = n_live;
-        for (int i = 0; i < w; ++i) before += s_wsum[i];
+        uint32_t before = n_live, total = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            before += i < w ? s_wsum[i] : 0u;
+            total += s_wsum[i];
+        }
         if (live) s_list[before + incl - 1] = (uint16_t)((t - t_begin) | (full << 15));
-        n_live += s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+        n_live += total;
         __syncthreads();
     }
 
     // Tile copies go global -> LDS directly (global_load_lds_dwordx4: lane l
     // writes 16 bytes at M0 + 16 l), issued from asm so the compiler adds no
     // wait for them; the loop waits for them itself before each barrier.  The
-    // asm restores M0, which the compiler reserves.  Wave w
-    // copies the 1 KB chunks w, w+4, ... of the tile's K then V, and wave 0 also
+    // asm restores M0, which the compiler reserves.  Wave w copies the 1 KB
+    // chunks w, w+NW, ... of the tile's K and of its V (source and LDS
+    // addresses are scalar; the lane offset is one register), and wave 0 also
     // the tile's 64 cell positions.
-    constexpr int CH = 2 * 64 * D * 2 / 1024;           // 1 KB chunks per tile (K + V)
+    constexpr int CHW = 64 * D * 2 / 1024 / NW;         // 1 KB chunks of one K (or V) tile per wave
     const uint64_t hb = (uint64_t)h * a.n_tiles;
     const uint32_t lds_kv = (uint32_t)(uintptr_t)(kvm_lds_ptr)&s_kv[0][0];
     const uint32_t lds_cp = (uint32_t)(uintptr_t)(kvm_lds_ptr)&s_cp[0][0];
+    const uint32_t loff = 16u * l;                       // this lane's bytes in a 1 KB chunk
+    const uint32_t wofs = __builtin_amdgcn_readfirstlane(1024u * w);
     auto dma_tile = [&](uint32_t t, int buf) {
-        const uint8_t *ksrc = (const uint8_t *)(a.kh + (hb + t) * TILE_H) + 16 * l;
-        const uint8_t *vsrc = (const uint8_t *)(a.vh + (hb + t) * TILE_H) + 16 * l;
+        t = __builtin_amdgcn_readfirstlane(t);
+        const uint8_t *kb = (const uint8_t *)(a.kh + (hb + t) * TILE_H) + wofs;
+        const uint8_t *vb = (const uint8_t *)(a.vh + (hb + t) * TILE_H) + wofs;
+        const uint32_t dk = lds_kv + (uint32_t)buf * (2 * TILE_H * 2) + wofs;
+        const uint32_t dv = dk + TILE_H * 2;
 #pragma unroll
-        for (int j = 0; j < CH / 4; ++j) {
-            const int ch = w + 4 * j;
-            const uint8_t *src = ch < CH / 2 ? ksrc + ch * 1024 : vsrc + (ch - CH / 2) * 1024;
-            const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_kv + (uint32_t)buf * (2 * TILE_H * 2) + ch * 1024);
+        for (int j = 0; j < 2 * CHW; ++j) {
+            const uint8_t *src = j < CHW ? kb + 1024 * NW * j : vb + 1024 * NW * (j - CHW);
+            const uint32_t dst = j < CHW ? dk + 1024 * NW * j : dv + 1024 * NW * (j - CHW);
             uint32_t m0_saved;
-            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                         : "=&s"(m0_saved) : "v"(src), "s"(dst) : "memory");
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\ts_mov_b32 m0, %0"
+                         : "=&s"(m0_saved) : "v"(loff), "s"(dst), "s"(src) : "memory");
         }
         if (w == 0) {
-            const int32_t *src = a.cell_pos + (uint64_t)t * 64 + l;
+            const int32_t *src = a.cell_pos + (uint64_t)t * 64;
             const uint32_t dst = lds_cp + (uint32_t)buf * 256;
             uint32_t m0_saved;
-            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                         : "=&s"(m0_saved) : "v"(src), "s"(dst) : "memory");
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, %3\n\ts_mov_b32 m0, %0"
+                         : "=&s"(m0_saved) : "v"(4u * l), "s"(dst), "s"(src) : "memory");
         }
     };
 
-    kvm_f32x4 O[2][DT];
+    kvm_f32x4 O[RT][DT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) O[rt][dt] = kvm_f32x4{0.f, 0.f, 0.f, 0.f};
-    float ms[2] = {-INFINITY, -INFINITY};   // running max of each row, times c
-    float lp[2] = {0.f, 0.f};               // this lane's share of each row's sum
+    float ms[RT], lp[RT];                   // running max of each row (times c), lane's share of its sum
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        ms[rt] = -INFINITY;
+        lp[rt] = 0.0f;
+    }
     const float c = a.c;
 
     if (n_live > 0) dma_tile(t_begin + (s_list[0] & 0x7fffu), 0);
@@ -321,36 +339,37 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
         const _Float16 *sv = s_kv[b] + TILE_H;
 
         // S^T = K Q^T: sub tile s holds keys 16s + 4g + r of row m
-        kvm_f32x4 S[4][2];
+        kvm_f32x4 S[4][RT];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) S[s][rt] = kvm_f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int rt = 0; rt < RT; ++rt) S[s][rt] = kvm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const kvm_f16x8 kop = *(const kvm_f16x8 *)(sk + ((s * KS + ks) * 64 + l) * 8);
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
+                for (int rt = 0; rt < RT; ++rt)
                     S[s][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[rt][ks], S[s][rt], 0, 0, 0);
             }
         if (masked) {
+            asm volatile("" ::: "memory");                // keep the mask on this (rare) path
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const kvm_i32x4 cp = *(const kvm_i32x4 *)&s_cp[b][16 * s + 4 * g];
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
+                for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         if (!(cp[r] >= 0 && cp[r] <= qpos[rt])) S[s][rt][r] = -INFINITY;
             }
         }
         // online softmax per row
-        float tmax[2];
-        bool up[2];
+        float tmax[RT];
+        bool up[RT], any = false;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
             float x = S[0][rt][0];
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -360,10 +379,11 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
             x = fmaxf(x, __shfl_xor(x, 32, 64));
             tmax[rt] = x;
             up[rt] = fmaf(x, c, -ms[rt]) > KVM_PF_LAZY;   // false for a row with nothing visible yet
+            any = any || up[rt];
         }
-        if (__builtin_amdgcn_ballot_w64(up[0] || up[1]) != 0) {
+        if (__builtin_amdgcn_ballot_w64(any) != 0) {
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
+            for (int rt = 0; rt < RT; ++rt) {
                 const float mnew = up[rt] ? tmax[rt] * c : ms[rt];
                 const float alpha = up[rt] ? __builtin_amdgcn_exp2f(ms[rt] - mnew) : 1.0f;
                 ms[rt] = mnew;
@@ -372,18 +392,20 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
                 for (int dt = 0; dt < DT; ++dt) O[rt][dt] *= alpha;
             }
         }
-        kvm_f16x8 pB[2][2];
+        kvm_f16x8 pB[RT][2];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
             const float msr = ms[rt] == -INFINITY ? 0.0f : ms[rt];
             float sum = 0.0f;
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const _Float16 p = (_Float16)__builtin_amdgcn_exp2f(fmaf(S[s][rt][r], c, -msr));
-                    pB[rt][s >> 1][4 * (s & 1) + r] = p;
-                    sum += (float)p;
+                    // the row sum takes p before its rounding to the fp16 operand:
+                    // within 2^-11 of it per element
+                    const float p = __builtin_amdgcn_exp2f(fmaf(S[s][rt][r], c, -msr));
+                    pB[rt][s >> 1][4 * (s & 1) + r] = (_Float16)p;
+                    sum += p;
                 }
             lp[rt] += sum;
         }
@@ -394,7 +416,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
             for (int dt = 0; dt < DT; ++dt) {
                 const kvm_f16x8 vop = *(const kvm_f16x8 *)(sv + ((dt * 2 + kk) * 64 + l) * 8);
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
+                for (int rt = 0; rt < RT; ++rt)
                     O[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pB[rt][kk], O[rt][dt], 0, 0, 0);
             }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the next tile's copies
@@ -403,7 +425,7 @@ __global__ void __launch_bounds__(256) k_pf_attn(pf_args a) {
 
     // ---- results
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
         float lr = lp[rt];
         lr += __shfl_xor(lr, 16, 64);
         lr += __shfl_xor(lr, 32, 64);
@@ -454,6 +476,7 @@ __global__ void __launch_bounds__(256) k_pf_combine(pf_args a) {
 
 // Key splits: the fewest that keep the whole device busy, for one resident
 // workgroup per CU (the double-buffered K/V tiles take 128 KB of LDS at D 256).
+// KVM_PF_SPLITS in the environment fixes the count.
 static uint32_t pf_choose_splits(uint32_t n_units, uint32_t n_tiles, int n_cu) {
     if (const char *e = getenv("KVM_PF_SPLITS")) {
         const int v = atoi(e);
@@ -475,7 +498,9 @@ static uint32_t pf_choose_splits(uint32_t n_units, uint32_t n_tiles, int n_cu) {
 template <int D>
 static void pf_launch(const pf_args &a, const pf_stage_args &sa, hipStream_t stream) {
     hipLaunchKernelGGL(k_pf_stage<D>, dim3(sa.n_tiles, a.H), dim3(256), 0, stream, sa);
-    hipLaunchKernelGGL(k_pf_attn<D>, dim3(a.n_row_tiles * a.H * a.n_splits), dim3(256), 0, stream, a);
+    // 8 waves of 16 rows: two waves per SIMD, so one wave's softmax overlaps
+    // the other's matrix-core work
+    hipLaunchKernelGGL((k_pf_attn<D, 1>), dim3(a.n_row_tiles * a.H * a.n_splits), dim3(512), 0, stream, a);
     if (a.n_splits > 1)
         hipLaunchKernelGGL(k_pf_combine<D>, dim3(kvm_cdiv(a.n_rows, 256 / (D / 4)), a.H), dim3(256), 0, stream, a);
 }
