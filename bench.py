@@ -64,18 +64,18 @@ def measured_traffic():
     return None
 
 
-def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02):
+def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HIST_TOKENS, mtp=MTP):
     from kvmem_amd import workload as W
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    n_blocks = HIST_TOKENS // BT
+    n_blocks = hist_tokens // BT
     # pinned host history: raw (pre-RoPE) K as q8_0 rows, V as q4_0 rows
-    kbuf = api.HostBuffer(HIST_TOKENS * K_ROW)
-    vbuf = api.HostBuffer(HIST_TOKENS * V_ROW)
+    kbuf = api.HostBuffer(hist_tokens * K_ROW)
+    vbuf = api.HostBuffer(hist_tokens * V_ROW)
     ix0 = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT)
     chunk = 16384
-    for t0 in range(0, HIST_TOKENS, chunk):
+    for t0 in range(0, hist_tokens, chunk):
         k = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
         v = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
         ix0.add(0, t0, k)
@@ -84,13 +84,13 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02):
         torch.from_numpy(kbuf.u8[t0 * K_ROW:(t0 + chunk) * K_ROW]).copy_(kq.view(-1).cpu())
         torch.from_numpy(vbuf.u8[t0 * V_ROW:(t0 + chunk) * V_ROW]).copy_(vq.view(-1).cpu())
     hist = api.History.__new__(api.History)
-    hist.kbuf, hist.vbuf, hist.n_tokens = kbuf, vbuf, HIST_TOKENS
-    hist.c = L.History(kbuf.ptr, vbuf.ptr, HIST_TOKENS)
+    hist.kbuf, hist.vbuf, hist.n_tokens = kbuf, vbuf, hist_tokens
+    hist.c = L.History(kbuf.ptr, vbuf.ptr, hist_tokens)
     # query: 4 tokens whose pre-RoPE rows point at 16 planted blocks
     planted = W.distinct_ids(seed, 0, PLANTED, 1, n_blocks)
     means = ix0.block_sums()[0][torch.from_numpy(planted).to(dev)].T / float(BT)   # [H*D, 16]
     qsum_kv = means.sum(1).view(H_KV, D)
-    qrows = qsum_kv.repeat_interleave(G, 0).reshape(1, N_HEAD * D).repeat(MTP, 1)
+    qrows = qsum_kv.repeat_interleave(G, 0).reshape(1, N_HEAD * D).repeat(mtp, 1)
     qrows = qrows + 0.1 * torch.randn(qrows.shape, generator=gen, device=dev)
     qa = api.QueryAcc(st, 1, N_HEAD, D)
     qa.reset()
@@ -117,10 +117,36 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02):
     res = reps[0][2].result()
     assert res["status"] == 0 and len(res["ids"]) == RETRIEVED // BT, res
     assert set(planted.tolist()) <= set(res["ids"].tolist()), "planted blocks not retrieved"
-    q = torch.randn((MTP, N_HEAD, D), generator=gen, device=dev).to(torch.bfloat16)
-    q_pos = torch.arange(WINDOW - MTP, WINDOW, dtype=torch.int32, device=dev)
+    q = torch.randn((mtp, N_HEAD, D), generator=gen, device=dev).to(torch.bfloat16)
+    q_pos = torch.arange(WINDOW - mtp, WINDOW, dtype=torch.int32, device=dev)
     return dict(hist=hist, qa=qa, n_tokens=n_tokens, reps=reps, q=q, q_pos=q_pos, planted=planted,
-                ids=res["ids"])
+                ids=res["ids"], hist_tokens=hist_tokens)
+
+
+def prepare_decode(st, api, wl, out):
+    """The three calls of a decode step for every layer replica, marshalled once."""
+    n_blocks = wl["hist_tokens"] // BT
+    return [(api.prepare_score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel),
+             api.prepare_stagein(st, wl["hist"], w, sel, N_ROT, FREQ_BASE),
+             api.prepare_fa_decode(st, w, wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out))
+            for ix, w, sel in wl["reps"]]
+
+
+def time_steps(torch, step, steps, warmup):
+    """Warm up, then time `steps` calls of step(i, fa_events) on the stream:
+    (ms per step, ms of the attention launch per step)."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    fa_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        step(i, fa_ev[i])
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps, sum(a.elapsed_time(b) for a, b in fa_ev) / steps
 
 
 def check_full_size(st, api, L, torch, np, wl):
@@ -130,7 +156,7 @@ def check_full_size(st, api, L, torch, np, wl):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     ix, w, sel = wl["reps"][0]
-    api.score_topk(st, ix, wl["qa"], HIST_TOKENS // BT, wl["n_tokens"], RETRIEVED // BT, 1, 0, None, w, sel)
+    api.score_topk(st, ix, wl["qa"], wl["hist_tokens"] // BT, wl["n_tokens"], RETRIEVED // BT, 1, 0, None, w, sel)
     res = sel.result()
     assert np.array_equal(res["to_base"], np.arange(0, RETRIEVED, BT)), "window layout"
     assert len(res["stage_slots"]) == 0 and res["total"] == RETRIEVED, "steady state restages nothing"
@@ -281,10 +307,242 @@ def run_prefill(args, st, api, L, torch, np):
     print(json.dumps(rec), flush=True)
 
 
+# ---- stage-in + RoPE re-application (128 selected blocks) --------------------
+SI_BLOCKS = 128
+SI_BYTES = SI_BLOCKS * BT * (K_ROW + V_ROW)                             # 27,262,976
+
+
+def run_stagein(args, st, api, L, torch, np):
+    """Stage-in of 128 selected 128-token blocks (q8_0 K re-RoPE'd from its
+    original position to its window position, FWHT and requantised; q4_0 V moved
+    unchanged) from pinned host memory into a 16,384-cell window.  Every step
+    restages all 128 blocks (the window's slot table is reset first)."""
+    from kvmem_amd import workload as W
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC0FFEE03)
+    n_blocks = HIST_TOKENS // BT
+    kbuf = api.HostBuffer(HIST_TOKENS * K_ROW)
+    vbuf = api.HostBuffer(HIST_TOKENS * V_ROW)
+    chunk = 16384
+    for t0 in range(0, HIST_TOKENS, chunk):
+        k = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
+        v = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
+        torch.from_numpy(kbuf.u8[t0 * K_ROW:(t0 + chunk) * K_ROW]).copy_(api.quantize_rows(st, L.T_Q8_0, k).view(-1).cpu())
+        torch.from_numpy(vbuf.u8[t0 * V_ROW:(t0 + chunk) * V_ROW]).copy_(api.quantize_rows(st, L.T_Q4_0, v).view(-1).cpu())
+    hist = api.History.__new__(api.History)
+    hist.kbuf, hist.vbuf, hist.n_tokens = kbuf, vbuf, HIST_TOKENS
+    hist.c = L.History(kbuf.ptr, vbuf.ptr, HIST_TOKENS)
+    chosen = np.sort(W.distinct_ids(0xC0FFEE03, 0, SI_BLOCKS, 0, n_blocks))
+    scores = torch.zeros(n_blocks, dtype=torch.float64, device=dev)
+    scores[torch.from_numpy(chosen).to(dev)] = 1.0
+    n_tokens = torch.full((n_blocks,), BT, dtype=torch.int32, device=dev)
+    w = api.KVWindow(st, SI_BLOCKS * BT, H_KV, D, BT)
+    sel = api.select_topk(st, scores, n_tokens, SI_BLOCKS, 0, 0, None, w)
+    res = sel.result()
+    assert np.array_equal(res["ids"], chosen) and len(res["stage_slots"]) == SI_BLOCKS, res
+
+    def step():
+        w.reset()
+        api.select_topk(st, scores, n_tokens, SI_BLOCKS, 0, 0, None, w, sel)
+        api.stagein_selection(st, hist, w, sel, N_ROT, FREQ_BASE)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        w.reset()
+        api.select_topk(st, scores, n_tokens, SI_BLOCKS, 0, 0, None, w, sel)
+        evs[i][0].record()
+        api.stagein_selection(st, hist, w, sel, N_ROT, FREQ_BASE)
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
+    # the same bytes as one plain pinned-host -> device copy, for the link's reach
+    dst = torch.empty(SI_BYTES, dtype=torch.uint8, device=dev)
+    src = torch.from_numpy(kbuf.u8[:SI_BYTES])
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        dst.copy_(src, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbps = SI_BYTES * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    # bit-exact check of every staged block against the oracle
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    theta = O.rope_theta(FREQ_BASE, 1.0, N_ROT)
+    ek, ev = w.export_rows(0, SI_BLOCKS * BT)
+    ek, ev = ek.cpu().numpy(), ev.cpu().numpy()
+    t_cpu = 0.0
+    for k, b in enumerate(chosen):
+        hk = kbuf.u8[b * BT * K_ROW:(b + 1) * BT * K_ROW]
+        t1 = time.perf_counter()
+        want = O.stagein_k(hk, BT, H_KV, D, N_ROT, 256, k * BT, theta)
+        t_cpu += time.perf_counter() - t1
+        assert np.array_equal(ek[k * BT:(k + 1) * BT].reshape(-1), want), f"K of block {b}"
+        assert np.array_equal(ev[k * BT:(k + 1) * BT].reshape(-1), vbuf.u8[b * BT * V_ROW:(b + 1) * BT * V_ROW])
+    log("stage-in bytes of all %d blocks equal the oracle's" % SI_BLOCKS)
+    gbps = SI_BYTES / (ms * 1e-3) / 1e9
+    rec = {
+        "metric": "stage-in + RoPE re-application host->device GB/s (128 selected blocks)",
+        "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q8_0 K (fp32 RoPE/FWHT, requantised) / q4_0 V bytes", "data": "synthetic N(0,1), seed 0xC0FFEE03",
+        "config": {"workload": "stage-in: 128 distinct 128-token blocks drawn uniformly from 2048, pinned host "
+                               "q8_0 K / q4_0 V -> 16384-cell window, 4 kv heads, head_dim 256, NeoX RoPE on 64 dims "
+                               "(theta 1e7) from the original to the window position, FWHT 256, q8_0 requant",
+                   "bytes_h2d": SI_BYTES},
+        "roofline": {"bound": "host-link", "kernel": "kvm_stagein_selection (k_stagein)",
+                     "achieved": round(gbps, 2), "peak": round(copy_gbps, 2), "unit": "GB/s",
+                     "frac": round(gbps / copy_gbps, 4), "traffic": None, "launch_us": round(ms * 1e3, 2),
+                     "peak_source": "plain pinned-host->device copy of the same bytes on this box"},
+        "cpu_baseline": {"value": round(SI_BYTES / t_cpu / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"oracle C stage-in (dequant, RoPE, FWHT, requant) of K for all {SI_BLOCKS} "
+                                   f"blocks ({t_cpu:.2f} s, one thread; V is a byte copy)"},
+    }
+    print(json.dumps(rec), flush=True)
+
+
+# ---- multi-lane decode (4 conversations) -------------------------------------
+LANE_HIST = (65536, 131072, 196608, 262144)
+
+
+def run_lanes(args, st, api, L, torch, np):
+    """Four conversations, each with its own 32K-cell window, mean-K index and
+    pinned host history (64K / 128K / 192K / 256K tokens), one bf16 query token
+    each: retrieval for all lanes in one launch sequence (scoring grid over every
+    lane's blocks + one top-k workgroup per lane), stage-in per lane, attention
+    for all lanes in one launch."""
+    n_rep = 2
+    wls = []
+    for i, ht in enumerate(LANE_HIST):
+        log("building lane %d (%d-token history)" % (i, ht))
+        wls.append(build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE05 + i, hist_tokens=ht, mtp=1))
+    outs = [torch.empty((1, N_HEAD, D), dtype=torch.float32, device="cuda") for _ in wls]
+    scale = D ** -0.5
+    preps = []
+    for r in range(n_rep):
+        lanes = [dict(index=wl["reps"][r][0], query=wl["qa"], n_blocks=wl["hist_tokens"] // BT,
+                      n_tokens=wl["n_tokens"], budget_blocks=RETRIEVED // BT, sink_blocks=1,
+                      window=wl["reps"][r][1], sel=wl["reps"][r][2]) for wl in wls]
+        preps.append((api.prepare_score_topk_lanes(st, lanes),
+                      [api.prepare_stagein(st, wl["hist"], wl["reps"][r][1], wl["reps"][r][2], N_ROT, FREQ_BASE)
+                       for wl in wls],
+                      api.prepare_fa_decode_lanes(st, [wl["reps"][r][1] for wl in wls], [wl["q"] for wl in wls],
+                                                  [wl["q_pos"] for wl in wls], N_HEAD, scale, outs)))
+
+    def step(i, ev=None):
+        score, stageins, fa = preps[i % n_rep]
+        score()
+        for si in stageins:
+            si()
+        if ev is not None:
+            ev[0].record()
+        fa()
+        if ev is not None:
+            ev[1].record()
+
+    ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
+    # checks: each lane's selection equals its single-lane one, nothing to restage,
+    # and its attention equals the single-lane kernel's and the oracle's
+    r = (args.steps - 1) % n_rep
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    for i, wl in enumerate(wls):
+        ix, w, sel = wl["reps"][r]
+        res = sel.result()
+        assert np.array_equal(res["ids"], wl["ids"]) and len(res["stage_slots"]) == 0, i
+        one = api.fa_decode(st, w, wl["q"], wl["q_pos"], N_HEAD, scale).cpu().numpy()
+        np.testing.assert_allclose(outs[i].cpu().numpy(), one, rtol=1e-3, atol=1e-4)
+    ek, ev = wls[0]["reps"][r][1].export_rows(0, WINDOW)
+    ref = O.fa_ggml(O.T_Q8_0, O.T_Q4_0, wls[0]["q"].float().cpu().numpy()[:, :G], ek.cpu().numpy()[:, :K_ROW // H_KV],
+                    ev.cpu().numpy()[:, :V_ROW // H_KV], wls[0]["reps"][r][1].cell_pos.cpu().numpy(),
+                    wls[0]["q_pos"].cpu().numpy(), G, 1, D, scale, n_threads=min(16, os.cpu_count() or 1))
+    got = outs[0].cpu().numpy()[:, :G]
+    err = float(np.abs(got - ref).max())
+    assert err <= 2e-3 and err <= 1e-3 * float(np.abs(ref).max()), err
+    log("multi-lane checks passed")
+    n_blocks = [h // BT for h in LANE_HIST]
+    fa_bytes = len(wls) * (FA_KV_BYTES + N_HEAD * D * (2 + 4))
+    step_bytes = fa_bytes + sum(nb * (H_KV * D * 4 + 8) for nb in n_blocks)
+    fa_gbps = fa_bytes / (fa_ms * 1e-3) / 1e9
+    rec = {
+        "metric": "multi-lane decode aggregate tokens/s (4 lanes, 64K-256K histories, 32K windows)",
+        "value": round(len(wls) / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q8_0/q4_0 KV (int8 + fp16 MFMA), bf16 Q, fp32 softmax",
+        "data": "synthetic N(0,1), seeds 0xC0FFEE05 + lane, 16 planted blocks per lane",
+        "config": {"workload": "4 lanes: histories of 65536/131072/196608/262144 tokens (pinned host q8_0 K / "
+                               "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; score + top-k for all "
+                               "lanes in one launch sequence, stage-in per lane, FA decode for all lanes in one "
+                               "launch; 24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
+                   "lanes": len(wls), "step_bytes": step_bytes},
+        "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode_lanes (k_fa_decode split-K + k_fa_combine)",
+                     "achieved": round(fa_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "launch_us": round(fa_ms * 1e3, 3), "algorithmic_bytes": fa_bytes},
+    }
+    print(json.dumps(rec), flush=True)
+
+
+# ---- history sweep of the decode step ------------------------------------------
+SWEEP_HIST = (32768, 65536, 131072, 262144)
+
+
+def run_sweep(args, st, api, L, torch, np):
+    """The decode step at 32K / 64K / 128K / 256K-token histories (same window,
+    query and replicas); one JSON line with a row per history size."""
+    rows = []
+    out = torch.empty((MTP, N_HEAD, D), dtype=torch.float32, device="cuda")
+    for ht in SWEEP_HIST:
+        log("history %d" % ht)
+        wl = build_workload(st, api, L, torch, np, args.replicas, hist_tokens=ht)
+        preps = prepare_decode(st, api, wl, out)
+
+        def step(i, ev=None):
+            score, stagein, fa = preps[i % len(preps)]
+            score()
+            stagein()
+            if ev is not None:
+                ev[0].record()
+            fa()
+            if ev is not None:
+                ev[1].record()
+
+        ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
+        nb = ht // BT
+        step_bytes = nb * (H_KV * D * 4 + 8) + FA_KV_BYTES + QO_BYTES
+        rows.append({"history_tokens": ht, "blocks": nb, "us_per_token": round(ms * 1e3, 2),
+                     "fa_us": round(fa_ms * 1e3, 2), "step_bytes": step_bytes,
+                     "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                     "roofline_step_us": round(step_bytes / (HBM_PEAK_GBPS * 1e9) * 1e6, 3)})
+        log(json.dumps(rows[-1]))
+        del preps, wl
+        torch.cuda.synchronize()
+    last = rows[-1]
+    rec = {
+        "metric": "decode attn+retrieval µs/token and HBM GB/s, history sweep 32K-256K, 32K window",
+        "value": last["us_per_token"], "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q8_0/q4_0 KV (int8 + fp16 MFMA), bf16 Q, fp32 softmax", "data": "synthetic N(0,1), seed 0xC0FFEE02",
+        "config": {"workload": "decode step (score + top-k + stage plan + stage-in + FA decode over a 32768-cell "
+                               "window, 4 bf16 query tokens) at each history size", "replicas": args.replicas},
+        "sweep": rows,
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill"],
-                    help="decode: the headline decode step (default); prefill: chunked-prefill attention")
+    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "stagein", "lanes", "sweep"],
+                    help="decode: the headline decode step (default); prefill: chunked-prefill attention; "
+                         "stagein: stage-in + RoPE of 128 blocks; lanes: 4-lane decode; sweep: decode step "
+                         "at 32K-256K histories")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -304,6 +562,12 @@ def main():
     st = api.State(0)
     if args.workload == "prefill":
         return run_prefill(args, st, api, L, torch, np)
+    if args.workload == "stagein":
+        return run_stagein(args, st, api, L, torch, np)
+    if args.workload == "lanes":
+        return run_lanes(args, st, api, L, torch, np)
+    if args.workload == "sweep":
+        return run_sweep(args, st, api, L, torch, np)
     log("building workload (256K history, 32K window, %d replicas)" % args.replicas)
     t0 = time.time()
     wl = build_workload(st, api, L, torch, np, args.replicas)
@@ -311,33 +575,20 @@ def main():
     O = check_full_size(st, api, L, torch, np, wl)
     log("full-size checks passed")
 
-    n_blocks = HIST_TOKENS // BT
     out = torch.empty((MTP, N_HEAD, D), dtype=torch.float32, device="cuda")
-    scale = D ** -0.5
+    preps = prepare_decode(st, api, wl, out)
 
     def step(i, ev=None):
-        ix, w, sel = wl["reps"][i % len(wl["reps"])]
-        api.score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, None, w, sel)
-        api.stagein_selection(st, wl["hist"], w, sel, N_ROT, FREQ_BASE)
+        score, stagein, fa = preps[i % len(preps)]
+        score()
+        stagein()
         if ev is not None:
             ev[0].record()
-        api.fa_decode(st, w, wl["q"], wl["q_pos"], N_HEAD, scale, out)
+        fa()
         if ev is not None:
             ev[1].record()
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    fa_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        step(i, fa_ev[i])
-    stop.record()
-    torch.cuda.synchronize()
-    step_ms = start.elapsed_time(stop) / args.steps
-    fa_ms = sum(a.elapsed_time(b) for a, b in fa_ev) / args.steps
+    step_ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
     out_gpu = out.cpu().numpy()
     if args.calibrate_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

@@ -209,6 +209,22 @@ typedef struct kvm_selection {
 int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
                    const kvm_select_params *p, const kvm_window *w, const kvm_selection *out);
 
+/* Several independent retrievals (conversation lanes, each with its own
+ * index, query accumulator, parameters, window and outputs) in one launch
+ * sequence: one scoring grid over every lane's blocks, then one top-k
+ * workgroup per lane.  Each lane's results equal kvm_score_topk on that lane
+ * alone.  The reference runs score_retrieval + pick_topk_blocks once per lane
+ * from the host (docs/multi-lane-conversations.md:1-20,
+ * llama-memory-kvmem.cpp:4149-4196).  n_lanes <= 8. */
+typedef struct kvm_retrieval_lane {
+    const kvm_meank_index *ix;
+    const kvm_query_acc *q;
+    const kvm_select_params *p;
+    const kvm_window *w;
+    const kvm_selection *out;
+} kvm_retrieval_lane;
+int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes);
+
 /* Top-k + layout on caller-provided scores (KvMemStore::set_retrieval_scores,
  * kvmem_store.cpp:242-248, then pick_topk_blocks as above): `scores` is a device
  * double [p->n_blocks]; out->scores is not written. */

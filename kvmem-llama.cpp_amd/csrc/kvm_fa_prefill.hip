@@ -26,7 +26,7 @@
 // global memory straight into LDS (double buffered, one barrier per tile); the
 // tiles of the workgroup's key range that some row can see are listed in LDS
 // once at the start.  Q stays in registers as f16 B
-// operands; O^T (32 rows x D) lives in the accumulators.  Online softmax in the
+// operands; O^T (16 rows x D per wave) lives in the accumulators.  Online softmax in the
 // log2 domain with a lazy running maximum (rescale only when a row max grows
 // by more than 2^8).  Tiles no row of the workgroup can see are skipped;
 // tiles every row sees in full skip the mask.

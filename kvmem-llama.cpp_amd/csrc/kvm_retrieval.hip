@@ -143,6 +143,7 @@ struct score_args {
     const uint32_t *mean_tokens;
     double *layer_score;    // [n_layer][cap]
     uint32_t n_blocks, cap, n_tiles, n_layer, n_head, H;
+    uint32_t n_tiles_used;  // tiles holding the first n_blocks blocks
 };
 
 // Workgroup barrier for LDS traffic only (no wait for outstanding global
@@ -280,8 +281,16 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
     KVM_LDS_BARRIER();                   // chunk c's LDS reads done before chunk c+1 writes
 }
 
+// Independent retrievals (conversation lanes) in one launch: lane = blockIdx.z.
+#define KVM_RET_LANES 8
+struct score_lanes {
+    score_args lane[KVM_RET_LANES];
+};
+
 template <int D>
-__global__ void __launch_bounds__(256) k_score(score_args a) {
+__global__ void __launch_bounds__(256) k_score(score_lanes sl) {
+    const score_args &a = sl.lane[blockIdx.z];
+    if (blockIdx.x >= a.n_tiles_used || blockIdx.y >= a.n_layer) return;
     constexpr uint32_t TW = KVM_MEANK_TILE;       // blocks per tile
     constexpr uint32_t HC = 64 / TW;              // heads per chunk
     __shared__ float s_k[D][64];                  // kh as [dim][lane]
@@ -378,7 +387,12 @@ __device__ inline void hist_add(uint32_t *s_hist, uint32_t bin, bool active) {
 // order-preserving 64-bit keys narrows to the bin holding the need-th largest
 // key; it stops as soon as that bin is taken whole, otherwise ties on the full
 // key are broken by descending block id.
-__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_args a) {
+struct topk_lanes {
+    topk_args lane[KVM_RET_LANES];
+};
+
+__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
+    const topk_args &a = tl.lane[blockIdx.x];
     __shared__ uint64_t s_key[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint32_t s_ntok[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
@@ -566,19 +580,23 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_args a) {
     }
 }
 
-static int launch_topk(kvm_state *st, const double *scores, const double *layer_score,
-                       const kvm_meank_index *ix, const kvm_query_acc *q, const kvm_select_params *p,
-                       const kvm_window *w, const kvm_selection *out) {
+static int make_topk(kvm_state *st, const double *scores, const double *layer_score,
+                     const kvm_meank_index *ix, const kvm_query_acc *q, const kvm_select_params *p,
+                     const kvm_window *w, const kvm_selection *out, topk_args *ta) {
     if (w && (kvm_window_check(w) || !w->slot_block || !w->slot_base))
         return kvm_fail(st, KVM_EINVAL, "topk: bad window or window without slot map");
-    topk_args ta{scores, layer_score, q ? q->q_count : nullptr, ix ? ix->present : nullptr, out->scores,
-                 p->n_tokens, p->mandatory,
-                 w ? w->slot_block : nullptr, w ? w->slot_base : nullptr,
-                 out->ids, out->to_base, out->stage_slots, out->info,
-                 p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
-                 w ? w->n_cells / w->block_tokens : 0u, out->cap,
-                 ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u};
-    hipLaunchKernelGGL(k_topk, dim3(1), dim3(KVM_TOPK_THREADS), 0, st->stream, ta);
+    *ta = topk_args{scores, layer_score, q ? q->q_count : nullptr, ix ? ix->present : nullptr, out->scores,
+                    p->n_tokens, p->mandatory,
+                    w ? w->slot_block : nullptr, w ? w->slot_base : nullptr,
+                    out->ids, out->to_base, out->stage_slots, out->info,
+                    p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
+                    w ? w->n_cells / w->block_tokens : 0u, out->cap,
+                    ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u};
+    return KVM_OK;
+}
+
+static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes) {
+    hipLaunchKernelGGL(k_topk, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl);
     KVM_LAUNCH_CHECK(st, "topk");
     return KVM_OK;
 }
@@ -601,18 +619,21 @@ extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_se
     if (rc) return rc;
     if (p->n_blocks && !scores) return kvm_fail(st, KVM_EINVAL, "select_topk: null scores");
     KVM_HIP(st, hipSetDevice(st->device));
-    return launch_topk(st, scores, nullptr, nullptr, nullptr, p, w, out);
+    topk_lanes tl{};
+    rc = make_topk(st, scores, nullptr, nullptr, nullptr, p, w, out, &tl.lane[0]);
+    if (rc) return rc;
+    return launch_topk(st, tl, 1);
 }
 
-extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
-                              const kvm_select_params *p, const kvm_window *w,
-                              const kvm_selection *out) {
-    if (!st) return KVM_EINVAL;
-    if (!ix || !q) return kvm_fail(st, KVM_EINVAL, "score_topk: null argument");
-    int rc = check_select(st, p, out);
+static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
+    const kvm_meank_index *ix = r.ix;
+    const kvm_query_acc *q = r.q;
+    const kvm_select_params *p = r.p;
+    if (!ix || !q) return kvm_fail(st, KVM_EINVAL, "score_topk: lane %u: null argument", i);
+    int rc = check_select(st, p, r.out);
     if (rc) return rc;
-    if (!ix->k_sum || !ix->mean_tokens || !q->q_sum || !q->q_count || !out->scores)
-        return kvm_fail(st, KVM_EINVAL, "score_topk: null buffer");
+    if (!ix->k_sum || !ix->mean_tokens || !q->q_sum || !q->q_count || !r.out->scores)
+        return kvm_fail(st, KVM_EINVAL, "score_topk: lane %u: null buffer", i);
     if (p->n_blocks > ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "score_topk: n_blocks %u > index capacity %u", p->n_blocks, ix->n_blocks);
     if (q->n_layer != ix->n_layer || q->head_dim != ix->head_dim) return kvm_fail(st, KVM_EINVAL, "score_topk: query/index shape mismatch");
     if (ix->head_dim != 128 && ix->head_dim != 256) return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: head_dim %u", ix->head_dim);
@@ -620,18 +641,55 @@ extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kv
         q->n_head / ix->n_head_kv > KVM_SCORE_GMAX)
         return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: n_head %u / n_head_kv %u (at most %d kv heads, groups of at most %d)",
                         q->n_head, ix->n_head_kv, KVM_SCORE_HMAX, KVM_SCORE_GMAX);
+    return KVM_OK;
+}
+
+extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes) {
+    if (!st) return KVM_EINVAL;
+    if (!lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk: no lanes");
+    if (n_lanes > KVM_RET_LANES) return kvm_fail(st, KVM_ERANGE, "score_topk: %u lanes > %d", n_lanes, KVM_RET_LANES);
+    size_t ls_total = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        int rc = check_score(st, lanes[i], i);
+        if (rc) return rc;
+        if (lanes[i].ix->head_dim != lanes[0].ix->head_dim)
+            return kvm_fail(st, KVM_EINVAL, "score_topk: lanes differ in head_dim");
+        ls_total += (size_t)lanes[i].ix->n_layer * lanes[i].ix->n_blocks;
+    }
     KVM_HIP(st, hipSetDevice(st->device));
-    if (p->n_blocks == 0) return launch_topk(st, out->scores, nullptr, nullptr, nullptr, p, w, out);
-    double *ls = (double *)kvm_workspace(st, (size_t)ix->n_layer * ix->n_blocks * sizeof(double));
+    double *ls = (double *)kvm_workspace(st, ls_total * sizeof(double) + 8);
     if (!ls) return kvm_fail(st, KVM_ENOMEM, "score_topk: workspace");
-    const uint32_t n_tiles = kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE);
-    score_args sa{q->q_sum, q->q_count, ix->k_sum, ix->mean_tokens, ls,
-                  p->n_blocks, ix->n_blocks, n_tiles, ix->n_layer, q->n_head, ix->n_head_kv};
-    const dim3 grid(kvm_cdiv(p->n_blocks, KVM_MEANK_TILE), ix->n_layer), block(256);
-    if (ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sa);
-    else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sa);
-    KVM_LAUNCH_CHECK(st, "score");
-    return launch_topk(st, nullptr, ls, ix, q, p, w, out);
+    score_lanes sl{};
+    topk_lanes tl{};
+    uint32_t max_tiles = 0, max_layer = 0;
+    size_t off = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        const kvm_retrieval_lane &r = lanes[i];
+        const kvm_meank_index *ix = r.ix;
+        const uint32_t used = r.p->n_blocks ? kvm_cdiv(r.p->n_blocks, KVM_MEANK_TILE) : 0u;
+        sl.lane[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, ls + off,
+                                r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
+                                r.q->n_head, ix->n_head_kv, used};
+        // a lane without blocks reduces nothing: top-k reads its own (empty) score array
+        int rc = r.p->n_blocks ? make_topk(st, nullptr, ls + off, ix, r.q, r.p, r.w, r.out, &tl.lane[i])
+                               : make_topk(st, r.out->scores, nullptr, nullptr, nullptr, r.p, r.w, r.out, &tl.lane[i]);
+        if (rc) return rc;
+        off += (size_t)ix->n_layer * ix->n_blocks;
+        max_tiles = used > max_tiles ? used : max_tiles;
+        max_layer = ix->n_layer > max_layer ? ix->n_layer : max_layer;
+    }
+    if (max_tiles) {
+        const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
+        if (lanes[0].ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sl);
+        else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sl);
+        KVM_LAUNCH_CHECK(st, "score");
+    }
+    return launch_topk(st, tl, n_lanes);
+}
 
-
+extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
+                              const kvm_select_params *p, const kvm_window *w,
+                              const kvm_selection *out) {
+    const kvm_retrieval_lane lane{ix, q, p, w, out};
+    return kvm_score_topk_lanes(st, &lane, 1);
 }

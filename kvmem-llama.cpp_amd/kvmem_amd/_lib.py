@@ -54,6 +54,11 @@ class Selection(C.Structure):
                 ("to_base", C.c_void_p), ("stage_slots", C.c_void_p), ("info", C.c_void_p)]
 
 
+class RetrievalLane(C.Structure):
+    _fields_ = [("ix", C.POINTER(MeanKIndex)), ("q", C.POINTER(QueryAcc)), ("p", C.POINTER(SelectParams)),
+                ("w", C.POINTER(Window)), ("out", C.POINTER(Selection))]
+
+
 class RopeParams(C.Structure):
     _fields_ = [("n_rot", C.c_uint32), ("freq_base", C.c_float), ("freq_scale", C.c_float),
                 ("hadamard_nrot", C.c_int32)]
@@ -97,6 +102,7 @@ SIGNATURES = {
     "kvm_meank_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32, _P]),
     "kvm_score_topk": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
                                  C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
+    "kvm_score_topk_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), _u32]),
     "kvm_select_topk": (C.c_int, [_P, _P, C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
     "kvm_stagein_selection": (C.c_int, [_P, C.POINTER(History), _PW, C.POINTER(Selection),
                                         C.POINTER(RopeParams)]),

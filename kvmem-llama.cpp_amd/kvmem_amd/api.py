@@ -226,6 +226,21 @@ def score_topk(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks=
     return sel
 
 
+def score_topk_lanes(st, lanes):
+    """lanes: list of dicts with index, query, n_blocks, n_tokens, budget_blocks,
+    sink_blocks, recent_blocks, window, sel (as score_topk).  One launch sequence."""
+    keep = []
+    arr = (L.RetrievalLane * len(lanes))()
+    for i, ln in enumerate(lanes):
+        p = L.SelectParams(ln["n_blocks"], ln["budget_blocks"], ln.get("sink_blocks", 1), ln.get("recent_blocks", 0),
+                           None, 0, ln["n_tokens"].data_ptr())
+        keep.append(p)
+        arr[i] = L.RetrievalLane(C.pointer(ln["index"].c), C.pointer(ln["query"].c), C.pointer(p),
+                                 C.pointer(ln["window"].c), C.pointer(ln["sel"].c))
+    st.check(st.lib.kvm_score_topk_lanes(st.h, arr, len(lanes)))
+    return [ln["sel"] for ln in lanes]
+
+
 def select_topk(st, scores, n_tokens, budget_blocks, sink_blocks=1, recent_blocks=0, mandatory=None,
                 window=None, sel=None):
     """Top-k + layout on given scores (device float64 [n_blocks])."""
@@ -297,6 +312,61 @@ def fa_decode_lanes(st, windows, qs, q_poss, n_head, scale, outs=None):
     qt = L.T_BF16 if qs[0].dtype == torch.bfloat16 else L.T_F32
     st.check(st.lib.kvm_fa_decode_lanes(st.h, lanes, n, qt, n_head, float(scale)))
     return outs
+
+
+class Prepared:
+    """One library call with its ctypes arguments built once, for step loops:
+    calling it costs one foreign call and no argument marshalling."""
+
+    def __init__(self, st, fn, args, keep=()):
+        self.st, self.fn, self.args, self.keep = st, fn, args, keep
+
+    def __call__(self):
+        rc = self.fn(*self.args)
+        if rc:
+            self.st.check(rc)
+
+
+def prepare_score_topk(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window, sel):
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks, None, 0, n_tokens.data_ptr())
+    return Prepared(st, st.lib.kvm_score_topk,
+                    (st.h, C.byref(index.c), C.byref(query.c), C.byref(p), C.byref(window.c), C.byref(sel.c)),
+                    (p, index, query, window, sel, n_tokens))
+
+
+def prepare_score_topk_lanes(st, lanes):
+    keep, arr = [], (L.RetrievalLane * len(lanes))()
+    for i, ln in enumerate(lanes):
+        p = L.SelectParams(ln["n_blocks"], ln["budget_blocks"], ln.get("sink_blocks", 1), ln.get("recent_blocks", 0),
+                           None, 0, ln["n_tokens"].data_ptr())
+        keep += [p, ln]
+        arr[i] = L.RetrievalLane(C.pointer(ln["index"].c), C.pointer(ln["query"].c), C.pointer(p),
+                                 C.pointer(ln["window"].c), C.pointer(ln["sel"].c))
+    return Prepared(st, st.lib.kvm_score_topk_lanes, (st.h, arr, len(lanes)), (keep, arr))
+
+
+def prepare_stagein(st, history, window, sel, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    return Prepared(st, st.lib.kvm_stagein_selection,
+                    (st.h, C.byref(history.c), C.byref(window.c), C.byref(sel.c), C.byref(r)),
+                    (r, history, window, sel))
+
+
+def prepare_fa_decode(st, window, q, q_pos, n_head, scale, out):
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_fa_decode,
+                    (st.h, C.byref(window.c), _ptr(q), qt, _ptr(q_pos), q.shape[0], n_head, float(scale), _ptr(out)),
+                    (window, q, q_pos, out))
+
+
+def prepare_fa_decode_lanes(st, windows, qs, q_poss, n_head, scale, outs):
+    n = len(windows)
+    lanes = (L.Lane * n)()
+    for i, (w, q, qp, o) in enumerate(zip(windows, qs, q_poss, outs)):
+        lanes[i] = L.Lane(C.pointer(w.c), q.data_ptr(), qp.data_ptr(), o.data_ptr(), q.shape[0])
+    qt = L.T_BF16 if qs[0].dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_fa_decode_lanes, (st.h, lanes, n, qt, n_head, float(scale)),
+                    (lanes, windows, qs, q_poss, outs))
 
 
 def quantize_rows(st, ty, x):

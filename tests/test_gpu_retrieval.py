@@ -99,6 +99,39 @@ def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
     assert np.array_equal(res["to_base"], to_base) and res["total"] == total and res["status"] == 0
 
 
+def test_score_topk_lanes_match_single_lane(kvm_state):
+    """Four lanes of different sizes (multi-lane decode) in one launch sequence:
+    every lane's scores, ids, layout and stage plan equal the oracle's and a
+    single-lane call's."""
+    H, n_head, D = 4, 24, 256
+    lanes, single, cases = [], [], []
+    for i, n_blocks in enumerate((512, 1024, 1536, 2048)):
+        q, qc, k_sum, mt, planted = _case(200 + i, n_blocks, 1, n_head, H, D)
+        ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+        qa = api.QueryAcc(kvm_state, 1, n_head, D)
+        qa.q_sum.copy_(dev(q))
+        qa.q_count.copy_(dev(qc.astype(np.int32)))
+        n_tokens = dev(np.full(n_blocks, 128, np.int32))
+        w = api.KVWindow(kvm_state, 128 * 128, H, D, 128)
+        sel = api.SelectionBuffers(kvm_state, n_blocks, 128)
+        lanes.append(dict(index=ix, query=qa, n_blocks=n_blocks, n_tokens=n_tokens, budget_blocks=128,
+                          sink_blocks=1, window=w, sel=sel))
+        w1 = api.KVWindow(kvm_state, 128 * 128, H, D, 128)
+        single.append(api.score_topk(kvm_state, ix, qa, n_blocks, n_tokens, 128, 1, 0, None, w1))
+        cases.append((q, qc, k_sum, mt, planted))
+    api.score_topk_lanes(kvm_state, lanes)
+    for ln, one, (q, qc, k_sum, mt, planted) in zip(lanes, single, cases):
+        r, r1 = ln["sel"].result(), one.result()
+        for key in ("ids", "to_base", "stage_slots"):
+            assert np.array_equal(r[key], r1[key]), key
+        assert r["total"] == r1["total"] and r["status"] == r1["status"] == 0
+        want = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
+        got = host(ln["sel"].scores)[:ln["n_blocks"]]
+        assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+        assert np.array_equal(r["ids"], O.pick_topk(want, 128, 1, 0))
+        assert set(planted) <= set(r["ids"])
+
+
 KATS = [
     # (scores, budget, sink, recent, mandatory, expected) -- kvmem_store_test.cpp
     ({5: 100.0, 6: 90.0, 3: 10.0}, 4, 1, 1, [], [0, 5, 6, 9]),
