@@ -132,21 +132,24 @@ def prepare_decode(st, api, wl, out):
             for ix, w, sel in wl["reps"]]
 
 
-def time_steps(torch, step, steps, warmup):
-    """Warm up, then time `steps` calls of step(i, fa_events) on the stream:
-    (ms per step, ms of the attention launch per step)."""
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    fa_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(steps):
-        step(i, fa_ev[i])
-    stop.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps, sum(a.elapsed_time(b) for a, b in fa_ev) / steps
+def time_steps(torch, step, fa, steps, warmup):
+    """Eager (ms per step, ms per attention launch), each from one pair of
+    events around a loop: an event recorded between two launches would itself
+    open a gap of several microseconds in the stream.  `step(i)` runs step i;
+    `fa(i)` runs only the attention launch of step i (back to back over the
+    replicas, so every launch streams its window from HBM)."""
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(i)
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+    return timed(step), timed(fa)
 
 
 def check_full_size(st, api, L, torch, np, wl):
@@ -435,18 +438,14 @@ def run_lanes(args, st, api, L, torch, np):
                       api.prepare_fa_decode_lanes(st, [wl["reps"][r][1] for wl in wls], [wl["q"] for wl in wls],
                                                   [wl["q_pos"] for wl in wls], N_HEAD, scale, outs)))
 
-    def step(i, ev=None):
+    def step(i):
         score, stageins, fa = preps[i % n_rep]
         score()
         for si in stageins:
             si()
-        if ev is not None:
-            ev[0].record()
         fa()
-        if ev is not None:
-            ev[1].record()
 
-    ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
+    ms, fa_ms = time_steps(torch, step, lambda i: preps[i % n_rep][2](), args.steps, args.warmup)
     # checks: each lane's selection equals its single-lane one, nothing to restage,
     # and its attention equals the single-lane kernel's and the oracle's
     r = (args.steps - 1) % n_rep
@@ -504,17 +503,13 @@ def run_sweep(args, st, api, L, torch, np):
         wl = build_workload(st, api, L, torch, np, args.replicas, hist_tokens=ht)
         preps = prepare_decode(st, api, wl, out)
 
-        def step(i, ev=None):
+        def step(i):
             score, stagein, fa = preps[i % len(preps)]
             score()
             stagein()
-            if ev is not None:
-                ev[0].record()
             fa()
-            if ev is not None:
-                ev[1].record()
 
-        ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
+        ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][2](), args.steps, args.warmup)
         nb = ht // BT
         step_bytes = nb * (H_KV * D * 4 + 8) + FA_KV_BYTES + QO_BYTES
         rows.append({"history_tokens": ht, "blocks": nb, "us_per_token": round(ms * 1e3, 2),
@@ -578,17 +573,13 @@ def main():
     out = torch.empty((MTP, N_HEAD, D), dtype=torch.float32, device="cuda")
     preps = prepare_decode(st, api, wl, out)
 
-    def step(i, ev=None):
+    def step(i):
         score, stagein, fa = preps[i % len(preps)]
         score()
         stagein()
-        if ev is not None:
-            ev[0].record()
         fa()
-        if ev is not None:
-            ev[1].record()
 
-    step_ms, fa_ms = time_steps(torch, step, args.steps, args.warmup)
+    step_ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][2](), args.steps, args.warmup)
     out_gpu = out.cpu().numpy()
     if args.calibrate_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

@@ -152,9 +152,10 @@ struct score_args {
 #define KVM_SCORE_GMAX 16   // largest query group (n_head / n_head_kv)
 #define KVM_SCORE_HMAX 16   // largest n_head_kv
 
-// One head chunk of a tile (up to 8 heads): slab batches of 32 dims for all
-// the chunk's heads stream into LDS as kh while the chains advance batch by
-// batch.  UPB = 16-byte slab units per thread and batch (1 for <= 4 heads).
+// One head chunk of a tile (up to 8 heads): the chunk's slab (every load
+// issued first) goes into LDS as kh, then one wave per chain (dot, nk, nq)
+// walks the dims in order.  UPB = 16-byte slab units per thread and 32-dim
+// batch (1 for <= 4 heads).
 template <int D, int UPB>
 __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile, uint32_t c,
                                             uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[64],
@@ -222,7 +223,8 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
         inv4[j] = mt4[j] ? kvm_fdiv(1.0f, (float)mt4[j]) : 0.0f;
         keep4[j] = mt4[j] ? 0xffffffffu : 0u;
     }
-    // ---- batches: write kh, then the chains take 32 more dims
+    // ---- kh for all dims into LDS (one barrier), then the chains run straight
+    // through the D dims in the reference's order
     const uint32_t hh = lane / TW;
     const float *qrow = s_qv[hh < nh ? hh : 0u];
     const float *nqrow = s_qv[lane < nh ? lane : 0u];
@@ -241,31 +243,31 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
                 *(float4 *)&s_k[32 * k + r][hu * TW + 4 * quad] = kh;
             }
         }
-        KVM_LDS_BARRIER();
-        if (w == 0) {
-#pragma unroll
-            for (int d = 32 * k; d < (int)(32 * k + 32); d += 4) {
-                const float4 q4 = *(const float4 *)&qrow[d];
-                chain = kvm_fadd(chain, kvm_fmul(q4.x, s_k[d][lane]));
-                chain = kvm_fadd(chain, kvm_fmul(q4.y, s_k[d + 1][lane]));
-                chain = kvm_fadd(chain, kvm_fmul(q4.z, s_k[d + 2][lane]));
-                chain = kvm_fadd(chain, kvm_fmul(q4.w, s_k[d + 3][lane]));
-            }
-        } else if (w == 1) {
-#pragma unroll
-            for (int d = 32 * k; d < (int)(32 * k + 32); ++d) {
-                const float kh = s_k[d][lane];
-                chain = kvm_fadd(chain, kvm_fmul(kh, kh));
-            }
-        } else if (w == 2) {
-#pragma unroll
-            for (int d = 32 * k; d < (int)(32 * k + 32); d += 4) {
-                const float4 q4 = *(const float4 *)&nqrow[d];
-                chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
-                chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
-                chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
-                chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
-            }
+    }
+    KVM_LDS_BARRIER();
+    if (w == 0) {
+#pragma unroll 16
+        for (int d = 0; d < D; d += 4) {
+            const float4 q4 = *(const float4 *)&qrow[d];
+            chain = kvm_fadd(chain, kvm_fmul(q4.x, s_k[d][lane]));
+            chain = kvm_fadd(chain, kvm_fmul(q4.y, s_k[d + 1][lane]));
+            chain = kvm_fadd(chain, kvm_fmul(q4.z, s_k[d + 2][lane]));
+            chain = kvm_fadd(chain, kvm_fmul(q4.w, s_k[d + 3][lane]));
+        }
+    } else if (w == 1) {
+#pragma unroll 16
+        for (int d = 0; d < D; ++d) {
+            const float kh = s_k[d][lane];
+            chain = kvm_fadd(chain, kvm_fmul(kh, kh));
+        }
+    } else if (w == 2) {
+#pragma unroll 16
+        for (int d = 0; d < D; d += 4) {
+            const float4 q4 = *(const float4 *)&nqrow[d];
+            chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
+            chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
+            chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
+            chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
         }
     }
     if (w == 1) s_nk[lane] = chain;
@@ -341,6 +343,7 @@ struct topk_args {
 };
 
 #define KVM_TOPK_THREADS 1024
+#define KVM_TOPK_SLOTS 2048       // slot-map entries held in LDS
 #define KVM_TOPK_LOAD (KVM_MAX_TOPK_BLOCKS / KVM_TOPK_THREADS)
 
 // order-preserving map of a double to uint64 (-0.0 folded onto +0.0, so the
@@ -385,8 +388,8 @@ __device__ inline void hist_add(uint32_t *s_hist, uint32_t bin, bool active) {
 // Selection of the `need` best candidates under the strict order
 // (score desc, block id desc): an MSB-first radix select over the
 // order-preserving 64-bit keys narrows to the bin holding the need-th largest
-// key; it stops as soon as that bin is taken whole, otherwise ties on the full
-// key are broken by descending block id.
+// key; it stops as soon as that bin is taken whole, otherwise ties on the
+// full key are broken by descending block id.
 struct topk_lanes {
     topk_args lane[KVM_RET_LANES];
 };
@@ -400,8 +403,18 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     __shared__ uint32_t s_tmp[2 * (KVM_TOPK_THREADS / 64)];
     __shared__ uint32_t s_count, s_k, s_done, s_need;
     __shared__ uint64_t s_prefix;
+    __shared__ uint32_t s_sblk[KVM_TOPK_SLOTS];
+    __shared__ int32_t s_sbase[KVM_TOPK_SLOTS];
     const uint32_t tid = threadIdx.x, lane = tid & 63, n = a.n;
     const bool all = a.budget == 0 || n <= a.budget;
+    // the window's slot map for the ranks the stage plan compares (loaded with
+    // the scores, so the compaction needs no second memory round trip)
+    const uint32_t n_sl = a.slot_block ? (a.n_slots < a.cap ? a.n_slots : a.cap) : 0u;
+    const uint32_t n_sl_lds = n_sl < KVM_TOPK_SLOTS ? n_sl : KVM_TOPK_SLOTS;
+    for (uint32_t i = tid; i < n_sl_lds; i += KVM_TOPK_THREADS) {
+        s_sblk[i] = a.slot_block[i];
+        s_sbase[i] = a.slot_base[i];
+    }
     // ---- phase A: scores, keys, token counts (all loads first)
     const uint32_t kpt = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
     double sv[KVM_TOPK_LOAD];
@@ -552,7 +565,10 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
             if (!s_kept[i]) continue;
             a.ids[rank] = i;
             a.to_base[rank] = (int32_t)base;
-            if (rank < ns && (!a.slot_block || a.slot_block[rank] != i || a.slot_base[rank] != (int32_t)base)) {
+            const bool in_lds = rank < n_sl_lds;
+            if (rank < ns && (!a.slot_block ||
+                              (in_lds ? s_sblk[rank] : a.slot_block[rank]) != i ||
+                              (in_lds ? s_sbase[rank] : a.slot_base[rank]) != (int32_t)base)) {
                 need_mask |= 1u << k;
                 ++need_local;
             }

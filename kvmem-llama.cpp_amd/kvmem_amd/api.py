@@ -38,6 +38,23 @@ class State:
     def sync(self):
         self.check(self.lib.kvm_state_sync(self.h))
 
+    def capture(self, fns):
+        """Capture the library calls made by fns() (one HIP graph, replayed with
+        .replay() on the current stream).  The state's stream is switched to
+        the capture stream for the capture and restored after; the calls must
+        need no workspace growth (run them once eagerly first)."""
+        cap = torch.cuda.Stream(self.device)
+        old = self.lib.kvm_state_stream(self.h)
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize(self.device)
+        self.check(self.lib.kvm_state_set_stream(self.h, C.c_void_p(cap.cuda_stream)))
+        try:
+            with torch.cuda.graph(g, stream=cap):
+                fns()
+        finally:
+            self.check(self.lib.kvm_state_set_stream(self.h, C.c_void_p(old)))
+        return g
+
     def close(self):
         if self.h:
             self.lib.kvm_state_free(self.h)
