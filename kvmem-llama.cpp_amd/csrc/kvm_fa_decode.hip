@@ -54,22 +54,25 @@ __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
 }
 
 // 8 q4_0 nibbles of one word (key j in byte j%4, high nibble for j >= 4) ->
-// 8 fp16 values nibble - 8 in key order.  Each v_perm packs two nibble bytes
-// under an 0x64 high byte, giving the fp16 1024 + n; subtracting 1032 is exact.
-__device__ inline kvm_f16x8 nib8_to_f16(uint32_t w) {
+// 8 fp16 denormals n * 2^-24 in key order (each v_perm puts a nibble byte
+// under a zero high byte).  The matrix cores take fp16 denormals exactly; the
+// "- 8" of q4_0 and the 2^24 are applied to the accumulated sums (see
+// k_fa_decode), so no per-element subtraction is needed.
+__device__ inline kvm_f16x8 nib8_to_f16den(uint32_t w) {
     const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-    const uint32_t c64 = 0x64646464u;
     uint32_t r[4];
-    r[0] = __builtin_amdgcn_perm(c64, lo, 0x04010400u);
-    r[1] = __builtin_amdgcn_perm(c64, lo, 0x04030402u);
-    r[2] = __builtin_amdgcn_perm(c64, hi, 0x04010400u);
-    r[3] = __builtin_amdgcn_perm(c64, hi, 0x04030402u);
+    r[0] = __builtin_amdgcn_perm(0u, lo, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(0u, lo, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(0u, hi, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(0u, hi, 0x04030402u);
     kvm_f16x8 v;
     __builtin_memcpy(&v, r, 16);
-    const kvm_f16x8 off = {(_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f,
-                           (_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f, (_Float16)1032.0f};
-    return v - off;
+    return v;
 }
+
+// Running maximum of a row before any visible key: finite, so exp2(s - m)
+// needs no guard (a visible key always moves it, see k_fa_decode).
+#define KVM_M_NONE (-1.0e30f)
 
 typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -133,11 +136,12 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
     __shared__ __align__(16) int8_t s_qq[QUANT ? RMAX : 1][D];
     __shared__ __align__(16) _Float16 s_qh[QUANT ? 1 : RMAX][D];
     __shared__ float s_dq[RMAX][NB];
-    __shared__ float s_max[4][RMAX];
+    __shared__ float s_max[4][4][RMAX];      // [key quarter][lane group][row]: max of 4 keys
     __shared__ float s_alpha[RMAX];
     __shared__ int32_t s_rescale[NRT];
+    __shared__ __align__(8) uint8_t s_up[2][8];   // per wave: a row's maximum moved (tile parity)
     __shared__ float s_l[4][RMAX];
-    __shared__ __align__(16) _Float16 s_p[RMAX][PSTR];
+    __shared__ __align__(16) _Float16 s_p[2][RMAX][PSTR];   // P of the tile (tile parity)
 
     // ---- query rows (row r = token r/G, query head h*G + r%G): task (t, lane)
     // covers dims 32b + 8q4 .. +7 of row r.  The raw rows are loaded first,
@@ -261,6 +265,7 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
             *(kvm_f16x8 *)&s_qh[r][32 * b + 8 * g] = hv;
         }
     }
+    if (tid < 16) s_up[tid >> 3][tid & 7] = 0;   // flags of absent waves stay clear
     KVM_LDS_BARRIER();
     // B operands (Q^T) of this wave's row tile: lane (row m, k-group g)
     long qop_i[QUANT ? NB : 1];
@@ -272,15 +277,25 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
         else qop_h[b] = *(const kvm_f16x8 *)&s_qh[myrow][32 * b + 8 * g];
     }
 #pragma unroll
-    for (int gi = 0; gi < NG; ++gi) dqo[gi] = QUANT ? s_dq[myrow][4 * gi + g] : 0.0f;
+    for (int gi = 0; gi < NG; ++gi) dqo[gi] = QUANT ? s_dq[myrow][4 * gi + g] * a.scale_log2 : 0.0f;
 
     kvm_f32x4 O[NRT][NT];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.0f;   // row myrow over this wave's keys
+    // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and Oc
+    // P * dv * 8 * 2^-24 per row and 32-dim V block; O - Oc, times 2^24, is P V
+    kvm_f32x4 Oc[NRT][NBW];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+        for (int bw = 0; bw < NBW; ++bw) Oc[rt][bw] = {0.f, 0.f, 0.f, 0.f};
+    const kvm_f16x8 eight_den = {(_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f,
+                                 (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f};
+    float m_run = KVM_M_NONE, l_run = 0.0f;   // row myrow over this wave's keys
 
+    int par = 0;                         // parity of the tile: P and flag buffers
     auto compute_tile = [&](const Regs &rg, Regs &nx, uint32_t inext) {
         const uint32_t Tn = tile_index(inext);
         load_k(nx, Tn);
@@ -313,63 +328,86 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[i] = acc[i];
         }
-        float mx = -INFINITY;
+        // mask; the scores are in the log2 domain (q8_0: kq_scale * log2(e) is
+        // folded into the query scales)
+        float mx = -INFINITY;                // over this lane's 4 keys
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int32_t cpos = (int32_t)rg.cp[i];
             const bool vis = cpos >= 0 && cpos <= qp;
-            s[i] = vis ? s[i] * a.scale_log2 : -INFINITY;
+            s[i] = vis ? (QUANT ? s[i] : s[i] * a.scale_log2) : -INFINITY;
             mx = fmaxf(mx, s[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        if (g == 0) s_max[kq][myrow] = mx;
-        load_s(nx, Tn);
-        KVM_LDS_BARRIER();
+        s_max[kq][g][myrow] = mx;
         // ---------------- softmax of the tile (lazy running maximum) ----------
-        {
-            const float tm = fmaxf(fmaxf(s_max[0][myrow], s_max[1][myrow]), fmaxf(s_max[2][myrow], s_max[3][myrow]));
-            const bool up = tm > m_run + KVM_LAZY_MAX;
-            const float mn = up ? tm : m_run;
-            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
-            float psum = 0.0f;
-            _Float16 ph[4];
+        // P against the current maximum; a wave with a row whose maximum moves
+        // by more than 2^KVM_LAZY_MAX says so, and then (rarely) every wave takes
+        // the row maxima from LDS and redoes its P.  Before a row's first
+        // visible key m_run is KVM_M_NONE, which every finite score moves.
+        const bool up_w = mx > m_run + KVM_LAZY_MAX;
+        float psum = 0.0f;
+        _Float16 ph[4];
+        auto make_p = [&](float mn) {
+            psum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float p = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[i] - mn);
+                const float p = __builtin_amdgcn_exp2f(s[i] - mn);
                 const _Float16 p16 = (_Float16)p;
                 ph[i] = p16;
                 psum += (float)p16;
             }
+            __builtin_memcpy(&s_p[par][myrow][16 * kq + 4 * g], ph, 8);
+        };
+        make_p(m_run);
+        const bool wave_up = __builtin_amdgcn_ballot_w64(up_w) != 0;   // any row of this wave
+        if (l == 0) s_up[par][w] = wave_up;
+        load_s(nx, Tn);
+        load_v(nx, Tn);
+        KVM_LDS_BARRIER();
+        const bool moved = *(const uint64_t *)&s_up[par][0] != 0;
+        if (moved) {
+            asm volatile("" ::: "memory");      // keep this (rare) path a branch
+            float tm = s_max[0][0][myrow];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) tm = fmaxf(tm, s_max[j >> 2][j & 3][myrow]);
+            const bool up = tm > m_run + KVM_LAZY_MAX;
+            const float mn = up ? tm : m_run;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
+            make_p(mn);
             l_run = l_run * alpha + psum;
             m_run = mn;
-            __builtin_memcpy(&s_p[myrow][16 * kq + 4 * g], ph, 8);
             if (kq == 0) {
                 if (g == 0) s_alpha[myrow] = alpha;
                 const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
                 if (l == 0) s_rescale[rq] = any;
             }
-        }
-        load_v(nx, Tn);
-        KVM_LDS_BARRIER();
-        // ---------------- phase 2: O[:, dims of wave w] += P V ----------------
+            KVM_LDS_BARRIER();
+            // ---------------- O of the rows whose maximum moved ---------------
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            if (s_rescale[rt]) {
-                float ar[4];
+            for (int rt = 0; rt < NRT; ++rt) {
+                if (s_rescale[rt]) {
+                    float ar[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
+                    for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
+                    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
+                        for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
+#pragma unroll
+                    for (int bw = 0; bw < NBW; ++bw)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) Oc[rt][bw][r] *= ar[r];
+                }
             }
+        } else {
+            l_run += psum;
         }
+        // ---------------- phase 2: O[:, dims of wave w] += P V ----------------
         kvm_f16x8 pa[2][NRT];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[16 * rt + m][32 * ks + 8 * g];
+            for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[par][16 * rt + m][32 * ks + 8 * g];
 #pragma unroll
         for (int bw = 0; bw < NBW; ++bw) {
             kvm_f16x8 pp[2][NRT];
@@ -379,7 +417,10 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
                     kvm_f16x8 dv;
                     __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
 #pragma unroll
-                    for (int rt = 0; rt < NRT; ++rt) pp[ks][rt] = pa[ks][rt] * dv;
+                    for (int rt = 0; rt < NRT; ++rt) {
+                        pp[ks][rt] = pa[ks][rt] * dv;
+                        Oc[rt][bw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], eight_den, Oc[rt][bw], 0, 0, 0);
+                    }
                 }
             }
 #pragma unroll
@@ -388,7 +429,7 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
                 if constexpr (QUANT) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const kvm_f16x8 vb = nib8_to_f16(rg.vq[nt][ks]);
+                        const kvm_f16x8 vb = nib8_to_f16den(rg.vq[nt][ks]);
 #pragma unroll
                         for (int rt = 0; rt < NRT; ++rt)
                             O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], vb, O[rt][nt], 0, 0, 0);
@@ -405,6 +446,7 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
                 }
             }
         }
+        par ^= 1;
     };
 
     // three register buffers, two tiles in flight.  The loop body is straight
@@ -433,7 +475,7 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
     const uint64_t pidx = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits + split;
     float *po = a.ws + pidx * RMAX * D;
     if (kq == 0 && g == 0 && myrow < R) {
-        a.ws_ml[(pidx * RMAX + myrow) * 2 + 0] = m_run;
+        a.ws_ml[(pidx * RMAX + myrow) * 2 + 0] = m_run == KVM_M_NONE ? -INFINITY : m_run;
         a.ws_ml[(pidx * RMAX + myrow) * 2 + 1] = s_l[0][myrow] + s_l[1][myrow] + s_l[2][myrow] + s_l[3][myrow];
     }
 #pragma unroll
@@ -443,7 +485,8 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = 16 * rt + 4 * g + r;
-                if (row < R) po[row * D + DW * w + 16 * nt + m] = O[rt][nt][r];
+                if (row < R)
+                    po[row * D + DW * w + 16 * nt + m] = QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r];
             }
 }
 

@@ -158,7 +158,7 @@ struct score_args {
 // batch (1 for <= 4 heads).
 template <int D, int UPB>
 __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile, uint32_t c,
-                                            uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[64],
+                                            uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[D + 4],
                                             float (*s_qv)[D + 4], float *s_nq, float *s_nk,
                                             float (*s_cos)[KVM_MEANK_TILE], float *dot_out) {
     constexpr uint32_t TW = KVM_MEANK_TILE, HC = 64 / TW, NBAT = D / 32;
@@ -240,28 +240,38 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
                 kh.y = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][1], inv4[1])) & keep4[1]);
                 kh.z = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][2], inv4[2])) & keep4[2]);
                 kh.w = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][3], inv4[3])) & keep4[3]);
-                *(float4 *)&s_k[32 * k + r][hu * TW + 4 * quad] = kh;
+                float *col = &s_k[hu * TW + 4 * quad][32 * k + r];
+                col[0] = kh.x;
+                col[D + 4] = kh.y;
+                col[2 * (D + 4)] = kh.z;
+                col[3 * (D + 4)] = kh.w;
             }
         }
     }
     KVM_LDS_BARRIER();
+    // (fully unrolled so the 16-byte LDS reads run well ahead of the chain)
+    const float *krow = s_k[lane];
     if (w == 0) {
-#pragma unroll 16
+#pragma unroll
         for (int d = 0; d < D; d += 4) {
             const float4 q4 = *(const float4 *)&qrow[d];
-            chain = kvm_fadd(chain, kvm_fmul(q4.x, s_k[d][lane]));
-            chain = kvm_fadd(chain, kvm_fmul(q4.y, s_k[d + 1][lane]));
-            chain = kvm_fadd(chain, kvm_fmul(q4.z, s_k[d + 2][lane]));
-            chain = kvm_fadd(chain, kvm_fmul(q4.w, s_k[d + 3][lane]));
+            const float4 k4 = *(const float4 *)&krow[d];
+            chain = kvm_fadd(chain, kvm_fmul(q4.x, k4.x));
+            chain = kvm_fadd(chain, kvm_fmul(q4.y, k4.y));
+            chain = kvm_fadd(chain, kvm_fmul(q4.z, k4.z));
+            chain = kvm_fadd(chain, kvm_fmul(q4.w, k4.w));
         }
     } else if (w == 1) {
-#pragma unroll 16
-        for (int d = 0; d < D; ++d) {
-            const float kh = s_k[d][lane];
-            chain = kvm_fadd(chain, kvm_fmul(kh, kh));
+#pragma unroll
+        for (int d = 0; d < D; d += 4) {
+            const float4 k4 = *(const float4 *)&krow[d];
+            chain = kvm_fadd(chain, kvm_fmul(k4.x, k4.x));
+            chain = kvm_fadd(chain, kvm_fmul(k4.y, k4.y));
+            chain = kvm_fadd(chain, kvm_fmul(k4.z, k4.z));
+            chain = kvm_fadd(chain, kvm_fmul(k4.w, k4.w));
         }
     } else if (w == 2) {
-#pragma unroll 16
+#pragma unroll
         for (int d = 0; d < D; d += 4) {
             const float4 q4 = *(const float4 *)&nqrow[d];
             chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
@@ -295,7 +305,7 @@ __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     if (blockIdx.x >= a.n_tiles_used || blockIdx.y >= a.n_layer) return;
     constexpr uint32_t TW = KVM_MEANK_TILE;       // blocks per tile
     constexpr uint32_t HC = 64 / TW;              // heads per chunk
-    __shared__ float s_k[D][64];                  // kh as [dim][lane]
+    __shared__ __align__(16) float s_k[64][D + 4];   // kh as [lane][dim], rows padded against bank conflicts
     __shared__ __align__(16) float s_qv[HC][D + 4];
     __shared__ float s_nq[HC];
     __shared__ float s_nk[64];
