@@ -9,19 +9,21 @@
 // f16/f16 cache Q is rounded to fp16 and Q.K is an fp16 dot with fp32
 // accumulation.
 //
-// Work split (gfx950, wave64; one workgroup per (lane, kv head, key split) with
-// 4 waves per 16 padded query rows, i.e. 4 or 8 waves):
-//   tiles:   each wave loads its own operands of a 64-cell tile straight from
-//            HBM into registers (three buffers, two tiles in flight);
-//   phase 1: wave (kq, rt) scores keys 16kq..16kq+15 of the tile against the
-//            16 rows of row tile rt with v_mfma_i32_16x16x32_i8 (one MFMA per
-//            32-dim block; the d_k*d_q products of four blocks come from one
-//            v_mfma_f32_16x16x1_4b_f32 outer product), masks by cell position
-//            and reduces the row max; maxima are exchanged in LDS;
-//   phase 2: wave w accumulates O[:, dims D/W*w ..] += P V for all rows with
-//            v_mfma_f32_16x16x32_f16; the q4_0 block scale of V is folded
-//            into P so V enters the MFMA as exact integers (nibble - 8).
-// Partial (m, l, O) of each split go to a workspace and k_fa_combine merges them.
+// Work split (gfx950, wave64; one workgroup of 8 waves per (lane, kv head,
+// key split); every wave loads its own operands of each 64-cell tile straight
+// from HBM into registers, three buffers, two tiles in flight):
+//   waves 0-3 score: wave kq takes keys 16kq..16kq+15 of the tile against all
+//     padded query rows with v_mfma_i32_16x16x32_i8 (one MFMA per 32-dim block
+//     and row tile; the d_k*d_q products of four blocks come from one
+//     v_mfma_f32_16x16x1_4b_f32 outer product), masks by cell position and
+//     writes P (fp16) of its keys to LDS, keeping the online softmax state;
+//   waves 4-7 accumulate: wave 4+dq takes O[:, dims D/4*dq ..] += P V with
+//     v_mfma_f32_16x16x32_f16; the q4_0 block scale is folded into P and V
+//     enters the MFMA as exact fp16 denormals (nibble * 2^-24).
+// One barrier per tile: the scoring waves score tile t+1 while the P V waves
+// multiply tile t, so each SIMD holds one wave of each kind in different
+// phases.  Partial (m, l, O) of each split go to a workspace and
+// k_fa_combine merges them.
 #include "kvm_internal.h"
 
 #include <cmath>
@@ -86,47 +88,50 @@ typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
 // stay below 2^KVM_LAZY_MAX, well inside fp16.
 #define KVM_LAZY_MAX 8.0f
 
-// One wave's operands of one 64-cell tile, loaded straight from HBM in MFMA
-// operand order (the window's tile layout is built for this):
-//   phase 1 (key quarter kq): K quants of keys 16kq+m (lane l = 16g+m holds
-//            dims 32b+8g..+7 of every block b), the fp16 scales of key 16kq+m
-//            for blocks 4gi+g (q8_0), positions of keys 16kq+4g..+3;
-//   phase 2 (dim slice w): q4_0 nibble words of dims DW*w+16nt+m for keys
-//            32ks+8g..+7, and the V scales of those keys for each dim block.
-template <int D, bool QUANT, int NT, int NBW>
-struct fa_tile_regs {
+// Operands of one 64-cell tile, loaded straight from HBM into registers in
+// MFMA operand order (the window's tile layout is built for this).
+// Scoring wave kq (keys 16kq..16kq+15): K quants of key 16kq+m (lane l = 16g+m
+// holds dims 32b+8g..+7 of every block b), the fp16 scales of key 16kq+m for
+// blocks 4gi+g (q8_0), positions of keys 16kq+4g..+3.
+template <int D, bool QUANT>
+struct fa_k_regs {
     static constexpr int NB = D / 32;
     kvm_u32x4 k[QUANT ? NB / 2 : NB];     // q8_0: 2 blocks per 16 B; f16: one k-step
     uint32_t dk[QUANT ? NB / 4 : 1];      // fp16 scale (low half)
     kvm_u32x4 cp;                          // 4 cell positions
+};
+// P V wave dq (dims D/4*dq ..): q4_0 nibble words of dims D/4*dq+16nt+m for
+// keys 32ks+8g..+7 and the V scales of those keys per 32-dim block, or f16 V.
+template <int D, bool QUANT, int NT, int NBW>
+struct fa_v_regs {
     kvm_u32x2 vq[QUANT ? NT : 1];          // both ks nibble words
     kvm_u32x4 vs[QUANT ? NBW : 1][2];      // V scales [block][ks]
     kvm_u32x4 vh[QUANT ? 1 : NT][2];       // f16 V [ks]
 };
 
 template <int D, int NRT, bool QUANT>
-__global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
-    constexpr int WAVES = 4 * NRT;
+__global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     constexpr int NB = D / 32;          // 32-dim blocks per row
     constexpr int NG = QUANT ? NB / 4 : 1;   // 4-block scale groups
     constexpr int RMAX = 16 * NRT;      // padded query rows
-    constexpr int DW = D / WAVES;       // output dims per wave (phase 2)
-    constexpr int NT = DW / 16;         // 16-dim output tiles per wave
-    constexpr int NBW = DW >= 32 ? DW / 32 : 1;   // V scale blocks per wave
+    constexpr int DW = D / 4;           // output dims per P V wave
+    constexpr int NT = DW / 16;         // 16-dim output tiles per P V wave
+    constexpr int NBW = DW >= 32 ? DW / 32 : 1;   // V scale blocks per P V wave
     constexpr int NTB = NT / NBW;       // output tiles per V scale block
     constexpr uint32_t KTILE = QUANT ? 64u * D + 64u * NB * 2u : 64u * D * 2u;
     constexpr uint32_t VTILE = QUANT ? D * 32u + NB * 64u * 2u : 64u * D * 2u;
-    constexpr int QT = RMAX * NB / (WAVES * 16);  // query quantisation tasks per lane
+    constexpr int NITEM = RMAX * NB;    // query quantisation items (row, block)
+    constexpr int QT = (NITEM + 127) / 128;   // items per lane group (8 waves x 16)
     constexpr int PSTR = 64 + 8;        // padded fp16 row stride of P in LDS
-    static_assert(NT >= 1 && NT % NBW == 0, "phase-2 dim split");
-    static_assert(QT >= 1 && QT * WAVES * 16 == RMAX * NB, "query task split");
-    using Regs = fa_tile_regs<D, QUANT, NT, NBW>;
+    static_assert(NT >= 1 && NT % NBW == 0, "P V dim split");
+    using KRegs = fa_k_regs<D, QUANT>;
+    using VRegs = fa_v_regs<D, QUANT, NT, NBW>;
 
     const fa_lane ln = a.lanes[blockIdx.z];
     const uint32_t h = blockIdx.y, split = blockIdx.x;
     const int tid = threadIdx.x, l = tid & 63, g = l >> 4, m = l & 15;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kq = w & 3, rq = w >> 2;  // phase 1: key quarter, row tile
+    const bool scorer = w < 4;          // waves 0-3 score (key quarter w), 4-7 do P V (dim quarter w-4)
     const int R = (int)(ln.n_tokens * a.G);
     const uint32_t tps = (ln.n_tiles + a.n_splits - 1) / a.n_splits;
     const uint32_t t_begin = split * tps;
@@ -139,355 +144,386 @@ __global__ void __launch_bounds__(256 * NRT) k_fa_decode(fa_args a) {
     __shared__ float s_max[4][4][RMAX];      // [key quarter][lane group][row]: max of 4 keys
     __shared__ float s_alpha[RMAX];
     __shared__ int32_t s_rescale[NRT];
-    __shared__ __align__(8) uint8_t s_up[2][8];   // per wave: a row's maximum moved (tile parity)
+    __shared__ __align__(4) uint8_t s_up[2][4];    // per scoring wave: a row's maximum moved (tile parity)
     __shared__ float s_l[4][RMAX];
     __shared__ __align__(16) _Float16 s_p[2][RMAX][PSTR];   // P of the tile (tile parity)
 
-    // ---- query rows (row r = token r/G, query head h*G + r%G): task (t, lane)
-    // covers dims 32b + 8q4 .. +7 of row r.  The raw rows are loaded first,
-    // unconditionally (rows past R re-read row 0, zeroed later; a bf16 row
-    // loads its 16 bytes twice), so that the tile prologue can be issued
-    // behind them and the quantisation waits for the query only.
     if (R == 0) return;                  // lane without query rows: no partials
-    const int myrow = 16 * rq + m;
-    const int32_t qp = myrow < R ? ln.q_pos[myrow / a.G] : -1;
+
+    // ---- query rows: item (row r = token r/G, query head h*G + r%G; block b),
+    // four lanes per item, 8 dims each, quantised to q8_0 per 32 dims as
+    // ggml's vec_dot path does, or rounded to fp16.  Every wave loads its items
+    // first (unconditionally: items past the rows re-read row 0 and are zeroed;
+    // a bf16 row loads its 16 bytes twice) and waits for them before any tile
+    // load is issued: behind the whole grid's tile prologue the query would
+    // arrive last.
     kvm_u32x4 qraw[QT][2];
     {
         const uint32_t esz = a.q_bf16 ? 2u : 4u;
 #pragma unroll
         for (int t = 0; t < QT; ++t) {
-            const int item = (t * WAVES + w) * 16 + m, rr = item / NB, b = item % NB;
-            const int r = rr < R ? rr : 0;
+            const int item = (t * 8 + w) * 16 + m, rr = item / NB, b = item % NB;
+            const int r = item < NITEM && rr < R ? rr : 0;
             const uint64_t e0 = ((uint64_t)(r / a.G) * a.n_head + h * a.G + r % a.G) * D + 32 * b + 8 * g;
             const uint8_t *qb = (const uint8_t *)ln.q + e0 * esz;
             qraw[t][0] = *(const kvm_u32x4 *)qb;
             qraw[t][1] = *(const kvm_u32x4 *)(qb + (esz == 4u ? 16u : 0u));
         }
     }
-    asm volatile("" ::: "memory");       // keep the query loads ahead of the tile loads
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // (the scoring waves call it behind their K prologue, the P V waves ahead
+    // of their V prologue; it ends with the barrier)
+    auto quantise_q = [&]() {
+#pragma unroll
+        for (int t = 0; t < QT; ++t) {
+            const int item = (t * 8 + w) * 16 + m, r = item / NB, b = item % NB;
+            if (item >= NITEM) continue;
+            float qx[8];
+            if (r >= R) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qx[j] = 0.0f;
+            } else if (a.q_bf16) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    qx[2 * j] = __uint_as_float(qraw[t][0][j] << 16);
+                    qx[2 * j + 1] = __uint_as_float(qraw[t][0][j] & 0xffff0000u);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    qx[j] = __uint_as_float(qraw[t][0][j]);
+                    qx[4 + j] = __uint_as_float(qraw[t][1][j]);
+                }
+            }
+            if constexpr (QUANT) {
+                float amax = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qx[j]));
+                amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                const float d = kvm_fdiv(amax, 127.0f);
+                const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+                uint32_t q01[2] = {0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    q01[j >> 2] |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(qx[j], id)) << (8 * (j & 3));
+                *(kvm_u32x2 *)&s_qq[r][32 * b + 8 * g] = kvm_u32x2{q01[0], q01[1]};
+                if (g == 0) s_dq[r][b] = kvm_h2f(kvm_f2h(d));
+            } else {
+                kvm_f16x8 hv;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) hv[j] = (_Float16)qx[j];
+                *(kvm_f16x8 *)&s_qh[r][32 * b + 8 * g] = hv;
+            }
+        }
+        if (tid < 8) s_up[tid >> 2][tid & 3] = 0;
+        KVM_LDS_BARRIER();
+    };
 
-    // ---- per-lane tile addressing (the tile index is wave-uniform)
-    const uint8_t *kbase = ln.wk + (uint64_t)h * ln.n_tiles * KTILE;
-    const uint8_t *vbase = ln.wv + (uint64_t)h * ln.n_tiles * VTILE;
-    const uint32_t k_off = QUANT ? (uint32_t)((kq * (NB / 2) * 64 + l) << 4) : (uint32_t)((kq * NB * 64 + l) << 4);
-    const uint32_t dk_off = 64u * D + (uint32_t)(((kq * NB + g) * 16 + m) << 1);
-    const uint32_t cp_off = (uint32_t)(16 * kq + 4 * g) * 4u;
-    const uint32_t vq_off = kvm_vq_word((uint32_t)(DW * w + m), (uint32_t)g, 0);
-    const uint32_t vs_off = D * 32u + (uint32_t)(((((DW * w) / 32) * 2) * 4 + g) * 8 * 2);
-    const uint32_t vh_off = kvm_vh_idx((uint32_t)(8 * g), (uint32_t)(DW * w + m)) << 1;
-    // loads of one tile in three parts (K; scales and positions; V), so that
-    // a step can spread them over its phases instead of stalling on the
-    // address queue all at once
     // tile to load for step i: past the split's last tile the loads re-read it,
     // and an empty split reads tile 0 (every window has one), so every step
     // issues the same loads and the prologue needs no branch
     auto tile_index = [&](uint32_t i) { return n_t == 0 ? 0u : t_begin + (i < n_t ? i : n_t - 1); };
-    auto load_k = [&](Regs &rg, uint32_t T) {
-        const uint8_t *kt = kbase + (uint64_t)T * KTILE;
-#pragma unroll
-        for (int p = 0; p < (QUANT ? NB / 2 : NB); ++p) rg.k[p] = *(const kvm_u32x4 *)(kt + k_off + 1024u * p);
-    };
-    auto load_s = [&](Regs &rg, uint32_t T) {
-        const uint8_t *kt = kbase + (uint64_t)T * KTILE;
-        if constexpr (QUANT) {
-#pragma unroll
-            for (int gi = 0; gi < NG; ++gi) rg.dk[gi] = *(const uint16_t *)(kt + dk_off + 128u * gi);
+    // Both roles step through the same tiles with the same barriers: one per
+    // tile, and a second one when a row's running maximum moves.  Buffers of
+    // the three-register ring: two tiles in flight.  The loop body is straight
+    // line so the compiler's wait counts see the same loads in flight on every
+    // trip; the last one or two tiles are handled after the loop.
+    auto run_tiles = [&](auto &b0, auto &b1, auto &b2, auto &&step) {
+        uint32_t it = 0;
+        for (; it + 3 <= n_t; it += 3) {
+            step(b0, b2, it + 2);
+            step(b1, b0, it + 3);
+            step(b2, b1, it + 4);
         }
-        rg.cp = *(const kvm_u32x4 *)((const uint8_t *)(ln.cell_pos + (uint64_t)T * 64) + cp_off);
-    };
-    auto load_v = [&](Regs &rg, uint32_t T) {
-        const uint8_t *vt = vbase + (uint64_t)T * VTILE;
-        if constexpr (QUANT) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) rg.vq[nt] = *(const kvm_u32x2 *)(vt + vq_off + 512u * nt);
-#pragma unroll
-            for (int bw = 0; bw < NBW; ++bw)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) rg.vs[bw][ks] = *(const kvm_u32x4 *)(vt + vs_off + 128u * bw + 64u * ks);
-        } else {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) rg.vh[nt][ks] = *(const kvm_u32x4 *)(vt + vh_off + 2048u * nt + 16u * ks);
+        if (it < n_t) {
+            step(b0, b2, it + 2);
+            if (it + 1 < n_t) step(b1, b0, it + 3);
         }
     };
-    auto load_tile = [&](Regs &rg, uint32_t i) {
-        const uint32_t T = tile_index(i);
-        load_k(rg, T);
-        load_s(rg, T);
-        load_v(rg, T);
-    };
-    Regs b0, b1, b2;
-    load_tile(b0, 0);
-    load_tile(b1, 1);
-    asm volatile("" ::: "memory");       // ... and the tile prologue ahead of the query's use
+    const uint64_t pidx = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits + split;
 
-    // ---- quantise the query rows (q8_0 per 32 dims, as ggml's vec_dot path)
-    // or round them to fp16; four lanes share a 32-dim block
+    if (scorer) {
+        // ================= scoring waves: S = K Q^T, softmax, P to LDS =====
+        const int kq = w;
+        const uint8_t *kbase = ln.wk + (uint64_t)h * ln.n_tiles * KTILE;
+        const uint32_t k_off = QUANT ? (uint32_t)((kq * (NB / 2) * 64 + l) << 4) : (uint32_t)((kq * NB * 64 + l) << 4);
+        const uint32_t dk_off = 64u * D + (uint32_t)(((kq * NB + g) * 16 + m) << 1);
+        const uint32_t cp_off = (uint32_t)(16 * kq + 4 * g) * 4u;
+        auto load_k = [&](KRegs &rg, uint32_t T) {
+            const uint8_t *kt = kbase + (uint64_t)T * KTILE;
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-        const int item = (t * WAVES + w) * 16 + m, r = item / NB, b = item % NB;
-        float qx[8];
-        if (r >= R) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qx[j] = 0.0f;
-        } else if (a.q_bf16) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qx[2 * j] = __uint_as_float(qraw[t][0][j] << 16);
-                qx[2 * j + 1] = __uint_as_float(qraw[t][0][j] & 0xffff0000u);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qx[j] = __uint_as_float(qraw[t][0][j]);
-                qx[4 + j] = __uint_as_float(qraw[t][1][j]);
-            }
-        }
-        if constexpr (QUANT) {
-            float amax = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qx[j]));
-            amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-            const float d = kvm_fdiv(amax, 127.0f);
-            const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
-            uint32_t q01[2] = {0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                q01[j >> 2] |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(qx[j], id)) << (8 * (j & 3));
-            *(kvm_u32x2 *)&s_qq[r][32 * b + 8 * g] = kvm_u32x2{q01[0], q01[1]};
-            if (g == 0) s_dq[r][b] = kvm_h2f(kvm_f2h(d));
-        } else {
-            kvm_f16x8 hv;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) hv[j] = (_Float16)qx[j];
-            *(kvm_f16x8 *)&s_qh[r][32 * b + 8 * g] = hv;
-        }
-    }
-    if (tid < 16) s_up[tid >> 3][tid & 7] = 0;   // flags of absent waves stay clear
-    KVM_LDS_BARRIER();
-    // B operands (Q^T) of this wave's row tile: lane (row m, k-group g)
-    long qop_i[QUANT ? NB : 1];
-    kvm_f16x8 qop_h[QUANT ? 1 : NB];
-    float dqo[NG];                       // scale MFMA B operand: dq of (row m, block 4gi+g)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        if constexpr (QUANT) __builtin_memcpy(&qop_i[b], &s_qq[myrow][32 * b + 8 * g], 8);
-        else qop_h[b] = *(const kvm_f16x8 *)&s_qh[myrow][32 * b + 8 * g];
-    }
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) dqo[gi] = QUANT ? s_dq[myrow][4 * gi + g] * a.scale_log2 : 0.0f;
-
-    kvm_f32x4 O[NRT][NT];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
-    // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and Oc
-    // P * dv * 8 * 2^-24 per row and 32-dim V block; O - Oc, times 2^24, is P V
-    kvm_f32x4 Oc[NRT][NBW];
-#pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int bw = 0; bw < NBW; ++bw) Oc[rt][bw] = {0.f, 0.f, 0.f, 0.f};
-    const kvm_f16x8 eight_den = {(_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f,
-                                 (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f};
-    float m_run = KVM_M_NONE, l_run = 0.0f;   // row myrow over this wave's keys
-
-    int par = 0;                         // parity of the tile: P and flag buffers
-    auto compute_tile = [&](const Regs &rg, Regs &nx, uint32_t inext) {
-        const uint32_t Tn = tile_index(inext);
-        load_k(nx, Tn);
-        // ---------------- phase 1: scores of keys 16kq + 4g + i, row myrow -----
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (QUANT) {
-            // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
-            kvm_f32x16 dd[NG];
-#pragma unroll
-            for (int gi = 0; gi < NG; ++gi)
-                dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[gi],
-                                                               kvm_f32x16{}, 0, 0, 0);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                const kvm_u32x4 kw = rg.k[b >> 1];
-                const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
-                const long av = (long)(lo32 | (hi32 << 32));
-                const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[i]);
-            }
-        } else {
-            kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < NB; ++ks) {
-                kvm_f16x8 av;
-                __builtin_memcpy(&av, &rg.k[ks], 16);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[ks], acc, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[i] = acc[i];
-        }
-        // mask; the scores are in the log2 domain (q8_0: kq_scale * log2(e) is
-        // folded into the query scales)
-        float mx = -INFINITY;                // over this lane's 4 keys
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int32_t cpos = (int32_t)rg.cp[i];
-            const bool vis = cpos >= 0 && cpos <= qp;
-            s[i] = vis ? (QUANT ? s[i] : s[i] * a.scale_log2) : -INFINITY;
-            mx = fmaxf(mx, s[i]);
-        }
-        s_max[kq][g][myrow] = mx;
-        // ---------------- softmax of the tile (lazy running maximum) ----------
-        // P against the current maximum; a wave with a row whose maximum moves
-        // by more than 2^KVM_LAZY_MAX says so, and then (rarely) every wave takes
-        // the row maxima from LDS and redoes its P.  Before a row's first
-        // visible key m_run is KVM_M_NONE, which every finite score moves.
-        const bool up_w = mx > m_run + KVM_LAZY_MAX;
-        float psum = 0.0f;
-        _Float16 ph[4];
-        auto make_p = [&](float mn) {
-            psum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float p = __builtin_amdgcn_exp2f(s[i] - mn);
-                const _Float16 p16 = (_Float16)p;
-                ph[i] = p16;
-                psum += (float)p16;
-            }
-            __builtin_memcpy(&s_p[par][myrow][16 * kq + 4 * g], ph, 8);
-        };
-        make_p(m_run);
-        const bool wave_up = __builtin_amdgcn_ballot_w64(up_w) != 0;   // any row of this wave
-        if (l == 0) s_up[par][w] = wave_up;
-        load_s(nx, Tn);
-        load_v(nx, Tn);
-        KVM_LDS_BARRIER();
-        const bool moved = *(const uint64_t *)&s_up[par][0] != 0;
-        if (moved) {
-            asm volatile("" ::: "memory");      // keep this (rare) path a branch
-            float tm = s_max[0][0][myrow];
-#pragma unroll
-            for (int j = 1; j < 16; ++j) tm = fmaxf(tm, s_max[j >> 2][j & 3][myrow]);
-            const bool up = tm > m_run + KVM_LAZY_MAX;
-            const float mn = up ? tm : m_run;
-            const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
-            make_p(mn);
-            l_run = l_run * alpha + psum;
-            m_run = mn;
-            if (kq == 0) {
-                if (g == 0) s_alpha[myrow] = alpha;
-                const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
-                if (l == 0) s_rescale[rq] = any;
-            }
-            KVM_LDS_BARRIER();
-            // ---------------- O of the rows whose maximum moved ---------------
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) {
-                if (s_rescale[rt]) {
-                    float ar[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
-#pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
-#pragma unroll
-                    for (int bw = 0; bw < NBW; ++bw)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) Oc[rt][bw][r] *= ar[r];
-                }
-            }
-        } else {
-            l_run += psum;
-        }
-        // ---------------- phase 2: O[:, dims of wave w] += P V ----------------
-        kvm_f16x8 pa[2][NRT];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[par][16 * rt + m][32 * ks + 8 * g];
-#pragma unroll
-        for (int bw = 0; bw < NBW; ++bw) {
-            kvm_f16x8 pp[2][NRT];
+            for (int p = 0; p < (QUANT ? NB / 2 : NB); ++p) rg.k[p] = *(const kvm_u32x4 *)(kt + k_off + 1024u * p);
             if constexpr (QUANT) {
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    kvm_f16x8 dv;
-                    __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
+                for (int gi = 0; gi < NG; ++gi) rg.dk[gi] = *(const uint16_t *)(kt + dk_off + 128u * gi);
+            }
+            rg.cp = *(const kvm_u32x4 *)((const uint8_t *)(ln.cell_pos + (uint64_t)T * 64) + cp_off);
+        };
+        KRegs b0, b1, b2;
+        load_k(b0, tile_index(0));
+        load_k(b1, tile_index(1));
+        quantise_q();
+
+        // B operands (Q^T) of every row tile: lane (row 16rt+m, k-group g)
+        long qop_i[QUANT ? NRT : 1][QUANT ? NB : 1];
+        kvm_f16x8 qop_h[QUANT ? 1 : NRT][QUANT ? 1 : NB];
+        float dqo[NRT][NG];                  // scale MFMA B operand: dq * kq_scale * log2(e)
+        int32_t qp[NRT];
+        float m_run[NRT], l_run[NRT];        // row 16rt+m over this lane's keys
 #pragma unroll
-                    for (int rt = 0; rt < NRT; ++rt) {
-                        pp[ks][rt] = pa[ks][rt] * dv;
-                        Oc[rt][bw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], eight_den, Oc[rt][bw], 0, 0, 0);
+        for (int rt = 0; rt < NRT; ++rt) {
+            const int row = 16 * rt + m;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if constexpr (QUANT) __builtin_memcpy(&qop_i[rt][b], &s_qq[row][32 * b + 8 * g], 8);
+                else qop_h[rt][b] = *(const kvm_f16x8 *)&s_qh[row][32 * b + 8 * g];
+            }
+#pragma unroll
+            for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
+            qp[rt] = row < R ? ln.q_pos[row / a.G] : -1;
+            m_run[rt] = KVM_M_NONE;
+            l_run[rt] = 0.0f;
+        }
+        int par = 0;                         // tile parity: P and flag buffers
+
+        auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
+            load_k(nx, tile_index(inext));
+            // ---- scores of keys 16kq + 4g + i, rows 16rt + m (log2 domain; q8_0:
+            // kq_scale * log2(e) is folded into the query scales), masked
+            float s[NRT][4];
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                if constexpr (QUANT) {
+                    // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
+                    kvm_f32x16 dd[NG];
+#pragma unroll
+                    for (int gi = 0; gi < NG; ++gi)
+                        dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[rt][gi],
+                                                                       kvm_f32x16{}, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const kvm_u32x4 kw = rg.k[b >> 1];
+                        const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
+                        const long av = (long)(lo32 | (hi32 << 32));
+                        const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[rt][i]);
+                    }
+                } else {
+                    kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < NB; ++ks) {
+                        kvm_f16x8 av;
+                        __builtin_memcpy(&av, &rg.k[ks], 16);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[rt][ks], acc, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[rt][i] = acc[i] * a.scale_log2;
+                }
+            }
+            // ---- mask; per lane maxima; P against the current maxima.  A wave
+            // with a row whose maximum moves by more than 2^KVM_LAZY_MAX says so,
+            // and then (rarely) the scoring waves take the row maxima from LDS
+            // and redo P.  Before a row's first visible key m_run is KVM_M_NONE,
+            // which every finite score moves.
+            bool up_w = false;
+            float psum[NRT];
+            auto make_p = [&](int rt, float mn) {
+                _Float16 ph[4];
+                psum[rt] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const _Float16 p16 = (_Float16)__builtin_amdgcn_exp2f(s[rt][i] - mn);
+                    ph[i] = p16;
+                    psum[rt] += (float)p16;
+                }
+                __builtin_memcpy(&s_p[par][16 * rt + m][16 * kq + 4 * g], ph, 8);
+            };
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int32_t cpos = (int32_t)rg.cp[i];
+                    if (!(cpos >= 0 && cpos <= qp[rt])) s[rt][i] = -INFINITY;
+                    mx = fmaxf(mx, s[rt][i]);
+                }
+                s_max[kq][g][16 * rt + m] = mx;
+                up_w = up_w || mx > m_run[rt] + KVM_LAZY_MAX;
+                make_p(rt, m_run[rt]);
+            }
+            const bool wave_up = __builtin_amdgcn_ballot_w64(up_w) != 0;
+            if (l == 0) s_up[par][kq] = wave_up;
+            KVM_LDS_BARRIER();
+            if (*(const uint32_t *)&s_up[par][0] != 0) {
+                asm volatile("" ::: "memory");      // keep this (rare) path a branch
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) {
+                    const int row = 16 * rt + m;
+                    float tm = s_max[0][0][row];
+#pragma unroll
+                    for (int j = 1; j < 16; ++j) tm = fmaxf(tm, s_max[j >> 2][j & 3][row]);
+                    const bool up = tm > m_run[rt] + KVM_LAZY_MAX;
+                    const float mn = up ? tm : m_run[rt];
+                    const float alpha = up ? __builtin_amdgcn_exp2f(m_run[rt] - mn) : 1.0f;
+                    make_p(rt, mn);
+                    l_run[rt] = l_run[rt] * alpha + psum[rt];
+                    m_run[rt] = mn;
+                    if (kq == 0) {
+                        if (g == 0) s_alpha[row] = alpha;
+                        const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
+                        if (l == 0) s_rescale[rt] = any;
+                    }
+                }
+                KVM_LDS_BARRIER();
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) l_run[rt] += psum[rt];
+            }
+            par ^= 1;
+        };
+        run_tiles(b0, b1, b2, score);
+
+        // ---- (m, l) of this split's rows
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+            float lr = l_run[rt];
+            lr += __shfl_xor(lr, 16, 64);
+            lr += __shfl_xor(lr, 32, 64);
+            if (g == 0) s_l[kq][16 * rt + m] = lr;
+        }
+        __syncthreads();
+        if (kq == 0 && g == 0) {
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+                const int row = 16 * rt + m;
+                if (row < R) {
+                    a.ws_ml[(pidx * RMAX + row) * 2 + 0] = m_run[rt] == KVM_M_NONE ? -INFINITY : m_run[rt];
+                    a.ws_ml[(pidx * RMAX + row) * 2 + 1] = s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row];
+                }
+            }
+        }
+    } else {
+        // ================= P V waves: O[:, dims DW*dq ..] += P V ============
+        const int dq = w - 4;
+        const uint8_t *vbase = ln.wv + (uint64_t)h * ln.n_tiles * VTILE;
+        const uint32_t vq_off = kvm_vq_word((uint32_t)(DW * dq + m), (uint32_t)g, 0);
+        const uint32_t vs_off = D * 32u + (uint32_t)(((((DW * dq) / 32) * 2) * 4 + g) * 8 * 2);
+        const uint32_t vh_off = kvm_vh_idx((uint32_t)(8 * g), (uint32_t)(DW * dq + m)) << 1;
+        auto load_v = [&](VRegs &rg, uint32_t T) {
+            const uint8_t *vt = vbase + (uint64_t)T * VTILE;
+            if constexpr (QUANT) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) rg.vq[nt] = *(const kvm_u32x2 *)(vt + vq_off + 512u * nt);
+#pragma unroll
+                for (int bw = 0; bw < NBW; ++bw)
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) rg.vs[bw][ks] = *(const kvm_u32x4 *)(vt + vs_off + 128u * bw + 64u * ks);
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) rg.vh[nt][ks] = *(const kvm_u32x4 *)(vt + vh_off + 2048u * nt + 16u * ks);
+            }
+        };
+        quantise_q();                            // V is needed a tile later than K
+        VRegs b0, b1, b2;
+        load_v(b0, tile_index(0));
+        load_v(b1, tile_index(1));
+
+        kvm_f32x4 O[NRT][NT];
+        // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and
+        // Oc P * dv * 8 * 2^-24 per row and 32-dim V block; (O - Oc) * 2^24 is P V
+        kvm_f32x4 Oc[NRT][NBW];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int bw = 0; bw < NBW; ++bw) Oc[rt][bw] = {0.f, 0.f, 0.f, 0.f};
+        }
+        const kvm_f16x8 eight_den = {(_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f,
+                                     (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f};
+        int par = 0;
+
+        auto accumulate = [&](const VRegs &rg, VRegs &nx, uint32_t inext) {
+            load_v(nx, tile_index(inext));
+            KVM_LDS_BARRIER();                   // P of this tile is in LDS
+            if (*(const uint32_t *)&s_up[par][0] != 0) {
+                asm volatile("" ::: "memory");
+                KVM_LDS_BARRIER();               // ... redone against the moved maxima
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) {
+                    if (s_rescale[rt]) {
+                        float ar[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
+#pragma unroll
+                        for (int bw = 0; bw < NBW; ++bw)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) Oc[rt][bw][r] *= ar[r];
                     }
                 }
             }
+            kvm_f16x8 pa[2][NRT];
 #pragma unroll
-            for (int ntb = 0; ntb < NTB; ++ntb) {
-                const int nt = bw * NTB + ntb;
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[par][16 * rt + m][32 * ks + 8 * g];
+#pragma unroll
+            for (int bw = 0; bw < NBW; ++bw) {
+                kvm_f16x8 pp[2][NRT];
                 if constexpr (QUANT) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const kvm_f16x8 vb = nib8_to_f16den(rg.vq[nt][ks]);
+                        kvm_f16x8 dv;
+                        __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
 #pragma unroll
-                        for (int rt = 0; rt < NRT; ++rt)
-                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], vb, O[rt][nt], 0, 0, 0);
+                        for (int rt = 0; rt < NRT; ++rt) {
+                            pp[ks][rt] = pa[ks][rt] * dv;
+                            Oc[rt][bw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], eight_den, Oc[rt][bw], 0, 0, 0);
+                        }
                     }
-                } else {
+                }
+#pragma unroll
+                for (int ntb = 0; ntb < NTB; ++ntb) {
+                    const int nt = bw * NTB + ntb;
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
                         kvm_f16x8 vb;
-                        __builtin_memcpy(&vb, &rg.vh[nt][ks], 16);
+                        if constexpr (QUANT) vb = nib8_to_f16den(rg.vq[nt][ks]);
+                        else __builtin_memcpy(&vb, &rg.vh[nt][ks], 16);
 #pragma unroll
                         for (int rt = 0; rt < NRT; ++rt)
-                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ks][rt], vb, O[rt][nt], 0, 0, 0);
+                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(QUANT ? pp[ks][rt] : pa[ks][rt], vb, O[rt][nt], 0, 0, 0);
                     }
                 }
             }
-        }
-        par ^= 1;
-    };
+            par ^= 1;
+        };
+        run_tiles(b0, b1, b2, accumulate);
 
-    // three register buffers, two tiles in flight.  The loop body is straight
-    // line so the compiler's wait counts see the same loads in flight on every
-    // trip (a conditional step would make it wait for all of them); the last
-    // one or two tiles are handled after the loop.
-    uint32_t it = 0;
-    for (; it + 3 <= n_t; it += 3) {
-        compute_tile(b0, b2, it + 2);
-        compute_tile(b1, b0, it + 3);
-        compute_tile(b2, b1, it + 4);
-    }
-    if (it < n_t) {
-        compute_tile(b0, b2, it + 2);
-        if (it + 1 < n_t) compute_tile(b1, b0, it + 3);
-    }
-
-    // ---- partial results of this split
-    {
-        float lr = l_run;
-        lr += __shfl_xor(lr, 16, 64);
-        lr += __shfl_xor(lr, 32, 64);
-        if (g == 0) s_l[kq][myrow] = lr;
-    }
-    __syncthreads();
-    const uint64_t pidx = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits + split;
-    float *po = a.ws + pidx * RMAX * D;
-    if (kq == 0 && g == 0 && myrow < R) {
-        a.ws_ml[(pidx * RMAX + myrow) * 2 + 0] = m_run == KVM_M_NONE ? -INFINITY : m_run;
-        a.ws_ml[(pidx * RMAX + myrow) * 2 + 1] = s_l[0][myrow] + s_l[1][myrow] + s_l[2][myrow] + s_l[3][myrow];
-    }
+        __syncthreads();                          // pairs with the scoring waves' (m, l) exchange
+        float *po = a.ws + pidx * RMAX * D;
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
+        for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * rt + 4 * g + r;
-                if (row < R)
-                    po[row * D + DW * w + 16 * nt + m] = QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r];
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 16 * rt + 4 * g + r;
+                    if (row < R)
+                        po[row * D + DW * dq + 16 * nt + m] =
+                            QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r];
+                }
+    }
 }
 
 // Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
@@ -561,7 +597,7 @@ static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
 
 template <int D, int NRT, bool QUANT>
 static void launch_decode(const fa_args &a, uint32_t n_lanes, hipStream_t stream) {
-    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT>), dim3(a.n_splits, a.H, n_lanes), dim3(256 * NRT), 0, stream, a);
+    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT>), dim3(a.n_splits, a.H, n_lanes), dim3(512), 0, stream, a);
 }
 
 static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
