@@ -526,10 +526,33 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     }
 }
 
+// Max / sum of a float over the wave (DPP row shifts and broadcasts; lane 63
+// holds the result, read back to every lane)
+__device__ inline float wave_max_f32(float x) {
+    const int ninf = __float_as_int(-INFINITY);
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x111, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x112, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x114, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x118, 0xf, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x142, 0xa, 0xf, false)));
+    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x143, 0xc, 0xf, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+__device__ inline float wave_sum_f32(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 // Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
 // output dim.  Every load is issued before any use (split maxima and sums one
 // per lane, the partial outputs KVM_COMBINE_BATCH splits per lane), so the
-// merge costs one memory round trip for up to that many splits.
+// merge costs one memory round trip for up to that many splits; the split
+// weights go through LDS (broadcast reads), the reductions through DPP.
 #define KVM_MAX_SPLITS 512
 #define KVM_COMBINE_BATCH 64
 template <int D>
@@ -551,23 +574,23 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     for (int j = 0; j < KVM_COMBINE_BATCH; ++j) v[j] = po[(uint64_t)(j < (int)S ? j : 0) * ostride];
     const float m_l = l < S ? ml[l * mstride] : -INFINITY;
     const float l_l = l < S ? ml[l * mstride + 1] : 0.0f;
-    float M = m_l;
-    for (uint32_t s = l + 64; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
     const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
     float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
-    if (M == -INFINITY) {                     // no visible cell for this row
+    float M = m_l;
+    for (uint32_t s = l + 64; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
+    M = wave_max_f32(M);
+    if (M == -INFINITY) {
         *out = 0.0f;
         return;
     }
     float L = 0.0f;
     for (uint32_t s = l; s < S; s += 64) {
         const float m = s == l ? m_l : ml[s * mstride];
-        const float wgt = m == -INFINITY ? 0.0f : exp2f(m - M);
+        const float wgt = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
         s_w[s] = wgt;
         L += (s == l ? l_l : ml[s * mstride + 1]) * wgt;
     }
-    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+    L = wave_sum_f32(L);
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll
