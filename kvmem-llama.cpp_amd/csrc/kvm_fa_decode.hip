@@ -526,28 +526,6 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     }
 }
 
-// Max / sum of a float over the wave (DPP row shifts and broadcasts; lane 63
-// holds the result, read back to every lane)
-__device__ inline float wave_max_f32(float x) {
-    const int ninf = __float_as_int(-INFINITY);
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x111, 0xf, 0xf, false)));
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x112, 0xf, 0xf, false)));
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x114, 0xf, 0xf, false)));
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x118, 0xf, 0xf, false)));
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x142, 0xa, 0xf, false)));
-    x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(x), 0x143, 0xc, 0xf, false)));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
-__device__ inline float wave_sum_f32(float x) {
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
-}
-
 // Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
 // output dim.  Every load is issued before any use (split maxima and sums one
 // per lane, the partial outputs KVM_COMBINE_BATCH splits per lane), so the
@@ -578,7 +556,7 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
     float M = m_l;
     for (uint32_t s = l + 64; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
-    M = wave_max_f32(M);
+    M = kvm_wave_max_f32(M);
     if (M == -INFINITY) {
         *out = 0.0f;
         return;
@@ -590,7 +568,7 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
         s_w[s] = wgt;
         L += (s == l ? l_l : ml[s * mstride + 1]) * wgt;
     }
-    L = wave_sum_f32(L);
+    L = kvm_wave_sum_f32(L);
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll

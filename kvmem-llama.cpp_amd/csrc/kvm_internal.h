@@ -169,6 +169,25 @@ __device__ inline uint32_t kvm_wave_incl_scan(uint32_t x) {
     x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
     return x;
 }
+// Max / min / sum of a float over the wave (DPP row shifts and broadcasts as in
+// kvm_wave_incl_scan; lanes without a source contribute the identity), read back
+// from lane 63 to every lane.
+#define KVM_WAVE_REDUCE_F32(NAME, OP, IDENT)                                                          \
+    __device__ inline float NAME(float x) {                                                          \
+        const int id = __float_as_int(IDENT);                                                        \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x111, 0xf, 0xf, false))); \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x112, 0xf, 0xf, false))); \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x114, 0xf, 0xf, false))); \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x118, 0xf, 0xf, false))); \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x142, 0xa, 0xf, false))); \
+        x = OP(x, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(x), 0x143, 0xc, 0xf, false))); \
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));                     \
+    }
+__device__ inline float kvm_add_f32(float a, float b) { return a + b; }
+KVM_WAVE_REDUCE_F32(kvm_wave_max_f32, fmaxf, -INFINITY)
+KVM_WAVE_REDUCE_F32(kvm_wave_min_f32, fminf, INFINITY)
+KVM_WAVE_REDUCE_F32(kvm_wave_sum_f32, kvm_add_f32, 0.0f)
+#undef KVM_WAVE_REDUCE_F32
 // IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
 // The empty asm keeps the conversion a separate instruction: fused with its
 // producer (fptrunc(x * c) -> v_fma_mix(x, c, +0)) a -0.0 result turns into +0.0.

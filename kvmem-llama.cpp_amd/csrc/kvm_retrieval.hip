@@ -355,6 +355,9 @@ struct topk_args {
 #define KVM_TOPK_THREADS 1024
 #define KVM_TOPK_SLOTS 2048       // slot-map entries held in LDS
 #define KVM_TOPK_LOAD (KVM_MAX_TOPK_BLOCKS / KVM_TOPK_THREADS)
+#define KVM_TOPK_FINE 1024        // linear bins of the one-pass select (64 coarse bins of 16)
+#define KVM_TOPK_GATHER 64        // largest threshold bin ranked exactly
+static_assert(KVM_TOPK_GATHER * KVM_TOPK_GATHER % KVM_TOPK_THREADS == 0 && KVM_TOPK_FINE <= KVM_TOPK_THREADS, "top-k select");
 
 // order-preserving map of a double to uint64 (-0.0 folded onto +0.0, so the
 // two compare equal as in the reference's `sa != sb` test)
@@ -415,6 +418,12 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     __shared__ uint64_t s_prefix;
     __shared__ uint32_t s_sblk[KVM_TOPK_SLOTS];
     __shared__ int32_t s_sbase[KVM_TOPK_SLOTS];
+    __shared__ uint32_t s_fine[KVM_TOPK_FINE], s_coarse[KVM_TOPK_FINE / 16];
+    __shared__ float s_wmm[2][KVM_TOPK_THREADS / 64];
+    __shared__ uint32_t s_wc[KVM_TOPK_THREADS / 64];
+    __shared__ uint32_t s_sel[4];
+    __shared__ __align__(16) kvm_u32x4 s_gath[KVM_TOPK_GATHER];
+    __shared__ uint32_t s_rank[KVM_TOPK_GATHER];
     const uint32_t tid = threadIdx.x, lane = tid & 63, n = a.n;
     const bool all = a.budget == 0 || n <= a.budget;
     // the window's slot map for the ranks the stage plan compares (loaded with
@@ -428,6 +437,8 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     // ---- phase A: scores, keys, token counts (all loads first)
     const uint32_t kpt = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
     double sv[KVM_TOPK_LOAD];
+    uint64_t kr[KVM_TOPK_LOAD];          // keys of blocks tid + 1024 k (kept for the select)
+    float sf[KVM_TOPK_LOAD];             // their scores rounded to fp32
     uint32_t nt[KVM_TOPK_LOAD];
     uint32_t pr[KVM_TOPK_LOAD];
     const uint32_t qc0 = a.layer_score ? a.q_count[0] : 0u;
@@ -441,6 +452,10 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
         }
     }
     if (tid < 256) s_hist[0][tid] = 0;
+    if (tid < KVM_TOPK_FINE) s_fine[tid] = 0;
+    if (tid < KVM_TOPK_FINE / 16) s_coarse[tid] = 0;
+    if (tid < KVM_TOPK_GATHER) s_rank[tid] = 0;
+    if (tid == 0) s_sel[3] = 0;
 #pragma unroll
     for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
         const uint32_t i = tid + k * KVM_TOPK_THREADS;
@@ -457,7 +472,9 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
                 if (!pr[k]) sc = 0.0;
                 a.scores_out[i] = sc;
             }
-            s_key[i] = ord_key(sc);
+            kr[k] = ord_key(sc);
+            sf[k] = (float)sc;
+            s_key[i] = kr[k];
             s_ntok[i] = nt[k];
             s_kept[i] = all ? 1 : 0;
         }
@@ -486,7 +503,126 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
         }
         KVM_LDS_BARRIER();
         const uint32_t count = s_count;
+        bool fallback = count < a.budget;
         if (count < a.budget) {
+            // ---- one pass over a linear histogram of the fp32 scores.  Rounding
+            // to fp32 and the bin map are monotonic, so a key in a higher bin is
+            // larger; only the bin holding the need-th key is ranked exactly (by
+            // 64-bit key, then id).  A crowded bin, or scores that are not finite,
+            // fall back to the radix select below.
+            constexpr uint32_t NW = KVM_TOPK_THREADS / 64;
+            const uint32_t wid = tid >> 6;
+            uint32_t cand = 0;
+            float fmn = INFINITY, fmx = -INFINITY;
+            uint32_t c = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
+                const uint32_t i = tid + k * KVM_TOPK_THREADS;
+                if (k < kpt && i < n && !s_kept[i]) {
+                    cand |= 1u << k;
+                    fmn = fminf(fmn, sf[k]);
+                    fmx = sf[k] != sf[k] ? INFINITY : fmaxf(fmx, sf[k]);   // a NaN score: fall back
+                    ++c;
+                }
+            }
+            fmn = kvm_wave_min_f32(fmn);
+            fmx = kvm_wave_max_f32(fmx);
+            c = __builtin_amdgcn_readlane(kvm_wave_incl_scan(c), 63);
+            if (lane == 0) {
+                s_wmm[0][wid] = fmn;
+                s_wmm[1][wid] = fmx;
+                s_wc[wid] = c;
+            }
+            KVM_LDS_BARRIER();
+            const float mn = kvm_wave_min_f32(lane < NW ? s_wmm[0][lane] : INFINITY);
+            const float mx = kvm_wave_max_f32(lane < NW ? s_wmm[1][lane] : -INFINITY);
+            const uint32_t ncand = __builtin_amdgcn_readlane(kvm_wave_incl_scan(lane < NW ? s_wc[lane] : 0u), 63);
+            const uint32_t need = a.budget - count < ncand ? a.budget - count : ncand;
+            const bool finite = mn >= -3.0e38f && mx <= 3.0e38f;
+            if (need == ncand || finite) {
+                const float sc = mx > mn ? (float)KVM_TOPK_FINE / (mx - mn) : 0.0f;
+                auto bin_of = [&](float f) {
+                    const float b = (f - mn) * sc;
+                    return b >= (float)(KVM_TOPK_FINE - 1) ? KVM_TOPK_FINE - 1 : (b > 0.0f ? (uint32_t)b : 0u);
+                };
+                uint32_t T = 0, above = 0, cnt = ncand;
+                if (need < ncand) {
+#pragma unroll
+                    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k)
+                        if (cand >> k & 1u) {
+                            const uint32_t b = bin_of(sf[k]);
+                            atomicAdd(&s_fine[b], 1u);
+                            atomicAdd(&s_coarse[b >> 4], 1u);
+                        }
+                    KVM_LDS_BARRIER();
+                    if (tid < 64) {
+                        // coarse bin 63 - lane (descending), then the 16 fine bins of
+                        // the one holding the need-th key
+                        const uint32_t cc = s_coarse[63 - lane];
+                        const uint32_t ci = kvm_wave_incl_scan(cc);
+                        const uint64_t h1 = __builtin_amdgcn_ballot_w64(ci - cc < need && need <= ci);
+                        const uint32_t l1 = (uint32_t)__builtin_ctzll(h1);
+                        const uint32_t cb = 63u - l1, above_c = __builtin_amdgcn_readlane(ci - cc, l1);
+                        const uint32_t cf = lane < 16 ? s_fine[cb * 16 + 15 - lane] : 0u;
+                        const uint32_t fi = above_c + kvm_wave_incl_scan(cf);
+                        const uint64_t h2 = __builtin_amdgcn_ballot_w64(fi - cf < need && need <= fi);
+                        const uint32_t l2 = (uint32_t)__builtin_ctzll(h2);
+                        if (lane == l2) {
+                            s_sel[0] = cb * 16 + 15 - lane;
+                            s_sel[1] = fi - cf;
+                            s_sel[2] = cf;
+                        }
+                    }
+                    KVM_LDS_BARRIER();
+                    T = s_sel[0];
+                    above = s_sel[1];
+                    cnt = s_sel[2];
+                }
+                const uint32_t kk = need - above;      // keys still to take, from bin T
+                if (kk == cnt || cnt <= KVM_TOPK_GATHER) {
+                    fallback = false;
+                    // keys above bin T are taken, and bin T whole when kk == cnt;
+                    // otherwise its keys are gathered and ranked
+#pragma unroll
+                    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k)
+                        if (cand >> k & 1u) {
+                            const uint32_t i = tid + k * KVM_TOPK_THREADS, b = need == ncand ? 0u : bin_of(sf[k]);
+                            if (need == ncand || b > T || (b == T && kk == cnt)) {
+                                s_kept[i] = 2;
+                            } else if (b == T) {
+                                const uint32_t slot = atomicAdd(&s_sel[3], 1u);
+                                s_gath[slot] = kvm_u32x4{(uint32_t)kr[k], (uint32_t)(kr[k] >> 32), i, 0u};
+                            }
+                        }
+                    if (kk != cnt) {
+                        KVM_LDS_BARRIER();
+                        // rank of entry j among the cnt gathered: keys larger, or equal
+                        // with a larger id; thread (part, j) counts 4 of them
+                        const uint32_t j = tid & (KVM_TOPK_GATHER - 1), part = tid / KVM_TOPK_GATHER;
+                        constexpr uint32_t PER = KVM_TOPK_GATHER * KVM_TOPK_GATHER / KVM_TOPK_THREADS;
+                        if (j < cnt) {
+                            const kvm_u32x4 e = s_gath[j];
+                            const uint64_t kj = (uint64_t)e[0] | ((uint64_t)e[1] << 32);
+                            uint32_t r = 0;
+#pragma unroll
+                            for (uint32_t q = 0; q < PER; ++q) {
+                                const uint32_t o = part * PER + q;
+                                if (o < cnt) {
+                                    const kvm_u32x4 x = s_gath[o];
+                                    const uint64_t ko = (uint64_t)x[0] | ((uint64_t)x[1] << 32);
+                                    r += ko > kj || (ko == kj && x[2] > e[2]);
+                                }
+                            }
+                            if (r) atomicAdd(&s_rank[j], r);
+                        }
+                        KVM_LDS_BARRIER();
+                        if (tid < cnt && s_rank[tid] < kk) s_kept[s_gath[tid][2]] = 2;
+                    }
+                    KVM_LDS_BARRIER();
+                }
+            }
+        }
+        if (fallback) {
             // radix passes: histogram into buffer p&1 -> barrier -> wave 0 picks
             // the bin and clears the other buffer -> barrier
             uint64_t mask = 0;

@@ -156,13 +156,29 @@ def test_select_topk_reference_kats(kvm_state, kat):
     assert list(res["ids"]) == want
 
 
+def _scores(rng, trial, n):
+    """Score sets for the selection: integers (long ties: the radix select),
+    normals (the one-pass histogram, threshold bin ranked exactly), normals
+    rounded to 2 decimals (equal keys inside the ranked bin: ties by id) and
+    normals with infinities (not finite: the radix select)."""
+    kind = trial % 4
+    if kind == 0:
+        return rng.integers(-3, 4, n).astype(np.float64)
+    s = rng.standard_normal(n)
+    if kind == 2:
+        s = np.round(s, 2)
+    if kind == 3:
+        s[rng.choice(n, min(n, 3), replace=False)] = [np.inf, -np.inf, np.inf][:min(n, 3)]
+    return s
+
+
 def test_select_topk_random_vs_oracle(kvm_state):
     rng = np.random.default_rng(3)
-    for trial in range(40):
+    for trial in range(60):
         n = int(rng.integers(1, 8192))
         budget = int(rng.integers(0, min(n + 3, 600)))
         sink, recent = int(rng.integers(0, 4)), int(rng.integers(0, 4))
-        s = rng.integers(-3, 4, n).astype(np.float64) if trial % 2 else rng.standard_normal(n)
+        s = _scores(rng, trial, n)
         mand = rng.integers(0, n, int(rng.integers(0, 6))).astype(np.int32)
         nt = np.full(n, 128, np.int32)
         res = api.select_topk(kvm_state, dev(s), dev(nt), budget, sink, recent,
