@@ -124,13 +124,14 @@ struct stage_args {
 };
 
 
+#define KVM_STAGEIN_WGS 256       // one per CU of an MI355X (the rows buffer takes most of the LDS)
+
+// One workgroup per CU walks the (plan entry, 64-token tile) items, so an
+// empty plan (the steady state) costs one short launch; the plan length is
+// only known on the device (info[2]).
 template <int D>
-__global__ void __launch_bounds__(256) k_stagein(stage_args a) {
-    extern __shared__ __align__(16) uint8_t s_rows[];
+__device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt) {
     constexpr uint32_t NB = D / 32;
-    const uint32_t tps = a.bt / 64;
-    const uint32_t si = blockIdx.x / tps, tt = blockIdx.x % tps;
-    if (si >= a.info[2] || a.info[3] != 0) return;
     const uint32_t slot = a.stage_slots[si];
     const uint32_t id = a.ids[slot];
     const int32_t base = a.to_base[slot];
@@ -210,6 +211,17 @@ __global__ void __launch_bounds__(256) k_stagein(stage_args a) {
     }
 }
 
+template <int D>
+__global__ void __launch_bounds__(256) k_stagein(stage_args a) {
+    extern __shared__ __align__(16) uint8_t s_rows[];
+    const uint32_t tps = a.bt / 64;
+    const uint32_t n_items = a.info[3] != 0 ? 0u : a.info[2] * tps;
+    for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+        stagein_item<D>(a, s_rows, item / tps, item % tps);
+        __syncthreads();                 // LDS rows of this item read before the next overwrites them
+    }
+}
+
 
 static int rope_ctx_for(kvm_state *st, const float *theta, uint32_t n_half, int32_t nrot,
                         uint32_t max_pos, rope_ctx *rc) {
@@ -275,7 +287,8 @@ extern "C" int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const 
     a.stage_slots = sel->stage_slots;
     a.info = sel->info;
     const uint32_t max_slots = sel->cap < a.n_slots ? sel->cap : a.n_slots;
-    const dim3 grid(max_slots * (w->block_tokens / 64));
+    const uint32_t max_items = max_slots * (w->block_tokens / 64);
+    const dim3 grid(max_items < KVM_STAGEIN_WGS ? max_items : KVM_STAGEIN_WGS);
     if (w->head_dim == 256) {
         KVM_HIP(st, hipFuncSetAttribute((const void *)k_stagein<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(k_stagein<256>, grid, dim3(256), lds, st->stream, a);
