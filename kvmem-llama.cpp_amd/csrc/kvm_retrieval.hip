@@ -249,36 +249,59 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
         }
     }
     KVM_LDS_BARRIER();
-    // (fully unrolled so the 16-byte LDS reads run well ahead of the chain)
+    // Each chain reads 32 dims ahead (16-byte LDS reads into a second register
+    // buffer, kept ahead of the arithmetic by a scheduling barrier), so the
+    // dependent adds never wait on LDS.
     const float *krow = s_k[lane];
+    constexpr int CH = 8;                // float4 per 32-dim chunk
+    auto chain_over = [&](auto &&ld, auto &&step) {
+        float4 buf[2][2][CH];
+        ld(buf[0], 0);
+#pragma unroll
+        for (int c = 0; c < D / (4 * CH); ++c) {
+            if (c + 1 < D / (4 * CH)) ld(buf[(c + 1) & 1], c + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < CH; ++j) step(buf[c & 1][0][j], buf[c & 1][1][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     if (w == 0) {
+        chain_over([&](float4 (&b)[2][CH], int c) {
 #pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const float4 q4 = *(const float4 *)&qrow[d];
-            const float4 k4 = *(const float4 *)&krow[d];
-            chain = kvm_fadd(chain, kvm_fmul(q4.x, k4.x));
-            chain = kvm_fadd(chain, kvm_fmul(q4.y, k4.y));
-            chain = kvm_fadd(chain, kvm_fmul(q4.z, k4.z));
-            chain = kvm_fadd(chain, kvm_fmul(q4.w, k4.w));
-        }
+                       for (int j = 0; j < CH; ++j) {
+                           b[0][j] = *(const float4 *)&qrow[4 * (CH * c + j)];
+                           b[1][j] = *(const float4 *)&krow[4 * (CH * c + j)];
+                       }
+                   },
+                   [&](const float4 &q4, const float4 &k4) {
+                       chain = kvm_fadd(chain, kvm_fmul(q4.x, k4.x));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.y, k4.y));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.z, k4.z));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.w, k4.w));
+                   });
     } else if (w == 1) {
+        chain_over([&](float4 (&b)[2][CH], int c) {
 #pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const float4 k4 = *(const float4 *)&krow[d];
-            chain = kvm_fadd(chain, kvm_fmul(k4.x, k4.x));
-            chain = kvm_fadd(chain, kvm_fmul(k4.y, k4.y));
-            chain = kvm_fadd(chain, kvm_fmul(k4.z, k4.z));
-            chain = kvm_fadd(chain, kvm_fmul(k4.w, k4.w));
-        }
+                       for (int j = 0; j < CH; ++j) b[1][j] = *(const float4 *)&krow[4 * (CH * c + j)];
+                   },
+                   [&](const float4 &, const float4 &k4) {
+                       chain = kvm_fadd(chain, kvm_fmul(k4.x, k4.x));
+                       chain = kvm_fadd(chain, kvm_fmul(k4.y, k4.y));
+                       chain = kvm_fadd(chain, kvm_fmul(k4.z, k4.z));
+                       chain = kvm_fadd(chain, kvm_fmul(k4.w, k4.w));
+                   });
     } else if (w == 2) {
+        chain_over([&](float4 (&b)[2][CH], int c) {
 #pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const float4 q4 = *(const float4 *)&nqrow[d];
-            chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
-            chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
-            chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
-            chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
-        }
+                       for (int j = 0; j < CH; ++j) b[0][j] = *(const float4 *)&nqrow[4 * (CH * c + j)];
+                   },
+                   [&](const float4 &q4, const float4 &) {
+                       chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
+                       chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
+                   });
     }
     if (w == 1) s_nk[lane] = chain;
     if (w == 2 && lane < nh) s_nq[lane] = chain;
