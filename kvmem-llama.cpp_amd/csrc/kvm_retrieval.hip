@@ -165,17 +165,19 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t HD = a.H * D;
-    // ---- all loads first: query gathers, token counts, slab batches
-    float qg[2][8][D / 64];
+    // ---- all loads first: query gathers, token counts, slab batches.  Query
+    // item u = tid + 256x is (head u / (D/4), dims 4(u % (D/4)) .. +3); its
+    // group's rows come in 16 bytes at a time.
+    constexpr uint32_t NQI = (HC * (D / 4) + 255) / 256;
+    kvm_f32x4 qg[NQI][8];
 #pragma unroll
-    for (int hs = 0; hs < 2; ++hs) {
-        const uint32_t hl = w + 4 * hs, h = c * HC + (hl < nh ? hl : 0u);
+    for (uint32_t x = 0; x < NQI; ++x) {
+        const uint32_t u = tid + 256u * x, hl = u / (D / 4), d4 = u % (D / 4);
+        const uint32_t h = c * HC + (hl < nh ? hl : 0u);
 #pragma unroll
         for (int gi = 0; gi < 8; ++gi) {
             const uint32_t gc = (uint32_t)gi < g ? (uint32_t)gi : 0u;
-#pragma unroll
-            for (int j = 0; j < D / 64; ++j)
-                qg[hs][gi][j] = a.q_sum[((uint64_t)il * a.n_head + h * g + gc) * D + lane + 64 * j];
+            qg[x][gi] = *(const kvm_f32x4 *)&a.q_sum[((uint64_t)il * a.n_head + h * g + gc) * D + 4 * d4];
         }
     }
     const uint32_t quad = tid % (TW / 4);
@@ -197,22 +199,22 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
             kv[k][x] = __builtin_nontemporal_load(slab + row * (TW / 4) + quad);
         }
     if (qc == 0) return;                 // layer without queries: skipped by the reduction
-    // ---- qv of heads w, w + 4 (the group's q rows summed in order, scaled)
+    // ---- qv of the chunk's heads (the group's q rows summed in order, scaled)
     const float invq = kvm_fdiv(1.0f, (float)(qc * (g > 1u ? g : 1u)));
 #pragma unroll
-    for (int hs = 0; hs < 2; ++hs) {
-        const uint32_t hl = w + 4 * hs;
+    for (uint32_t x = 0; x < NQI; ++x) {
+        const uint32_t u = tid + 256u * x, hl = u / (D / 4), d4 = u % (D / 4);
         if (hl < nh) {
             const uint32_t h = c * HC + hl;
 #pragma unroll
-            for (int j = 0; j < D / 64; ++j) {
+            for (int e = 0; e < 4; ++e) {
                 float qh = 0.0f;
 #pragma unroll
                 for (int gi = 0; gi < 8; ++gi)
-                    if ((uint32_t)gi < g) qh = kvm_fadd(qh, qg[hs][gi][j]);
+                    if ((uint32_t)gi < g) qh = kvm_fadd(qh, qg[x][gi][e]);
                 for (uint32_t g0 = 8; g0 < g; ++g0)              // groups above 8 (rare)
-                    qh = kvm_fadd(qh, a.q_sum[((uint64_t)il * a.n_head + h * g + g0) * D + lane + 64 * j]);
-                s_qv[hl][lane + 64 * j] = kvm_fmul(qh, invq);
+                    qh = kvm_fadd(qh, a.q_sum[((uint64_t)il * a.n_head + h * g + g0) * D + 4 * d4 + e]);
+                s_qv[hl][4 * d4 + e] = kvm_fmul(qh, invq);
             }
         }
     }
