@@ -199,8 +199,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
                 float amax = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qx[j]));
-                amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-                amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+                amax = kvm_max_xor32(kvm_max_xor16(amax));
                 const float d = kvm_fdiv(amax, 127.0f);
                 const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
                 uint32_t q01[2] = {0u, 0u};
@@ -391,8 +390,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             float lr = l_run[rt];
-            lr += __shfl_xor(lr, 16, 64);
-            lr += __shfl_xor(lr, 32, 64);
+            lr = kvm_add_xor32(kvm_add_xor16(lr));
             if (g == 0) s_l[kq][16 * rt + m] = lr;
         }
         __syncthreads();

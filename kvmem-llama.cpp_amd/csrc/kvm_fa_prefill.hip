@@ -375,8 +375,7 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) x = fmaxf(x, S[s][rt][r]);
-            x = fmaxf(x, __shfl_xor(x, 16, 64));
-            x = fmaxf(x, __shfl_xor(x, 32, 64));
+            x = kvm_max_xor32(kvm_max_xor16(x));
             tmax[rt] = x;
             up[rt] = fmaf(x, c, -ms[rt]) > KVM_PF_LAZY;   // false for a row with nothing visible yet
             any = any || up[rt];
@@ -427,8 +426,7 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         float lr = lp[rt];
-        lr += __shfl_xor(lr, 16, 64);
-        lr += __shfl_xor(lr, 32, 64);
+        lr = kvm_add_xor32(kvm_add_xor16(lr));
         const uint32_t row = rows[rt];
         if (row >= a.n_rows) continue;
         if (a.n_splits == 1) {

@@ -188,6 +188,25 @@ KVM_WAVE_REDUCE_F32(kvm_wave_max_f32, fmaxf, -INFINITY)
 KVM_WAVE_REDUCE_F32(kvm_wave_min_f32, fminf, INFINITY)
 KVM_WAVE_REDUCE_F32(kvm_wave_sum_f32, kvm_add_f32, 0.0f)
 #undef KVM_WAVE_REDUCE_F32
+// Max / sum with lane l ^ 16 or l ^ 32 without LDS: v_permlane16_swap /
+// v_permlane32_swap with both operands x hand each lane the pair {x[l],
+// x[l ^ 16 or 32]} (order unspecified; max and + do not care).
+__device__ inline float kvm_max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float kvm_max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float kvm_add_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float kvm_add_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 // IEEE round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
 // The empty asm keeps the conversion a separate instruction: fused with its
 // producer (fptrunc(x * c) -> v_fma_mix(x, c, +0)) a -0.0 result turns into +0.0.
