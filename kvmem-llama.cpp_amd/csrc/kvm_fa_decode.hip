@@ -170,6 +170,13 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             qraw[t][1] = *(const kvm_u32x4 *)(qb + (esz == 4u ? 16u : 0u));
         }
     }
+    // positions of the rows a scoring lane holds (row 16rt + m), with the query
+    int32_t qpos_raw[NRT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+        const int row = 16 * rt + m;
+        qpos_raw[rt] = ln.q_pos[(row < R ? row : 0) / a.G];
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // (the scoring waves call it behind their K prologue, the P V waves ahead
     // of their V prologue; it ends with the barrier)
@@ -280,7 +287,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             }
 #pragma unroll
             for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
-            qp[rt] = row < R ? ln.q_pos[row / a.G] : -1;
+            qp[rt] = row < R ? qpos_raw[rt] : -1;
             m_run[rt] = KVM_M_NONE;
             l_run[rt] = 0.0f;
         }
