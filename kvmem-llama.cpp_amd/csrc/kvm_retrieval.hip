@@ -433,7 +433,7 @@ struct topk_lanes {
 };
 
 __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
-    const topk_args &a = tl.lane[blockIdx.x];
+    const topk_args a = tl.lane[blockIdx.x];     // one copy out of the argument segment
     __shared__ uint64_t s_key[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint32_t s_ntok[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
@@ -455,25 +455,46 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     // the scores, so the compaction needs no second memory round trip)
     const uint32_t n_sl = a.slot_block ? (a.n_slots < a.cap ? a.n_slots : a.cap) : 0u;
     const uint32_t n_sl_lds = n_sl < KVM_TOPK_SLOTS ? n_sl : KVM_TOPK_SLOTS;
-    for (uint32_t i = tid; i < n_sl_lds; i += KVM_TOPK_THREADS) {
-        s_sblk[i] = a.slot_block[i];
-        s_sbase[i] = a.slot_base[i];
+    // ---- phase A: every load issued before any use and none under a branch
+    // (the compiler waits for all loads in flight at a branch's join): indices
+    // are clamped, and absent inputs read a stand-in whose values are unused
+    constexpr uint32_t SLT = KVM_TOPK_SLOTS / KVM_TOPK_THREADS;
+    const uint32_t *sbp = a.slot_block ? a.slot_block : a.n_tokens;
+    const int32_t *sbb = a.slot_base ? a.slot_base : (const int32_t *)a.n_tokens;
+    const uint32_t nsl1 = n_sl_lds ? n_sl_lds - 1 : 0u, n1 = n ? n - 1 : 0u;
+    uint32_t sl_blk[SLT];
+    int32_t sl_base[SLT];
+#pragma unroll
+    for (uint32_t j = 0; j < SLT; ++j) {
+        const uint32_t i = tid + j * KVM_TOPK_THREADS;
+        sl_blk[j] = sbp[i < nsl1 ? i : nsl1];
+        sl_base[j] = sbb[i < nsl1 ? i : nsl1];
     }
-    // ---- phase A: scores, keys, token counts (all loads first)
     const uint32_t kpt = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
+    const bool have_ls = a.layer_score != nullptr, have_pr = have_ls && a.present != nullptr;
+    const double *scp = have_ls ? a.layer_score : a.scores_in;
+    const uint8_t *prp = have_pr ? a.present : (const uint8_t *)a.n_tokens;
     double sv[KVM_TOPK_LOAD];
     uint64_t kr[KVM_TOPK_LOAD];          // keys of blocks tid + 1024 k (kept for the select)
     float sf[KVM_TOPK_LOAD];             // their scores rounded to fp32
     uint32_t nt[KVM_TOPK_LOAD];
     uint32_t pr[KVM_TOPK_LOAD];
-    const uint32_t qc0 = a.layer_score ? a.q_count[0] : 0u;
+    const uint32_t qc0 = have_ls ? a.q_count[0] : 0u;
 #pragma unroll
     for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
-        if (k < kpt) {
-            const uint32_t i = tid + k * KVM_TOPK_THREADS, ic = i < n ? i : n - 1;
-            sv[k] = a.layer_score ? a.layer_score[ic] : a.scores_in[ic];
-            nt[k] = a.n_tokens[ic];
-            pr[k] = a.layer_score && a.present ? a.present[ic] : 1u;
+        const uint32_t i = tid + k * KVM_TOPK_THREADS, ic = i < n1 ? i : n1;
+        sv[k] = scp[ic];
+        nt[k] = a.n_tokens[ic];
+        pr[k] = prp[ic];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) pr[k] = have_pr ? pr[k] : 1u;
+#pragma unroll
+    for (uint32_t j = 0; j < SLT; ++j) {
+        const uint32_t i = tid + j * KVM_TOPK_THREADS;
+        if (i < n_sl_lds) {
+            s_sblk[i] = sl_blk[j];
+            s_sbase[i] = sl_base[j];
         }
     }
     if (tid < 256) s_hist[0][tid] = 0;
