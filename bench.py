@@ -418,8 +418,8 @@ def run_lanes(args, st, api, L, torch, np):
     """Four conversations, each with its own 32K-cell window, mean-K index and
     pinned host history (64K / 128K / 192K / 256K tokens), one bf16 query token
     each: retrieval for all lanes in one launch sequence (scoring grid over every
-    lane's blocks + one top-k workgroup per lane), stage-in per lane, attention
-    for all lanes in one launch."""
+    lane's blocks + one top-k workgroup per lane), stage-in of every lane's plan
+    in one launch, attention for all lanes in one launch."""
     n_rep = 2
     wls = []
     for i, ht in enumerate(LANE_HIST):
@@ -433,16 +433,15 @@ def run_lanes(args, st, api, L, torch, np):
                       n_tokens=wl["n_tokens"], budget_blocks=RETRIEVED // BT, sink_blocks=1,
                       window=wl["reps"][r][1], sel=wl["reps"][r][2]) for wl in wls]
         preps.append((api.prepare_score_topk_lanes(st, lanes),
-                      [api.prepare_stagein(st, wl["hist"], wl["reps"][r][1], wl["reps"][r][2], N_ROT, FREQ_BASE)
-                       for wl in wls],
+                      api.prepare_stagein_lanes(st, [(wl["hist"], wl["reps"][r][1], wl["reps"][r][2]) for wl in wls],
+                                                N_ROT, FREQ_BASE),
                       api.prepare_fa_decode_lanes(st, [wl["reps"][r][1] for wl in wls], [wl["q"] for wl in wls],
                                                   [wl["q_pos"] for wl in wls], N_HEAD, scale, outs)))
 
     def step(i):
-        score, stageins, fa = preps[i % n_rep]
+        score, stagein, fa = preps[i % n_rep]
         score()
-        for si in stageins:
-            si()
+        stagein()
         fa()
 
     ms, fa_ms = time_steps(torch, step, lambda i: preps[i % n_rep][2](), args.steps, args.warmup)
@@ -477,7 +476,7 @@ def run_lanes(args, st, api, L, torch, np):
         "data": "synthetic N(0,1), seeds 0xC0FFEE05 + lane, 16 planted blocks per lane",
         "config": {"workload": "4 lanes: histories of 65536/131072/196608/262144 tokens (pinned host q8_0 K / "
                                "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; score + top-k for all "
-                               "lanes in one launch sequence, stage-in per lane, FA decode for all lanes in one "
+                               "lanes in one launch sequence, stage-in of all lanes in one launch, FA decode for all lanes in one "
                                "launch; 24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
                    "lanes": len(wls), "step_bytes": step_bytes},
         "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),

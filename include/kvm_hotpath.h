@@ -264,6 +264,19 @@ typedef struct kvm_history {
 int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
                           const kvm_selection *sel, const kvm_rope_params *rope);
 
+/* Several lanes' stage-in plans in one launch (multi-lane decode,
+ * docs/multi-lane-conversations.md:1-20): the reference queues every lane's
+ * write_block_to_gpu items and kvmem_stagein_flush runs them as one fused launch
+ * (llama-kvmem-stagein.cu:669-790).  At most 8 lanes; all windows share head_dim;
+ * each lane is staged exactly as kvm_stagein_selection would stage it. */
+typedef struct kvm_stagein_lane {
+    const kvm_history *h;
+    const kvm_window *w;
+    const kvm_selection *sel;
+} kvm_stagein_lane;
+int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
+                                const kvm_rope_params *rope);
+
 /* Item-at-a-time form with the reference's arguments
  * (src/adapter/llama-kvmem-stagein.h:36-46).  `dst` is (window, first cell)
  * instead of a raw cache pointer; packed rows are copied into the state's

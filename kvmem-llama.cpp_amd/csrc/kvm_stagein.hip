@@ -211,9 +211,18 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     }
 }
 
+// Every lane's plan in one launch (blockIdx.y = lane): the lanes' windows,
+// histories and plans are independent, so the workgroups of one lane never touch
+// another lane's memory.
+#define KVM_STAGEIN_LANES 8
+struct stage_lanes {
+    stage_args lane[KVM_STAGEIN_LANES];
+};
+
 template <int D>
-__global__ void __launch_bounds__(256) k_stagein(stage_args a) {
+__global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     extern __shared__ __align__(16) uint8_t s_rows[];
+    const stage_args &a = sl.lane[blockIdx.y];
     const uint32_t tps = a.bt / 64;
     const uint32_t n_items = a.info[3] != 0 ? 0u : a.info[2] * tps;
     for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
@@ -248,9 +257,10 @@ static bool hadamard_ok(int nrot, uint32_t D) {
     return nrot == 0 || (nrot >= 64 && nrot <= (int)D && !(nrot & (nrot - 1)) && D % nrot == 0);
 }
 
-extern "C" int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
-                                     const kvm_selection *sel, const kvm_rope_params *rope) {
-    if (!st || !h || !w || !sel || !rope) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
+// Checks one lane and fills its kernel arguments (all but the RoPE context).
+static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window *w,
+                           const kvm_selection *sel, stage_args *a, uint32_t *max_items) {
+    if (!h || !w || !sel) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
     int rc = kvm_window_check(w);
     if (rc) return kvm_fail(st, rc, "stagein: bad window");
     if (w->k_type != KVM_TYPE_Q8_0) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: re-RoPE stage-in needs q8_0 K");
@@ -261,43 +271,76 @@ extern "C" int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const 
     const uint32_t NB = w->head_dim / 32;
     const size_t lds = (size_t)64 * w->n_head_kv * NB * (34 + 18);
     if (lds > 150 * 1024) return kvm_fail(st, KVM_ERANGE, "stagein: %u kv heads x %u dims exceed the staging tile", w->n_head_kv, w->head_dim);
-    if (rope->n_rot < 8 || rope->n_rot > w->head_dim || rope->n_rot % 8)
+    a->hk = (const uint8_t *)h->k_raw;
+    a->hv = (const uint8_t *)h->v;
+    a->h_tokens = h->n_tokens;
+    a->wk = (uint8_t *)w->k;
+    a->wv = (uint8_t *)w->v;
+    a->cell_pos = w->cell_pos;
+    a->slot_block = w->slot_block;
+    a->slot_base = w->slot_base;
+    a->n_tiles = w->n_cells / 64;
+    a->H = w->n_head_kv;
+    a->bt = w->block_tokens;
+    a->n_slots = w->n_cells / w->block_tokens;
+    a->ids = sel->ids;
+    a->to_base = sel->to_base;
+    a->stage_slots = sel->stage_slots;
+    a->info = sel->info;
+    const uint32_t max_slots = sel->cap < a->n_slots ? sel->cap : a->n_slots;
+    *max_items = max_slots * (w->block_tokens / 64);
+    return KVM_OK;
+}
+
+extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
+                                           const kvm_rope_params *rope) {
+    if (!st || !lanes || !rope) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
+    if (n_lanes == 0) return KVM_OK;
+    if (n_lanes > KVM_STAGEIN_LANES) return kvm_fail(st, KVM_ERANGE, "stagein: %u lanes > %d", n_lanes, KVM_STAGEIN_LANES);
+    stage_lanes sl;
+    std::memset(&sl, 0, sizeof(sl));
+    uint32_t max_items = 0, max_cells = 0, max_h = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        uint32_t items = 0;
+        int rc = stage_lane_args(st, lanes[i].h, lanes[i].w, lanes[i].sel, &sl.lane[i], &items);
+        if (rc) return rc;
+        if (lanes[i].w->head_dim != lanes[0].w->head_dim)
+            return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: lanes with head_dim %u and %u", lanes[0].w->head_dim, lanes[i].w->head_dim);
+        max_items = items > max_items ? items : max_items;
+        max_cells = lanes[i].w->n_cells > max_cells ? lanes[i].w->n_cells : max_cells;
+        max_h = lanes[i].w->n_head_kv > max_h ? lanes[i].w->n_head_kv : max_h;
+    }
+    const kvm_window *w0 = lanes[0].w;
+    if (rope->n_rot < 8 || rope->n_rot > w0->head_dim || rope->n_rot % 8)
         return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: n_rot %u (needs a multiple of 8 <= head_dim)", rope->n_rot);
-    const int nrot = hadamard_width(w, rope->hadamard_nrot);
-    if (!hadamard_ok(nrot, w->head_dim)) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: hadamard width %d", nrot);
+    const int nrot = hadamard_width(w0, rope->hadamard_nrot);
+    if (!hadamard_ok(nrot, w0->head_dim)) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: hadamard width %d", nrot);
     KVM_HIP(st, hipSetDevice(st->device));
     const std::vector<float> theta = kvm_rope_theta(rope->freq_base, rope->freq_scale, rope->n_rot);
-    stage_args a;
-    rc = rope_ctx_for(st, theta.data(), rope->n_rot / 2, nrot, w->n_cells, &a.rc);
+    rope_ctx rc0;
+    int rc = rope_ctx_for(st, theta.data(), rope->n_rot / 2, nrot, max_cells, &rc0);
     if (rc) return rc;
-    a.hk = (const uint8_t *)h->k_raw;
-    a.hv = (const uint8_t *)h->v;
-    a.h_tokens = h->n_tokens;
-    a.wk = (uint8_t *)w->k;
-    a.wv = (uint8_t *)w->v;
-    a.cell_pos = w->cell_pos;
-    a.slot_block = w->slot_block;
-    a.slot_base = w->slot_base;
-    a.n_tiles = w->n_cells / 64;
-    a.H = w->n_head_kv;
-    a.bt = w->block_tokens;
-    a.n_slots = w->n_cells / w->block_tokens;
-    a.ids = sel->ids;
-    a.to_base = sel->to_base;
-    a.stage_slots = sel->stage_slots;
-    a.info = sel->info;
-    const uint32_t max_slots = sel->cap < a.n_slots ? sel->cap : a.n_slots;
-    const uint32_t max_items = max_slots * (w->block_tokens / 64);
-    const dim3 grid(max_items < KVM_STAGEIN_WGS ? max_items : KVM_STAGEIN_WGS);
-    if (w->head_dim == 256) {
+    for (uint32_t i = 0; i < n_lanes; ++i) sl.lane[i].rc = rc0;
+    const size_t lds = (size_t)64 * max_h * (w0->head_dim / 32) * (34 + 18);
+    // about one workgroup per CU in all: an empty plan (the steady state) is one short launch
+    const uint32_t per_lane = (KVM_STAGEIN_WGS + n_lanes - 1) / n_lanes;
+    const dim3 grid(max_items < per_lane ? max_items : per_lane, n_lanes);
+    if (grid.x == 0) return KVM_OK;
+    if (w0->head_dim == 256) {
         KVM_HIP(st, hipFuncSetAttribute((const void *)k_stagein<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(k_stagein<256>, grid, dim3(256), lds, st->stream, a);
+        hipLaunchKernelGGL(k_stagein<256>, grid, dim3(256), lds, st->stream, sl);
     } else {
         KVM_HIP(st, hipFuncSetAttribute((const void *)k_stagein<128>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(k_stagein<128>, grid, dim3(256), lds, st->stream, a);
+        hipLaunchKernelGGL(k_stagein<128>, grid, dim3(256), lds, st->stream, sl);
     }
     KVM_LAUNCH_CHECK(st, "stagein");
     return KVM_OK;
+}
+
+extern "C" int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
+                                     const kvm_selection *sel, const kvm_rope_params *rope) {
+    const kvm_stagein_lane one = {h, w, sel};
+    return kvm_stagein_selection_lanes(st, &one, 1, rope);
 }
 
 // ---------------------------------------------------------------------------

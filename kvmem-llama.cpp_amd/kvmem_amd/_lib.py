@@ -68,6 +68,10 @@ class History(C.Structure):
     _fields_ = [("k_raw", C.c_void_p), ("v", C.c_void_p), ("n_tokens", C.c_uint32)]
 
 
+class StageinLane(C.Structure):
+    _fields_ = [("h", C.POINTER(History)), ("w", C.POINTER(Window)), ("sel", C.POINTER(Selection))]
+
+
 class Lane(C.Structure):
     _fields_ = [("w", C.POINTER(Window)), ("q", C.c_void_p), ("q_pos", C.c_void_p),
                 ("out", C.c_void_p), ("n_tokens", C.c_uint32)]
@@ -106,6 +110,7 @@ SIGNATURES = {
     "kvm_select_topk": (C.c_int, [_P, _P, C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
     "kvm_stagein_selection": (C.c_int, [_P, C.POINTER(History), _PW, C.POINTER(Selection),
                                         C.POINTER(RopeParams)]),
+    "kvm_stagein_selection_lanes": (C.c_int, [_P, C.POINTER(StageinLane), _u32, C.POINTER(RopeParams)]),
     "kvm_stagein_enqueue_k": (C.c_int, [_P, C.c_int, _P, _sz, _PW, _u32, _i64, _i64, C.c_int,
                                         C.c_int, C.c_int, C.c_int, _i32, _P, C.c_int]),
     "kvm_stagein_enqueue_v": (C.c_int, [_P, _P, _sz, _PW, _u32, _i64]),

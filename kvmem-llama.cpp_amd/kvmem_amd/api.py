@@ -369,6 +369,19 @@ def prepare_stagein(st, history, window, sel, n_rot, freq_base, freq_scale=1.0, 
                     (r, history, window, sel))
 
 
+def prepare_stagein_lanes(st, lanes, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    """lanes: (history, window, selection) triples, staged in one launch."""
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    arr = (L.StageinLane * len(lanes))()
+    for i, (h, w, sel) in enumerate(lanes):
+        arr[i] = L.StageinLane(C.pointer(h.c), C.pointer(w.c), C.pointer(sel.c))
+    return Prepared(st, st.lib.kvm_stagein_selection_lanes, (st.h, arr, len(lanes), C.byref(r)), (r, arr, lanes))
+
+
+def stagein_selection_lanes(st, lanes, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    prepare_stagein_lanes(st, lanes, n_rot, freq_base, freq_scale, hadamard_nrot)()
+
+
 def prepare_fa_decode(st, window, q, q_pos, n_head, scale, out):
     qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
     return Prepared(st, st.lib.kvm_fa_decode,

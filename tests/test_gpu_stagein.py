@@ -77,6 +77,53 @@ def test_stagein_reselect_moves_only_changed_slots(kvm_state):
         assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want)
 
 
+def test_stagein_lanes_match_single_lane(kvm_state):
+    """Three lanes (different kv-head counts, histories, budgets and a partial
+    last block) staged in one launch leave every window, cell position and slot
+    map byte-equal to single-lane stage-ins, and lane 0 equal to the oracle."""
+    D, bt = 256, 128
+    cases = [(4, 40, 12, 16), (2, 25, 6, 8), (4, 60, 16, 20)]      # (H, n_blocks, budget, window slots)
+    lanes, single, ref = [], [], []
+    for i, (H, n_blocks, budget, slots) in enumerate(cases):
+        n_hist = n_blocks * bt - (37 if i == 2 else 0)
+        hist, kr, vr = _history(30 + i, n_hist, H, D)
+        rng = np.random.default_rng(40 + i)
+        s = rng.standard_normal(n_blocks)
+        s[n_blocks - 1] = 10.0
+        nt = dev(np.array([min(bt, n_hist - b * bt) for b in range(n_blocks)], np.int32))
+        pair = []
+        for _ in range(2):
+            w = api.KVWindow(kvm_state, slots * bt, H, D, bt)
+            sel = api.select_topk(kvm_state, dev(s), nt, budget, 1, 0, None, window=w)
+            pair.append((hist, w, sel))
+        lanes.append(pair[0])
+        single.append(pair[1])
+        ref.append((kr, vr, nt, H))
+    api.stagein_selection_lanes(kvm_state, lanes, 64, 1e7)
+    for h1, w1, sel1 in single:
+        api.stagein_selection(kvm_state, h1, w1, sel1, 64, 1e7)
+    for (_, w, sel), (_, w1, sel1) in zip(lanes, single):
+        for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+            assert torch.equal(getattr(w, name), getattr(w1, name)), name
+        assert sel.result()["status"] == 0
+    kr, vr, nt, H = ref[0]
+    _, w, sel = lanes[0]
+    res = sel.result()
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, ev = w.export_rows(0, len(res["ids"]) * bt)
+    for k, (bid, base) in enumerate(zip(res["ids"], res["to_base"])):
+        want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, int(base), theta)
+        assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want), k
+        assert np.array_equal(host(ev)[k * bt:(k + 1) * bt], vr[bid * bt:(bid + 1) * bt])
+    # bad lane sets are refused before any launch
+    with pytest.raises(L.KvmError):
+        api.stagein_selection_lanes(kvm_state, [lanes[0]] * 9, 64, 1e7)            # more than 8 lanes
+    w128 = api.KVWindow(kvm_state, 256, 4, 128, 128)
+    sel128 = api.SelectionBuffers(kvm_state, 2, 2)
+    with pytest.raises(L.KvmError):
+        api.stagein_selection_lanes(kvm_state, [lanes[0], (lanes[0][0], w128, sel128)], 64, 1e7)
+
+
 def test_enqueue_flush_api(kvm_state):
     """Reference-shaped item API (llama-kvmem-stagein.h:36-46) at arbitrary cells."""
     H, D = 4, 256
