@@ -165,6 +165,10 @@ struct pf_args {
 
 template <int D, int RT>
 __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
+    // LDS operand rings: K runs KR-1 k-steps ahead of its MFMAs, V VR-1
+    // operands ahead (the first ones in flight during the softmax), so the
+    // LDS latency hides behind matrix-core work instead of a wait per MFMA
+    constexpr int KR = 3, VR = 6;
     constexpr int NW = 8 / RT;                            // waves; NW x RT x 16 = 128 rows
     constexpr int KS = D / 32, DT = D / 16;
     constexpr uint32_t TILE_H = 64u * D;                  // halves per K (or V) tile
@@ -344,15 +348,31 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
         for (int s = 0; s < 4; ++s)
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) S[s][rt] = kvm_f32x4{0.f, 0.f, 0.f, 0.f};
+        // K operands run KR-1 k-steps ahead of their MFMAs (a register ring)
+        kvm_f16x8 kr[KR][4];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
+        for (int p = 0; p < KR - 1; ++p)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const kvm_f16x8 kop = *(const kvm_f16x8 *)(sk + ((s * KS + ks) * 64 + l) * 8);
+            for (int s = 0; s < 4; ++s) kr[p][s] = *(const kvm_f16x8 *)(sk + ((s * KS + p) * 64 + l) * 8);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks + KR - 1 < KS) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    kr[(ks + KR - 1) % KR][s] = *(const kvm_f16x8 *)(sk + ((s * KS + ks + KR - 1) * 64 + l) * 8);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
-                    S[s][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[rt][ks], S[s][rt], 0, 0, 0);
-            }
+                    S[s][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[ks % KR][s], qop[rt][ks], S[s][rt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // the first V operands, in flight during the softmax
+        kvm_f16x8 vr[VR];
+#pragma unroll
+        for (int i = 0; i < VR - 1; ++i) vr[i] = *(const kvm_f16x8 *)(sv + (((i % DT) * 2 + i / DT) * 64 + l) * 8);
         if (masked) {
             asm volatile("" ::: "memory");                // keep the mask on this (rare) path
 #pragma unroll
@@ -409,15 +429,17 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
             lp[rt] += sum;
         }
         // O^T += V^T P^T
+        // operand i = (kk, dt) = (i / DT, i % DT); the ring stays VR-1 ahead
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int i = 0; i < 2 * DT; ++i) {
+            const int kk = i / DT, dt = i % DT, n = i + VR - 1;
+            if (n < 2 * DT) vr[n % VR] = *(const kvm_f16x8 *)(sv + (((n % DT) * 2 + n / DT) * 64 + l) * 8);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const kvm_f16x8 vop = *(const kvm_f16x8 *)(sv + ((dt * 2 + kk) * 64 + l) * 8);
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    O[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pB[rt][kk], O[rt][dt], 0, 0, 0);
-            }
+            for (int rt = 0; rt < RT; ++rt)
+                O[rt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vr[i % VR], pB[rt][kk], O[rt][dt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the next tile's copies
         __syncthreads();
     }
