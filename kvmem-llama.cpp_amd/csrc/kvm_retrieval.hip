@@ -152,16 +152,17 @@ struct score_args {
 #define KVM_SCORE_GMAX 16   // largest query group (n_head / n_head_kv)
 #define KVM_SCORE_HMAX 16   // largest n_head_kv
 
-// One head chunk of a tile (up to 8 heads): the chunk's slab (every load
-// issued first) goes into LDS as kh, then one wave per chain (dot, nk, nq)
-// walks the dims in order.  UPB = 16-byte slab units per thread and 32-dim
-// batch (1 for <= 4 heads).
-template <int D, int UPB>
-__device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile, uint32_t c,
+// One head chunk of NT consecutive tiles (HC = 8 / NT heads, so NT tiles x HC
+// heads x 8 blocks = 64 (tile, head, block) rows): the chunk's slabs (every
+// load issued first) go into LDS as kh, row (t HC + head) 8 + block, then one
+// wave per chain (dot, nk, nq) walks the dims in order.  UPB = 16-byte slab
+// units per thread and 32-dim batch (1 for a single tile of <= 4 heads).
+template <int D, int UPB, int NT>
+__device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile0, uint32_t c,
                                             uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[D + 4],
                                             float (*s_qv)[D + 4], float *s_nq, float *s_nk,
-                                            float (*s_cos)[KVM_MEANK_TILE], float *dot_out) {
-    constexpr uint32_t TW = KVM_MEANK_TILE, HC = 64 / TW, NBAT = D / 32;
+                                            float (*s_cos)[KVM_MEANK_TILE * 8], float *dot_out) {
+    constexpr uint32_t TW = KVM_MEANK_TILE, HC = 8 / NT, NBAT = D / 32;
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t HD = a.H * D;
@@ -181,22 +182,31 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
         }
     }
     const uint32_t quad = tid % (TW / 4);
-    uint32_t mt4[4];
+    // unit tid + 256x of batch k: hu = unit/64 = (tile t, head) = (hu / HC, hu % HC)
+    // (wave-uniform), dim 32k + (unit%64)/2, blocks 4 quad .. +3
+    const kvm_f32x4 *slab[UPB];
+    uint32_t mt4[UPB][4];
+    bool unit_live[UPB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t b = tile * TW + 4 * quad + j;
-        mt4[j] = a.mean_tokens[(uint64_t)il * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
+    for (int x = 0; x < UPB; ++x) {
+        const uint32_t hu = (tid >> 6) + 4u * x, t = hu / HC, head = hu % HC;
+        const uint32_t tile = tile0 + t < a.n_tiles_used ? tile0 + t : a.n_tiles_used - 1;
+        unit_live[x] = head < nh;
+        slab[x] = (const kvm_f32x4 *)(a.k_sum + (((uint64_t)il * a.n_tiles + tile) * HD +
+                                                 ((uint64_t)c * HC + (head < nh ? head : 0u)) * D) * TW);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = tile * TW + 4 * quad + j;
+            mt4[x][j] = a.mean_tokens[(uint64_t)il * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
+        }
     }
-    // unit t + 256*x of batch k: head hu = unit/64, dim 32k + (unit%64)/2, quad
-    const kvm_f32x4 *slab = (const kvm_f32x4 *)(a.k_sum + (((uint64_t)il * a.n_tiles + tile) * HD + (uint64_t)c * HC * D) * TW);
     kvm_f32x4 kv[NBAT][UPB];
 #pragma unroll
     for (uint32_t k = 0; k < NBAT; ++k)
 #pragma unroll
         for (int x = 0; x < UPB; ++x) {
-            const uint32_t u = tid + 256u * x, hu = u / 64, r = (u % 64) / 2;
-            const uint32_t row = (hu < nh ? hu : 0u) * D + 32 * k + r;
-            kv[k][x] = __builtin_nontemporal_load(slab + row * (TW / 4) + quad);
+            const uint32_t r = (tid % 64) / 2;
+            kv[k][x] = __builtin_nontemporal_load(slab[x] + (32 * k + r) * (TW / 4) + quad);
         }
     if (qc == 0) return;                 // layer without queries: skipped by the reduction
     // ---- qv of the chunk's heads (the group's q rows summed in order, scaled)
@@ -218,16 +228,18 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
             }
         }
     }
-    float inv4[4];
-    uint32_t keep4[4];
+    float inv4[UPB][4];
+    uint32_t keep4[UPB][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        inv4[j] = mt4[j] ? kvm_fdiv(1.0f, (float)mt4[j]) : 0.0f;
-        keep4[j] = mt4[j] ? 0xffffffffu : 0u;
-    }
+    for (int x = 0; x < UPB; ++x)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            inv4[x][j] = mt4[x][j] ? kvm_fdiv(1.0f, (float)mt4[x][j]) : 0.0f;
+            keep4[x][j] = mt4[x][j] ? 0xffffffffu : 0u;
+        }
     // ---- kh for all dims into LDS (one barrier), then the chains run straight
     // through the D dims in the reference's order
-    const uint32_t hh = lane / TW;
+    const uint32_t hh = (lane / TW) % HC, tl = lane / (TW * HC);   // the chain's head and tile
     const float *qrow = s_qv[hh < nh ? hh : 0u];
     const float *nqrow = s_qv[lane < nh ? lane : 0u];
     float chain = 0.0f;
@@ -236,12 +248,12 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
 #pragma unroll
         for (int x = 0; x < UPB; ++x) {
             const uint32_t u = tid + 256u * x, hu = u / 64, r = (u % 64) / 2;
-            if (hu < nh) {
+            if (unit_live[x]) {
                 float4 kh;
-                kh.x = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][0], inv4[0])) & keep4[0]);
-                kh.y = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][1], inv4[1])) & keep4[1]);
-                kh.z = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][2], inv4[2])) & keep4[2]);
-                kh.w = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][3], inv4[3])) & keep4[3]);
+                kh.x = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][0], inv4[x][0])) & keep4[x][0]);
+                kh.y = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][1], inv4[x][1])) & keep4[x][1]);
+                kh.z = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][2], inv4[x][2])) & keep4[x][2]);
+                kh.w = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][3], inv4[x][3])) & keep4[x][3]);
                 float *col = &s_k[hu * TW + 4 * quad][32 * k + r];
                 col[0] = kh.x;
                 col[D + 4] = kh.y;
@@ -309,10 +321,10 @@ __device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, ui
     if (w == 2 && lane < nh) s_nq[lane] = chain;
     KVM_LDS_BARRIER();
     // ---- cosines of the chunk
-    const uint32_t bi = lane % TW, b = tile * TW + bi;
+    const uint32_t bi = lane % TW, b = (tile0 + tl) * TW + bi;
     if (w == 0 && hh < nh && b < a.n_blocks) {
         const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[hh]), kvm_fsqrt(s_nk[lane])), 1e-6f);
-        s_cos[c * HC + hh][bi] = kvm_fdiv(chain, den);
+        s_cos[c * HC + hh][tl * TW + bi] = kvm_fdiv(chain, den);
     }
     *dot_out = chain;
     KVM_LDS_BARRIER();                   // chunk c's LDS reads done before chunk c+1 writes
@@ -324,18 +336,21 @@ struct score_lanes {
     score_args lane[KVM_RET_LANES];
 };
 
-template <int D>
+// Workgroup = NT consecutive tiles of one layer: NT = 8 / HC tiles for head
+// chunks of HC heads, so that a chunk fills the 64 chain lanes (NT = 2 at 4 kv
+// heads: 16 blocks per workgroup).
+template <int D, int NT>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     const score_args &a = sl.lane[blockIdx.z];
-    if (blockIdx.x >= a.n_tiles_used || blockIdx.y >= a.n_layer) return;
+    if (blockIdx.x * NT >= a.n_tiles_used || blockIdx.y >= a.n_layer) return;
     constexpr uint32_t TW = KVM_MEANK_TILE;       // blocks per tile
-    constexpr uint32_t HC = 64 / TW;              // heads per chunk
+    constexpr uint32_t HC = 8 / NT;               // heads per chunk
     __shared__ __align__(16) float s_k[64][D + 4];   // kh as [lane][dim], rows padded against bank conflicts
     __shared__ __align__(16) float s_qv[HC][D + 4];
     __shared__ float s_nq[HC];
     __shared__ float s_nk[64];
-    __shared__ float s_cos[KVM_SCORE_HMAX][TW];
-    const uint32_t tile = blockIdx.x, il = blockIdx.y;
+    __shared__ float s_cos[KVM_SCORE_HMAX][TW * 8];
+    const uint32_t tile = blockIdx.x * NT, il = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t qc = a.q_count[il];
@@ -343,11 +358,11 @@ __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     for (uint32_t c = 0; c * HC < a.H; ++c) {
         const uint32_t nh = a.H - c * HC < HC ? a.H - c * HC : HC;
         float dot;
-        if (nh <= 4) score_chunk<D, 1>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
-        else score_chunk<D, 2>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
+        if (NT == 1 && nh <= 4) score_chunk<D, 1, NT>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
+        else score_chunk<D, 2, NT>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
         if (qc == 0) return;
     }
-    if (w == 0 && lane < TW && tile * TW + lane < a.n_blocks) {
+    if (w == 0 && lane < TW * NT && tile * TW + lane < a.n_blocks) {
         double layer = 0.0;
         for (uint32_t h = 0; h < a.H; ++h) layer += (double)s_cos[h][lane];
         a.layer_score[(uint64_t)il * a.cap + tile * TW + lane] = layer / (double)(a.H > 1 ? a.H : 1);
@@ -833,6 +848,12 @@ extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_se
     return launch_topk(st, tl, 1);
 }
 
+template <int NT>
+static void launch_score(bool d256, dim3 grid, dim3 block, hipStream_t stream, const score_lanes &sl) {
+    if (d256) hipLaunchKernelGGL((k_score<256, NT>), grid, block, 0, stream, sl);
+    else hipLaunchKernelGGL((k_score<128, NT>), grid, block, 0, stream, sl);
+}
+
 static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
     const kvm_meank_index *ix = r.ix;
     const kvm_query_acc *q = r.q;
@@ -887,9 +908,19 @@ extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lan
         max_layer = ix->n_layer > max_layer ? ix->n_layer : max_layer;
     }
     if (max_tiles) {
-        const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
-        if (lanes[0].ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sl);
-        else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sl);
+        // tiles per workgroup: head chunks of HC = 8 / NT heads fill the 64 chain
+        // lanes; lanes with different kv-head counts share the largest chunk
+        uint32_t max_h = 0;
+        for (uint32_t i = 0; i < n_lanes; ++i) max_h = lanes[i].ix->n_head_kv > max_h ? lanes[i].ix->n_head_kv : max_h;
+        const int nt = max_h > 4 ? 1 : max_h > 2 ? 2 : max_h == 2 ? 4 : 8;
+        const dim3 grid(kvm_cdiv(max_tiles, (uint32_t)nt), max_layer, n_lanes), block(256);
+        const bool d256 = lanes[0].ix->head_dim == 256;
+        switch (nt) {
+        case 1: launch_score<1>(d256, grid, block, st->stream, sl); break;
+        case 2: launch_score<2>(d256, grid, block, st->stream, sl); break;
+        case 4: launch_score<4>(d256, grid, block, st->stream, sl); break;
+        default: launch_score<8>(d256, grid, block, st->stream, sl); break;
+        }
         KVM_LAUNCH_CHECK(st, "score");
     }
     return launch_topk(st, tl, n_lanes);

@@ -77,7 +77,11 @@ def _case(seed, n_blocks, n_layer=1, n_head=24, H=4, D=256, planted=16):
 
 
 @pytest.mark.parametrize("n_blocks,n_layer,n_head,H,D", [(2048, 1, 24, 4, 256), (128, 1, 8, 2, 128),
-                                                       (300, 3, 24, 4, 256), (5000, 1, 24, 4, 256)])
+                                                       (300, 3, 24, 4, 256), (5000, 1, 24, 4, 256),
+                                                       # tiles per workgroup 1 (8 and 16 kv heads), 2 with a
+                                                       # partly filled head chunk (3), 8 (1 kv head)
+                                                       (700, 2, 8, 8, 128), (260, 1, 32, 16, 128),
+                                                       (500, 1, 12, 3, 128), (333, 1, 3, 1, 256)])
 def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
     q, qc, k_sum, mt, planted = _case(n_blocks + n_layer, n_blocks, n_layer, n_head, H, D)
     ix = _build_index(kvm_state, k_sum, mt, n_blocks + 5, H, D)
