@@ -282,36 +282,53 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
     }
 
     // Tile copies go global -> LDS directly (global_load_lds_dwordx4: lane l
-    // writes 16 bytes at M0 + 16 l), issued from asm so the compiler adds no
-    // wait for them; the loop waits for them itself before each barrier.  The
-    // asm restores M0, which the compiler reserves.  Wave w copies the 1 KB
-    // chunks w, w+NW, ... of the tile's K and of its V (source and LDS
-    // addresses are scalar; the lane offset is one register), and wave 0 also
-    // the tile's 64 cell positions.
-    constexpr int CHW = 64 * D * 2 / 1024 / NW;         // 1 KB chunks of one K (or V) tile per wave
-    const uint64_t hb = (uint64_t)h * a.n_tiles;
+    // writes 16 bytes at M0 + offset + 16 l), issued from asm so the compiler
+    // adds no wait for them; the loop waits for them itself before each
+    // barrier.  The asm restores M0, which the compiler reserves.  Wave w copies
+    // bytes [CW w, CW (w+1)) of the tile's K and of its V: CW / 1 KB copies per
+    // part under one M0 value, the immediate offset moving the global and the
+    // LDS address alike.  Wave 0 also copies the tile's 64 cell positions.
+    constexpr uint32_t CW = TILE_H * 2 / NW;             // bytes of one K (or V) tile per wave
+    static_assert(CW == 4096 || CW == 2048, "copy layout");
     const uint32_t lds_kv = (uint32_t)(uintptr_t)(kvm_lds_ptr)&s_kv[0][0];
     const uint32_t lds_cp = (uint32_t)(uintptr_t)(kvm_lds_ptr)&s_cp[0][0];
-    const uint32_t loff = 16u * l;                       // this lane's bytes in a 1 KB chunk
-    const uint32_t wofs = __builtin_amdgcn_readfirstlane(1024u * w);
+    const uint32_t loff = 16u * l;                       // this lane's bytes in a 1 KB copy
+    const uint32_t wofs = __builtin_amdgcn_readfirstlane(CW * w);
+    const uint8_t *k_head = (const uint8_t *)(a.kh + (uint64_t)h * a.n_tiles * TILE_H) + wofs;
+    const uint8_t *v_head = (const uint8_t *)(a.vh + (uint64_t)h * a.n_tiles * TILE_H) + wofs;
     auto dma_tile = [&](uint32_t t, int buf) {
         t = __builtin_amdgcn_readfirstlane(t);
-        const uint8_t *kb = (const uint8_t *)(a.kh + (hb + t) * TILE_H) + wofs;
-        const uint8_t *vb = (const uint8_t *)(a.vh + (hb + t) * TILE_H) + wofs;
+        const uint8_t *kb = k_head + (uint64_t)t * (TILE_H * 2);
+        const uint8_t *vb = v_head + (uint64_t)t * (TILE_H * 2);
         const uint32_t dk = lds_kv + (uint32_t)buf * (2 * TILE_H * 2) + wofs;
         const uint32_t dv = dk + TILE_H * 2;
-#pragma unroll
-        for (int j = 0; j < 2 * CHW; ++j) {
-            const uint8_t *src = j < CHW ? kb + 1024 * NW * j : vb + 1024 * NW * (j - CHW);
-            const uint32_t dst = j < CHW ? dk + 1024 * NW * j : dv + 1024 * NW * (j - CHW);
-            uint32_t m0_saved;
-            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %3\n\ts_mov_b32 m0, %0"
-                         : "=&s"(m0_saved) : "v"(loff), "s"(dst), "s"(src) : "memory");
+        uint32_t m0_saved;
+        if constexpr (CW == 4096) {
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                         "global_load_lds_dwordx4 %1, %4\n\t"
+                         "global_load_lds_dwordx4 %1, %4 offset:1024\n\t"
+                         "global_load_lds_dwordx4 %1, %4 offset:2048\n\t"
+                         "global_load_lds_dwordx4 %1, %4 offset:3072\n\t"
+                         "s_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                         "global_load_lds_dwordx4 %1, %5\n\t"
+                         "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+                         "global_load_lds_dwordx4 %1, %5 offset:2048\n\t"
+                         "global_load_lds_dwordx4 %1, %5 offset:3072\n\t"
+                         "s_mov_b32 m0, %0"
+                         : "=&s"(m0_saved) : "v"(loff), "s"(dk), "s"(dv), "s"(kb), "s"(vb) : "memory");
+        } else {
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                         "global_load_lds_dwordx4 %1, %4\n\t"
+                         "global_load_lds_dwordx4 %1, %4 offset:1024\n\t"
+                         "s_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                         "global_load_lds_dwordx4 %1, %5\n\t"
+                         "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+                         "s_mov_b32 m0, %0"
+                         : "=&s"(m0_saved) : "v"(loff), "s"(dk), "s"(dv), "s"(kb), "s"(vb) : "memory");
         }
         if (w == 0) {
             const int32_t *src = a.cell_pos + (uint64_t)t * 64;
             const uint32_t dst = lds_cp + (uint32_t)buf * 256;
-            uint32_t m0_saved;
             asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, %3\n\ts_mov_b32 m0, %0"
                          : "=&s"(m0_saved) : "v"(4u * l), "s"(dst), "s"(src) : "memory");
         }
@@ -330,13 +347,18 @@ __global__ void __launch_bounds__(64 * (8 / RT)) k_pf_attn(pf_args a) {
     }
     const float c = a.c;
 
-    if (n_live > 0) dma_tile(t_begin + (s_list[0] & 0x7fffu), 0);
+    // list entries k and k+1 are in registers at the top of tile k; entry k+2
+    // is read during tile k
+    uint32_t e_cur = n_live > 0 ? s_list[0] : 0u, e_nxt = n_live > 1 ? s_list[1] : e_cur;
+    if (n_live > 0) dma_tile(t_begin + (e_cur & 0x7fffu), 0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (uint32_t k = 0; k < n_live; ++k) {
         const int b = k & 1;
-        const uint32_t e = s_list[k];
-        const uint32_t en = s_list[k + 1 < n_live ? k + 1 : k];
+        const uint32_t e = __builtin_amdgcn_readfirstlane(e_cur);
+        const uint32_t en = __builtin_amdgcn_readfirstlane(e_nxt);
+        e_cur = en;
+        e_nxt = s_list[k + 2 < n_live ? k + 2 : n_live - 1];
         dma_tile(t_begin + (en & 0x7fffu), b ^ 1);        // next tile, in flight during this one
         const bool masked = (e >> 15) == 0;
         const _Float16 *sk = s_kv[b];
