@@ -408,7 +408,9 @@ __device__ inline uint64_t ord_key(double x) {
 }
 
 // exclusive prefix sums of two values over the workgroup (DPP wave scans,
-// one LDS exchange of the wave totals); totals through t1, t2
+// one LDS exchange of the wave totals); totals through t1, t2.  s_tmp holds
+// 2 * waves words; consecutive calls must use different s_tmp buffers (a call
+// returns without a second barrier, while other waves may still read its buffer)
 __device__ void block_scan2(uint32_t v1, uint32_t v2, uint32_t *s_tmp, uint32_t &e1, uint32_t &e2,
                             uint32_t &t1, uint32_t &t2) {
     constexpr uint32_t NW = KVM_TOPK_THREADS / 64;
@@ -422,7 +424,6 @@ __device__ void block_scan2(uint32_t v1, uint32_t v2, uint32_t *s_tmp, uint32_t 
     e2 = x2 - v2 + __builtin_amdgcn_readlane(i2 - w2, wid);
     t1 = __builtin_amdgcn_readlane(i1, NW - 1);
     t2 = __builtin_amdgcn_readlane(i2, NW - 1);
-    KVM_LDS_BARRIER();
 }
 
 // s_hist[bin] += 1 for every active lane, one atomic per distinct bin run:
@@ -453,12 +454,12 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     __shared__ uint32_t s_ntok[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
     __shared__ uint32_t s_hist[2][256];
-    __shared__ uint32_t s_tmp[2 * (KVM_TOPK_THREADS / 64)];
+    __shared__ uint32_t s_tmp[2][2 * (KVM_TOPK_THREADS / 64)];   // block_scan2 buffers, used alternately
     __shared__ uint32_t s_count, s_k, s_done, s_need;
     __shared__ uint64_t s_prefix;
     __shared__ uint32_t s_sblk[KVM_TOPK_SLOTS];
     __shared__ int32_t s_sbase[KVM_TOPK_SLOTS];
-    __shared__ uint32_t s_fine[KVM_TOPK_FINE], s_coarse[KVM_TOPK_FINE / 16];
+    __shared__ __align__(16) uint32_t s_fine[KVM_TOPK_FINE];
     __shared__ float s_wmm[2][KVM_TOPK_THREADS / 64];
     __shared__ uint32_t s_wc[KVM_TOPK_THREADS / 64];
     __shared__ uint32_t s_sel[4];
@@ -514,9 +515,25 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     }
     if (tid < 256) s_hist[0][tid] = 0;
     if (tid < KVM_TOPK_FINE) s_fine[tid] = 0;
-    if (tid < KVM_TOPK_FINE / 16) s_coarse[tid] = 0;
     if (tid < KVM_TOPK_GATHER) s_rank[tid] = 0;
-    if (tid == 0) s_sel[3] = 0;
+    if (tid == 0) {
+        s_sel[3] = 0;
+        s_prefix = 0;
+        s_done = 0;
+    }
+    // With no mandatory ids the sink / recent pass (kvmem_store.cpp:520-545)
+    // has a closed form: the sink_c oldest blocks (sink_c = min(sink, budget))
+    // and, newest first, the recent blocks not in the sink while the budget
+    // lasts, i.e. blocks [n - tail_c, n).  Every thread knows its own flags.
+    const bool closed = !all && a.n_mand == 0;
+    uint32_t sink_c = 0, tail_c = 0;
+    if (closed) {
+        const uint32_t sink = a.sink < n ? a.sink : n, recent = a.recent < n ? a.recent : n;
+        sink_c = sink < a.budget ? sink : a.budget;
+        const uint32_t lo = sink_c > n - recent ? sink_c : n - recent;
+        tail_c = n - lo < a.budget - sink_c ? n - lo : a.budget - sink_c;
+    }
+    auto kept0 = [&](uint32_t i) { return all || (closed && (i < sink_c || i >= n - tail_c)); };
 #pragma unroll
     for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
         const uint32_t i = tid + k * KVM_TOPK_THREADS;
@@ -537,33 +554,35 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
             sf[k] = (float)sc;
             s_key[i] = kr[k];
             s_ntok[i] = nt[k];
-            s_kept[i] = all ? 1 : 0;
+            s_kept[i] = kept0(i) ? 1 : 0;
         }
     }
     KVM_LDS_BARRIER();
     const uint32_t per = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
     const uint32_t i0 = tid * per < n ? tid * per : n, i1 = i0 + per < n ? i0 + per : n;
     if (!all) {
-        // sink prefix, mandatory ids newest first, recent tail (kvmem_store.cpp:520-545)
-        if (tid == 0) {
-            uint32_t count = 0;
-            const uint32_t sink = a.sink < n ? a.sink : n, recent = a.recent < n ? a.recent : n;
-            for (uint32_t i = 0; i < sink && count < a.budget; ++i)
-                if (!s_kept[i]) { s_kept[i] = 1; ++count; }
-            for (uint32_t i = a.n_mand; i > 0 && count < a.budget; --i) {
-                const uint32_t id = a.mandatory[i - 1];
-                if (id < n && !s_kept[id]) { s_kept[id] = 1; ++count; }
+        // sink prefix, mandatory ids newest first, recent tail (kvmem_store.cpp:520-545):
+        // in closed form above, or one thread walks it when mandatory ids are given
+        uint32_t count = sink_c + tail_c;
+        if (!closed) {
+            if (tid == 0) {
+                uint32_t c = 0;
+                const uint32_t sink = a.sink < n ? a.sink : n, recent = a.recent < n ? a.recent : n;
+                for (uint32_t i = 0; i < sink && c < a.budget; ++i)
+                    if (!s_kept[i]) { s_kept[i] = 1; ++c; }
+                for (uint32_t i = a.n_mand; i > 0 && c < a.budget; --i) {
+                    const uint32_t id = a.mandatory[i - 1];
+                    if (id < n && !s_kept[id]) { s_kept[id] = 1; ++c; }
+                }
+                for (uint32_t i = 0; i < recent && c < a.budget; ++i) {
+                    const uint32_t id = n - 1 - i;
+                    if (!s_kept[id]) { s_kept[id] = 1; ++c; }
+                }
+                s_count = c;
             }
-            for (uint32_t i = 0; i < recent && count < a.budget; ++i) {
-                const uint32_t id = n - 1 - i;
-                if (!s_kept[id]) { s_kept[id] = 1; ++count; }
-            }
-            s_count = count;
-            s_prefix = 0;
-            s_done = 0;
+            KVM_LDS_BARRIER();
+            count = s_count;
         }
-        KVM_LDS_BARRIER();
-        const uint32_t count = s_count;
         bool fallback = count < a.budget;
         if (count < a.budget) {
             // ---- one pass over a linear histogram of the fp32 scores.  Rounding
@@ -575,11 +594,21 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
             const uint32_t wid = tid >> 6;
             uint32_t cand = 0;
             float fmn = INFINITY, fmx = -INFINITY;
-            uint32_t c = 0;
+            uint32_t c = 0, kept_bits = 0;
+            if (closed) {
+#pragma unroll
+                for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) kept_bits |= (uint32_t)kept0(tid + k * KVM_TOPK_THREADS) << k;
+            } else {
+#pragma unroll
+                for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
+                    const uint32_t i = tid + k * KVM_TOPK_THREADS;
+                    kept_bits |= (uint32_t)(k < kpt && i < n && s_kept[i] != 0) << k;
+                }
+            }
 #pragma unroll
             for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
                 const uint32_t i = tid + k * KVM_TOPK_THREADS;
-                if (k < kpt && i < n && !s_kept[i]) {
+                if (k < kpt && i < n && !(kept_bits >> k & 1u)) {
                     cand |= 1u << k;
                     fmn = fminf(fmn, sf[k]);
                     fmx = sf[k] != sf[k] ? INFINITY : fmaxf(fmx, sf[k]);   // a NaN score: fall back
@@ -613,13 +642,15 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
                         if (cand >> k & 1u) {
                             const uint32_t b = bin_of(sf[k]);
                             atomicAdd(&s_fine[b], 1u);
-                            atomicAdd(&s_coarse[b >> 4], 1u);
                         }
                     KVM_LDS_BARRIER();
                     if (tid < 64) {
-                        // coarse bin 63 - lane (descending), then the 16 fine bins of
-                        // the one holding the need-th key
-                        const uint32_t cc = s_coarse[63 - lane];
+                        // coarse bin 63 - lane (descending) = its 16 fine bins, then
+                        // the 16 fine bins of the one holding the need-th key
+                        const kvm_u32x4 *fb = (const kvm_u32x4 *)&s_fine[(63 - lane) * 16];
+                        const kvm_u32x4 f0 = fb[0], f1 = fb[1], f2 = fb[2], f3 = fb[3];
+                        const kvm_u32x4 fs = f0 + f1 + f2 + f3;
+                        const uint32_t cc = fs[0] + fs[1] + fs[2] + fs[3];
                         const uint32_t ci = kvm_wave_incl_scan(cc);
                         const uint64_t h1 = __builtin_amdgcn_ballot_w64(ci - cc < need && need <= ci);
                         const uint32_t l1 = (uint32_t)__builtin_ctzll(h1);
@@ -644,17 +675,25 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
                     fallback = false;
                     // keys above bin T are taken, and bin T whole when kk == cnt;
                     // otherwise its keys are gathered and ranked
+                    // a wave reserves its gathered keys' slots with one atomic
 #pragma unroll
-                    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k)
-                        if (cand >> k & 1u) {
-                            const uint32_t i = tid + k * KVM_TOPK_THREADS, b = need == ncand ? 0u : bin_of(sf[k]);
-                            if (need == ncand || b > T || (b == T && kk == cnt)) {
-                                s_kept[i] = 2;
-                            } else if (b == T) {
-                                const uint32_t slot = atomicAdd(&s_sel[3], 1u);
-                                s_gath[slot] = kvm_u32x4{(uint32_t)kr[k], (uint32_t)(kr[k] >> 32), i, 0u};
-                            }
+                    for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
+                        if (k >= kpt) break;                 // uniform: no thread holds block tid + 1024 k
+                        const bool ck = (cand >> k & 1u) != 0;
+                        const uint32_t i = tid + k * KVM_TOPK_THREADS, b = ck && need != ncand ? bin_of(sf[k]) : 0u;
+                        const bool take = ck && (need == ncand || b > T || (b == T && kk == cnt));
+                        const bool gath = ck && !take && b == T;
+                        if (take) s_kept[i] = 2;
+                        const uint64_t gm = __builtin_amdgcn_ballot_w64(gath);
+                        if (gm) {
+                            const uint32_t lead = (uint32_t)__builtin_ctzll(gm);
+                            uint32_t base = 0;
+                            if (lane == lead) base = atomicAdd(&s_sel[3], (uint32_t)__builtin_popcountll(gm));
+                            base = __builtin_amdgcn_readlane(base, lead);
+                            const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(gm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)gm, 0u));
+                            if (gath) s_gath[base + below] = kvm_u32x4{(uint32_t)kr[k], (uint32_t)(kr[k] >> 32), i, 0u};
                         }
+                    }
                     if (kk != cnt) {
                         KVM_LDS_BARRIER();
                         // rank of entry j among the cnt gathered: keys larger, or equal
@@ -741,7 +780,7 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
             if (!whole && need)
                 for (uint32_t i = i0; i < i1; ++i) ties += !s_kept[i] && (s_key[i] & mask) == T;
             uint32_t before = 0, n_ties = 0, z0, z1;
-            if (!whole && need) block_scan2(ties, 0u, s_tmp, before, z0, n_ties, z1);
+            if (!whole && need) block_scan2(ties, 0u, s_tmp[1], before, z0, n_ties, z1);
             for (uint32_t i = i0; i < i1 && need; ++i) {
                 if (s_kept[i]) continue;
                 const uint64_t km = s_key[i] & mask;
@@ -761,7 +800,7 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     for (uint32_t i = i0; i < i1; ++i)
         if (s_kept[i]) { ++local; tok += s_ntok[i]; }
     uint32_t rank0, base0, n_sel, total;
-    block_scan2(local, tok, s_tmp, rank0, base0, n_sel, total);
+    block_scan2(local, tok, s_tmp[0], rank0, base0, n_sel, total);
     const bool fits = n_sel <= a.cap;
     const uint32_t ns = fits ? (n_sel < a.n_slots ? n_sel : a.n_slots) : 0;
     // slots whose (block, base) differ from the new layout
@@ -785,7 +824,7 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
         }
     }
     uint32_t pos, n_stage, z2, z3;
-    block_scan2(need_local, 0u, s_tmp, pos, z2, n_stage, z3);
+    block_scan2(need_local, 0u, s_tmp[1], pos, z2, n_stage, z3);
     if (need_mask) {
         uint32_t rank = rank0, k = 0;
         for (uint32_t i = i0; i < i1; ++i) {
