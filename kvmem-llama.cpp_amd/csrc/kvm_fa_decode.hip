@@ -78,10 +78,6 @@ __device__ inline kvm_f16x8 nib8_to_f16den(uint32_t w) {
 
 typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
 
-// Workgroup barrier that orders LDS traffic only: it waits for this wave's LDS
-// operations but not for its outstanding global loads (a __syncthreads fence
-// would drain the tile prefetch and serialise the pipeline).
-#define KVM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 // A row's running maximum moves only when a tile raises it by more than
 // 2^KVM_LAZY_MAX (log2 domain), so most tiles skip rescaling O; probabilities

@@ -172,6 +172,11 @@ __device__ inline uint32_t kvm_wave_incl_scan(uint32_t x) {
 // Max / min / sum of a float over the wave (DPP row shifts and broadcasts as in
 // kvm_wave_incl_scan; lanes without a source contribute the identity), read back
 // from lane 63 to every lane.
+// Workgroup barrier that orders LDS traffic only: it waits for this wave's LDS
+// operations but not for its outstanding global loads or stores (a
+// __syncthreads fence would drain a tile prefetch and serialise the pipeline).
+#define KVM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
 #define KVM_WAVE_REDUCE_F32(NAME, OP, IDENT)                                                          \
     __device__ inline float NAME(float x) {                                                          \
         const int id = __float_as_int(IDENT);                                                        \

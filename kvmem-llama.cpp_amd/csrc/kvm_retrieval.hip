@@ -146,9 +146,6 @@ struct score_args {
     uint32_t n_tiles_used;  // tiles holding the first n_blocks blocks
 };
 
-// Workgroup barrier for LDS traffic only (no wait for outstanding global
-// stores, which a __syncthreads fence would add).
-#define KVM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 #define KVM_SCORE_GMAX 16   // largest query group (n_head / n_head_kv)
 #define KVM_SCORE_HMAX 16   // largest n_head_kv
 
