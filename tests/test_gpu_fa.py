@@ -80,6 +80,46 @@ def test_fa_decode_masks_and_empty_rows(kvm_state):
     check_attention(out, ref)
 
 
+def _v_rows(vt, vr, n, H, D):
+    if vt == L.T_F16:
+        return np.ascontiguousarray(vr).view(np.float16).astype(np.float32).reshape(n, H, D)
+    return O.dequant(vt, np.ascontiguousarray(vr).reshape(-1), n * H * D).reshape(n, H, D)
+
+
+@pytest.mark.parametrize("kt,vt", [(L.T_Q8_0, L.T_Q4_0), (L.T_F16, L.T_F16)])
+@pytest.mark.parametrize("T", [4, 1])
+def test_fa_decode_closed_forms(kvm_state, kt, vt, T):
+    """Two cases the mathematics fixes without an attention oracle: identical
+    keys (every visible score equals the maximum, P = 1, the output is the mean
+    of the visible V rows) and a single visible key (the output is that cell's
+    V row); V rows from the dequantiser."""
+    rng = np.random.default_rng(31 + T)
+    H, G, D, n = 4, 6, 256, 2048
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, kt, vt)
+    kr[:] = kr[0]                                           # identical keys
+    w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    qp = np.array([0, 7, 1000, n - 1][-T:], np.int32)       # token t sees cells 0..qp[t]
+    out = host(api.fa_decode(kvm_state, w, dev(q), dev(qp), H * G, D ** -0.5))
+    V = _v_rows(vt, vr, n, H, D)
+    for t, p in enumerate(qp):
+        want = V[:p + 1].astype(np.float64).mean(0)
+        for h in range(H * G):
+            np.testing.assert_allclose(out[t, h], want[h // G], rtol=0, atol=1e-5, err_msg=str((t, h)))
+    # one visible cell (mid-tile), the rest empty; a token before it sees nothing
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, kt, vt)
+    cp[:] = -1
+    cp[777] = 5
+    w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    qp = np.array([5, 4, 100, 2000][-T:], np.int32)
+    out = host(api.fa_decode(kvm_state, w, dev(q), dev(qp), H * G, D ** -0.5))
+    V = _v_rows(vt, vr, n, H, D)
+    for t, p in enumerate(qp):
+        for h in range(H * G):
+            want = V[777, h // G] if p >= 5 else np.zeros(D, np.float32)
+            np.testing.assert_allclose(out[t, h], want, rtol=0, atol=1e-6, err_msg=str((t, h)))
+
+
 def test_fa_decode_lanes_match_single_lane(kvm_state):
     rng = np.random.default_rng(8)
     H, G, D = 4, 6, 256
@@ -169,6 +209,28 @@ def test_fa_prefill_mfma(kvm_state, case, monkeypatch):
     scale = 1.0 / np.sqrt(D)
     out = host(api.fa_prefill(kvm_state, w, qd, dev(pos), H * G, scale))
     _prefill_check(out, q, kr, vr, cp, pos, H, G, D, kt, vt, scale)
+
+
+@pytest.mark.parametrize("kt,vt", [(L.T_Q8_0, L.T_Q4_0), (L.T_F16, L.T_F16)])
+def test_fa_prefill_identical_keys(kvm_state, kt, vt):
+    """Identical keys on the MFMA prefill path: every visible score equals the
+    row maximum, P = 1, so each token's output is the mean of the fp16 V
+    operands over the cells it sees (causal by position, holes skipped)."""
+    rng = np.random.default_rng(41)
+    H, G, D, n, T = 4, 6, 256, 1536, 96
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, kt, vt, holes=30)
+    kr[:] = kr[0]
+    pos = np.arange(n - T, n, dtype=np.int32)
+    cp[n - T:] = pos
+    w.import_rows(0, dev(kr), dev(vr), dev(cp))
+    q = rng.standard_normal((T, H * G, D)).astype(np.float32)
+    out = host(api.fa_prefill(kvm_state, w, dev(q), dev(pos), H * G, D ** -0.5))
+    V = _f16_rows(vt, vr, n, H, D).view(np.float16).astype(np.float64).reshape(n, H, D)
+    for t in range(0, T, 7):
+        vis = (cp >= 0) & (cp <= pos[t])
+        want = V[vis].mean(0)
+        for h in range(H * G):
+            np.testing.assert_allclose(out[t, h], want[h // G], rtol=0, atol=1e-5, err_msg=str((t, h)))
 
 
 def test_fa_prefill_blind_rows_and_single_key(kvm_state):
