@@ -202,3 +202,17 @@ def test_stage_plan_against_slot_map(kvm_state):
     res = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w).result()
     assert list(res["ids"]) == [0, 4, 9, 13]
     assert list(res["stage_slots"]) == [1, 2, 3]
+
+
+def test_select_topk_maximum_size(kvm_state):
+    """n = 8192 blocks (the most the selection takes) with long ties, distinct
+    scores and infinities, each against the oracle; one block more is refused."""
+    rng = np.random.default_rng(12)
+    n = 8192
+    nt = dev(np.full(n, 128, np.int32))
+    for kind, budget in ((0, 700), (1, 700), (3, 4096), (2, 8192)):
+        s = _scores(rng, kind, n)
+        res = api.select_topk(kvm_state, dev(s), nt, budget, 1, 2).result()
+        assert np.array_equal(res["ids"], O.pick_topk(s, budget, 1, 2)), (kind, budget)
+    with pytest.raises(L.KvmError):
+        api.select_topk(kvm_state, dev(np.zeros(n + 1)), dev(np.full(n + 1, 128, np.int32)), 8, 1, 0)

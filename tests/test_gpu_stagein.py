@@ -162,3 +162,40 @@ def test_stagein_rejects_bad_arguments(kvm_state):
     wf = api.KVWindow(kvm_state, 256, 4, 128, 128, L.T_F16, L.T_F16)
     with pytest.raises(L.KvmError):
         api.stagein_selection(kvm_state, hist, wf, sel, 64, 1e7)    # re-RoPE stage-in needs q8_0 K
+
+
+def test_stagein_plan_that_does_not_fit_stages_nothing(kvm_state):
+    """A selection larger than the window's slots (status 2) stages nothing:
+    window bytes, cell positions and slot map are left as they were."""
+    H, D, bt = 4, 256, 128
+    hist, _, _ = _history(13, 20 * bt, H, D)
+    w = api.KVWindow(kvm_state, 4 * bt, H, D, bt)              # 4 slots
+    s = np.random.default_rng(2).standard_normal(20)
+    sel = api.select_topk(kvm_state, dev(s), dev(np.full(20, bt, np.int32)), 8, 1, 0, None, window=w)
+    assert sel.result()["status"] == 2
+    before = [t.clone() for t in (w.k, w.v, w.cell_pos, w.slot_block, w.slot_base)]
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    torch.cuda.synchronize()
+    for b, a in zip(before, (w.k, w.v, w.cell_pos, w.slot_block, w.slot_base)):
+        assert torch.equal(a, b)
+
+
+def test_stagein_block_outside_history(kvm_state):
+    """A selected block past the end of the pinned history is skipped and
+    flagged (status bit 4); the other blocks are staged byte for byte and the
+    skipped slot keeps no live cells."""
+    H, D, bt = 4, 256, 128
+    hist, kr, _ = _history(14, 10 * bt, H, D)                   # 10 blocks of history
+    w = api.KVWindow(kvm_state, 8 * bt, H, D, bt)
+    s = np.zeros(14)
+    s[[3, 12, 6]] = [3.0, 2.0, 1.0]                            # block 12 is past the history
+    sel = api.select_topk(kvm_state, dev(s), dev(np.full(14, bt, np.int32)), 4, 1, 0, None, window=w)
+    assert list(sel.result()["ids"]) == [0, 3, 6, 12]
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    assert sel.result()["status"] & 4
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, _ = w.export_rows(0, 3 * bt)
+    for k, bid in enumerate([0, 3, 6]):
+        want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, k * bt, theta)
+        assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want), k
+    assert np.all(host(w.cell_pos)[3 * bt:4 * bt] == -1)
