@@ -124,10 +124,12 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HI
 
 
 def prepare_decode(st, api, wl, out):
-    """The three calls of a decode step for every layer replica, marshalled once."""
+    """The two calls of a decode step for every layer replica, marshalled once:
+    retrieval + stage-in (kvm_score_topk_stagein: scoring, then a top-k
+    workgroup that stages its own plan) and FA decode."""
     n_blocks = wl["hist_tokens"] // BT
-    return [(api.prepare_score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel),
-             api.prepare_stagein(st, wl["hist"], w, sel, N_ROT, FREQ_BASE),
+    return [(api.prepare_score_topk_stagein(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel,
+                                            wl["hist"], N_ROT, FREQ_BASE),
              api.prepare_fa_decode(st, w, wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out))
             for ix, w, sel in wl["reps"]]
 
@@ -418,8 +420,8 @@ def run_lanes(args, st, api, L, torch, np):
     """Four conversations, each with its own 32K-cell window, mean-K index and
     pinned host history (64K / 128K / 192K / 256K tokens), one bf16 query token
     each: retrieval for all lanes in one launch sequence (scoring grid over every
-    lane's blocks + one top-k workgroup per lane), stage-in of every lane's plan
-    in one launch, attention for all lanes in one launch."""
+    lane's blocks + one top-k workgroup per lane, which then stages the lane's
+    plan), attention for all lanes in one launch."""
     n_rep = 2
     wls = []
     for i, ht in enumerate(LANE_HIST):
@@ -431,20 +433,17 @@ def run_lanes(args, st, api, L, torch, np):
     for r in range(n_rep):
         lanes = [dict(index=wl["reps"][r][0], query=wl["qa"], n_blocks=wl["hist_tokens"] // BT,
                       n_tokens=wl["n_tokens"], budget_blocks=RETRIEVED // BT, sink_blocks=1,
-                      window=wl["reps"][r][1], sel=wl["reps"][r][2]) for wl in wls]
-        preps.append((api.prepare_score_topk_lanes(st, lanes),
-                      api.prepare_stagein_lanes(st, [(wl["hist"], wl["reps"][r][1], wl["reps"][r][2]) for wl in wls],
-                                                N_ROT, FREQ_BASE),
+                      window=wl["reps"][r][1], sel=wl["reps"][r][2], history=wl["hist"]) for wl in wls]
+        preps.append((api.prepare_score_topk_stagein_lanes(st, lanes, N_ROT, FREQ_BASE),
                       api.prepare_fa_decode_lanes(st, [wl["reps"][r][1] for wl in wls], [wl["q"] for wl in wls],
                                                   [wl["q_pos"] for wl in wls], N_HEAD, scale, outs)))
 
     def step(i):
-        score, stagein, fa = preps[i % n_rep]
-        score()
-        stagein()
+        retrieve, fa = preps[i % n_rep]
+        retrieve()
         fa()
 
-    ms, fa_ms = time_steps(torch, step, lambda i: preps[i % n_rep][2](), args.steps, args.warmup)
+    ms, fa_ms = time_steps(torch, step, lambda i: preps[i % n_rep][1](), args.steps, args.warmup)
     # checks: each lane's selection equals its single-lane one, nothing to restage,
     # and its attention equals the single-lane kernel's and the oracle's
     r = (args.steps - 1) % n_rep
@@ -476,7 +475,7 @@ def run_lanes(args, st, api, L, torch, np):
         "data": "synthetic N(0,1), seeds 0xC0FFEE05 + lane, 16 planted blocks per lane",
         "config": {"workload": "4 lanes: histories of 65536/131072/196608/262144 tokens (pinned host q8_0 K / "
                                "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; score + top-k for all "
-                               "lanes in one launch sequence, stage-in of all lanes in one launch, FA decode for all lanes in one "
+                               "lanes in one launch sequence (the top-k workgroups stage the plans), FA decode for all lanes in one "
                                "launch; 24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
                    "lanes": len(wls), "step_bytes": step_bytes},
         "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
@@ -503,12 +502,11 @@ def run_sweep(args, st, api, L, torch, np):
         preps = prepare_decode(st, api, wl, out)
 
         def step(i):
-            score, stagein, fa = preps[i % len(preps)]
-            score()
-            stagein()
+            retrieve, fa = preps[i % len(preps)]
+            retrieve()
             fa()
 
-        ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][2](), args.steps, args.warmup)
+        ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][1](), args.steps, args.warmup)
         nb = ht // BT
         step_bytes = nb * (H_KV * D * 4 + 8) + FA_KV_BYTES + QO_BYTES
         rows.append({"history_tokens": ht, "blocks": nb, "us_per_token": round(ms * 1e3, 2),
@@ -573,12 +571,11 @@ def main():
     preps = prepare_decode(st, api, wl, out)
 
     def step(i):
-        score, stagein, fa = preps[i % len(preps)]
-        score()
-        stagein()
+        retrieve, fa = preps[i % len(preps)]
+        retrieve()
         fa()
 
-    step_ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][2](), args.steps, args.warmup)
+    step_ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][1](), args.steps, args.warmup)
     out_gpu = out.cpu().numpy()
     if args.calibrate_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

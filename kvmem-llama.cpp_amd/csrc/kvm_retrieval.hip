@@ -5,7 +5,7 @@
 // same fp32 operation order, each operation one IEEE rounding (this file is
 // compiled with -ffp-contract=off and correctly rounded `/` and sqrtf), and the
 // per-head/per-layer accumulation in double in the same order.
-#include "kvm_internal.h"
+#include "kvm_stagein_dev.h"
 
 // ---------------------------------------------------------------------------
 // Query accumulator (llama-memory-kvmem.cpp:3300-3315, 3417-3433)
@@ -445,17 +445,23 @@ struct topk_lanes {
     topk_args lane[KVM_RET_LANES];
 };
 
-__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
+// SD > 0: the workgroup then stages its own plan (head_dim SD) through the
+// LDS buffer s_big, which the selection no longer needs by then.
+#define KVM_TOPK_BIG (KVM_MAX_TOPK_BLOCKS * 13u + KVM_TOPK_SLOTS * 8u)   // bytes of s_big
+template <int SD>
+__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_lanes sl) {
     const topk_args a = tl.lane[blockIdx.x];     // one copy out of the argument segment
-    __shared__ uint64_t s_key[KVM_MAX_TOPK_BLOCKS];
-    __shared__ uint32_t s_ntok[KVM_MAX_TOPK_BLOCKS];
-    __shared__ uint8_t s_kept[KVM_MAX_TOPK_BLOCKS];
+    // the largest arrays share one buffer: keys, token counts, kept flags, slot map
+    __shared__ __align__(16) uint8_t s_big[KVM_TOPK_BIG];
+    uint64_t *const s_key = (uint64_t *)s_big;
+    uint32_t *const s_ntok = (uint32_t *)(s_big + KVM_MAX_TOPK_BLOCKS * 8u);
+    uint8_t *const s_kept = s_big + KVM_MAX_TOPK_BLOCKS * 12u;
+    uint32_t *const s_sblk = (uint32_t *)(s_big + KVM_MAX_TOPK_BLOCKS * 13u);
+    int32_t *const s_sbase = (int32_t *)(s_big + KVM_MAX_TOPK_BLOCKS * 13u + KVM_TOPK_SLOTS * 4u);
     __shared__ uint32_t s_hist[2][256];
     __shared__ uint32_t s_tmp[2][2 * (KVM_TOPK_THREADS / 64)];   // block_scan2 buffers, used alternately
     __shared__ uint32_t s_count, s_k, s_done, s_need;
     __shared__ uint64_t s_prefix;
-    __shared__ uint32_t s_sblk[KVM_TOPK_SLOTS];
-    __shared__ int32_t s_sbase[KVM_TOPK_SLOTS];
     __shared__ __align__(16) uint32_t s_fine[KVM_TOPK_FINE];
     __shared__ float s_wmm[2][KVM_TOPK_THREADS / 64];
     __shared__ uint32_t s_wc[KVM_TOPK_THREADS / 64];
@@ -837,6 +843,20 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
         a.info[2] = n_stage;
         a.info[3] = fits ? (n_sel <= a.n_slots || a.n_slots == 0 ? 0u : 2u) : 1u;
     }
+    if constexpr (SD > 0) {
+        // stage the plan (kvm_stagein_selection's items, by this workgroup):
+        // only a plan that fits the window's slots, as the stage-in kernel does
+        const stage_args &sa = sl.lane[blockIdx.x];
+        const bool ok = fits && (n_sel <= a.n_slots || a.n_slots == 0);
+        if (ok && n_stage > 0) {
+            __syncthreads();                 // the plan is written; the selection's LDS is free
+            const uint32_t tps = sa.bt / 64;
+            for (uint32_t item = 0; item < n_stage * tps; ++item) {
+                stagein_item<SD, KVM_TOPK_THREADS>(sa, s_big, item / tps, item % tps);
+                __syncthreads();             // LDS rows of this item read before the next overwrites them
+            }
+        }
+    }
 }
 
 static int make_topk(kvm_state *st, const double *scores, const double *layer_score,
@@ -854,8 +874,14 @@ static int make_topk(kvm_state *st, const double *scores, const double *layer_sc
     return KVM_OK;
 }
 
-static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes) {
-    hipLaunchKernelGGL(k_topk, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl);
+// sd = head_dim of the windows when the top-k workgroups stage their plans
+// (sl filled by kvm_stage_prepare), 0 for the selection alone
+static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes, int sd = 0,
+                       const stage_lanes *sl = nullptr) {
+    static const stage_lanes none{};
+    if (sd == 256) hipLaunchKernelGGL(k_topk<256>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, *sl);
+    else if (sd == 128) hipLaunchKernelGGL(k_topk<128>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, *sl);
+    else hipLaunchKernelGGL(k_topk<0>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, none);
     KVM_LAUNCH_CHECK(st, "topk");
     return KVM_OK;
 }
@@ -909,7 +935,10 @@ static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
     return KVM_OK;
 }
 
-extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes) {
+// Scoring grid + top-k for every lane; sd > 0: the top-k workgroups also
+// stage their plans (stage arguments from kvm_stage_prepare).
+static int score_topk_impl(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, int sd,
+                           const stage_lanes *stl) {
     if (!st) return KVM_EINVAL;
     if (!lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk: no lanes");
     if (n_lanes > KVM_RET_LANES) return kvm_fail(st, KVM_ERANGE, "score_topk: %u lanes > %d", n_lanes, KVM_RET_LANES);
@@ -959,7 +988,40 @@ extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lan
         }
         KVM_LAUNCH_CHECK(st, "score");
     }
-    return launch_topk(st, tl, n_lanes);
+    return launch_topk(st, tl, n_lanes, sd, stl);
+}
+
+extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes) {
+    return score_topk_impl(st, lanes, n_lanes, 0, nullptr);
+}
+
+extern "C" int kvm_score_topk_stagein_lanes(kvm_state *st, const kvm_retrieval_lane *lanes,
+                                            const kvm_history *const *hist, uint32_t n_lanes,
+                                            const kvm_rope_params *rope) {
+    if (!st) return KVM_EINVAL;
+    if (!lanes || !hist || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein: no lanes");
+    if (n_lanes > KVM_RET_LANES) return kvm_fail(st, KVM_ERANGE, "score_topk_stagein: %u lanes > %d", n_lanes, KVM_RET_LANES);
+    kvm_stagein_lane sg[KVM_RET_LANES];
+    for (uint32_t i = 0; i < n_lanes; ++i) sg[i] = kvm_stagein_lane{hist[i], lanes[i].w, lanes[i].out};
+    stage_lanes stl;
+    uint32_t max_items = 0;
+    size_t lds = 0;
+    int rc = kvm_stage_prepare(st, sg, n_lanes, rope, &stl, &max_items, &lds);
+    if (rc) return rc;
+    const uint32_t hd = lanes[0].w->head_dim;
+    if (lds <= KVM_TOPK_BIG && (hd == 128 || hd == 256)) return score_topk_impl(st, lanes, n_lanes, (int)hd, &stl);
+    // a rows buffer larger than the top-k's LDS: the selection, then the stage-in kernel
+    rc = score_topk_impl(st, lanes, n_lanes, 0, nullptr);
+    if (rc) return rc;
+    return kvm_stagein_selection_lanes(st, sg, n_lanes, rope);
+}
+
+extern "C" int kvm_score_topk_stagein(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
+                                      const kvm_select_params *p, const kvm_window *w,
+                                      const kvm_selection *out, const kvm_history *h,
+                                      const kvm_rope_params *rope) {
+    const kvm_retrieval_lane lane{ix, q, p, w, out};
+    return kvm_score_topk_stagein_lanes(st, &lane, &h, 1, rope);
 }
 
 extern "C" int kvm_score_topk(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,

@@ -1,224 +1,18 @@
 // kvm_stagein.hip -- fused stage-in: pinned-host history -> tiled window.
-//
-// K: dequant q8_0 -> NeoX RoPE at the window position -> normalised
-// Walsh-Hadamard -> q8_0, the order of llama-kvmem-stagein.cu:731-786, fused in
-// one pass with the row held in registers (one wave per (token, head) row,
-// lane L owning dims DPL*L .. DPL*L+DPL-1).  Every operation is an explicitly
-// rounded IEEE op, so the output bytes equal the host restatement's.
-// V: q4_0 bytes are moved unchanged into the tiled layout (stagein.cu:733-744).
-#include "kvm_internal.h"
+// The kernels and the host entry points; the per-row and per-item device
+// routines (dequant -> RoPE -> Walsh-Hadamard -> q8_0 for K, V moved
+// unchanged) are in kvm_stagein_dev.h.
+#include "kvm_stagein_dev.h"
 
 #include <cmath>
 #include <cstring>
-
-struct rope_ctx {
-    const float2 *tab;     // [n_pos][n_half] (cos, sin)
-    uint32_t n_half;       // n_rot / 2
-    uint32_t n_pos;
-    int32_t nrot;          // Hadamard width, 0 = off
-    float hscale;          // 1 / sqrtf(nrot), computed on the host as the reference does
-};
-
-// One (token, head) row of D dims: src = NB q8_0 blocks (34 B each) readable by
-// every lane; writes the requantised row into K tile `kt` at cell c (0..63).
-template <int D>
-__device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, int32_t pos,
-                                   const rope_ctx &rc) {
-    constexpr int DPL = D / 64;
-    const int L = threadIdx.x & 63;
-    const int d0 = DPL * L;
-    const int b = d0 >> 5, e = d0 & 31;
-    const uint8_t *blk = src + b * 34;
-    const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
-    float x[DPL];
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) x[i] = (float)(int8_t)blk[2 + e + i] * dsc;
-
-    // NeoX RoPE: dims i and i + n_half rotate together for i < n_half.
-    const int nh = (int)rc.n_half;
-    if (nh > 0) {
-        const int pl = nh / DPL;                       // lane distance of the partner
-        const bool lo = d0 < nh, hi = d0 >= nh && d0 < 2 * nh;
-        float y[DPL];
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-            const float up = __shfl(x[i], (L + pl) & 63, 64);
-            const float dn = __shfl(x[i], (L - pl) & 63, 64);
-            y[i] = lo ? up : dn;
-        }
-        if (lo || hi) {
-            const float2 *cs = rc.tab + (size_t)pos * rc.n_half + (lo ? d0 : d0 - nh);
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                const float2 t = cs[i];
-                if (lo)   // x0' = x0 c - x1 s
-                    x[i] = kvm_fsub(kvm_fmul(x[i], t.x), kvm_fmul(y[i], t.y));
-                else      // x1' = x0 s + x1 c
-                    x[i] = kvm_fadd(kvm_fmul(y[i], t.y), kvm_fmul(x[i], t.x));
-            }
-        }
-    }
-
-    // normalised Walsh-Hadamard over nrot-wide chunks: pre-scale, then
-    // butterflies h = 1, 2, ..., nrot/2 (stagein.cu:105-131)
-    if (rc.nrot > 0) {
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
-#pragma unroll
-        for (int h = 1; h < DPL; h <<= 1) {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                if (!(i & h)) {
-                    const float a = x[i], bb = x[i + h];
-                    x[i] = kvm_fadd(a, bb);
-                    x[i + h] = kvm_fsub(a, bb);
-                }
-            }
-        }
-        for (int h = DPL; h < rc.nrot; h <<= 1) {
-            const int lx = h / DPL;
-            const bool first = (L & lx) == 0;
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                const float o = __shfl_xor(x[i], lx, 64);
-                x[i] = first ? kvm_fadd(x[i], o) : kvm_fsub(o, x[i]);
-            }
-        }
-    }
-
-    // q8_0 requantisation of each 32-dim block (32/DPL lanes per block)
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) amax = fmaxf(amax, fabsf(x[i]));
-#pragma unroll
-    for (int o = 1; o < 32 / DPL; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float d = kvm_fdiv(amax, 127.0f);
-    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
-    uint8_t *qd = kt + kvm_kq_off(D, c, d0);
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) qd[i] = (uint8_t)(int8_t)roundf(kvm_fmul(x[i], id));
-    if (e == 0) {
-        const uint16_t h16 = kvm_f2h(d);
-        uint8_t *sd = kt + kvm_kd_off(D, c, b);
-        sd[0] = (uint8_t)h16;
-        sd[1] = (uint8_t)(h16 >> 8);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Selection-driven stage-in: workgroup = (staged slot, 64-cell tile of it).
-// ---------------------------------------------------------------------------
-struct stage_args {
-    const uint8_t *hk, *hv;          // pinned host rows
-    uint32_t h_tokens;
-    uint8_t *wk, *wv;
-    int32_t *cell_pos;
-    uint32_t *slot_block;
-    int32_t *slot_base;
-    uint32_t n_tiles, H, bt, n_slots;
-    const uint32_t *ids;
-    const int32_t *to_base;
-    const uint32_t *stage_slots;
-    uint32_t *info;
-    rope_ctx rc;
-};
-
 
 #define KVM_STAGEIN_WGS 256       // one per CU of an MI355X (the rows buffer takes most of the LDS)
 
 // One workgroup per CU walks the (plan entry, 64-token tile) items, so an
 // empty plan (the steady state) costs one short launch; the plan length is
-// only known on the device (info[2]).
-template <int D>
-__device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt) {
-    constexpr uint32_t NB = D / 32;
-    const uint32_t slot = a.stage_slots[si];
-    const uint32_t id = a.ids[slot];
-    const int32_t base = a.to_base[slot];
-    // history blocks are consecutive block_tokens-sized runs (register_append,
-    // kvmem_store.cpp:179-205): block id covers [id*bt, min((id+1)*bt, h_tokens))
-    const uint64_t first = (uint64_t)id * a.bt;
-    const uint32_t tid = threadIdx.x;
-    if (first >= a.h_tokens) {
-        if (tid == 0) atomicOr(&a.info[3], 4u);     // block outside the history: skip it
-        return;
-    }
-    const uint32_t nt = a.h_tokens - first < a.bt ? (uint32_t)(a.h_tokens - first) : a.bt;
-    const uint32_t t0 = tt * 64;
-    const uint32_t count = nt > t0 ? (nt - t0 < 64 ? nt - t0 : 64) : 0;
-    const uint64_t htok0 = first + t0;
-    const uint32_t rowK = a.H * NB * 34, rowV = a.H * NB * 18;
-    uint8_t *lk = s_rows, *lv = s_rows + 64 * rowK;
-    // bulk copy of `count` consecutive token rows of K and V (contiguous in host memory)
-    const uint8_t *gk = a.hk + htok0 * rowK, *gv = a.hv + htok0 * rowV;
-    const uint32_t nk = count * rowK, nv = count * rowV;
-    const bool al16 = (((uintptr_t)gk | (uintptr_t)gv | rowK | rowV) & 15u) == 0;
-    if (al16) {
-#pragma unroll 4
-        for (uint32_t i = tid; i < nk / 16; i += 256) ((uint4 *)lk)[i] = ((const uint4 *)gk)[i];
-#pragma unroll 4
-        for (uint32_t i = tid; i < nv / 16; i += 256) ((uint4 *)lv)[i] = ((const uint4 *)gv)[i];
-    } else {
-        for (uint32_t i = tid; i < nk; i += 256) lk[i] = gk[i];
-        for (uint32_t i = tid; i < nv; i += 256) lv[i] = gv[i];
-    }
-    __syncthreads();
-
-    const uint32_t tile = (slot * a.bt + t0) / 64;
-    // K rows: wave w takes rows (cell j, head h) = r, r + 4, ...
-    const uint32_t wave = tid >> 6;
-    for (uint32_t r = wave; r < count * a.H; r += 4) {
-        const uint32_t j = r / a.H, h = r % a.H;
-        uint8_t *kt = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
-        stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, j, base + (int32_t)(t0 + j), a.rc);
-    }
-    // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
-    const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
-    for (uint32_t wi = tid; wi < a.H * D * 8; wi += 256) {
-        const uint32_t h = wi / (D * 8), r = wi % (D * 8);
-        const uint32_t X = r >> 1, ks = r & 1u;
-        const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
-        const uint32_t b = dd / 32, e = dd % 32;
-        uint32_t word = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < 8; ++j) {
-            const uint32_t cj = 32 * ks + 8 * gg + j;
-            uint32_t nib = 0;
-            if (cj < count) {
-                const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
-                nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
-            }
-            word |= nib << kvm_vq_nib_shift(j);
-        }
-        *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
-    }
-    for (uint32_t si2 = tid; si2 < a.H * 64 * NB; si2 += 256) {
-        const uint32_t h = si2 / (64 * NB), cj = (si2 / NB) % 64, b = si2 % NB;
-        uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, cj, b);
-        if (cj < count) {
-            const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
-            sd[0] = blk[0];
-            sd[1] = blk[1];
-        } else {
-            sd[0] = 0;
-            sd[1] = 0;
-        }
-    }
-    if (tid < 64) a.cell_pos[slot * a.bt + t0 + tid] = tid < count ? base + (int32_t)(t0 + tid) : -1;
-    if (tt == 0 && tid == 0) {
-        a.slot_block[slot] = id;
-        a.slot_base[slot] = base;
-    }
-}
-
-// Every lane's plan in one launch (blockIdx.y = lane): the lanes' windows,
-// histories and plans are independent, so the workgroups of one lane never touch
-// another lane's memory.
-#define KVM_STAGEIN_LANES 8
-struct stage_lanes {
-    stage_args lane[KVM_STAGEIN_LANES];
-};
-
+// only known on the device (info[2]).  Every lane's plan in one launch
+// (blockIdx.y = lane): the lanes' windows, histories and plans are independent.
 template <int D>
 __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     extern __shared__ __align__(16) uint8_t s_rows[];
@@ -226,7 +20,7 @@ __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     const uint32_t tps = a.bt / 64;
     const uint32_t n_items = a.info[3] != 0 ? 0u : a.info[2] * tps;
     for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        stagein_item<D>(a, s_rows, item / tps, item % tps);
+        stagein_item<D, 256>(a, s_rows, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }
 }
@@ -292,21 +86,22 @@ static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window
     return KVM_OK;
 }
 
-extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
-                                           const kvm_rope_params *rope) {
-    if (!st || !lanes || !rope) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
-    if (n_lanes == 0) return KVM_OK;
+int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
+                      const kvm_rope_params *rope, stage_lanes *sl, uint32_t *max_items, size_t *lds) {
+    if (!st || !lanes || !rope || !sl) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
     if (n_lanes > KVM_STAGEIN_LANES) return kvm_fail(st, KVM_ERANGE, "stagein: %u lanes > %d", n_lanes, KVM_STAGEIN_LANES);
-    stage_lanes sl;
-    std::memset(&sl, 0, sizeof(sl));
-    uint32_t max_items = 0, max_cells = 0, max_h = 0;
+    std::memset(sl, 0, sizeof(*sl));
+    *max_items = 0;
+    *lds = 0;
+    if (n_lanes == 0) return KVM_OK;
+    uint32_t max_cells = 0, max_h = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) {
         uint32_t items = 0;
-        int rc = stage_lane_args(st, lanes[i].h, lanes[i].w, lanes[i].sel, &sl.lane[i], &items);
+        int rc = stage_lane_args(st, lanes[i].h, lanes[i].w, lanes[i].sel, &sl->lane[i], &items);
         if (rc) return rc;
         if (lanes[i].w->head_dim != lanes[0].w->head_dim)
             return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: lanes with head_dim %u and %u", lanes[0].w->head_dim, lanes[i].w->head_dim);
-        max_items = items > max_items ? items : max_items;
+        *max_items = items > *max_items ? items : *max_items;
         max_cells = lanes[i].w->n_cells > max_cells ? lanes[i].w->n_cells : max_cells;
         max_h = lanes[i].w->n_head_kv > max_h ? lanes[i].w->n_head_kv : max_h;
     }
@@ -320,13 +115,25 @@ extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane
     rope_ctx rc0;
     int rc = rope_ctx_for(st, theta.data(), rope->n_rot / 2, nrot, max_cells, &rc0);
     if (rc) return rc;
-    for (uint32_t i = 0; i < n_lanes; ++i) sl.lane[i].rc = rc0;
-    const size_t lds = (size_t)64 * max_h * (w0->head_dim / 32) * (34 + 18);
+    for (uint32_t i = 0; i < n_lanes; ++i) sl->lane[i].rc = rc0;
+    *lds = (size_t)64 * max_h * (w0->head_dim / 32) * (34 + 18);
+    return KVM_OK;
+}
+
+extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
+                                           const kvm_rope_params *rope) {
+    if (!st) return KVM_EINVAL;
+    stage_lanes sl;
+    uint32_t max_items = 0;
+    size_t lds = 0;
+    int rc = kvm_stage_prepare(st, lanes, n_lanes, rope, &sl, &max_items, &lds);
+    if (rc) return rc;
+    if (n_lanes == 0) return KVM_OK;
     // about one workgroup per CU in all: an empty plan (the steady state) is one short launch
     const uint32_t per_lane = (KVM_STAGEIN_WGS + n_lanes - 1) / n_lanes;
     const dim3 grid(max_items < per_lane ? max_items : per_lane, n_lanes);
     if (grid.x == 0) return KVM_OK;
-    if (w0->head_dim == 256) {
+    if (lanes[0].w->head_dim == 256) {
         KVM_HIP(st, hipFuncSetAttribute((const void *)k_stagein<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(k_stagein<256>, grid, dim3(256), lds, st->stream, sl);
     } else {

@@ -107,6 +107,10 @@ SIGNATURES = {
     "kvm_score_topk": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
                                  C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
     "kvm_score_topk_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), _u32]),
+    "kvm_score_topk_stagein": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc), C.POINTER(SelectParams),
+                                         _PW, C.POINTER(Selection), C.POINTER(History), C.POINTER(RopeParams)]),
+    "kvm_score_topk_stagein_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), C.POINTER(C.POINTER(History)), _u32,
+                                               C.POINTER(RopeParams)]),
     "kvm_select_topk": (C.c_int, [_P, _P, C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
     "kvm_stagein_selection": (C.c_int, [_P, C.POINTER(History), _PW, C.POINTER(Selection),
                                         C.POINTER(RopeParams)]),

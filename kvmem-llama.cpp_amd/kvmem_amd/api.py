@@ -362,6 +362,40 @@ def prepare_score_topk_lanes(st, lanes):
     return Prepared(st, st.lib.kvm_score_topk_lanes, (st.h, arr, len(lanes)), (keep, arr))
 
 
+def prepare_score_topk_stagein(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks,
+                               window, sel, history, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    """Retrieval whose top-k workgroup stages its own plan (kvm_score_topk_stagein)."""
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks, None, 0, n_tokens.data_ptr())
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    return Prepared(st, st.lib.kvm_score_topk_stagein,
+                    (st.h, C.byref(index.c), C.byref(query.c), C.byref(p), C.byref(window.c), C.byref(sel.c),
+                     C.byref(history.c), C.byref(r)),
+                    (p, r, index, query, window, sel, n_tokens, history))
+
+
+def score_topk_stagein(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window,
+                       sel, history, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    prepare_score_topk_stagein(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks,
+                               window, sel, history, n_rot, freq_base, freq_scale, hadamard_nrot)()
+    return sel
+
+
+def prepare_score_topk_stagein_lanes(st, lanes, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    """lanes: score_topk_lanes dicts with a "history" each (kvm_score_topk_stagein_lanes)."""
+    keep, arr = [], (L.RetrievalLane * len(lanes))()
+    hists = (C.POINTER(L.History) * len(lanes))()
+    for i, ln in enumerate(lanes):
+        p = L.SelectParams(ln["n_blocks"], ln["budget_blocks"], ln.get("sink_blocks", 1), ln.get("recent_blocks", 0),
+                           None, 0, ln["n_tokens"].data_ptr())
+        keep += [p, ln]
+        arr[i] = L.RetrievalLane(C.pointer(ln["index"].c), C.pointer(ln["query"].c), C.pointer(p),
+                                 C.pointer(ln["window"].c), C.pointer(ln["sel"].c))
+        hists[i] = C.pointer(ln["history"].c)
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    return Prepared(st, st.lib.kvm_score_topk_stagein_lanes, (st.h, arr, hists, len(lanes), C.byref(r)),
+                    (keep, arr, hists, r))
+
+
 def prepare_stagein(st, history, window, sel, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
     r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
     return Prepared(st, st.lib.kvm_stagein_selection,

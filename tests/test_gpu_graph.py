@@ -11,7 +11,10 @@ from kvmem_amd import api, _lib as L
 pytestmark = pytest.mark.gpu
 
 
-def test_decode_step_graph_replays_equal_eager(kvm_state):
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_step_graph_replays_equal_eager(kvm_state, fused):
+    """fused: retrieval and stage-in in kvm_score_topk_stagein (the top-k
+    workgroup stages the plan) instead of kvm_score_topk + kvm_stagein_selection."""
     st = kvm_state
     rng = np.random.default_rng(21)
     H, G, D, BT, n_blocks = 4, 6, 256, 128, 64
@@ -33,9 +36,14 @@ def test_decode_step_graph_replays_equal_eager(kvm_state):
     stagein = api.prepare_stagein(st, hist, w, sel, 64, 1e7)
     fa = api.prepare_fa_decode(st, w, q, q_pos, H * G, D ** -0.5, out)
 
+    fused_retrieval = api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, 8, 1, 0, w, sel, hist, 64, 1e7)
+
     def step():
-        score()
-        stagein()
+        if fused:
+            fused_retrieval()
+        else:
+            score()
+            stagein()
         fa()
 
     step()                                   # stages the selection, sizes the workspace

@@ -199,3 +199,79 @@ def test_stagein_block_outside_history(kvm_state):
         want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, k * bt, theta)
         assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want), k
     assert np.all(host(w.cell_pos)[3 * bt:4 * bt] == -1)
+
+
+def _retrieval(st, seed, n_blocks, H, D, n_head, bt=128):
+    rng = np.random.default_rng(seed)
+    ix = api.MeanKIndex(st, 1, n_blocks, H, D, bt)
+    ix.set_block_sums(dev((rng.standard_normal((1, n_blocks, H * D)) * 128).astype(np.float32)))
+    ix.mean_tokens[:, :n_blocks] = 128
+    ix.present[:n_blocks] = 1
+    qa = api.QueryAcc(st, 1, n_head, D)
+    qa.q_sum.copy_(dev(rng.standard_normal((1, n_head * D)).astype(np.float32)))
+    qa.q_count.copy_(dev(np.array([1], np.int32)))
+    return ix, qa, rng
+
+
+def _same_selection_and_window(sa, wa, sb, wb):
+    ra, rb = sa.result(), sb.result()
+    for key in ("ids", "to_base", "stage_slots"):
+        assert np.array_equal(ra[key], rb[key]), key
+    assert ra["total"] == rb["total"] and ra["status"] == rb["status"] == 0
+    for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+        assert torch.equal(getattr(wa, name), getattr(wb, name)), name
+    return ra
+
+
+@pytest.mark.parametrize("H,n_head", [(4, 24), (5, 10)])
+def test_score_topk_stagein_matches_two_calls(kvm_state, H, n_head):
+    """The fused retrieval + stage-in (the top-k workgroup stages its plan; at 5
+    kv heads the rows exceed its LDS and the call falls back to the stage-in
+    kernel) against kvm_score_topk + kvm_stagein_selection on a second window:
+    a fresh window (full plan), a changed query (some slots restaged) and the
+    same query again (empty plan) give equal selections and equal windows."""
+    D, bt, n_blocks, budget, slots = 256, 128, 40, 12, 16
+    ix, qa, rng = _retrieval(kvm_state, 60 + H, n_blocks, H, D, n_head)
+    n_hist = n_blocks * bt - 30                                 # last block partial
+    hist, kr, _ = _history(70 + H, n_hist, H, D)
+    nt = dev(np.array([min(bt, n_hist - b * bt) for b in range(n_blocks)], np.int32))
+    wa, wb = (api.KVWindow(kvm_state, slots * bt, H, D, bt) for _ in range(2))
+    sa, sb = (api.SelectionBuffers(kvm_state, n_blocks, budget) for _ in range(2))
+    staged = []
+    for step in range(3):
+        if step == 1:
+            qa.q_sum.add_(dev((rng.standard_normal((1, n_head * D)) * 0.7).astype(np.float32)))
+        api.score_topk_stagein(kvm_state, ix, qa, n_blocks, nt, budget, 1, 0, wa, sa, hist, 64, 1e7)
+        api.score_topk(kvm_state, ix, qa, n_blocks, nt, budget, 1, 0, None, wb, sb)
+        api.stagein_selection(kvm_state, hist, wb, sb, 64, 1e7)
+        staged.append(len(_same_selection_and_window(sa, wa, sb, wb)["stage_slots"]))
+    assert staged[0] == budget and 0 < staged[1] < budget and staged[2] == 0, staged
+    res = sa.result()
+    k = 5
+    bid, base = int(res["ids"][k]), int(res["to_base"][k])
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, _ = wa.export_rows(k * bt, bt)
+    want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, base, theta)
+    assert np.array_equal(host(ek).reshape(-1), want)
+
+
+def test_score_topk_stagein_lanes_matches_two_calls(kvm_state):
+    """Three lanes (different histories and index sizes) in one fused launch
+    pair against kvm_score_topk_lanes + kvm_stagein_selection_lanes."""
+    H, D, n_head, bt, budget, slots = 4, 256, 24, 128, 10, 12
+    fused, two = [], []
+    for i, n_blocks in enumerate((20, 33, 48)):
+        ix, qa, _ = _retrieval(kvm_state, 80 + i, n_blocks, H, D, n_head)
+        hist, _, _ = _history(90 + i, n_blocks * bt, H, D)
+        nt = dev(np.full(n_blocks, bt, np.int32))
+        for group in (fused, two):
+            group.append(dict(index=ix, query=qa, n_blocks=n_blocks, n_tokens=nt, budget_blocks=budget,
+                              sink_blocks=1, window=api.KVWindow(kvm_state, slots * bt, H, D, bt),
+                              sel=api.SelectionBuffers(kvm_state, n_blocks, budget), history=hist))
+    for step in range(2):
+        api.prepare_score_topk_stagein_lanes(kvm_state, fused, 64, 1e7)()
+        api.score_topk_lanes(kvm_state, two)
+        api.stagein_selection_lanes(kvm_state, [(ln["history"], ln["window"], ln["sel"]) for ln in two], 64, 1e7)
+        for a, b in zip(fused, two):
+            r = _same_selection_and_window(a["sel"], a["window"], b["sel"], b["window"])
+            assert len(r["stage_slots"]) == (budget if step == 0 else 0)
