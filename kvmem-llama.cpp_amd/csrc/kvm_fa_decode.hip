@@ -14,7 +14,8 @@
 // from HBM into registers, three buffers, two tiles in flight):
 //   waves 0-3 score: wave kq takes keys 16kq..16kq+15 of the tile against all
 //     padded query rows with v_mfma_i32_16x16x32_i8 (one MFMA per 32-dim block
-//     and row tile; the d_k*d_q products of four blocks come from one
+//     and row tile; a last row tile of at most 8 rows takes two blocks per
+//     v_mfma_i32_16x16x64_i8; the d_k*d_q products of four blocks come from one
 //     v_mfma_f32_16x16x1_4b_f32 outer product), masks by cell position and
 //     writes P (fp16) of its keys to LDS, keeping the online softmax state;
 //   waves 4-7 accumulate: wave 4+dq takes O[:, dims D/4*dq ..] += P V with
@@ -84,16 +85,22 @@ typedef float kvm_f32x16 __attribute__((ext_vector_type(16)));
 // stay below 2^KVM_LAZY_MAX, well inside fp16.
 #define KVM_LAZY_MAX 8.0f
 
+// Register buffers per wave for the tile operands: two tiles in flight (a
+// third in flight measured no faster on the 24-row, 32K-cell workload).
+#define KVM_FA_NBUF 3
+
 // Operands of one 64-cell tile, loaded straight from HBM into registers in
 // MFMA operand order (the window's tile layout is built for this).
 // Scoring wave kq (keys 16kq..16kq+15): K quants of key 16kq+m (lane l = 16g+m
 // holds dims 32b+8g..+7 of every block b), the fp16 scales of key 16kq+m for
-// blocks 4gi+g (q8_0), positions of keys 16kq+4g..+3.
-template <int D, bool QUANT>
+// blocks 4gi+g (q8_0) and, for a packed row tile, for blocks 2g and 2g+1;
+// positions of keys 16kq+4g..+3.
+template <int D, bool QUANT, bool PK>
 struct fa_k_regs {
     static constexpr int NB = D / 32;
     kvm_u32x4 k[QUANT ? NB / 2 : NB];     // q8_0: 2 blocks per 16 B; f16: one k-step
     uint32_t dk[QUANT ? NB / 4 : 1];      // fp16 scale (low half)
+    uint32_t dkp[2];                      // packed row tile: scales of blocks 2g, 2g+1
     kvm_u32x4 cp;                          // 4 cell positions
 };
 // P V wave dq (dims D/4*dq ..): q4_0 nibble words of dims D/4*dq+16nt+m for
@@ -105,11 +112,13 @@ struct fa_v_regs {
     kvm_u32x4 vh[QUANT ? 1 : NT][2];       // f16 V [ks]
 };
 
-template <int D, int NRT, bool QUANT>
+template <int D, int NRT, bool QUANT, bool PK>
 __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     constexpr int NB = D / 32;          // 32-dim blocks per row
+    constexpr int NP = NB / 2;          // block pairs (packed row tile)
     constexpr int NG = QUANT ? NB / 4 : 1;   // 4-block scale groups
     constexpr int RMAX = 16 * NRT;      // padded query rows
+    static_assert(!PK || QUANT, "only the q8_0 scores pack two blocks per MFMA");
     constexpr int DW = D / 4;           // output dims per P V wave
     constexpr int NT = DW / 16;         // 16-dim output tiles per P V wave
     constexpr int NBW = DW >= 32 ? DW / 32 : 1;   // V scale blocks per P V wave
@@ -120,7 +129,14 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     constexpr int QT = (NITEM + 127) / 128;   // items per lane group (8 waves x 16)
     constexpr int PSTR = 64 + 8;        // padded fp16 row stride of P in LDS
     static_assert(NT >= 1 && NT % NBW == 0, "P V dim split");
-    using KRegs = fa_k_regs<D, QUANT>;
+    // A packed row tile (PK: the last one, at most 8 rows) scores two 32-dim
+    // blocks per v_mfma_i32_16x16x64_i8: column m < 8 is row 16rt+m against
+    // the even block of the pair, column m >= 8 the same row against the odd
+    // block (the query operand is zero in the other half), so half the MFMAs
+    // and scale FMAs of a padded tile; the two halves are summed across lanes
+    // m and m^8, which then both hold the row's scores.
+    auto is_pk = [](int rt) { return PK && rt == NRT - 1; };
+    using KRegs = fa_k_regs<D, QUANT, PK>;
     using VRegs = fa_v_regs<D, QUANT, NT, NBW>;
 
     const fa_lane ln = a.lanes[blockIdx.z];
@@ -166,11 +182,13 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             qraw[t][1] = *(const kvm_u32x4 *)(qb + (esz == 4u ? 16u : 0u));
         }
     }
-    // positions of the rows a scoring lane holds (row 16rt + m), with the query
+    // positions of the rows a scoring lane holds (row 16rt + m; 16rt + m % 8 in
+    // a packed row tile), with the query
+    auto srow = [&](int rt) { return is_pk(rt) ? 16 * rt + (m & 7) : 16 * rt + m; };
     int32_t qpos_raw[NRT];
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-        const int row = 16 * rt + m;
+        const int row = srow(rt);
         qpos_raw[rt] = ln.q_pos[(row < R ? row : 0) / a.G];
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -227,21 +245,19 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     // issues the same loads and the prologue needs no branch
     auto tile_index = [&](uint32_t i) { return n_t == 0 ? 0u : t_begin + (i < n_t ? i : n_t - 1); };
     // Both roles step through the same tiles with the same barriers: one per
-    // tile, and a second one when a row's running maximum moves.  Buffers of
-    // the three-register ring: two tiles in flight.  The loop body is straight
-    // line so the compiler's wait counts see the same loads in flight on every
-    // trip; the last one or two tiles are handled after the loop.
-    auto run_tiles = [&](auto &b0, auto &b1, auto &b2, auto &&step) {
+    // tile, and a second one when a row's running maximum moves.  A ring of
+    // KVM_FA_NBUF register buffers keeps KVM_FA_NBUF - 1 tiles in flight; the
+    // loop body is straight line so the compiler's wait counts see the same
+    // loads in flight on every trip; the last tiles are handled after the loop.
+    auto run_tiles = [&](auto (&bf)[KVM_FA_NBUF], auto &&step) {
         uint32_t it = 0;
-        for (; it + 3 <= n_t; it += 3) {
-            step(b0, b2, it + 2);
-            step(b1, b0, it + 3);
-            step(b2, b1, it + 4);
+        for (; it + KVM_FA_NBUF <= n_t; it += KVM_FA_NBUF) {
+#pragma unroll
+            for (int j = 0; j < KVM_FA_NBUF; ++j) step(bf[j], bf[(j + KVM_FA_NBUF - 1) % KVM_FA_NBUF], it + j + KVM_FA_NBUF - 1);
         }
-        if (it < n_t) {
-            step(b0, b2, it + 2);
-            if (it + 1 < n_t) step(b1, b0, it + 3);
-        }
+#pragma unroll
+        for (int j = 0; j < KVM_FA_NBUF - 1; ++j)
+            if (it + j < n_t) step(bf[j], bf[(j + KVM_FA_NBUF - 1) % KVM_FA_NBUF], it + j + KVM_FA_NBUF - 1);
     };
     const uint64_t pidx = ((uint64_t)blockIdx.z * a.H + h) * a.n_splits + split;
 
@@ -251,39 +267,59 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
         const uint8_t *kbase = ln.wk + (uint64_t)h * ln.n_tiles * KTILE;
         const uint32_t k_off = QUANT ? (uint32_t)((kq * (NB / 2) * 64 + l) << 4) : (uint32_t)((kq * NB * 64 + l) << 4);
         const uint32_t dk_off = 64u * D + (uint32_t)(((kq * NB + g) * 16 + m) << 1);
+        // packed row tile: scales of blocks 2g, 2g+1 (lane groups past the pairs read block 0)
+        const uint32_t dkp_off = 64u * D + (uint32_t)(((kq * NB + (g < NP ? 2 * g : 0)) * 16 + m) << 1);
         const uint32_t cp_off = (uint32_t)(16 * kq + 4 * g) * 4u;
         auto load_k = [&](KRegs &rg, uint32_t T) {
             const uint8_t *kt = kbase + (uint64_t)T * KTILE;
 #pragma unroll
             for (int p = 0; p < (QUANT ? NB / 2 : NB); ++p) rg.k[p] = *(const kvm_u32x4 *)(kt + k_off + 1024u * p);
-            if constexpr (QUANT) {
+            if constexpr (QUANT && !(PK && NRT == 1)) {
 #pragma unroll
                 for (int gi = 0; gi < NG; ++gi) rg.dk[gi] = *(const uint16_t *)(kt + dk_off + 128u * gi);
             }
+            if constexpr (PK) {
+                rg.dkp[0] = *(const uint16_t *)(kt + dkp_off);
+                rg.dkp[1] = *(const uint16_t *)(kt + dkp_off + 32u);
+            }
             rg.cp = *(const kvm_u32x4 *)((const uint8_t *)(ln.cell_pos + (uint64_t)T * 64) + cp_off);
         };
-        KRegs b0, b1, b2;
-        load_k(b0, tile_index(0));
-        load_k(b1, tile_index(1));
+        KRegs kb[KVM_FA_NBUF];
+#pragma unroll
+        for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_k(kb[j], tile_index(j));
         quantise_q();
 
         // B operands (Q^T) of every row tile: lane (row 16rt+m, k-group g)
         long qop_i[QUANT ? NRT : 1][QUANT ? NB : 1];
+        kvm_i32x4 qop_p[NP];                 // packed row tile: [even block | odd block] per pair
         kvm_f16x8 qop_h[QUANT ? 1 : NRT][QUANT ? 1 : NB];
         float dqo[NRT][NG];                  // scale MFMA B operand: dq * kq_scale * log2(e)
-        int32_t qp[NRT];
-        float m_run[NRT], l_run[NRT];        // row 16rt+m over this lane's keys
+        float dqp[2];                        // packed row tile: even-block / odd-block columns
+        uint32_t qlim[NRT];                  // cell visible iff (uint)cell_pos < qlim (= q_pos + 1; 0 for padding)
+        float m_run[NRT], l_run[NRT];        // row srow(rt) over this lane's keys
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
-            const int row = 16 * rt + m;
+            const int row = srow(rt);
+            if (is_pk(rt)) {
+                const bool odd = m >= 8;
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if constexpr (QUANT) __builtin_memcpy(&qop_i[rt][b], &s_qq[row][32 * b + 8 * g], 8);
-                else qop_h[rt][b] = *(const kvm_f16x8 *)&s_qh[row][32 * b + 8 * g];
+                for (int p = 0; p < NP; ++p) {
+                    kvm_u32x2 v;
+                    __builtin_memcpy(&v, &s_qq[row][32 * (2 * p + odd) + 8 * g], 8);
+                    qop_p[p] = odd ? kvm_i32x4{0, 0, (int)v[0], (int)v[1]} : kvm_i32x4{(int)v[0], (int)v[1], 0, 0};
+                }
+                dqp[0] = !odd && g < NP ? s_dq[row][2 * g] * a.scale_log2 : 0.0f;
+                dqp[1] = odd && g < NP ? s_dq[row][2 * g + 1] * a.scale_log2 : 0.0f;
+            } else {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    if constexpr (QUANT) __builtin_memcpy(&qop_i[rt][b], &s_qq[row][32 * b + 8 * g], 8);
+                    else qop_h[rt][b] = *(const kvm_f16x8 *)&s_qh[row][32 * b + 8 * g];
+                }
+#pragma unroll
+                for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
             }
-#pragma unroll
-            for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
-            qp[rt] = row < R ? qpos_raw[rt] : -1;
+            qlim[rt] = row < R && qpos_raw[rt] >= 0 ? (uint32_t)qpos_raw[rt] + 1u : 0u;
             m_run[rt] = KVM_M_NONE;
             l_run[rt] = 0.0f;
         }
@@ -291,28 +327,48 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
 
         auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
             load_k(nx, tile_index(inext));
-            // ---- scores of keys 16kq + 4g + i, rows 16rt + m (log2 domain; q8_0:
+            // ---- scores of keys 16kq + 4g + i, rows srow(rt) (log2 domain; q8_0:
             // kq_scale * log2(e) is folded into the query scales), masked
             float s[NRT][4];
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
                 if constexpr (QUANT) {
-                    // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
-                    kvm_f32x16 dd[NG];
+                    if (is_pk(rt)) {
+                        // d_k * d_q of (key 4g+i, column m) for the four pairs: the
+                        // even-block product in columns m < 8, the odd one in m >= 8
+                        kvm_f32x16 dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[0]), dqp[0],
+                                                                            kvm_f32x16{}, 0, 0, 0);
+                        dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[1]), dqp[1], dd, 0, 0, 0);
 #pragma unroll
-                    for (int gi = 0; gi < NG; ++gi)
-                        dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[rt][gi],
-                                                                       kvm_f32x16{}, 0, 0, 0);
+                        for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+                        for (int p = 0; p < NP; ++p) {
+                            kvm_i32x4 kw;
+                            __builtin_memcpy(&kw, &rg.k[p], 16);
+                            const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw, qop_p[p], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                    for (int b = 0; b < NB; ++b) {
-                        const kvm_u32x4 kw = rg.k[b >> 1];
-                        const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
-                        const long av = (long)(lo32 | (hi32 << 32));
-                        const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
+                            for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[4 * p + i], s[rt][i]);
+                        }
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[rt][i]);
+                        for (int i = 0; i < 4; ++i) s[rt][i] += kvm_ror8_f32(s[rt][i]);
+                    } else {
+                        // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
+                        kvm_f32x16 dd[NG];
+#pragma unroll
+                        for (int gi = 0; gi < NG; ++gi)
+                            dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[rt][gi],
+                                                                           kvm_f32x16{}, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+#pragma unroll
+                        for (int b = 0; b < NB; ++b) {
+                            const kvm_u32x4 kw = rg.k[b >> 1];
+                            const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
+                            const long av = (long)(lo32 | (hi32 << 32));
+                            const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[rt][i]);
+                        }
                     }
                 } else {
                     kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -349,8 +405,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
                 float mx = -INFINITY;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int32_t cpos = (int32_t)rg.cp[i];
-                    if (!(cpos >= 0 && cpos <= qp[rt])) s[rt][i] = -INFINITY;
+                    if (!(rg.cp[i] < qlim[rt])) s[rt][i] = -INFINITY;    // empty (-1) or after the row
                     mx = fmaxf(mx, s[rt][i]);
                 }
                 s_max[kq][g][16 * rt + m] = mx;
@@ -387,12 +442,13 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             }
             par ^= 1;
         };
-        run_tiles(b0, b1, b2, score);
+        run_tiles(kb, score);
 
-        // ---- (m, l) of this split's rows
+        // ---- (m, l) of this split's rows (a packed row tile: the lanes m >= 8
+        // repeat the rows of lanes m - 8 and are left out of the sum)
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
-            float lr = l_run[rt];
+            float lr = is_pk(rt) && m >= 8 ? 0.0f : l_run[rt];
             lr = kvm_add_xor32(kvm_add_xor16(lr));
             if (g == 0) s_l[kq][16 * rt + m] = lr;
         }
@@ -431,9 +487,9 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             }
         };
         quantise_q();                            // V is needed a tile later than K
-        VRegs b0, b1, b2;
-        load_v(b0, tile_index(0));
-        load_v(b1, tile_index(1));
+        VRegs vbuf[KVM_FA_NBUF];
+#pragma unroll
+        for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_v(vbuf[j], tile_index(j));
 
         kvm_f32x4 O[NRT][NT];
         // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and
@@ -509,7 +565,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             }
             par ^= 1;
         };
-        run_tiles(b0, b1, b2, accumulate);
+        run_tiles(vbuf, accumulate);
 
         __syncthreads();                          // pairs with the scoring waves' (m, l) exchange
         float *po = a.ws + pidx * RMAX * D;
@@ -597,9 +653,26 @@ static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
     return s < n_tiles ? s : n_tiles;
 }
 
-template <int D, int NRT, bool QUANT>
+template <int D, int NRT, bool QUANT, bool PK>
 static void launch_decode(const fa_args &a, uint32_t n_lanes, hipStream_t stream) {
-    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT>), dim3(a.n_splits, a.H, n_lanes), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((k_fa_decode<D, NRT, QUANT, PK>), dim3(a.n_splits, a.H, n_lanes), dim3(512), 0, stream, a);
+}
+
+// Row tiles of 16 query rows; with a q8_0 K a last tile of at most 8 rows is packed.
+template <int D>
+static void launch_decode_d(const fa_args &a, uint32_t n_lanes, uint32_t max_rows, bool quant, hipStream_t stream) {
+    const int NRT = max_rows <= 16 ? 1 : 2;
+    const bool pk = quant && max_rows - 16u * (NRT - 1) <= 8u;
+    if (!quant) {
+        if (NRT == 1) launch_decode<D, 1, false, false>(a, n_lanes, stream);
+        else launch_decode<D, 2, false, false>(a, n_lanes, stream);
+    } else if (NRT == 1) {
+        if (pk) launch_decode<D, 1, true, true>(a, n_lanes, stream);
+        else launch_decode<D, 1, true, false>(a, n_lanes, stream);
+    } else {
+        if (pk) launch_decode<D, 2, true, true>(a, n_lanes, stream);
+        else launch_decode<D, 2, true, false>(a, n_lanes, stream);
+    }
 }
 
 static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
@@ -643,13 +716,8 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     a.ws_ml = ws + n_part * D;
     KVM_HIP(st, hipSetDevice(st->device));
     const bool quant = w0->k_type == KVM_TYPE_Q8_0;
-    if (D == 256) {
-        if (quant) { if (NRT == 1) launch_decode<256, 1, true>(a, n_lanes, st->stream); else launch_decode<256, 2, true>(a, n_lanes, st->stream); }
-        else       { if (NRT == 1) launch_decode<256, 1, false>(a, n_lanes, st->stream); else launch_decode<256, 2, false>(a, n_lanes, st->stream); }
-    } else {
-        if (quant) { if (NRT == 1) launch_decode<128, 1, true>(a, n_lanes, st->stream); else launch_decode<128, 2, true>(a, n_lanes, st->stream); }
-        else       { if (NRT == 1) launch_decode<128, 1, false>(a, n_lanes, st->stream); else launch_decode<128, 2, false>(a, n_lanes, st->stream); }
-    }
+    if (D == 256) launch_decode_d<256>(a, n_lanes, max_rows, quant, st->stream);
+    else launch_decode_d<128>(a, n_lanes, max_rows, quant, st->stream);
     KVM_LAUNCH_CHECK(st, "fa_decode");
     if (D == 256)
         hipLaunchKernelGGL(k_fa_combine<256>, dim3(rmax * 4, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
