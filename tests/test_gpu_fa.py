@@ -65,6 +65,23 @@ def test_fa_decode_parity(kvm_state, case, qdt):
         assert np.abs(out - ref).max() <= 2e-2 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("T", [4, 1])
+def test_fa_decode_full_window(kvm_state, T):
+    """The decode workload at its real shape: a 32,768-cell q8_0/q4_0 window,
+    24 query heads over 4 kv heads, head_dim 256, bf16 query; 4 tokens (24 rows
+    per kv head: one full row tile and one packed) or 1 token (6 rows: one
+    packed tile), with empty cells spread through the window."""
+    rng = np.random.default_rng(40 + T)
+    H, G, D, n = 4, 6, 256, 32768
+    w, kr, vr, cp = _window(kvm_state, rng, n, H, D, L.T_Q8_0, L.T_Q4_0, holes=300)
+    qt = torch.from_numpy(rng.standard_normal((T, H * G, D)).astype(np.float32)).to(torch.bfloat16)
+    q = qt.float().numpy()
+    qp = np.arange(n - T, n, dtype=np.int32)
+    out = host(api.fa_decode(kvm_state, w, qt.cuda(), dev(qp), H * G, D ** -0.5))
+    ref = O.fa_ggml(L.T_Q8_0, L.T_Q4_0, q, kr, vr, cp, qp, H * G, H, D, D ** -0.5)
+    check_attention(out, ref)
+
+
 def test_fa_decode_masks_and_empty_rows(kvm_state):
     rng = np.random.default_rng(7)
     H, G, D, n = 4, 6, 256, 1024
