@@ -640,14 +640,14 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     *out = L > 0.0f ? acc / L : 0.0f;
 }
 
-static uint32_t choose_splits(uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
+static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
     if (const char *e = getenv("KVM_FA_SPLITS")) {
         uint32_t v = (uint32_t)atoi(e);
         if (v > KVM_MAX_SPLITS) v = KVM_MAX_SPLITS;
         if (v > 0) return v < n_tiles ? v : n_tiles;
     }
-    // about one workgroup per CU on a 256-CU device
-    uint32_t s = (256 + n_lanes * H - 1) / (n_lanes * H);
+    // about one workgroup per CU
+    uint32_t s = (n_cu + n_lanes * H - 1) / (n_lanes * H);
     if (s < 1) s = 1;
     if (s > KVM_MAX_SPLITS) s = KVM_MAX_SPLITS;
     return s < n_tiles ? s : n_tiles;
@@ -706,7 +706,7 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     a.H = H;
     a.G = n_head / H;
     a.n_head = n_head;
-    a.n_splits = choose_splits(n_lanes, H, max_tiles);
+    a.n_splits = choose_splits(st->n_cu, n_lanes, H, max_tiles);
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_type == KVM_TYPE_BF16;
     const size_t n_part = (size_t)n_lanes * H * a.n_splits * rmax;

@@ -29,6 +29,7 @@ struct kvm_stage_item {          // one queued enqueue_k / enqueue_v
 
 struct kvm_state {
     int device = 0;
+    uint32_t n_cu = 256;         // compute units of the device (launch sizing)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string err;

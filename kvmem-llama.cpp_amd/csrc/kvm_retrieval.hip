@@ -977,7 +977,21 @@ static int score_topk_impl(kvm_state *st, const kvm_retrieval_lane *lanes, uint3
         // lanes; lanes with different kv-head counts share the largest chunk
         uint32_t max_h = 0;
         for (uint32_t i = 0; i < n_lanes; ++i) max_h = lanes[i].ix->n_head_kv > max_h ? lanes[i].ix->n_head_kv : max_h;
-        const int nt = max_h > 4 ? 1 : max_h > 2 ? 2 : max_h == 2 ? 4 : 8;
+        int nt = max_h > 4 ? 1 : max_h > 2 ? 2 : max_h == 2 ? 4 : 8;
+        // fewer tiles per workgroup (some chain lanes idle) while the scoring
+        // workgroups still all run at once, two per CU: one memory round trip and
+        // one chain per workgroup either way, so more of them finish sooner (a
+        // 256K-token lane at 4 kv heads: 256 workgroups of 8 blocks score and
+        // select in 15.8 us against 16.8 with 128 of 16)
+        while (nt > 1) {
+            uint64_t wgs = 0;
+            for (uint32_t i = 0; i < n_lanes; ++i) {
+                const uint32_t used = lanes[i].p->n_blocks ? kvm_cdiv(lanes[i].p->n_blocks, KVM_MEANK_TILE) : 0u;
+                wgs += (uint64_t)kvm_cdiv(used, (uint32_t)nt / 2) * lanes[i].ix->n_layer;
+            }
+            if (wgs > 2ull * st->n_cu) break;
+            nt /= 2;
+        }
         const dim3 grid(kvm_cdiv(max_tiles, (uint32_t)nt), max_layer, n_lanes), block(256);
         const bool d256 = lanes[0].ix->head_dim == 256;
         switch (nt) {

@@ -31,6 +31,9 @@ extern "C" kvm_state *kvm_state_create(int device) {
         return nullptr;
     }
     st->stream = st->own_stream;
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n_cu > 0)
+        st->n_cu = (uint32_t)n_cu;
     return st;
 }
 
