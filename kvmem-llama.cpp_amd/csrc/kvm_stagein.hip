@@ -7,9 +7,10 @@
 #include <cmath>
 #include <cstring>
 
-#define KVM_STAGEIN_WGS 256       // one per CU of an MI355X (the rows buffer takes most of the LDS)
+#define KVM_STAGEIN_IT 32         // tokens per item: half a window tile
+#define KVM_STAGEIN_WGS_PER_CU 2  // workgroups per CU (a 32-token rows buffer takes a third of the LDS)
 
-// One workgroup per CU walks the (plan entry, 64-token tile) items, so an
+// Two workgroups per CU walk the (plan entry, 32-token run) items, so an
 // empty plan (the steady state) costs one short launch; the plan length is
 // only known on the device (info[2]).  Every lane's plan in one launch
 // (blockIdx.y = lane): the lanes' windows, histories and plans are independent.
@@ -17,10 +18,10 @@ template <int D>
 __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     extern __shared__ __align__(16) uint8_t s_rows[];
     const stage_args &a = sl.lane[blockIdx.y];
-    const uint32_t tps = a.bt / 64;
+    const uint32_t tps = a.bt / KVM_STAGEIN_IT;
     const uint32_t n_items = a.info[3] != 0 ? 0u : a.info[2] * tps;
     for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        stagein_item<D, 256>(a, s_rows, item / tps, item % tps);
+        stagein_item<D, 256, KVM_STAGEIN_IT>(a, s_rows, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }
 }
@@ -129,8 +130,11 @@ extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane
     int rc = kvm_stage_prepare(st, lanes, n_lanes, rope, &sl, &max_items, &lds);
     if (rc) return rc;
     if (n_lanes == 0) return KVM_OK;
-    // about one workgroup per CU in all: an empty plan (the steady state) is one short launch
-    const uint32_t per_lane = (KVM_STAGEIN_WGS + n_lanes - 1) / n_lanes;
+    // kvm_stage_prepare sizes 64-token items; this kernel's are 32 tokens.  About
+    // two workgroups per CU in all: an empty plan (the steady state) is one short launch
+    max_items *= 64 / KVM_STAGEIN_IT;
+    lds = lds * KVM_STAGEIN_IT / 64;
+    const uint32_t wgs = KVM_STAGEIN_WGS_PER_CU * st->n_cu, per_lane = (wgs + n_lanes - 1) / n_lanes;
     const dim3 grid(max_items < per_lane ? max_items : per_lane, n_lanes);
     if (grid.x == 0) return KVM_OK;
     if (lanes[0].w->head_dim == 256) {

@@ -123,10 +123,12 @@ struct stage_args {
 };
 
 
-// One (plan entry, 64-token tile) item, staged by a workgroup of NTH threads
-// through the LDS rows buffer s_rows (64 * n_head_kv * (D/32) * 52 bytes).
-template <int D, int NTH>
+// One (plan entry, IT-token run) item, staged by a workgroup of NTH threads
+// through the LDS rows buffer s_rows (IT * n_head_kv * (D/32) * 52 bytes).  An
+// item of 32 tokens fills one key half (ks) of a 64-cell window tile.
+template <int D, int NTH, int IT = 64>
 __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt) {
+    static_assert(IT == 64 || IT == 32, "stage-in item size");
     constexpr uint32_t NB = D / 32;
     const uint32_t slot = a.stage_slots[si];
     const uint32_t id = a.ids[slot];
@@ -140,11 +142,11 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         return;
     }
     const uint32_t nt = a.h_tokens - first < a.bt ? (uint32_t)(a.h_tokens - first) : a.bt;
-    const uint32_t t0 = tt * 64;
-    const uint32_t count = nt > t0 ? (nt - t0 < 64 ? nt - t0 : 64) : 0;
+    const uint32_t t0 = tt * IT;
+    const uint32_t count = nt > t0 ? (nt - t0 < IT ? nt - t0 : IT) : 0;
     const uint64_t htok0 = first + t0;
     const uint32_t rowK = a.H * NB * 34, rowV = a.H * NB * 18;
-    uint8_t *lk = s_rows, *lv = s_rows + 64 * rowK;
+    uint8_t *lk = s_rows, *lv = s_rows + IT * rowK;
     // bulk copy of `count` consecutive token rows of K and V (contiguous in host memory)
     const uint8_t *gk = a.hk + htok0 * rowK, *gv = a.hv + htok0 * rowV;
     const uint32_t nk = count * rowK, nv = count * rowV;
@@ -160,25 +162,26 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     }
     __syncthreads();
 
-    const uint32_t tile = (slot * a.bt + t0) / 64;
+    const uint32_t tile = (slot * a.bt + t0) / 64, c0 = t0 % 64;   // c0: the item's first cell in the tile
     // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ...
     const uint32_t wave = tid >> 6;
     for (uint32_t r = wave; r < count * a.H; r += NTH / 64) {
         const uint32_t j = r / a.H, h = r % a.H;
         uint8_t *kt = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
-        stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, j, base + (int32_t)(t0 + j), a.rc);
+        stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, c0 + j, base + (int32_t)(t0 + j), a.rc);
     }
     // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
-    for (uint32_t wi = tid; wi < a.H * D * 8; wi += NTH) {
-        const uint32_t h = wi / (D * 8), r = wi % (D * 8);
-        const uint32_t X = r >> 1, ks = r & 1u;
+    constexpr uint32_t NKS = IT / 32;    // key halves of the tile this item fills
+    for (uint32_t wi = tid; wi < a.H * D * 4 * NKS; wi += NTH) {
+        const uint32_t h = wi / (D * 4 * NKS), r = wi % (D * 4 * NKS);
+        const uint32_t X = r / NKS, ks = NKS == 2 ? (r & 1u) : c0 / 32;
         const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
         const uint32_t b = dd / 32, e = dd % 32;
         uint32_t word = 0;
 #pragma unroll
         for (uint32_t j = 0; j < 8; ++j) {
-            const uint32_t cj = 32 * ks + 8 * gg + j;
+            const uint32_t cj = 32 * ks + 8 * gg + j - c0;    // key within the item
             uint32_t nib = 0;
             if (cj < count) {
                 const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
@@ -188,9 +191,9 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         }
         *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
     }
-    for (uint32_t si2 = tid; si2 < a.H * 64 * NB; si2 += NTH) {
-        const uint32_t h = si2 / (64 * NB), cj = (si2 / NB) % 64, b = si2 % NB;
-        uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, cj, b);
+    for (uint32_t si2 = tid; si2 < a.H * IT * NB; si2 += NTH) {
+        const uint32_t h = si2 / (IT * NB), cj = (si2 / NB) % IT, b = si2 % NB;
+        uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, c0 + cj, b);
         if (cj < count) {
             const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
             sd[0] = blk[0];
@@ -200,7 +203,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
             sd[1] = 0;
         }
     }
-    if (tid < 64) a.cell_pos[slot * a.bt + t0 + tid] = tid < count ? base + (int32_t)(t0 + tid) : -1;
+    if (tid < IT) a.cell_pos[slot * a.bt + t0 + tid] = tid < count ? base + (int32_t)(t0 + tid) : -1;
     if (tt == 0 && tid == 0) {
         a.slot_block[slot] = id;
         a.slot_base[slot] = base;
