@@ -78,8 +78,9 @@ def _case(seed, n_blocks, n_layer=1, n_head=24, H=4, D=256, planted=16):
 
 @pytest.mark.parametrize("n_blocks,n_layer,n_head,H,D", [(2048, 1, 24, 4, 256), (128, 1, 8, 2, 128),
                                                        (300, 3, 24, 4, 256), (5000, 1, 24, 4, 256),
-                                                       # tiles per workgroup 1 (8 and 16 kv heads), 2 with a
-                                                       # partly filled head chunk (3), 8 (1 kv head)
+                                                       # 8-block workgroups with full (8 kv heads), split
+                                                       # (16) and partly filled (3, 1) head chunks; 5000
+                                                       # blocks at 4 kv heads take 16-block workgroups
                                                        (700, 2, 8, 8, 128), (260, 1, 32, 16, 128),
                                                        (500, 1, 12, 3, 128), (333, 1, 3, 1, 256)])
 def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
@@ -134,6 +135,34 @@ def test_score_topk_lanes_match_single_lane(kvm_state):
         assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
         assert np.array_equal(r["ids"], O.pick_topk(want, 128, 1, 0))
         assert set(planted) <= set(r["ids"])
+
+
+@pytest.mark.parametrize("H,n_head,D", [(2, 8, 128), (1, 3, 256)])
+def test_score_topk_lanes_wide_grids(kvm_state, H, n_head, D):
+    """Four lanes of 8192 blocks (the top-k maximum) at 2 or 1 kv heads: the
+    scoring grid then takes 4 or 8 tiles (32 or 64 blocks) per workgroup; every
+    lane's scores are bit-exact and its ids equal the oracle's."""
+    n_blocks, lanes, cases = 8192, [], []
+    for i in range(4):
+        q, qc, k_sum, mt, _ = _case(300 + i, n_blocks, 1, n_head, H, D)
+        ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+        qa = api.QueryAcc(kvm_state, 1, n_head, D)
+        qa.q_sum.copy_(dev(q))
+        qa.q_count.copy_(dev(qc.astype(np.int32)))
+        lanes.append(dict(index=ix, query=qa, n_blocks=n_blocks, n_tokens=dev(np.full(n_blocks, 128, np.int32)),
+                          budget_blocks=128, sink_blocks=1, window=api.KVWindow(kvm_state, 128 * 128, H, D, 128),
+                          sel=api.SelectionBuffers(kvm_state, n_blocks, 128)))
+        cases.append((q, qc, k_sum, mt))
+    api.score_topk_lanes(kvm_state, lanes)
+    for ln, (q, qc, k_sum, mt) in zip(lanes, cases):
+        r = ln["sel"].result()
+        assert r["status"] == 0
+        want = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
+        got = host(ln["sel"].scores)[:n_blocks]
+        assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+        assert np.array_equal(r["ids"], O.pick_topk(want, 128, 1, 0))
+        # (no planted-block check: with 8192 blocks and 128- or 256-dim heads some
+        # random blocks outscore a planted one; the oracle's selection is the check)
 
 
 KATS = [
