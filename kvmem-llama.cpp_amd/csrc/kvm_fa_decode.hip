@@ -627,9 +627,11 @@ __global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
     }
     L = kvm_wave_sum_f32(L);
     __syncthreads();
-    float acc = 0.0f;
+    // four partial sums: a quarter of the dependent adds in the chain
+    float acc4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) acc += j < (int)S ? v[j] * s_w[j] : 0.0f;
+    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) acc4[j & 3] += j < (int)S ? v[j] * s_w[j] : 0.0f;
+    float acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
     for (uint32_t s0 = KVM_COMBINE_BATCH; s0 < S; s0 += 32) {
         float u[32];
 #pragma unroll
@@ -719,10 +721,11 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     if (D == 256) launch_decode_d<256>(a, n_lanes, max_rows, quant, st->stream);
     else launch_decode_d<128>(a, n_lanes, max_rows, quant, st->stream);
     KVM_LAUNCH_CHECK(st, "fa_decode");
+    // one wave per (row, 64 dims) of the rows some lane has
     if (D == 256)
-        hipLaunchKernelGGL(k_fa_combine<256>, dim3(rmax * 4, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
+        hipLaunchKernelGGL(k_fa_combine<256>, dim3(max_rows * 4, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
     else
-        hipLaunchKernelGGL(k_fa_combine<128>, dim3(rmax * 2, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
+        hipLaunchKernelGGL(k_fa_combine<128>, dim3(max_rows * 2, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
     KVM_LAUNCH_CHECK(st, "fa_combine");
     return KVM_OK;
 }
