@@ -345,6 +345,40 @@ int kvm_fa_prefill(kvm_state *st, const kvm_window *w, const void *q, int q_type
 int kvm_d2d_batched(kvm_state *st, const void *const *src, void *const *dst,
                     const size_t *nbytes, int n);
 
+/* ------------------------------------------------------------------------ */
+/* Host history from the reference's raw-store session snapshot: the format  */
+/* RawKvStore::snapshot_write emits (kvmem/src/host/raw_kv_store.cpp:1225-1247) */
+/* and snapshot_read checks (1249-1287).  Host-side parsing only, no GPU work; */
+/* st only receives the error message and may be NULL.                        */
+/* ------------------------------------------------------------------------ */
+typedef struct kvm_snapshot_info {
+    uint32_t n_layer, n_embd_k, n_embd_v, block_tokens;
+    uint64_t k_row_bytes;      /* unrotated K row (0 in the file = fp16 rows: 2 * n_embd_k) */
+    uint64_t k_gpu_row_bytes;  /* packed rotated K row, 0 = none */
+    uint64_t v_gpu_row_bytes;  /* packed V row, 0 = none */
+    uint64_t n_blocks;
+} kvm_snapshot_info;
+int kvm_snapshot_info_read(kvm_state *st, const void *snap, size_t bytes, kvm_snapshot_info *info);
+
+/* One layer's history, in the layout kvm_history_* and the stage-in read:
+ * K rows and packed V rows token-major, block b at row b * block_tokens (rows
+ * a block does not hold are zero); the mean-K sum (n_embd_k fp32), its token
+ * count and the block's token count per block.  NULL outputs are skipped.
+ * Snapshots with more than max_blocks blocks are refused (the reference
+ * reader's max_blocks, raw_kv_store.cpp:1255-1256); fp16-only V is refused. */
+typedef struct kvm_snapshot_layer {
+    uint8_t *k_rows;
+    size_t k_rows_bytes;       /* >= n_blocks * block_tokens * k_row_bytes */
+    uint8_t *v_rows;
+    size_t v_rows_bytes;       /* >= n_blocks * block_tokens * v_gpu_row_bytes */
+    float *k_sum;              /* n_blocks * n_embd_k */
+    uint32_t *mean_tokens;     /* n_blocks */
+    uint32_t *n_tokens;        /* n_blocks */
+    uint64_t max_blocks;
+} kvm_snapshot_layer;
+int kvm_snapshot_read_layer(kvm_state *st, const void *snap, size_t bytes, uint32_t layer,
+                            const kvm_snapshot_layer *out);
+
 #ifdef __cplusplus
 }
 #endif

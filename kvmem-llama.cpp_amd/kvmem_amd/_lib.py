@@ -77,6 +77,18 @@ class Lane(C.Structure):
                 ("out", C.c_void_p), ("n_tokens", C.c_uint32)]
 
 
+class SnapshotInfo(C.Structure):
+    _fields_ = [("n_layer", C.c_uint32), ("n_embd_k", C.c_uint32), ("n_embd_v", C.c_uint32),
+                ("block_tokens", C.c_uint32), ("k_row_bytes", C.c_uint64), ("k_gpu_row_bytes", C.c_uint64),
+                ("v_gpu_row_bytes", C.c_uint64), ("n_blocks", C.c_uint64)]
+
+
+class SnapshotLayer(C.Structure):
+    _fields_ = [("k_rows", C.c_void_p), ("k_rows_bytes", C.c_size_t), ("v_rows", C.c_void_p),
+                ("v_rows_bytes", C.c_size_t), ("k_sum", C.c_void_p), ("mean_tokens", C.c_void_p),
+                ("n_tokens", C.c_void_p), ("max_blocks", C.c_uint64)]
+
+
 _P = C.c_void_p
 _u32, _i32, _i64, _sz, _f = C.c_uint32, C.c_int32, C.c_int64, C.c_size_t, C.c_float
 _PW = C.POINTER(Window)
@@ -123,6 +135,8 @@ SIGNATURES = {
     "kvm_fa_decode_lanes": (C.c_int, [_P, C.POINTER(Lane), _u32, C.c_int, _u32, _f]),
     "kvm_fa_prefill": (C.c_int, [_P, _PW, _P, C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_d2d_batched": (C.c_int, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), C.c_int]),
+    "kvm_snapshot_info_read": (C.c_int, [_P, _P, _sz, C.POINTER(SnapshotInfo)]),
+    "kvm_snapshot_read_layer": (C.c_int, [_P, _P, _sz, _u32, C.POINTER(SnapshotLayer)]),
 }
 
 _lib = None

@@ -447,3 +447,31 @@ def dequantize_rows(st, ty, rows, n_per_row):
     out = torch.empty((n_rows, n_per_row), dtype=torch.float32, device=rows.device)
     st.check(st.lib.kvm_dequantize_rows(st.h, ty, _ptr(rows), _ptr(out), n_rows, n_per_row))
     return out
+
+
+def read_snapshot(data, max_blocks=1 << 20):
+    """Parse the reference's raw-store session snapshot (RawKvStore::snapshot_write,
+    raw_kv_store.cpp:1225-1247) into per-layer host arrays in the history layout:
+    k_rows / v_rows [n_blocks * block_tokens, row bytes] (uint8), k_sum [n_blocks,
+    n_embd_k], mean_tokens and n_tokens [n_blocks].  Host-side parsing only."""
+    lib = L.load()
+    buf = np.frombuffer(data, dtype=np.uint8)
+    info = L.SnapshotInfo()
+    rc = lib.kvm_snapshot_info_read(None, buf.ctypes.data, buf.size, C.byref(info))
+    if rc:
+        raise RuntimeError(f"kvm_snapshot_info_read: {rc}")
+    nb, bt = int(info.n_blocks), int(info.block_tokens)
+    layers = []
+    for il in range(info.n_layer):
+        k = np.zeros((nb * bt, int(info.k_row_bytes)), np.uint8)
+        v = np.zeros((nb * bt, int(info.v_gpu_row_bytes)), np.uint8)
+        ks = np.zeros((nb, int(info.n_embd_k)), np.float32)
+        mt = np.zeros(nb, np.uint32)
+        nt = np.zeros(nb, np.uint32)
+        out = L.SnapshotLayer(k.ctypes.data, k.nbytes, v.ctypes.data if v.size else None, v.nbytes,
+                              ks.ctypes.data, mt.ctypes.data, nt.ctypes.data, max_blocks)
+        rc = lib.kvm_snapshot_read_layer(None, buf.ctypes.data, buf.size, il, C.byref(out))
+        if rc:
+            raise RuntimeError(f"kvm_snapshot_read_layer: {rc}")
+        layers.append(dict(k_rows=k, v_rows=v, k_sum=ks, mean_tokens=mt, n_tokens=nt))
+    return {f: getattr(info, f) for f, _ in L.SnapshotInfo._fields_}, layers

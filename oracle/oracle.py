@@ -77,6 +77,9 @@ def ref():
         _r.ref_set_selection_seq.argtypes = [u32, u32, P, P, u32, P, u32, P, P, P, P, P, u32, P]
         _r.ref_mean_k.restype = C.c_int
         _r.ref_mean_k.argtypes = [u32, u32, u32, u32, P, P]
+        _r.ref_raw_snapshot.restype = C.c_longlong
+        _r.ref_raw_snapshot.argtypes = [u32, u32, u32, u32, C.c_uint64, C.c_uint64, u32, u32, P, P, P, P,
+                                        C.c_uint64]
         _r.ref_rope_neox.restype = None
         _r.ref_rope_neox.argtypes = [u32, u32, u32, f, f, P, u32, i32, P]
     return _r
@@ -250,6 +253,21 @@ def ref_set_selection_seq(total_tokens, block_tokens, selections):
     assert rc == 0
     return {"remaps": remaps[:n_remaps[0]], "stage_in": sin[:nin[0]].astype(np.int64),
             "stage_out": sout[:nout[0]].astype(np.int64), "total": int(total[0])}
+
+
+def ref_raw_snapshot(k_rows, k_f32, v_rows, n_embd_k, n_embd_v, block_tokens, chunk):
+    """The reference RawKvStore filled with [n_layer][n_tokens] K rows (+ their fp32
+    values for the mean) and packed V rows, then snapshot_write: the snapshot bytes."""
+    k_rows, v_rows = np.ascontiguousarray(k_rows, np.uint8), np.ascontiguousarray(v_rows, np.uint8)
+    k_f32 = np.ascontiguousarray(k_f32, np.float32)
+    n_layer, n_tokens, krb = k_rows.shape
+    vrb = v_rows.shape[2]
+    args = (n_layer, n_embd_k, n_embd_v, block_tokens, krb, vrb, n_tokens, chunk, _p(k_rows), _p(k_f32), _p(v_rows))
+    n = ref().ref_raw_snapshot(*args, None, 0)
+    assert n > 0
+    out = np.zeros(n, np.uint8)
+    assert ref().ref_raw_snapshot(*args, _p(out), n) == n
+    return out.tobytes()
 
 
 def ref_mean_k(k, block_tokens, chunk):

@@ -8,6 +8,7 @@
 #include "kvmem/kvmem_store.hpp"
 #include "kvmem/raw_kv_store.hpp"
 #include "kvmem/rope.hpp"
+#include "kvmem/snapshot.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -114,6 +115,46 @@ int ref_mean_k(uint32_t n_embd, uint32_t block_tokens, uint32_t n_tokens, uint32
         const uint32_t nb = (n_tokens + block_tokens - 1) / block_tokens;
         for (uint32_t b = 0; b < nb; ++b) raw.mean_k(b, 0, means + static_cast<size_t>(b) * n_embd);
         return static_cast<int>(nb);
+    } catch (const std::exception &) {
+        return -1;
+    }
+}
+
+// RawKvStore::write_layer_k_rows (raw_kv_store.cpp:560-598; the fp32 rows feed
+// the block mean-K sums) and write_layer_v_gpu (600-646) for every layer in
+// chunks of `chunk` tokens, then RawKvStore::snapshot_write (1225-1247) through
+// a SnapshotWriter (snapshot.hpp:21-48).  k_rows [n_layer][n_tokens][k_row_bytes],
+// k_f32 [n_layer][n_tokens][n_embd_k], v_rows [n_layer][n_tokens][v_gpu_row_bytes].
+// Returns the snapshot's byte count (copied to out only if it fits in cap), or -1.
+long long ref_raw_snapshot(uint32_t n_layer, uint32_t n_embd_k, uint32_t n_embd_v, uint32_t block_tokens,
+                           uint64_t k_row_bytes, uint64_t v_gpu_row_bytes, uint32_t n_tokens, uint32_t chunk,
+                           const uint8_t *k_rows, const float *k_f32, const uint8_t *v_rows, uint8_t *out,
+                           uint64_t cap) {
+    try {
+        kvmem::RawKvStoreConfig cfg;
+        cfg.n_layer = n_layer;
+        cfg.n_embd_k = n_embd_k;
+        cfg.n_embd_v = n_embd_v;
+        cfg.block_tokens = block_tokens;
+        cfg.k_row_bytes = k_row_bytes;
+        cfg.v_gpu_row_bytes = v_gpu_row_bytes;
+        kvmem::RawKvStore raw(cfg);
+        for (uint32_t il = 0; il < n_layer; ++il)
+            for (uint32_t pos = 0; pos < n_tokens;) {
+                const uint32_t n = std::min(chunk, n_tokens - pos);
+                const size_t t = static_cast<size_t>(il) * n_tokens + pos;
+                raw.write_layer_k_rows(pos, n, il, k_rows + t * k_row_bytes, k_f32 + t * n_embd_k);
+                raw.write_layer_v_gpu(pos, n, il, v_rows + t * v_gpu_row_bytes);
+                pos += n;
+            }
+        std::vector<uint8_t> bytes;
+        kvmem::SnapshotWriter w([&](const void *p, size_t n) {
+            const uint8_t *b = static_cast<const uint8_t *>(p);
+            bytes.insert(bytes.end(), b, b + n);
+        });
+        raw.snapshot_write(w);
+        if (bytes.size() <= cap) std::memcpy(out, bytes.data(), bytes.size());
+        return static_cast<long long>(bytes.size());
     } catch (const std::exception &) {
         return -1;
     }
