@@ -55,6 +55,38 @@ def test_stagein_selection_bytes(kvm_state, n_rot, hadamard, freq_base):
     assert len(sel2.result()["stage_slots"]) == 0
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
+def test_stagein_from_reference_snapshot(kvm_state):
+    """The host history format end to end: the reference's RawKvStore holds the
+    q8_0 K / q4_0 V rows and writes its session snapshot, kvm_snapshot_read_layer
+    turns it into the history, and the stage-in of a selection from it equals the
+    oracle's bytes for the original rows."""
+    H, D, bt, n_blocks = 4, 256, 128, 24
+    n_hist = n_blocks * bt - 40
+    rng = np.random.default_rng(77)
+    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    kf = rng.standard_normal((1, n_hist, H * D)).astype(np.float32)
+    snap = O.ref_raw_snapshot(kr[None], kf, vr[None], H * D, H * D, bt, 100)
+    info, layers = api.read_snapshot(snap)
+    assert info["n_blocks"] == n_blocks
+    hist = api.History(layers[0]["k_rows"][:n_hist], layers[0]["v_rows"][:n_hist])
+    w = api.KVWindow(kvm_state, 8 * bt, H, D, bt)
+    s = rng.standard_normal(n_blocks)
+    s[n_blocks - 1] = 10.0                          # the partial last block too
+    nt = layers[0]["n_tokens"].astype(np.int32)
+    sel = api.select_topk(kvm_state, dev(s), dev(nt), 8, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    res = sel.result()
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, ev = w.export_rows(0, 8 * bt)
+    ek, ev = host(ek), host(ev)
+    for k, (bid, base) in enumerate(zip(res["ids"], res["to_base"])):
+        n = int(nt[bid])
+        want = O.stagein_k(kr[bid * bt:bid * bt + n].reshape(-1), n, H, D, 64, 256, int(base), theta).reshape(n, -1)
+        assert np.array_equal(ek[k * bt:k * bt + n], want), (k, bid)
+        assert np.array_equal(ev[k * bt:k * bt + n], vr[bid * bt:bid * bt + n])
+
+
 def test_stagein_reselect_moves_only_changed_slots(kvm_state):
     H, D, bt, n_blocks = 4, 256, 128, 30
     hist, kr, vr = _history(9, n_blocks * bt, H, D)
