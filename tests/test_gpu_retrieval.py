@@ -165,6 +165,40 @@ def test_score_topk_lanes_wide_grids(kvm_state, H, n_head, D):
         # random blocks outscore a planted one; the oracle's selection is the check)
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
+def test_score_topk_from_reference_snapshot(kvm_state):
+    """The mean-K index read out of the reference's raw-store snapshot (block sums
+    and token counts the reference's RawKvStore accumulated) scores and selects
+    exactly as the oracle does on the same sums."""
+    H, n_head, D, bt, n_blocks = 4, 24, 256, 128, 300
+    n_hist = n_blocks * bt - 61
+    rng = np.random.default_rng(88)
+    kf = rng.standard_normal((1, n_hist, H * D)).astype(np.float32)
+    kr = rng.integers(0, 256, (1, n_hist, H * D // 32 * 34), dtype=np.uint8)
+    vr = rng.integers(0, 256, (1, n_hist, H * D // 32 * 18), dtype=np.uint8)
+    info, layers = api.read_snapshot(O.ref_raw_snapshot(kr, kf, vr, H * D, H * D, bt, 96))
+    k_sum, mt = layers[0]["k_sum"][None], layers[0]["mean_tokens"][None]
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+    planted = rng.choice(np.arange(1, n_blocks), 12, replace=False)
+    g = n_head // H
+    q = np.zeros((1, n_head * D), np.float32)
+    for b in planted:
+        mean = k_sum[0, b] * (np.float32(1.0) / np.float32(mt[0, b]))
+        for h in range(n_head):
+            q[0, h * D:(h + 1) * D] += mean[(h // g) * D:(h // g + 1) * D]
+    q += (rng.standard_normal(q.shape) * 0.1).astype(np.float32)
+    qc = np.array([4], np.uint32)
+    qa = api.QueryAcc(kvm_state, 1, n_head, D)
+    qa.q_sum.copy_(dev(q))
+    qa.q_count.copy_(dev(qc.astype(np.int32)))
+    nt = dev(layers[0]["n_tokens"].astype(np.int32))
+    sel = api.score_topk(kvm_state, ix, qa, n_blocks, nt, 32, 1, 0, None, api.KVWindow(kvm_state, 32 * bt, H, D, bt))
+    want = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
+    assert np.array_equal(host(sel.scores)[:n_blocks].view(np.uint64), want.view(np.uint64))
+    assert np.array_equal(sel.result()["ids"], O.pick_topk(want, 32, 1, 0))
+    assert set(planted) <= set(sel.result()["ids"])
+
+
 KATS = [
     # (scores, budget, sink, recent, mandatory, expected) -- kvmem_store_test.cpp
     ({5: 100.0, 6: 90.0, 3: 10.0}, 4, 1, 1, [], [0, 5, 6, 9]),
