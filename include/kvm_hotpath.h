@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 1
+#define KVM_ABI_VERSION 2
 
 enum kvm_status {
     KVM_OK = 0,
@@ -364,8 +364,13 @@ int kvm_snapshot_info_read(kvm_state *st, const void *snap, size_t bytes, kvm_sn
  * K rows and packed V rows token-major, block b at row b * block_tokens (rows
  * a block does not hold are zero); the mean-K sum (n_embd_k fp32), its token
  * count and the block's token count per block.  NULL outputs are skipped.
- * Snapshots with more than max_blocks blocks are refused (the reference
- * reader's max_blocks, raw_kv_store.cpp:1255-1256); fp16-only V is refused. */
+ * Refusals follow the reference reader (raw_kv_store.cpp:1249-1287): a snapshot
+ * of more than max_blocks + 1 blocks (max_blocks is the store's block count;
+ * UINT64_MAX = no limit), and, when `expect` is given, one whose geometry
+ * differs from it (its SnapshotReader::expect of each configured field).
+ * Without `expect` the header is bounded instead: n_embd_k, n_embd_v <= 2^20,
+ * block_tokens <= 2^16 and rows at most 4 bytes per value.  fp16-only V is
+ * refused.  The per-block outputs hold n_blocks (<= max_blocks + 1) entries. */
 typedef struct kvm_snapshot_layer {
     uint8_t *k_rows;
     size_t k_rows_bytes;       /* >= n_blocks * block_tokens * k_row_bytes */
@@ -375,6 +380,7 @@ typedef struct kvm_snapshot_layer {
     uint32_t *mean_tokens;     /* n_blocks */
     uint32_t *n_tokens;        /* n_blocks */
     uint64_t max_blocks;
+    const kvm_snapshot_info *expect;   /* the store's configuration, or NULL */
 } kvm_snapshot_layer;
 int kvm_snapshot_read_layer(kvm_state *st, const void *snap, size_t bytes, uint32_t layer,
                             const kvm_snapshot_layer *out);

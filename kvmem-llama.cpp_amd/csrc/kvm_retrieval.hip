@@ -864,8 +864,21 @@ static int make_topk(kvm_state *st, const double *scores, const double *layer_sc
                      const kvm_window *w, const kvm_selection *out, topk_args *ta) {
     if (w && (kvm_window_check(w) || !w->slot_block || !w->slot_base))
         return kvm_fail(st, KVM_EINVAL, "topk: bad window or window without slot map");
+    const uint32_t *ntok = p->n_tokens;
+    if (p->n_blocks == 0) {
+        // The kernel's first phase loads element 0 of the score and token-count
+        // arrays unconditionally (its values are unused when there is no block);
+        // a selection over no blocks may pass NULL or empty arrays, so those
+        // loads read the state's workspace instead.
+        void *z = kvm_workspace(st, 64);
+        if (!z) return kvm_fail(st, KVM_ENOMEM, "topk: workspace");
+        scores = (const double *)z;
+        layer_score = nullptr;
+        ntok = (const uint32_t *)z;
+        ix = nullptr;
+    }
     *ta = topk_args{scores, layer_score, q ? q->q_count : nullptr, ix ? ix->present : nullptr, out->scores,
-                    p->n_tokens, p->mandatory,
+                    ntok, p->mandatory,
                     w ? w->slot_block : nullptr, w ? w->slot_base : nullptr,
                     out->ids, out->to_base, out->stage_slots, out->info,
                     p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
@@ -888,7 +901,7 @@ static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes, in
 
 static int check_select(kvm_state *st, const kvm_select_params *p, const kvm_selection *out) {
     if (!p || !out) return kvm_fail(st, KVM_EINVAL, "select: null argument");
-    if (!p->n_tokens || !out->ids || !out->to_base || !out->stage_slots || !out->info)
+    if ((p->n_blocks && !p->n_tokens) || !out->ids || !out->to_base || !out->stage_slots || !out->info)
         return kvm_fail(st, KVM_EINVAL, "select: null buffer");
     if (p->n_blocks > KVM_MAX_TOPK_BLOCKS) return kvm_fail(st, KVM_ERANGE, "select: n_blocks %u > %u", p->n_blocks, KVM_MAX_TOPK_BLOCKS);
     const uint32_t want = p->budget_blocks == 0 || p->n_blocks <= p->budget_blocks ? p->n_blocks : p->budget_blocks;

@@ -16,6 +16,10 @@
 
 #include <cstring>
 
+// Bounds a reader without the store's configuration puts on header fields.
+#define KVM_SNAPSHOT_MAX_EMBD (1u << 20)
+#define KVM_SNAPSHOT_MAX_BLOCK_TOKENS (1u << 16)
+
 namespace {
 
 struct snap_cursor {
@@ -56,9 +60,36 @@ int read_header(kvm_state *st, snap_cursor &c, kvm_snapshot_info *info) {
     if (!c.ok) return kvm_fail(st, KVM_EINVAL, "snapshot: truncated header");
     if (info->n_layer == 0 || info->block_tokens == 0 || info->n_blocks > c.left / 8)
         return kvm_fail(st, KVM_EINVAL, "snapshot: invalid header");
-    // k_row_bytes 0 means fp16 K rows (raw_kv_store.hpp:29)
+    // k_row_bytes 0 means fp16 K rows (raw_kv_store.hpp:32)
     if (info->k_row_bytes == 0) info->k_row_bytes = (uint64_t)info->n_embd_k * 2;
+    // The reference reader compares every geometry field with its store's
+    // configuration (raw_kv_store.cpp:1251-1254).  A reader without one still
+    // bounds them: a row is at most fp32 wide, and a block holds at most
+    // KVM_SNAPSHOT_MAX_BLOCK_TOKENS rows, so every size product below stays far
+    // from 64-bit overflow.
+    if (info->n_embd_k == 0 || info->n_embd_k > KVM_SNAPSHOT_MAX_EMBD || info->n_embd_v > KVM_SNAPSHOT_MAX_EMBD ||
+        info->block_tokens > KVM_SNAPSHOT_MAX_BLOCK_TOKENS || info->k_row_bytes > 4ull * info->n_embd_k ||
+        info->k_gpu_row_bytes > 4ull * info->n_embd_k || info->v_gpu_row_bytes > 4ull * info->n_embd_v)
+        return kvm_fail(st, KVM_EINVAL, "snapshot: row geometry out of bounds");
     return KVM_OK;
+}
+
+// The reference's SnapshotReader::expect of each configured field
+// (raw_kv_store.cpp:1251-1254); k_row_bytes 0 stands for fp16 rows on both sides.
+int check_expected(kvm_state *st, const kvm_snapshot_info &in, const kvm_snapshot_info *ex) {
+    if (!ex) return KVM_OK;
+    const uint64_t ekr = ex->k_row_bytes ? ex->k_row_bytes : (uint64_t)ex->n_embd_k * 2;
+    if (in.n_layer != ex->n_layer || in.n_embd_k != ex->n_embd_k || in.n_embd_v != ex->n_embd_v ||
+        in.block_tokens != ex->block_tokens || in.k_row_bytes != ekr || in.k_gpu_row_bytes != ex->k_gpu_row_bytes ||
+        in.v_gpu_row_bytes != ex->v_gpu_row_bytes)
+        return kvm_fail(st, KVM_EINVAL, "snapshot: geometry differs from the store's configuration");
+    return KVM_OK;
+}
+
+// a * b * c, false on 64-bit overflow
+bool mul3(uint64_t a, uint64_t b, uint64_t c, uint64_t *r) {
+    uint64_t t;
+    return !__builtin_mul_overflow(a, b, &t) && !__builtin_mul_overflow(t, c, r);
 }
 
 }  // namespace
@@ -76,16 +107,24 @@ extern "C" int kvm_snapshot_read_layer(kvm_state *st, const void *snap, size_t b
     kvm_snapshot_info in{};
     int rc = read_header(st, c, &in);
     if (rc) return rc;
+    rc = check_expected(st, in, out->expect);
+    if (rc) return rc;
     if (layer >= in.n_layer) return kvm_fail(st, KVM_ERANGE, "snapshot: layer %u of %u", layer, in.n_layer);
     const uint64_t bt = in.block_tokens, nb = in.n_blocks;
-    if (nb > out->max_blocks)
-        return kvm_fail(st, KVM_ERANGE, "snapshot: %llu blocks > %llu", (unsigned long long)nb, (unsigned long long)out->max_blocks);
-    if (out->k_rows && out->k_rows_bytes < nb * bt * in.k_row_bytes)
+    // the reference reader's block-count rule: a store of max_blocks blocks may
+    // hold one more, partly filled (raw_kv_store.cpp:1255-1257)
+    if (out->max_blocks != UINT64_MAX && nb > out->max_blocks + 1)
+        return kvm_fail(st, KVM_ERANGE, "snapshot: %llu blocks > %llu + 1", (unsigned long long)nb,
+                        (unsigned long long)out->max_blocks);
+    uint64_t k_need = 0, v_need = 0;
+    if (!mul3(nb, bt, in.k_row_bytes, &k_need) || !mul3(nb, bt, in.v_gpu_row_bytes, &v_need))
+        return kvm_fail(st, KVM_EINVAL, "snapshot: history size overflows");
+    if (out->k_rows && out->k_rows_bytes < k_need)
         return kvm_fail(st, KVM_ERANGE, "snapshot: K rows buffer of %zu bytes < %llu", out->k_rows_bytes,
-                        (unsigned long long)(nb * bt * in.k_row_bytes));
-    if (out->v_rows && out->v_rows_bytes < nb * bt * in.v_gpu_row_bytes)
+                        (unsigned long long)k_need);
+    if (out->v_rows && out->v_rows_bytes < v_need)
         return kvm_fail(st, KVM_ERANGE, "snapshot: V rows buffer of %zu bytes < %llu", out->v_rows_bytes,
-                        (unsigned long long)(nb * bt * in.v_gpu_row_bytes));
+                        (unsigned long long)v_need);
     for (uint64_t b = 0; b < nb; ++b) {
         const uint64_t size = c.scalar<uint64_t>();
         if (!c.ok || size > c.left) return kvm_fail(st, KVM_EINVAL, "snapshot: truncated block %llu", (unsigned long long)b);

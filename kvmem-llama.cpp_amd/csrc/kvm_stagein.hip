@@ -19,7 +19,9 @@ __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     extern __shared__ __align__(16) uint8_t s_rows[];
     const stage_args &a = sl.lane[blockIdx.y];
     const uint32_t tps = a.bt / KVM_STAGEIN_IT;
-    const uint32_t n_items = a.info[3] != 0 ? 0u : a.info[2] * tps;
+    // the plan bits of the status (1 = over capacity, 2 = more blocks than
+    // slots); bit 4, a block past the history, is set by this kernel itself
+    const uint32_t n_items = (a.info[3] & 3u) != 0 ? 0u : a.info[2] * tps;
     for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
         stagein_item<D, 256, KVM_STAGEIN_IT>(a, s_rows, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
@@ -165,7 +167,8 @@ struct kitem_desc {
     int32_t *cell_pos;
     uint32_t n_tiles, H, cell0, nt;
     int32_t pos0;
-    int32_t nrot;
+    int32_t nrot;       // Hadamard width of this item, 0 = off
+    float hscale;       // 1 / sqrtf(nrot), per item: items of different widths may share a flush
 };
 
 template <int D>
@@ -177,7 +180,7 @@ __global__ void __launch_bounds__(256) k_stagein_items(const kitem_desc *items, 
     if (t >= it.nt) return;
     rope_ctx rc = rc0;
     rc.nrot = it.nrot;
-    rc.hscale = it.nrot > 0 ? rc0.hscale : 1.0f;
+    rc.hscale = it.hscale;
     const uint32_t cell = it.cell0 + t;
     uint8_t *kt = it.wk + ((uint64_t)h * it.n_tiles + cell / 64) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
     stage_k_row<D>(it.src + (uint64_t)t * it.H * NB * 34 + h * NB * 34, kt, cell % 64,
@@ -290,7 +293,6 @@ extern "C" int kvm_stagein_flush(kvm_state *st) {
     for (int D : {128, 256}) {
         std::vector<kitem_desc> ds;
         uint32_t max_rows = 0, max_pos = 0, n_half = 0;
-        float hscale = 1.0f;
         for (const auto &it : items) {
             if (it.kind != 0 || it.w.head_dim != (uint32_t)D) continue;
             kitem_desc d;
@@ -303,11 +305,12 @@ extern "C" int kvm_stagein_flush(kvm_state *st) {
             d.nt = it.nt;
             d.pos0 = it.pos0;
             d.nrot = it.nrot;
+            // the reference computes the scale on the host (llama-kvmem-stagein.cu:594)
+            d.hscale = it.nrot > 0 ? 1.0f / sqrtf((float)it.nrot) : 1.0f;
             ds.push_back(d);
             max_rows = std::max(max_rows, it.nt * it.w.n_head_kv);
             max_pos = std::max(max_pos, (uint32_t)std::max(0, it.pos0) + it.nt);
             n_half = it.n_rot / 2;
-            if (it.nrot > 0) hscale = 1.0f / sqrtf((float)it.nrot);
             if (it.pos0 < 0) rc = kvm_fail(st, KVM_EINVAL, "flush: negative pos0");
         }
         if (ds.empty() || rc) continue;
@@ -315,7 +318,6 @@ extern "C" int kvm_stagein_flush(kvm_state *st) {
         rope_ctx rcx;
         rc = rope_ctx_for(st, st->theta.data(), n_half, 0, max_pos, &rcx);
         if (rc) break;
-        rcx.hscale = hscale;
         void *dd = kvm_upload_desc(st, ds.data(), ds.size() * sizeof(kitem_desc));
         if (!dd) { rc = kvm_fail(st, KVM_ENOMEM, "flush: descriptor upload"); break; }
         const dim3 grid(kvm_cdiv(max_rows, 4), (uint32_t)ds.size());

@@ -138,7 +138,15 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint64_t first = (uint64_t)id * a.bt;
     const uint32_t tid = threadIdx.x;
     if (first >= a.h_tokens) {
-        if (tid == 0) atomicOr(&a.info[3], 4u);     // block outside the history: skip it
+        // a block outside the history is not staged: report it, and empty the
+        // slot's cells of this item (and, once, its slot map entry) so attention
+        // never reads what the slot held before and the next plan restages it
+        if (tid == 0) atomicOr(&a.info[3], 4u);
+        if (tid < IT) a.cell_pos[slot * a.bt + tt * IT + tid] = -1;
+        if (tt == 0 && tid == 0) {
+            a.slot_block[slot] = 0xffffffffu;
+            a.slot_base[slot] = -1;
+        }
         return;
     }
     const uint32_t nt = a.h_tokens - first < a.bt ? (uint32_t)(a.h_tokens - first) : a.bt;

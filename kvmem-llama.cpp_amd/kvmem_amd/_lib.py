@@ -86,7 +86,7 @@ class SnapshotInfo(C.Structure):
 class SnapshotLayer(C.Structure):
     _fields_ = [("k_rows", C.c_void_p), ("k_rows_bytes", C.c_size_t), ("v_rows", C.c_void_p),
                 ("v_rows_bytes", C.c_size_t), ("k_sum", C.c_void_p), ("mean_tokens", C.c_void_p),
-                ("n_tokens", C.c_void_p), ("max_blocks", C.c_uint64)]
+                ("n_tokens", C.c_void_p), ("max_blocks", C.c_uint64), ("expect", C.POINTER(SnapshotInfo))]
 
 
 _P = C.c_void_p

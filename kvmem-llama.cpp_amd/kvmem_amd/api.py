@@ -449,17 +449,23 @@ def dequantize_rows(st, ty, rows, n_per_row):
     return out
 
 
-def read_snapshot(data, max_blocks=1 << 20):
+def read_snapshot(data, max_blocks=(1 << 64) - 1, expect=None):
     """Parse the reference's raw-store session snapshot (RawKvStore::snapshot_write,
     raw_kv_store.cpp:1225-1247) into per-layer host arrays in the history layout:
     k_rows / v_rows [n_blocks * block_tokens, row bytes] (uint8), k_sum [n_blocks,
-    n_embd_k], mean_tokens and n_tokens [n_blocks].  Host-side parsing only."""
+    n_embd_k], mean_tokens and n_tokens [n_blocks].  Host-side parsing only.
+    max_blocks: the store's block count (the reader accepts max_blocks + 1 blocks,
+    raw_kv_store.cpp:1255-1256); expect: dict of the store's geometry
+    (SnapshotInfo field names) the header must equal, or None."""
     lib = L.load()
     buf = np.frombuffer(data, dtype=np.uint8)
     info = L.SnapshotInfo()
     rc = lib.kvm_snapshot_info_read(None, buf.ctypes.data, buf.size, C.byref(info))
     if rc:
         raise RuntimeError(f"kvm_snapshot_info_read: {rc}")
+    ex = None
+    if expect is not None:
+        ex = L.SnapshotInfo(**{f: expect.get(f, 0) for f, _ in L.SnapshotInfo._fields_})
     nb, bt = int(info.n_blocks), int(info.block_tokens)
     layers = []
     for il in range(info.n_layer):
@@ -469,7 +475,8 @@ def read_snapshot(data, max_blocks=1 << 20):
         mt = np.zeros(nb, np.uint32)
         nt = np.zeros(nb, np.uint32)
         out = L.SnapshotLayer(k.ctypes.data, k.nbytes, v.ctypes.data if v.size else None, v.nbytes,
-                              ks.ctypes.data, mt.ctypes.data, nt.ctypes.data, max_blocks)
+                              ks.ctypes.data, mt.ctypes.data, nt.ctypes.data, max_blocks,
+                              C.pointer(ex) if ex is not None else None)
         rc = lib.kvm_snapshot_read_layer(None, buf.ctypes.data, buf.size, il, C.byref(out))
         if rc:
             raise RuntimeError(f"kvm_snapshot_read_layer: {rc}")

@@ -34,3 +34,23 @@ def check_attention(out, ref, atol=2e-3, rtol=1e-3):
     assert err <= atol, (err, scale)
     assert err <= rtol * scale, (err, scale)
     return err, scale
+
+
+def golden_snapshot(name):
+    """A raw-store snapshot the reference's RawKvStore wrote (tests/golden/, made by
+    make_snapshots.py on the CPU): (snapshot bytes, case metadata, the K rows, V
+    rows and fp32 K the store was filled with, regenerated from the seed and
+    checked against the digest recorded with the fixture)."""
+    import gzip
+    import json
+    import os
+    import make_snapshots as MS
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    with open(os.path.join(here, "snapshots.json")) as f:
+        meta = json.load(f)[name]
+    with open(os.path.join(here, name + ".bin.gz"), "rb") as f:
+        snap = gzip.decompress(f.read())
+    kr, vr, kf = MS.case_inputs(meta["seed"], meta["n_head_kv"], meta["head_dim"], meta["block_tokens"],
+                                meta["n_blocks"], meta["short"], meta["random_rows"])
+    assert MS.digest(kr, vr, kf) == meta["inputs_sha256"], "regenerated inputs differ from the fixture's"
+    return snap, meta, kr, vr, kf

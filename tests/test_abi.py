@@ -31,4 +31,4 @@ def test_binding_covers_header():
 
 
 def test_abi_version_without_gpu():
-    assert L.load().kvm_abi_version() == 1
+    assert L.load().kvm_abi_version() == 2

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import dev, host
+from gpu_util import dev, golden_snapshot, host
 from kvmem_amd import api, _lib as L
 
 pytestmark = pytest.mark.gpu
@@ -165,20 +165,20 @@ def test_score_topk_lanes_wide_grids(kvm_state, H, n_head, D):
         # random blocks outscore a planted one; the oracle's selection is the check)
 
 
-@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
 def test_score_topk_from_reference_snapshot(kvm_state):
-    """The mean-K index read out of the reference's raw-store snapshot (block sums
-    and token counts the reference's RawKvStore accumulated) scores and selects
-    exactly as the oracle does on the same sums."""
-    H, n_head, D, bt, n_blocks = 4, 24, 256, 128, 300
-    n_hist = n_blocks * bt - 61
-    rng = np.random.default_rng(88)
-    kf = rng.standard_normal((1, n_hist, H * D)).astype(np.float32)
-    kr = rng.integers(0, 256, (1, n_hist, H * D // 32 * 34), dtype=np.uint8)
-    vr = rng.integers(0, 256, (1, n_hist, H * D // 32 * 18), dtype=np.uint8)
-    info, layers = api.read_snapshot(O.ref_raw_snapshot(kr, kf, vr, H * D, H * D, bt, 96))
+    """The mean-K index read out of a raw-store snapshot the reference's RawKvStore
+    wrote (tests/golden/snap_score.bin.gz: block sums and token counts the store
+    accumulated) scores and selects exactly as the oracle does on the same sums."""
+    snap, meta, _, _, kf = golden_snapshot("snap_score")
+    H, D, bt, n_blocks = meta["n_head_kv"], meta["head_dim"], meta["block_tokens"], meta["n_blocks"]
+    n_head = 6 * H
+    info, layers = api.read_snapshot(snap)
     k_sum, mt = layers[0]["k_sum"][None], layers[0]["mean_tokens"][None]
+    # the store's sums are the ordered fp32 sums of the rows it was filled with
+    want_sums, want_mt = O.meank_sums(kf[0], bt)
+    assert np.array_equal(k_sum[0], want_sums) and np.array_equal(mt[0], want_mt)
     ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+    rng = np.random.default_rng(88)
     planted = rng.choice(np.arange(1, n_blocks), 12, replace=False)
     g = n_head // H
     q = np.zeros((1, n_head * D), np.float32)

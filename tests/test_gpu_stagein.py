@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import dev, host, rand_rows
+from gpu_util import dev, golden_snapshot, host, rand_rows
 from kvmem_amd import api, _lib as L
 
 pytestmark = pytest.mark.gpu
@@ -55,30 +55,30 @@ def test_stagein_selection_bytes(kvm_state, n_rot, hadamard, freq_base):
     assert len(sel2.result()["stage_slots"]) == 0
 
 
-@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
 def test_stagein_from_reference_snapshot(kvm_state):
-    """The host history format end to end: the reference's RawKvStore holds the
-    q8_0 K / q4_0 V rows and writes its session snapshot, kvm_snapshot_read_layer
-    turns it into the history, and the stage-in of a selection from it equals the
-    oracle's bytes for the original rows."""
-    H, D, bt, n_blocks = 4, 256, 128, 24
-    n_hist = n_blocks * bt - 40
-    rng = np.random.default_rng(77)
-    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
-    kf = rng.standard_normal((1, n_hist, H * D)).astype(np.float32)
-    snap = O.ref_raw_snapshot(kr[None], kf, vr[None], H * D, H * D, bt, 100)
+    """The host history format end to end: a session snapshot written by the
+    reference's RawKvStore holding q8_0 K / q4_0 V rows (tests/golden/
+    snap_stagein.bin.gz), read by kvm_snapshot_read_layer into the history; the
+    stage-in of a selection from it equals the oracle's bytes for the original
+    rows."""
+    snap, meta, kr, vr, _ = golden_snapshot("snap_stagein")
+    H, D, bt, n_blocks = meta["n_head_kv"], meta["head_dim"], meta["block_tokens"], meta["n_blocks"]
+    kr, vr = kr[0], vr[0]
+    n_hist = kr.shape[0]
     info, layers = api.read_snapshot(snap)
     assert info["n_blocks"] == n_blocks
+    assert np.array_equal(layers[0]["k_rows"][:n_hist], kr) and np.array_equal(layers[0]["v_rows"][:n_hist], vr)
     hist = api.History(layers[0]["k_rows"][:n_hist], layers[0]["v_rows"][:n_hist])
-    w = api.KVWindow(kvm_state, 8 * bt, H, D, bt)
-    s = rng.standard_normal(n_blocks)
+    w = api.KVWindow(kvm_state, 4 * bt, H, D, bt)
+    s = np.random.default_rng(7).standard_normal(n_blocks)
     s[n_blocks - 1] = 10.0                          # the partial last block too
     nt = layers[0]["n_tokens"].astype(np.int32)
-    sel = api.select_topk(kvm_state, dev(s), dev(nt), 8, 1, 0, None, window=w)
+    sel = api.select_topk(kvm_state, dev(s), dev(nt), 4, 1, 0, None, window=w)
     api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
     res = sel.result()
+    assert res["status"] == 0 and n_blocks - 1 in res["ids"]
     theta = O.rope_theta(1e7, 1.0, 64)
-    ek, ev = w.export_rows(0, 8 * bt)
+    ek, ev = w.export_rows(0, 4 * bt)
     ek, ev = host(ek), host(ev)
     for k, (bid, base) in enumerate(zip(res["ids"], res["to_base"])):
         n = int(nt[bid])
@@ -185,6 +185,29 @@ def test_enqueue_flush_api(kvm_state):
         assert np.array_equal(cp[c0:c0 + n], np.arange(pos0, pos0 + n))
 
 
+def test_enqueue_flush_mixed_hadamard_widths(kvm_state):
+    """Items of Hadamard width 256, 128 and 0 queued into one flush are each
+    rotated with their own 1/sqrt(width) scale."""
+    H, D = 4, 256
+    rng = np.random.default_rng(12)
+    w = api.KVWindow(kvm_state, 512, H, D, 128)
+    kr, _ = rand_rows(rng, 120, H, D, L.T_Q8_0, L.T_Q4_0)
+    theta = O.rope_theta(1e7, 1.0, 64)
+    lib = kvm_state.lib
+    items = [(0, 40, 900, 256, 0), (40, 50, 11, 128, 100), (90, 30, 300, 0, 300)]   # (row0, n, pos0, width, cell0)
+    for r0, n, pos0, nrot, c0 in items:
+        kb = np.ascontiguousarray(kr[r0:r0 + n])
+        kvm_state.check(lib.kvm_stagein_enqueue_k(kvm_state.h, L.T_Q8_0, kb.ctypes.data_as(C.c_void_p), kb.nbytes,
+                                                  C.byref(w.c), c0, n, H * D, nrot, H, D, 64, pos0,
+                                                  theta.ctypes.data_as(C.c_void_p), 32))
+    kvm_state.check(lib.kvm_stagein_flush(kvm_state.h))
+    ek, _ = w.export_rows(0, 512)
+    ek = host(ek)
+    for r0, n, pos0, nrot, c0 in items:
+        want = O.stagein_k(kr[r0:r0 + n].reshape(-1), n, H, D, 64, nrot, pos0, theta).reshape(n, -1)
+        assert np.array_equal(ek[c0:c0 + n], want), nrot
+
+
 def test_stagein_rejects_bad_arguments(kvm_state):
     w = api.KVWindow(kvm_state, 256, 4, 256, 128)
     hist, _, _ = _history(11, 256)
@@ -215,22 +238,54 @@ def test_stagein_plan_that_does_not_fit_stages_nothing(kvm_state):
 def test_stagein_block_outside_history(kvm_state):
     """A selected block past the end of the pinned history is skipped and
     flagged (status bit 4); the other blocks are staged byte for byte and the
-    skipped slot keeps no live cells."""
+    skipped slot keeps no live cells, also when it held another block before
+    the reselect: its cells are emptied and its slot map entry cleared, so the
+    next plan restages it."""
     H, D, bt = 4, 256, 128
     hist, kr, _ = _history(14, 10 * bt, H, D)                   # 10 blocks of history
     w = api.KVWindow(kvm_state, 8 * bt, H, D, bt)
+    nt = dev(np.full(14, bt, np.int32))
+    theta = O.rope_theta(1e7, 1.0, 64)
     s = np.zeros(14)
-    s[[3, 12, 6]] = [3.0, 2.0, 1.0]                            # block 12 is past the history
-    sel = api.select_topk(kvm_state, dev(s), dev(np.full(14, bt, np.int32)), 4, 1, 0, None, window=w)
-    assert list(sel.result()["ids"]) == [0, 3, 6, 12]
+    s[[3, 9, 6]] = [3.0, 2.0, 1.0]
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    assert list(sel.result()["ids"]) == [0, 3, 6, 9] and sel.result()["status"] == 0
+    assert np.all(host(w.cell_pos)[3 * bt:4 * bt] >= 0)             # slot 3 holds block 9
+    s[9], s[12] = 0.0, 2.0                                          # block 12 is past the history
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    assert list(sel.result()["ids"]) == [0, 3, 6, 12] and list(sel.result()["stage_slots"]) == [3]
     api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
     assert sel.result()["status"] & 4
-    theta = O.rope_theta(1e7, 1.0, 64)
     ek, _ = w.export_rows(0, 3 * bt)
     for k, bid in enumerate([0, 3, 6]):
         want = O.stagein_k(kr[bid * bt:(bid + 1) * bt].reshape(-1), bt, H, D, 64, 256, k * bt, theta)
         assert np.array_equal(host(ek)[k * bt:(k + 1) * bt].reshape(-1), want), k
     assert np.all(host(w.cell_pos)[3 * bt:4 * bt] == -1)
+    assert host(w.slot_block)[3] == -1 and host(w.slot_base)[3] == -1
+    # the same selection again still plans slot 3 (its entry no longer claims block 12)
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    assert list(sel.result()["stage_slots"]) == [3]
+    # and a selection of blocks in the history stages it byte for byte
+    s[12], s[8] = 0.0, 2.0
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    assert list(sel.result()["ids"]) == [0, 3, 6, 8] and sel.result()["status"] == 0
+    ek, _ = w.export_rows(3 * bt, bt)
+    want = O.stagein_k(kr[8 * bt:9 * bt].reshape(-1), bt, H, D, 64, 256, 3 * bt, theta)
+    assert np.array_equal(host(ek).reshape(-1), want)
+    assert np.array_equal(host(w.cell_pos)[3 * bt:4 * bt], np.arange(3 * bt, 4 * bt))
+
+
+def test_select_topk_over_no_blocks(kvm_state):
+    """A selection over an empty store (no scores, no token counts) selects
+    nothing and stages nothing; the kernel reads a stand-in, not address 0."""
+    w = api.KVWindow(kvm_state, 4 * 128, 4, 256, 128)
+    empty = torch.empty(0, dtype=torch.float64, device="cuda")
+    sel = api.select_topk(kvm_state, empty, torch.empty(0, dtype=torch.int32, device="cuda"), 4, 1, 0, None,
+                          window=w)
+    r = sel.result()
+    assert len(r["ids"]) == 0 and r["total"] == 0 and len(r["stage_slots"]) == 0 and r["status"] == 0
 
 
 def _retrieval(st, seed, n_blocks, H, D, n_head, bt=128):

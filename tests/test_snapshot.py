@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+from gpu_util import golden_snapshot
 from kvmem_amd import api
 
 needs_ref = pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs the reference sources)")
@@ -62,8 +63,11 @@ def test_snapshot_reader_refuses_what_the_reference_refuses():
         api.read_snapshot(bytes(bad))
     with pytest.raises(RuntimeError):                                # truncated
         api.read_snapshot(snap[:len(snap) - 5])
-    with pytest.raises(RuntimeError):                                # more blocks than allowed
-        api.read_snapshot(snap, max_blocks=1)
+    # a store of max_blocks blocks reads a snapshot of max_blocks + 1 (the partly
+    # filled tail block) and refuses more (raw_kv_store.cpp:1255-1256)
+    api.read_snapshot(snap, max_blocks=1)
+    with pytest.raises(RuntimeError):
+        api.read_snapshot(snap, max_blocks=0)
     bad = bytearray(snap)
     hdr = 4 + 4 * 4 + 3 * 8 + 8                                      # header, then the block's section length
     bad[hdr + 8:hdr + 12] = np.uint32(BT + 1).tobytes()              # first layer's n_tokens above the block
@@ -73,3 +77,54 @@ def test_snapshot_reader_refuses_what_the_reference_refuses():
     bad[hdr:hdr + 8] = np.uint64(np.frombuffer(snap[hdr:hdr + 8], np.uint64)[0] + 1).tobytes()
     with pytest.raises(RuntimeError):                                # section length disagrees
         api.read_snapshot(bytes(bad))
+
+
+def _header(n_layer, n_embd_k, n_embd_v, bt, k_row, k_gpu_row, v_gpu_row, n_blocks):
+    return (np.array([0x31564b52, n_layer, n_embd_k, n_embd_v, bt], np.uint32).tobytes() +
+            np.array([k_row, k_gpu_row, v_gpu_row, n_blocks], np.uint64).tobytes())
+
+
+def test_snapshot_reader_bounds_a_crafted_header():
+    """Header fields whose products would wrap 64 bits are refused before any
+    buffer is sized or written (block_tokens 1, k_row_bytes 2^63, 2 blocks:
+    2 * 1 * 2^63 wraps to 0)."""
+    lib = api.L.load()
+    body = b"\0" * 64
+    for hdr in (_header(1, 256, 256, 1, 1 << 63, 0, 0, 2),            # K row wider than fp32
+                _header(1, 256, 256, 1 << 20, 512, 0, 0, 2),          # block of 2^20 rows
+                _header(1, 1 << 30, 256, 128, 0, 0, 0, 2),            # n_embd_k past 2^20
+                _header(1, 256, 256, 128, 512, 0, 1 << 62, 2)):       # V row wider than fp32
+        buf = np.frombuffer(hdr + body, np.uint8)
+        info = api.L.SnapshotInfo()
+        assert lib.kvm_snapshot_info_read(None, buf.ctypes.data, buf.size, api.C.byref(info)) == api.L.KVM_EINVAL
+        with pytest.raises(RuntimeError):
+            api.read_snapshot(bytes(buf))
+
+
+def test_snapshot_reader_expects_the_store_geometry():
+    """With the store's configuration the reader refuses a snapshot of another
+    geometry, as SnapshotReader::expect does (raw_kv_store.cpp:1251-1254)."""
+    snap, meta, kr, vr, _ = golden_snapshot("snap_stagein")
+    E = meta["n_head_kv"] * meta["head_dim"]
+    want = dict(n_layer=1, n_embd_k=E, n_embd_v=E, block_tokens=meta["block_tokens"], k_row_bytes=E // 32 * 34,
+                k_gpu_row_bytes=0, v_gpu_row_bytes=E // 32 * 18)
+    api.read_snapshot(snap, expect=want)
+    for field, value in (("n_layer", 2), ("block_tokens", 64), ("k_row_bytes", 0), ("v_gpu_row_bytes", 0)):
+        with pytest.raises(RuntimeError):
+            api.read_snapshot(snap, expect=dict(want, **{field: value}))
+
+
+@pytest.mark.parametrize("name", ["snap_stagein", "snap_score"])
+def test_committed_snapshots_read_back(name):
+    """The committed snapshots (written by the reference's RawKvStore, see
+    tests/golden/make_snapshots.py) hand back the rows the store was filled with
+    and its ordered fp32 block sums, with no reference build present."""
+    snap, meta, kr, vr, kf = golden_snapshot(name)
+    info, layers = api.read_snapshot(snap)
+    bt, n = meta["block_tokens"], kr.shape[1]
+    assert info["n_blocks"] == meta["n_blocks"] and info["block_tokens"] == bt
+    ly = layers[0]
+    assert np.array_equal(ly["k_rows"][:n], kr[0]) and np.array_equal(ly["v_rows"][:n], vr[0])
+    sums, mt = O.meank_sums(kf[0], bt)
+    assert np.array_equal(ly["k_sum"].view(np.uint32), sums.view(np.uint32))
+    assert np.array_equal(ly["mean_tokens"], mt) and np.array_equal(ly["n_tokens"], mt)
