@@ -333,6 +333,22 @@ typedef struct kvm_lane {
 int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
                         uint32_t n_head, float scale);
 
+/* kvm_fa_decode without any allocation, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  It has no counterpart in the reference.  The split
+ * partials go to a fixed device array of KVM_NOALLOC_SCRATCH_BYTES that the
+ * library holds on each GPU until the process ends (looked up when the first
+ * kvm_state on the device is created), instead of the state's workspace; the
+ * key splits are reduced to fit it, and KVM_ERANGE is returned when even one
+ * split's partials (n_head_kv * 32 * (head_dim + 2) * 4 bytes) do not.  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two states) race and must be serialised by the caller.  Same
+ * arguments, rules and results as kvm_fa_decode. */
+#define KVM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int kvm_fa_decode_noalloc(kvm_state *st, const kvm_window *w, const void *q, int q_type,
+                          const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                          float *out);
+
 /* Chunked prefill / long MTP verify: any n_tokens; same visibility rule. */
 int kvm_fa_prefill(kvm_state *st, const kvm_window *w, const void *q, int q_type,
                    const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,

@@ -29,6 +29,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 #define KVM_MAX_LANES 8
 
@@ -677,8 +678,12 @@ static void launch_decode_d(const fa_args &a, uint32_t n_lanes, uint32_t max_row
     }
 }
 
+// scratch_cap == 0: the partials go to the state's workspace (grown with
+// hipMalloc when too small); otherwise to the caller's buffer `scratch` of
+// scratch_cap bytes, with fewer key splits if the partials would not fit, and
+// nothing is allocated.
 static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
-                          uint32_t n_head, float scale) {
+                          uint32_t n_head, float scale, void *scratch = nullptr, size_t scratch_cap = 0) {
     if (!st || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "fa_decode: no lanes");
     if (n_lanes > KVM_MAX_LANES) return kvm_fail(st, KVM_ERANGE, "fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
     if (q_type != KVM_TYPE_F32 && q_type != KVM_TYPE_BF16) return kvm_fail(st, KVM_EUNSUPPORTED, "fa_decode: q type %d", q_type);
@@ -711,9 +716,20 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     a.n_splits = choose_splits(st->n_cu, n_lanes, H, max_tiles);
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_type == KVM_TYPE_BF16;
+    const size_t part_bytes = (size_t)n_lanes * H * rmax * (D + 2) * sizeof(float);   // per key split
+    float *ws;
+    if (scratch_cap) {
+        const size_t fit = scratch_cap / part_bytes;
+        if (fit == 0)
+            return kvm_fail(st, KVM_ERANGE, "fa_decode: partials of one key split (%zu bytes) exceed the %zu-byte scratch",
+                            part_bytes, scratch_cap);
+        if (a.n_splits > fit) a.n_splits = (uint32_t)fit;
+        ws = (float *)scratch;
+    } else {
+        ws = (float *)kvm_workspace(st, part_bytes * a.n_splits);
+        if (!ws) return kvm_fail(st, KVM_ENOMEM, "fa_decode: workspace of %zu bytes", part_bytes * a.n_splits);
+    }
     const size_t n_part = (size_t)n_lanes * H * a.n_splits * rmax;
-    float *ws = (float *)kvm_workspace(st, n_part * (D + 2) * sizeof(float));
-    if (!ws) return kvm_fail(st, KVM_ENOMEM, "fa_decode: workspace of %zu bytes", n_part * (D + 2) * 4);
     a.ws = ws;
     a.ws_ml = ws + n_part * D;
     KVM_HIP(st, hipSetDevice(st->device));
@@ -740,6 +756,43 @@ extern "C" int kvm_fa_decode(kvm_state *st, const kvm_window *w, const void *q, 
 extern "C" int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
                                    uint32_t n_head, float scale) {
     return fa_decode_impl(st, lanes, n_lanes, q_type, n_head, scale);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split partials live in a fixed device array
+// instead of the state's workspace.  Each device holds its own copy of the
+// array (KVM_NOALLOC_SCRATCH_BYTES, until the process ends); its address on a
+// device is looked up once, with that device current, when the first state on
+// the device is created, and only that address is handed to kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[KVM_NOALLOC_SCRATCH_BYTES];
+
+#define KVM_MAX_DEVICES 64
+static void *g_scratch_ptr[KVM_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+int kvm_noalloc_setup(kvm_state *st) {
+    if (st->device < 0 || st->device >= KVM_MAX_DEVICES)
+        return kvm_fail(st, KVM_ERANGE, "noalloc: device %d beyond %d", st->device, KVM_MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[st->device]) {
+        void *ptr = nullptr;
+        KVM_HIP(st, hipSetDevice(st->device));
+        KVM_HIP(st, hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) return kvm_fail(st, KVM_EHIP, "noalloc: scratch has no address on device %d", st->device);
+        g_scratch_ptr[st->device] = ptr;
+    }
+    st->scratch = g_scratch_ptr[st->device];
+    return KVM_OK;
+}
+
+extern "C" int kvm_fa_decode_noalloc(kvm_state *st, const kvm_window *w, const void *q, int q_type,
+                                     const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                                     float *out) {
+    if (!st) return KVM_EINVAL;
+    if (!st->scratch) return kvm_fail(st, KVM_EHIP, "fa_decode_noalloc: scratch not set up on device %d", st->device);
+    kvm_lane lane{w, q, q_pos, out, n_tokens};
+    return fa_decode_impl(st, &lane, 1, q_type, n_head, scale, st->scratch, KVM_NOALLOC_SCRATCH_BYTES);
 }
 
 // Chunked prefill through the decode kernel: the query tokens are processed in

@@ -51,6 +51,9 @@ struct kvm_state {
     void *desc = nullptr;
     size_t desc_bytes = 0;
     hipEvent_t ev = nullptr;
+    // device address of the fixed scratch array of the allocation-free entry
+    // point on this state's device (kvm_noalloc_setup)
+    void *scratch = nullptr;
 };
 
 // error helpers ----------------------------------------------------------------
@@ -68,6 +71,9 @@ int kvm_fail(kvm_state *st, int code, const char *fmt, ...);
             return kvm_fail((st), KVM_EHIP, "%s launch: %s", (what), hipGetErrorString(e__)); \
     } while (0)
 
+// Looks up (once per device) the address of the allocation-free entry point's
+// scratch array on the state's device and records it in st->scratch.
+int kvm_noalloc_setup(kvm_state *st);
 // Ensures the state's workspace holds at least `bytes`; returns it or nullptr.
 void *kvm_workspace(kvm_state *st, size_t bytes);
 // Ensures a device copy of `bytes` of descriptor data; returns the device pointer.

@@ -34,6 +34,12 @@ extern "C" kvm_state *kvm_state_create(int device) {
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n_cu > 0)
         st->n_cu = (uint32_t)n_cu;
+    if (kvm_noalloc_setup(st) != KVM_OK) {
+        (void)hipEventDestroy(st->ev);
+        (void)hipStreamDestroy(st->own_stream);
+        delete st;
+        return nullptr;
+    }
     return st;
 }
 

@@ -15,6 +15,7 @@ KVM_OK, KVM_EINVAL, KVM_EHIP, KVM_ENOMEM, KVM_ERANGE, KVM_EUNSUPPORTED = 0, -1, 
 T_F32, T_F16, T_Q4_0, T_Q8_0, T_BF16 = 0, 1, 2, 8, 30
 TILE_CELLS = 64
 MAX_TOPK_BLOCKS = 8192
+NOALLOC_SCRATCH_BYTES = 16 << 20
 STATUS_NAMES = {0: "KVM_OK", -1: "KVM_EINVAL", -2: "KVM_EHIP", -3: "KVM_ENOMEM",
                 -4: "KVM_ERANGE", -5: "KVM_EUNSUPPORTED"}
 
@@ -133,6 +134,7 @@ SIGNATURES = {
     "kvm_stagein_flush": (C.c_int, [_P]),
     "kvm_fa_decode": (C.c_int, [_P, _PW, _P, C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_fa_decode_lanes": (C.c_int, [_P, C.POINTER(Lane), _u32, C.c_int, _u32, _f]),
+    "kvm_fa_decode_noalloc": (C.c_int, [_P, _PW, _P, C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_fa_prefill": (C.c_int, [_P, _PW, _P, C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_d2d_batched": (C.c_int, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), C.c_int]),
     "kvm_snapshot_info_read": (C.c_int, [_P, _P, _sz, C.POINTER(SnapshotInfo)]),
