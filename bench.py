@@ -652,7 +652,7 @@ def main():
                       "attention_us_per_token": round(fa_ms * 1e3, 3)},
         "step_bytes": STEP_BYTES,
         "roofline_step_us": round(STEP_BYTES / (HBM_PEAK_GBPS * 1e9) * 1e6, 3),
-        "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode (k_fa_decode split-K + k_fa_combine)",
+        "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode (k_fa_decode: split-K with the splits merged in-launch)",
                      "achieved": round(fa_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),

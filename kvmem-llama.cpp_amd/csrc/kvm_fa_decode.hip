@@ -9,9 +9,9 @@
 // f16/f16 cache Q is rounded to fp16 and Q.K is an fp16 dot with fp32
 // accumulation.
 //
-// Work split (gfx950, wave64; one workgroup of 8 waves per (lane, kv head,
-// key split); every wave loads its own operands of each 64-cell tile straight
-// from HBM into registers, three buffers, two tiles in flight):
+// One launch per call: one workgroup of 8 waves per (lane, kv head, key
+// split); every wave loads its own operands of each 64-cell tile straight from
+// HBM into registers, three buffers, two tiles in flight:
 //   waves 0-3 score: wave kq takes keys 16kq..16kq+15 of the tile against all
 //     padded query rows with v_mfma_i32_16x16x32_i8 (one MFMA per 32-dim block
 //     and row tile; a last row tile of at most 8 rows takes two blocks per
@@ -22,13 +22,16 @@
 //     v_mfma_f32_16x16x32_f16; the q4_0 block scale is folded into P and V
 //     enters the MFMA as exact fp16 denormals (nibble * 2^-24).
 // One barrier per tile: the scoring waves score tile t+1 while the P V waves
-// multiply tile t, so each SIMD holds one wave of each kind in different
-// phases.  Partial (m, l, O) of each split go to a workspace and
-// k_fa_combine merges them.
+// multiply tile t.  The query is quantised by all 8 waves at the start.  Each
+// split writes its partial (m, l, O) device-coherently and raises its flag
+// with this launch's epoch; splits 0 .. NM-1 of a head then wait for the
+// head's flags and each merges whole rows (or row chunks) of the head, so no
+// combine launch follows.
 #include "kvm_internal.h"
 
 #include <cmath>
 #include <cstdlib>
+#include <atomic>
 #include <mutex>
 
 #define KVM_MAX_LANES 8
@@ -48,10 +51,18 @@ struct fa_args {
     fa_lane lanes[KVM_MAX_LANES];
     float *ws;              // partial O  [lane][H][split][RMAX][D]
     float *ws_ml;           // partial m,l [lane][H][split][RMAX][2]
+    uint32_t *sync;         // [lane][H][split]: the epoch of the last launch that completed
+                            // the split's partials; sync[KVM_FA_SYNC_STATUS]: bit 0 = a
+                            // merge wait timed out
+    uint32_t epoch;         // this launch's epoch (nonzero, unlike any earlier launch's)
     uint32_t H, G, n_head, n_splits;
     float scale_log2;       // kq_scale * log2(e)
     int q_bf16;
 };
+#define KVM_FA_MAX_HEADS 64
+#define KVM_MAX_SPLITS 512
+#define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)
+#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_STATUS + 64)
 
 __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
     return bf16 ? kvm_bf2f(((const uint16_t *)q)[i]) : ((const float *)q)[i];
@@ -112,6 +123,117 @@ struct fa_v_regs {
     kvm_u32x4 vs[QUANT ? NBW : 1][2];      // V scales [block][ks]
     kvm_u32x4 vh[QUANT ? 1 : NT][2];       // f16 V [ks]
 };
+
+// Split partials are written and read device-coherently (relaxed atomics at
+// agent scope): the merging workgroup may run on another XCD, whose L2 holds no
+// copy of them, and may hold a stale one from an earlier launch.
+__device__ __forceinline__ void fa_store(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fa_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Longest wait of a merging workgroup for the other splits' flags (s_sleep
+// rounds of ~128 cycles each, about 0.2 s): every split raises its flag without
+// waiting on anything, so the wait ends unless workgroups cannot be scheduled;
+// past the limit the status word says so and the rows are left unmerged.
+#define KVM_FA_MERGE_SPIN (1u << 21)
+
+// Merge units j, j + nm, ... of (lane blockIdx.z, head h): unit u is row
+// u / dc, dims (u % dc) * D / dc .. + D / dc, over the S split partials:
+// M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s
+// (zeros when no split saw a visible cell).  512 threads: one thread per
+// split loads (m, l); thread t accumulates dim t % UD of the unit (UD = D / dc)
+// over the splits s = t / UD (mod 512 / UD), whose partial outputs it loads in
+// batches of KVM_FA_MERGE_BATCH before using any (the first batch in flight
+// together with (m, l): one memory round trip per unit); the 512 / UD sums are
+// then added in split-phase order.
+#define KVM_FA_MERGE_BATCH 16
+template <int D, int RMAX>
+__device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, uint32_t h, const uint32_t *flags,
+                                         uint32_t j, uint32_t nm, uint32_t dc, int R) {
+    __shared__ float s_w[KVM_MAX_SPLITS + 1];     // [KVM_MAX_SPLITS] stays 0: splits past the last
+    __shared__ float s_red[2][8];
+    __shared__ float s_acc[512];
+    __shared__ uint32_t s_ok;
+    const uint32_t tid = threadIdx.x, S = a.n_splits;
+    // thread t < S waits for split t's flag (device-coherent polling, no cache
+    // invalidation); the partials are then read device-coherently as well
+    uint32_t ok = 1;
+    if (tid < S) {
+        uint32_t it = 0;
+        while (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != a.epoch) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++it > KVM_FA_MERGE_SPIN) {
+                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+        }
+    }
+    if (tid == 0) s_ok = 1;
+    __syncthreads();
+    if (!ok) s_ok = 0;
+    __syncthreads();
+    const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
+    const uint32_t UD = D / dc, SP = 512 / UD;
+    if (s_ok) {
+        const uint32_t dd = tid % UD, sp = tid / UD;
+        for (uint32_t u = j; u < (uint32_t)R * dc; u += nm) {
+            const uint32_t row = u / dc, d = (u % dc) * UD + dd;
+            // every load unconditional (a conditional load makes the compiler
+            // wait for all loads in flight at the join): splits past S re-read
+            // split S - 1 and get weight 0
+            const float *po = a.ws + (p0 * RMAX + row) * D + d;
+            auto ld = [&](uint32_t s) { return fa_load(po + (uint64_t)(s < S ? s : S - 1) * RMAX * D); };
+            float v[KVM_FA_MERGE_BATCH];
+#pragma unroll
+            for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) v[i] = ld(sp + SP * i);
+            const uint32_t tc = tid < S ? tid : S - 1;
+            float m_t = fa_load(&a.ws_ml[((p0 + tc) * RMAX + row) * 2]);
+            float l_t = fa_load(&a.ws_ml[((p0 + tc) * RMAX + row) * 2 + 1]);
+            m_t = tid < S ? m_t : -INFINITY;
+            l_t = tid < S ? l_t : 0.0f;
+            float M = kvm_wave_max_f32(m_t);
+            if ((tid & 63) == 0) s_red[0][tid >> 6] = M;
+            __syncthreads();
+            M = s_red[0][0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) M = fmaxf(M, s_red[0][i]);
+            const float wt = m_t == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_t - M);
+            s_w[tid] = wt;                       // 0 for tid >= S
+            if (tid == 0) s_w[KVM_MAX_SPLITS] = 0.0f;
+            float L = kvm_wave_sum_f32(l_t * wt);
+            if ((tid & 63) == 0) s_red[1][tid >> 6] = L;
+            __syncthreads();
+            L = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) L += s_red[1][i];
+            float acc = 0.0f;
+            for (uint32_t s0 = sp;; ) {
+#pragma unroll
+                for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) {
+                    const uint32_t si = s0 + SP * i;
+                    acc += s_w[si < KVM_MAX_SPLITS ? si : KVM_MAX_SPLITS] * v[i];
+                }
+                s0 += SP * KVM_FA_MERGE_BATCH;
+                if (s0 >= S) break;
+#pragma unroll
+                for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) v[i] = ld(s0 + SP * i);
+            }
+            s_acc[tid] = acc;
+            __syncthreads();
+            if (sp == 0) {
+                float o = acc;
+                for (uint32_t i = 1; i < SP; ++i) o += s_acc[i * UD + dd];
+                const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
+                ln.out[((uint64_t)t * a.n_head + qh) * D + d] = M == -INFINITY || !(L > 0.0f) ? 0.0f : o / L;
+            }
+            __syncthreads();
+        }
+    }
+}
 
 template <int D, int NRT, bool QUANT, bool PK>
 __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
@@ -237,7 +359,6 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
                 *(kvm_f16x8 *)&s_qh[r][32 * b + 8 * g] = hv;
             }
         }
-        if (tid < 8) s_up[tid >> 2][tid & 3] = 0;
         KVM_LDS_BARRIER();
     };
 
@@ -297,7 +418,8 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
         float dqo[NRT][NG];                  // scale MFMA B operand: dq * kq_scale * log2(e)
         float dqp[2];                        // packed row tile: even-block / odd-block columns
         uint32_t qlim[NRT];                  // cell visible iff (uint)cell_pos < qlim (= q_pos + 1; 0 for padding)
-        float m_run[NRT], l_run[NRT];        // row srow(rt) over this lane's keys
+        float m_run[NRT], l_run[NRT];        // row 16rt + m (16rt + m % 8 packed) over this lane's keys
+        // B operands from the workgroup's quantised query in LDS
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
             const int row = srow(rt);
@@ -328,7 +450,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
 
         auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
             load_k(nx, tile_index(inext));
-            // ---- scores of keys 16kq + 4g + i, rows srow(rt) (log2 domain; q8_0:
+            // ---- scores of keys 16kq + 4g + i, rows 16rt + m (log2 domain; q8_0:
             // kq_scale * log2(e) is folded into the query scales), masked
             float s[NRT][4];
 #pragma unroll
@@ -459,8 +581,8 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
             for (int rt = 0; rt < NRT; ++rt) {
                 const int row = 16 * rt + m;
                 if (row < R) {
-                    a.ws_ml[(pidx * RMAX + row) * 2 + 0] = m_run[rt] == KVM_M_NONE ? -INFINITY : m_run[rt];
-                    a.ws_ml[(pidx * RMAX + row) * 2 + 1] = s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row];
+                    fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 0], m_run[rt] == KVM_M_NONE ? -INFINITY : m_run[rt]);
+                    fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 1], s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row]);
                 }
             }
         }
@@ -578,69 +700,27 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * rt + 4 * g + r;
                     if (row < R)
-                        po[row * D + DW * dq + 16 * nt + m] =
-                            QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r];
+                        fa_store(&po[row * D + DW * dq + 16 * nt + m],
+                                 QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r]);
                 }
     }
-}
 
-// Merge the splits of one (lane, kv head, row, 64-dim chunk): one wave, lane =
-// output dim.  Every load is issued before any use (split maxima and sums one
-// per lane, the partial outputs KVM_COMBINE_BATCH splits per lane), so the
-// merge costs one memory round trip for up to that many splits; the split
-// weights go through LDS (broadcast reads), the reductions through DPP.
-#define KVM_MAX_SPLITS 512
-#define KVM_COMBINE_BATCH 64
-template <int D>
-__global__ void __launch_bounds__(64) k_fa_combine(fa_args a, int rmax) {
-    __shared__ float s_w[KVM_MAX_SPLITS];
-    const fa_lane ln = a.lanes[blockIdx.z];
-    const uint32_t h = blockIdx.y, row = blockIdx.x / (D / 64);
-    const uint32_t R = ln.n_tokens * a.G;
-    if (row >= R) return;
-    const uint32_t l = threadIdx.x, d = (blockIdx.x % (D / 64)) * 64 + l, S = a.n_splits;
-    const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
-    const float *ml = a.ws_ml + (p0 * rmax + row) * 2;
-    const uint64_t mstride = (uint64_t)rmax * 2;
-    const float *po = a.ws + (p0 * rmax + row) * D + d;
-    const uint64_t ostride = (uint64_t)rmax * D;
-    // first batch of partial outputs, and this lane's split (m, l), in flight together
-    float v[KVM_COMBINE_BATCH];
-#pragma unroll
-    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) v[j] = po[(uint64_t)(j < (int)S ? j : 0) * ostride];
-    const float m_l = l < S ? ml[l * mstride] : -INFINITY;
-    const float l_l = l < S ? ml[l * mstride + 1] : 0.0f;
-    const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
-    float *out = ln.out + ((uint64_t)t * a.n_head + qh) * D + d;
-    float M = m_l;
-    for (uint32_t s = l + 64; s < S; s += 64) M = fmaxf(M, ml[s * mstride]);
-    M = kvm_wave_max_f32(M);
-    if (M == -INFINITY) {
-        *out = 0.0f;
-        return;
-    }
-    float L = 0.0f;
-    for (uint32_t s = l; s < S; s += 64) {
-        const float m = s == l ? m_l : ml[s * mstride];
-        const float wgt = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-        s_w[s] = wgt;
-        L += (s == l ? l_l : ml[s * mstride + 1]) * wgt;
-    }
-    L = kvm_wave_sum_f32(L);
+    // ---- arrival: the partials of this split are complete at device scope
+    // (device-coherent stores, each wave waits for its own), then the split's
+    // flag takes this launch's epoch.  Splits 0 .. NM-1 of the head then merge
+    // units j = split, split + NM, ... once every flag of the head is up.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // four partial sums: a quarter of the dependent adds in the chain
-    float acc4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int j = 0; j < KVM_COMBINE_BATCH; ++j) acc4[j & 3] += j < (int)S ? v[j] * s_w[j] : 0.0f;
-    float acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-    for (uint32_t s0 = KVM_COMBINE_BATCH; s0 < S; s0 += 32) {
-        float u[32];
-#pragma unroll
-        for (int j = 0; j < 32; ++j) u[j] = s0 + j < S ? po[(s0 + j) * ostride] : 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) acc += s0 + j < S ? u[j] * s_w[s0 + j] : 0.0f;
-    }
-    *out = L > 0.0f ? acc / L : 0.0f;
+    uint32_t *flags = a.sync + ((uint64_t)blockIdx.z * a.H + h) * a.n_splits;
+    if (tid == 0) __hip_atomic_store(flags + split, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // merge units: rows split into dc dim chunks (at least 64 dims) so that
+    // about every split of the head merges one unit
+    const uint32_t S = a.n_splits;
+    uint32_t dc = 1;
+    while (dc < D / 64 && (uint32_t)R * dc * 2 <= S) dc *= 2;
+    const uint32_t units = (uint32_t)R * dc, NM = units < S ? units : S;
+    if (split >= NM) return;
+    fa_merge<D, RMAX>(a, ln, h, flags, split, NM, dc, R);
 }
 
 static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
@@ -678,19 +758,26 @@ static void launch_decode_d(const fa_args &a, uint32_t n_lanes, uint32_t max_row
     }
 }
 
-// scratch_cap == 0: the partials go to the state's workspace (grown with
-// hipMalloc when too small); otherwise to the caller's buffer `scratch` of
-// scratch_cap bytes, with fewer key splits if the partials would not fit, and
-// nothing is allocated.
-static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
-                          uint32_t n_head, float scale, void *scratch = nullptr, size_t scratch_cap = 0) {
+// Checks the lanes and fills the launch arguments.  scratch_cap == 0: the
+// split partials go to the state's attention workspace
+// (grown with hipMalloc when too small); otherwise to the caller's buffer
+// `scratch` of scratch_cap bytes, with fewer key splits if the partials would
+// not fit, and nothing is allocated.  *rows = 0: nothing to compute.
+struct fa_plan {
+    fa_args a;
+    uint32_t n_lanes, rows, D;
+    bool quant;
+};
+static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type, uint32_t n_head,
+                      float scale, void *scratch, size_t scratch_cap, fa_plan *fp) {
     if (!st || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "fa_decode: no lanes");
     if (n_lanes > KVM_MAX_LANES) return kvm_fail(st, KVM_ERANGE, "fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
     if (q_type != KVM_TYPE_F32 && q_type != KVM_TYPE_BF16) return kvm_fail(st, KVM_EUNSUPPORTED, "fa_decode: q type %d", q_type);
     const kvm_window *w0 = lanes[0].w;
     if (!w0) return kvm_fail(st, KVM_EINVAL, "fa_decode: null window");
     uint32_t max_rows = 0, max_tiles = 0;
-    fa_args a{};
+    fa_args &a = fp->a;
+    a = fa_args{};
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_lane &L = lanes[i];
         int rc = kvm_window_check(L.w);
@@ -704,10 +791,14 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
         max_rows = rows > max_rows ? rows : max_rows;
         const uint32_t nt = L.w->n_cells / 64;
         max_tiles = nt > max_tiles ? nt : max_tiles;
-        a.lanes[i] = fa_lane{(const uint8_t *)L.w->k, (const uint8_t *)L.w->v, L.w->cell_pos, L.q, L.q_pos, L.out, nt, L.n_tokens};
+        a.lanes[i] = fa_lane{(const uint8_t *)L.w->k, (const uint8_t *)L.w->v, L.w->cell_pos, L.q, L.q_pos, L.out, nt,
+                             L.n_tokens};
     }
+    fp->n_lanes = n_lanes;
+    fp->rows = max_rows;
     if (max_rows == 0) return KVM_OK;
     const uint32_t D = w0->head_dim, H = w0->n_head_kv;
+    if (H > KVM_FA_MAX_HEADS) return kvm_fail(st, KVM_EUNSUPPORTED, "fa_decode: %u kv heads > %d", H, KVM_FA_MAX_HEADS);
     const int NRT = max_rows <= 16 ? 1 : 2;
     const uint32_t rmax = 16u * NRT;
     a.H = H;
@@ -716,35 +807,56 @@ static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes
     a.n_splits = choose_splits(st->n_cu, n_lanes, H, max_tiles);
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_type == KVM_TYPE_BF16;
+    const bool quant = w0->k_type == KVM_TYPE_Q8_0;
+    fp->D = D;
+    fp->quant = quant;
+    // workspace: the split partials, O then (m, l); with the caller's scratch,
+    // the split flags first
     const size_t part_bytes = (size_t)n_lanes * H * rmax * (D + 2) * sizeof(float);   // per key split
-    float *ws;
+    uint8_t *ws;
     if (scratch_cap) {
-        const size_t fit = scratch_cap / part_bytes;
+        const size_t sync_bytes = (KVM_FA_SYNC_WORDS * 4 + 255) & ~(size_t)255;
+        const size_t avail = scratch_cap > sync_bytes ? scratch_cap - sync_bytes : 0;
+        const size_t fit = avail / part_bytes;
         if (fit == 0)
-            return kvm_fail(st, KVM_ERANGE, "fa_decode: partials of one key split (%zu bytes) exceed the %zu-byte scratch",
-                            part_bytes, scratch_cap);
+            return kvm_fail(st, KVM_ERANGE, "fa_decode: the split flags and one key split's partials (%zu bytes) "
+                            "exceed the %zu-byte scratch", sync_bytes + part_bytes, scratch_cap);
         if (a.n_splits > fit) a.n_splits = (uint32_t)fit;
-        ws = (float *)scratch;
+        a.sync = (uint32_t *)scratch;
+        ws = (uint8_t *)scratch + sync_bytes;
     } else {
-        ws = (float *)kvm_workspace(st, part_bytes * a.n_splits);
+        ws = (uint8_t *)kvm_fa_workspace(st, part_bytes * a.n_splits);
         if (!ws) return kvm_fail(st, KVM_ENOMEM, "fa_decode: workspace of %zu bytes", part_bytes * a.n_splits);
+        a.sync = st->fa_sync;
     }
     const size_t n_part = (size_t)n_lanes * H * a.n_splits * rmax;
-    a.ws = ws;
-    a.ws_ml = ws + n_part * D;
-    KVM_HIP(st, hipSetDevice(st->device));
-    const bool quant = w0->k_type == KVM_TYPE_Q8_0;
-    if (D == 256) launch_decode_d<256>(a, n_lanes, max_rows, quant, st->stream);
-    else launch_decode_d<128>(a, n_lanes, max_rows, quant, st->stream);
-    KVM_LAUNCH_CHECK(st, "fa_decode");
-    // one wave per (row, 64 dims) of the rows some lane has
-    if (D == 256)
-        hipLaunchKernelGGL(k_fa_combine<256>, dim3(max_rows * 4, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
-    else
-        hipLaunchKernelGGL(k_fa_combine<128>, dim3(max_rows * 2, H, n_lanes), dim3(64), 0, st->stream, a, (int)rmax);
-    KVM_LAUNCH_CHECK(st, "fa_combine");
+    a.ws = (float *)ws;
+    a.ws_ml = a.ws + n_part * D;
     return KVM_OK;
 }
+
+// One launch on `stream`.  Every launch takes a new epoch: a split flag equals
+// it only once this launch has completed that split (flags start at 0, which
+// no launch uses).
+static int fa_launch(kvm_state *st, fa_plan &fp, hipStream_t stream) {
+    static std::atomic<uint32_t> g_epoch{0};
+    do fp.a.epoch = ++g_epoch; while (fp.a.epoch == 0);
+    KVM_HIP(st, hipSetDevice(st->device));
+    if (fp.D == 256) launch_decode_d<256>(fp.a, fp.n_lanes, fp.rows, fp.quant, stream);
+    else launch_decode_d<128>(fp.a, fp.n_lanes, fp.rows, fp.quant, stream);
+    KVM_LAUNCH_CHECK(st, "fa_decode");
+    return KVM_OK;
+}
+
+static int fa_decode_impl(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
+                          uint32_t n_head, float scale, void *scratch = nullptr, size_t scratch_cap = 0) {
+    fa_plan fp;
+    int rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, scratch, scratch_cap, &fp);
+    if (rc || fp.rows == 0) return rc;
+    return fa_launch(st, fp, st->stream);
+}
+
+size_t kvm_fa_sync_bytes() { return KVM_FA_SYNC_WORDS * sizeof(uint32_t); }
 
 extern "C" int kvm_fa_decode(kvm_state *st, const kvm_window *w, const void *q, int q_type,
                              const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,

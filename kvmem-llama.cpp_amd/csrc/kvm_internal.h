@@ -54,6 +54,13 @@ struct kvm_state {
     // device address of the fixed scratch array of the allocation-free entry
     // point on this state's device (kvm_noalloc_setup)
     void *scratch = nullptr;
+    // ticket counters of the decode attention's in-launch split merge (zero
+    // between launches; each launch leaves them zero), kvm_fa_sync_bytes()
+    uint32_t *fa_sync = nullptr;
+    // attention workspace (split partials), apart from `ws`, whose retrieval
+    // outputs a decode step's attention must not overwrite
+    void *fa_ws = nullptr;
+    size_t fa_ws_bytes = 0;
 };
 
 // error helpers ----------------------------------------------------------------
@@ -74,8 +81,12 @@ int kvm_fail(kvm_state *st, int code, const char *fmt, ...);
 // Looks up (once per device) the address of the allocation-free entry point's
 // scratch array on the state's device and records it in st->scratch.
 int kvm_noalloc_setup(kvm_state *st);
+// Bytes of the decode attention's counter block (kvm_state::fa_sync).
+size_t kvm_fa_sync_bytes();
 // Ensures the state's workspace holds at least `bytes`; returns it or nullptr.
 void *kvm_workspace(kvm_state *st, size_t bytes);
+// The same for the attention workspace (kvm_state::fa_ws).
+void *kvm_fa_workspace(kvm_state *st, size_t bytes);
 // Ensures a device copy of `bytes` of descriptor data; returns the device pointer.
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes);
 // theta_i = powf(base, -2i/n_rot) * scale for i < n_rot/2 (kvmem/src/host/rope.cpp:19-22)

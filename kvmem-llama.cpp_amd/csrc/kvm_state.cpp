@@ -34,7 +34,11 @@ extern "C" kvm_state *kvm_state_create(int device) {
     int n_cu = 0;
     if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && n_cu > 0)
         st->n_cu = (uint32_t)n_cu;
-    if (kvm_noalloc_setup(st) != KVM_OK) {
+    if (kvm_noalloc_setup(st) != KVM_OK || hipMalloc((void **)&st->fa_sync, kvm_fa_sync_bytes()) != hipSuccess ||
+        hipMemsetAsync(st->fa_sync, 0, kvm_fa_sync_bytes(), st->own_stream) != hipSuccess ||
+        hipStreamSynchronize(st->own_stream) != hipSuccess) {
+        if (st->fa_sync) (void)hipFree(st->fa_sync);
+    if (st->fa_ws) (void)hipFree(st->fa_ws);
         (void)hipEventDestroy(st->ev);
         (void)hipStreamDestroy(st->own_stream);
         delete st;
@@ -50,6 +54,8 @@ extern "C" void kvm_state_free(kvm_state *st) {
     if (st->ws) (void)hipFree(st->ws);
     if (st->rope_tab) (void)hipFree(st->rope_tab);
     if (st->desc) (void)hipFree(st->desc);
+    if (st->fa_sync) (void)hipFree(st->fa_sync);
+    if (st->fa_ws) (void)hipFree(st->fa_ws);
     if (st->slab) (void)hipHostFree(st->slab);
     if (st->ev) (void)hipEventDestroy(st->ev);
     if (st->own_stream) (void)hipStreamDestroy(st->own_stream);
@@ -74,23 +80,28 @@ extern "C" const char *kvm_state_last_error(const kvm_state *st) {
     return st ? st->err.c_str() : "null state";
 }
 
-void *kvm_workspace(kvm_state *st, size_t bytes) {
-    if (bytes <= st->ws_bytes) return st->ws;
+static void *grow(kvm_state *st, void **buf, size_t *have, size_t bytes) {
+    if (bytes <= *have) return *buf;
     // The old buffer may still be read by queued kernels: wait before freeing.
-    if (st->ws) {
+    if (*buf) {
         if (hipStreamSynchronize(st->stream) != hipSuccess) return nullptr;
-        (void)hipFree(st->ws);
-        st->ws = nullptr;
-        st->ws_bytes = 0;
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *have = 0;
     }
     size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (hipMalloc(&st->ws, want) != hipSuccess) {
-        st->ws = nullptr;
+    if (hipMalloc(buf, want) != hipSuccess) {
+        *buf = nullptr;
         return nullptr;
     }
-    st->ws_bytes = want;
-    return st->ws;
+    *have = want;
+    return *buf;
 }
+
+void *kvm_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->ws, &st->ws_bytes, bytes); }
+
+void *kvm_fa_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->fa_ws, &st->fa_ws_bytes, bytes); }
+
 
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes) {
     if (bytes > st->desc_bytes) {
