@@ -141,11 +141,31 @@ typedef struct kvm_query_acc {
     uint32_t *q_count;      /* device [n_layer] */
 } kvm_query_acc;
 
+/* A captured graph output as the attn-qk-capture hook sees it (patches/
+ * 0002-attn-qk-capture-hook.patch:275-290): ne2 tokens of ne1 heads of ne0
+ * values; element (token t, head h, dim d) at byte t*nb2 + h*nb1 + d*nb0 of
+ * `data` (device), of type F32, F16 or BF16.  The values enter every sum
+ * converted exactly to fp32, as the reference's token-major flattening does
+ * (bytes_to_f32_token_major, llama-memory-kvmem.cpp:3317-3341). */
+typedef struct kvm_view {
+    const void *data;
+    int type;
+    int64_t ne0, ne1, ne2;
+    size_t nb0, nb1, nb2;
+} kvm_view;
+
 int kvm_query_reset(kvm_state *st, const kvm_query_acc *acc);
 /* q_sum[il] += each of the n_rows pre-RoPE query rows in order; q_count[il] += n_rows.
  * q_rows: device fp32 [n_rows][n_head * head_dim]. */
 int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const float *q_rows,
                   uint32_t n_rows);
+/* The capture-format form (harvest_capture / harvest_from_host q-branch,
+ * llama-memory-kvmem.cpp:3417-3433, 3470-3483): the pre-RoPE Q view's tokens
+ * (ne0 * ne1 = n_head * head_dim) are added in token order, those with keep[t]
+ * != 0 only (the rows query_contains admits; keep is host [ne2], NULL = all);
+ * q_count[il] += the rows added. */
+int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const kvm_view *q,
+                       const uint8_t *keep);
 
 /* Mean-K index: per (layer, block) the ordered fp32 sum of pre-RoPE K rows and
  * its token count (RawKvStore k_sum / mean_tokens, raw_kv_store.cpp:215-234). */
@@ -161,6 +181,8 @@ typedef struct kvm_meank_index {
                              * kvm_meank_k_sum_floats() gives the size */
     uint32_t *mean_tokens;  /* device [n_layer][n_blocks] */
     uint8_t *present;       /* device [n_blocks] (RawKvStore::has_block), or NULL = all */
+    float *acc;             /* device [n_layer][n_head_kv * head_dim]: the decode running sum
+                             * (kvmem_meank_*, llama-kvmem-stagein.h:58-66), or NULL */
 } kvm_meank_index;
 
 /* Number of floats k_sum must hold for the index geometry in *ix. */
@@ -172,6 +194,24 @@ size_t kvm_meank_k_sum_floats(const kvm_meank_index *ix);
  * (llama-kvmem-stagein.cu:270-286). */
 int kvm_meank_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
                   uint32_t n, const float *k_rows);
+/* The same from a captured pre-RoPE K view (harvest_from_host k-branch,
+ * llama-memory-kvmem.cpp:3403-3416): its ne2 tokens at positions pos0 ..,
+ * ne0 * ne1 = n_head_kv * head_dim. */
+int kvm_meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
+                       const kvm_view *k);
+/* The decode running sum of accepted tokens, ix->acc (kvmem_meank_zero /
+ * kvmem_meank_add, llama-kvmem-stagein.cu:1066-1097): zero layer il; add view
+ * tokens tok0 .. tok0+n_keep-1 in order; flush it into the block holding
+ * positions pos0 .. pos0+n-1 as RawKvStore::write_layer_mean_sum does
+ * (raw_kv_store.cpp:707-731, called by decode_mean_flush,
+ * llama-memory-kvmem.cpp:3939-3993): the block's sum is zeroed when pos0
+ * starts the block, then += acc; mean_tokens as there.  Flushing does not
+ * zero the running sum (decode_mean_flush zeroes it next). */
+int kvm_meank_acc_zero(kvm_state *st, const kvm_meank_index *ix, uint32_t il);
+int kvm_meank_acc_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, const kvm_view *k,
+                      uint32_t tok0, uint32_t n_keep);
+int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
+                        uint32_t n);
 
 /* ------------------------------------------------------------------------ */
 /* Retrieval: scoring + top-k + chronological window layout                 */
@@ -196,6 +236,29 @@ typedef struct kvm_selection {
     uint32_t *stage_slots;      /* device [cap], slots whose contents must be (re)staged */
     uint32_t *info;             /* device [4] */
 } kvm_selection;
+
+/* A half-open range [begin, end) of original token positions (llama_kvmem_row_range,
+ * src/adapter/llama-kvmem-hooks.h:206-209). */
+typedef struct kvm_row_range {
+    int32_t begin;
+    int32_t end;
+} kvm_row_range;
+
+/* llama_memory_kvmem::retrieval_mandatory (llama-memory-kvmem.cpp:4306-4325): the
+ * block ids a retrieval must keep, for kvm_select_params.mandatory.  The ranges
+ * are the turn's explicit mandatory spans when n_spans > 0, else the query span
+ * [query_begin, query_end > 0 ? query_end : store end) when query_begin >= 0,
+ * else none; every block overlapping a range is listed once, in block order;
+ * then the block containing force_pos (KvMemStore::block_id_containing,
+ * kvmem/src/host/kvmem_store.cpp:158-177) is appended when force_pos >= 0 lies
+ * inside the store, even if already listed (the top-k counts each id once).
+ * n_tokens: host [n_blocks], block b covering original positions from
+ * sum_{i<b} n_tokens[i].  ids: host, capacity cap (n_blocks + 1 always fits).
+ * Host code only; st only receives the error message and may be NULL. */
+int kvm_retrieval_mandatory(kvm_state *st, const uint32_t *n_tokens, uint32_t n_blocks,
+                            const kvm_row_range *spans, uint32_t n_spans, int32_t query_begin,
+                            int32_t query_end, int32_t force_pos, uint32_t *ids, uint32_t cap,
+                            uint32_t *n_ids);
 
 /* score_retrieval (llama-memory-kvmem.cpp:4149-4196) + pick_topk_blocks
  * (kvmem/src/host/kvmem_store.cpp:357-359, 482-623, TopK policy, no media ranges)

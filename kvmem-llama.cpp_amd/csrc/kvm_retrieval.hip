@@ -8,17 +8,66 @@
 #include "kvm_stagein_dev.h"
 
 // ---------------------------------------------------------------------------
-// Query accumulator (llama-memory-kvmem.cpp:3300-3315, 3417-3433)
+// Captured views.  Element (token t, head hh, dim d) of a view lies at byte
+// t*nb2 + hh*nb1 + d*nb0 and is an fp32, fp16 or bf16 value; it enters every
+// sum converted exactly to fp32, as the reference's token-major flattening
+// does (bytes_to_f32_token_major, llama-memory-kvmem.cpp:3317-3341; the f16
+// K branch, 3405-3410, converts the same way).
 // ---------------------------------------------------------------------------
-__global__ void k_query_add(float *q_sum, uint32_t *q_count, uint32_t n_embd, const float *rows,
-                            uint32_t n_rows) {
-    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j < n_embd) {
-        float s = q_sum[j];
-        for (uint32_t r = 0; r < n_rows; ++r) s = kvm_fadd(s, rows[(uint64_t)r * n_embd + j]);
-        q_sum[j] = s;
+struct view_args {
+    const uint8_t *data;
+    int type;
+    uint32_t ne0;                // dims per head; embedding e = hh * ne0 + d
+    size_t nb0, nb1, nb2;
+};
+
+__device__ inline float view_load(const view_args &v, uint32_t t, uint32_t e) {
+    const uint8_t *p = v.data + (size_t)t * v.nb2 + (size_t)(e / v.ne0) * v.nb1 + (size_t)(e % v.ne0) * v.nb0;
+    if (v.type == KVM_TYPE_F16) return kvm_h2f(*(const uint16_t *)p);
+    if (v.type == KVM_TYPE_BF16) return kvm_bf2f(*(const uint16_t *)p);
+    return *(const float *)p;
+}
+
+static int view_check(kvm_state *st, const kvm_view *v, uint32_t n_embd, const char *what) {
+    if (!v || !v->data) return kvm_fail(st, KVM_EINVAL, "%s: null view", what);
+    if (v->type != KVM_TYPE_F32 && v->type != KVM_TYPE_F16 && v->type != KVM_TYPE_BF16)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "%s: view type %d", what, v->type);
+    if (v->ne0 <= 0 || v->ne1 <= 0 || v->ne2 < 0 || (uint64_t)v->ne0 * (uint64_t)v->ne1 != n_embd)
+        return kvm_fail(st, KVM_EINVAL, "%s: view of %lld x %lld values per token, expected %u", what,
+                        (long long)v->ne0, (long long)v->ne1, n_embd);
+    return KVM_OK;
+}
+
+static view_args view_of(const kvm_view *v) {
+    return view_args{(const uint8_t *)v->data, v->type, (uint32_t)v->ne0, v->nb0, v->nb1, v->nb2};
+}
+
+// Rows of one query-accumulation launch: their keep flags travel as a bitmask
+// in the kernel arguments.
+#define KVM_QVIEW_ROWS 2048u
+
+// ---------------------------------------------------------------------------
+// Query accumulator (llama-memory-kvmem.cpp:3300-3315 reset, 3417-3433 /
+// 3470-3483 add): q_sum[il][e] += row[e] for the kept rows in token order,
+// q_count[il] += kept rows.
+// ---------------------------------------------------------------------------
+struct qview_args {
+    view_args v;
+    float *q_sum;
+    uint32_t *q_count;
+    uint32_t n_embd, t0, n_rows, n_kept;
+    uint32_t keep[KVM_QVIEW_ROWS / 32];     // bit r: row t0 + r is added (all set without a mask)
+};
+
+__global__ void k_query_add(qview_args a) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < a.n_embd) {
+        float s = a.q_sum[e];
+        for (uint32_t r = 0; r < a.n_rows; ++r)
+            if (a.keep[r >> 5] >> (r & 31) & 1u) s = kvm_fadd(s, view_load(a.v, a.t0 + r, e));
+        a.q_sum[e] = s;
     }
-    if (j == 0) q_count[0] += n_rows;
+    if (e == 0) a.q_count[0] += a.n_kept;
 }
 
 __global__ void k_zero_f32(float *p, uint64_t n) {
@@ -42,17 +91,41 @@ extern "C" int kvm_query_reset(kvm_state *st, const kvm_query_acc *acc) {
     return KVM_OK;
 }
 
+extern "C" int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const kvm_view *q,
+                                  const uint8_t *keep) {
+    if (!st || !acc || !acc->q_sum || !acc->q_count) return kvm_fail(st, KVM_EINVAL, "query_add: args");
+    if (il >= acc->n_layer) return kvm_fail(st, KVM_ERANGE, "query_add: layer %u >= %u", il, acc->n_layer);
+    const uint32_t n_embd = acc->n_head * acc->head_dim;
+    int rc = view_check(st, q, n_embd, "query_add");
+    if (rc) return rc;
+    KVM_HIP(st, hipSetDevice(st->device));
+    for (uint64_t t0 = 0; t0 < (uint64_t)q->ne2; t0 += KVM_QVIEW_ROWS) {
+        qview_args a{};
+        a.v = view_of(q);
+        a.q_sum = acc->q_sum + (uint64_t)il * n_embd;
+        a.q_count = acc->q_count + il;
+        a.n_embd = n_embd;
+        a.t0 = (uint32_t)t0;
+        a.n_rows = (uint32_t)((uint64_t)q->ne2 - t0 < KVM_QVIEW_ROWS ? (uint64_t)q->ne2 - t0 : KVM_QVIEW_ROWS);
+        for (uint32_t r = 0; r < a.n_rows; ++r)
+            if (!keep || keep[t0 + r]) {
+                a.keep[r >> 5] |= 1u << (r & 31);
+                ++a.n_kept;
+            }
+        if (a.n_kept == 0) continue;
+        hipLaunchKernelGGL(k_query_add, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream, a);
+        KVM_LAUNCH_CHECK(st, "query_add");
+    }
+    return KVM_OK;
+}
+
 extern "C" int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t il,
                              const float *q_rows, uint32_t n_rows) {
-    if (!st || !acc || !acc->q_sum || !acc->q_count || !q_rows) return kvm_fail(st, KVM_EINVAL, "query_add: args");
-    if (il >= acc->n_layer) return kvm_fail(st, KVM_ERANGE, "query_add: layer %u >= %u", il, acc->n_layer);
-    if (n_rows == 0) return KVM_OK;
-    KVM_HIP(st, hipSetDevice(st->device));
-    const uint32_t n_embd = acc->n_head * acc->head_dim;
-    hipLaunchKernelGGL(k_query_add, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream,
-                       acc->q_sum + (uint64_t)il * n_embd, acc->q_count + il, n_embd, q_rows, n_rows);
-    KVM_LAUNCH_CHECK(st, "query_add");
-    return KVM_OK;
+    if (!st || !acc || !q_rows) return kvm_fail(st, KVM_EINVAL, "query_add: args");
+    const int64_t n_embd = (int64_t)acc->n_head * acc->head_dim;
+    const kvm_view v{q_rows, KVM_TYPE_F32, (int64_t)acc->head_dim, (int64_t)acc->n_head, (int64_t)n_rows,
+                     4, (size_t)acc->head_dim * 4, (size_t)n_embd * 4};
+    return n_rows ? kvm_query_add_view(st, acc, il, &v, nullptr) : KVM_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -74,9 +147,10 @@ extern "C" size_t kvm_meank_k_sum_floats(const kvm_meank_index *ix) {
     return (size_t)ix->n_layer * tiles * KVM_MEANK_TILE * ix->n_head_kv * ix->head_dim;
 }
 
+// One block's share (chunk ci of the positions pos0 .. pos0+n-1) per
+// blockIdx.y; the view's token pos - pos0 + tok0 holds position pos.
 __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *present, uint32_t cap,
-                            uint32_t n_embd, uint32_t bt, uint32_t pos0, uint32_t n,
-                            const float *rows) {
+                            uint32_t n_embd, uint32_t bt, uint32_t pos0, uint32_t n, view_args v, uint32_t tok0) {
     const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
     const uint32_t ci = blockIdx.y;                  // chunk = one block's share
     const uint32_t bid = pos0 / bt + ci;
@@ -88,7 +162,7 @@ __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *presen
     if (e < n_embd) {
         float *p = k_sum + kvm_meank_off(n_embd, e, bid);
         float s = off == 0 ? 0.0f : *p;
-        for (uint32_t t = start; t < end; ++t) s = kvm_fadd(s, rows[(uint64_t)(t - pos0) * n_embd + e]);
+        for (uint32_t t = start; t < end; ++t) s = kvm_fadd(s, view_load(v, t - pos0 + tok0, e));
         *p = s;
     }
     if (e == 0) {
@@ -98,24 +172,131 @@ __global__ void k_meank_add(float *k_sum, uint32_t *mean_tokens, uint8_t *presen
     }
 }
 
+static int meank_check(kvm_state *st, const kvm_meank_index *ix, uint32_t il, const char *what) {
+    if (!st || !ix || !ix->k_sum || !ix->mean_tokens || ix->block_tokens == 0)
+        return kvm_fail(st, KVM_EINVAL, "%s: args", what);
+    if (il >= ix->n_layer) return kvm_fail(st, KVM_ERANGE, "%s: layer %u", what, il);
+    return KVM_OK;
+}
+
+static uint64_t meank_layer_floats(const kvm_meank_index *ix) {
+    return (uint64_t)kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE) * KVM_MEANK_TILE * ix->n_head_kv * ix->head_dim;
+}
+
+// write_layer_mean_k from view tokens tok0 .. tok0+n-1 at positions pos0 ..
+static int meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0, const kvm_view *k,
+                          uint32_t tok0, uint32_t n) {
+    int rc = meank_check(st, ix, il, "meank_add");
+    if (rc) return rc;
+    const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
+    rc = view_check(st, k, n_embd, "meank_add");
+    if (rc) return rc;
+    if (n == 0) return KVM_OK;
+    if ((uint64_t)tok0 + n > (uint64_t)k->ne2) return kvm_fail(st, KVM_ERANGE, "meank_add: tokens past the view");
+    const uint32_t bt = ix->block_tokens;
+    const uint64_t last = ((uint64_t)pos0 + n - 1) / bt;
+    if (last >= ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "meank_add: block %llu >= capacity %u",
+                                              (unsigned long long)last, ix->n_blocks);
+    KVM_HIP(st, hipSetDevice(st->device));
+    const uint32_t n_chunks = (uint32_t)(last - pos0 / bt + 1);
+    hipLaunchKernelGGL(k_meank_add, dim3(kvm_cdiv(n_embd, 256), n_chunks), dim3(256), 0, st->stream,
+                       ix->k_sum + (uint64_t)il * meank_layer_floats(ix),
+                       ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present, ix->n_blocks, n_embd,
+                       bt, pos0, n, view_of(k), tok0);
+    KVM_LAUNCH_CHECK(st, "meank_add");
+    return KVM_OK;
+}
+
+extern "C" int kvm_meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
+                                  const kvm_view *k) {
+    if (!k) return kvm_fail(st, KVM_EINVAL, "meank_add: null view");
+    return meank_add_view(st, ix, il, pos0, k, 0, k->ne2 > 0 ? (uint32_t)k->ne2 : 0u);
+}
+
 extern "C" int kvm_meank_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
                              uint32_t n, const float *k_rows) {
-    if (!st || !ix || !ix->k_sum || !ix->mean_tokens || !k_rows || ix->block_tokens == 0)
-        return kvm_fail(st, KVM_EINVAL, "meank_add: args");
-    if (il >= ix->n_layer) return kvm_fail(st, KVM_ERANGE, "meank_add: layer %u", il);
-    if (n == 0) return KVM_OK;
-    const uint32_t bt = ix->block_tokens;
-    const uint32_t last = (pos0 + n - 1) / bt;
-    if (last >= ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "meank_add: block %u >= capacity %u", last, ix->n_blocks);
-    KVM_HIP(st, hipSetDevice(st->device));
+    if (!ix || !k_rows) return kvm_fail(st, KVM_EINVAL, "meank_add: args");
+    const int64_t n_embd = (int64_t)ix->n_head_kv * ix->head_dim;
+    const kvm_view v{k_rows, KVM_TYPE_F32, (int64_t)ix->head_dim, (int64_t)ix->n_head_kv, (int64_t)n,
+                     4, (size_t)ix->head_dim * 4, (size_t)n_embd * 4};
+    return meank_add_view(st, ix, il, pos0, &v, 0, n);
+}
+
+// ---------------------------------------------------------------------------
+// Decode running sum (kvmem_meank_zero / _add, llama-kvmem-stagein.cu:
+// 1066-1097; meank_add_* 270-320) and its flush into the index
+// (RawKvStore::write_layer_mean_sum, raw_kv_store.cpp:707-731, as
+// decode_mean_flush applies it, llama-memory-kvmem.cpp:3939-3993).
+// ---------------------------------------------------------------------------
+__global__ void k_meank_acc_add(float *acc, uint32_t n_embd, view_args v, uint32_t tok0, uint32_t n_keep) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_embd) return;
+    float s = acc[e];
+    for (uint32_t t = 0; t < n_keep; ++t) s = kvm_fadd(s, view_load(v, tok0 + t, e));
+    acc[e] = s;
+}
+
+// k_sum of block pos0 / bt: zeroed when the range starts the block, then
+// += acc[e]; mean_tokens as write_layer_mean_sum sets it.
+__global__ void k_meank_acc_flush(float *k_sum, uint32_t *mean_tokens, uint8_t *present, const float *acc,
+                                  uint32_t n_embd, uint32_t bid, uint32_t off, uint32_t take) {
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < n_embd) {
+        float *p = k_sum + kvm_meank_off(n_embd, e, bid);
+        *p = kvm_fadd(off == 0 ? 0.0f : *p, acc[e]);
+    }
+    if (e == 0) {
+        const uint32_t mt = mean_tokens[bid];
+        mean_tokens[bid] = off == 0 ? take : (mt > off + take ? mt : off + take);
+        if (present) present[bid] = 1;
+    }
+}
+
+extern "C" int kvm_meank_acc_zero(kvm_state *st, const kvm_meank_index *ix, uint32_t il) {
+    int rc = meank_check(st, ix, il, "meank_acc_zero");
+    if (rc) return rc;
+    if (!ix->acc) return kvm_fail(st, KVM_EINVAL, "meank_acc_zero: index without a running sum");
     const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
-    const uint32_t n_chunks = last - pos0 / bt + 1;
-    const uint64_t layer_floats = (uint64_t)kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE) * KVM_MEANK_TILE * n_embd;
-    hipLaunchKernelGGL(k_meank_add, dim3(kvm_cdiv(n_embd, 256), n_chunks), dim3(256), 0, st->stream,
-                       ix->k_sum + (uint64_t)il * layer_floats,
-                       ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present, ix->n_blocks, n_embd,
-                       bt, pos0, n, k_rows);
-    KVM_LAUNCH_CHECK(st, "meank_add");
+    KVM_HIP(st, hipSetDevice(st->device));
+    hipLaunchKernelGGL(k_zero_f32, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream,
+                       ix->acc + (uint64_t)il * n_embd, (uint64_t)n_embd);
+    KVM_LAUNCH_CHECK(st, "meank_acc_zero");
+    return KVM_OK;
+}
+
+extern "C" int kvm_meank_acc_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, const kvm_view *k,
+                                 uint32_t tok0, uint32_t n_keep) {
+    int rc = meank_check(st, ix, il, "meank_acc_add");
+    if (rc) return rc;
+    if (!ix->acc) return kvm_fail(st, KVM_EINVAL, "meank_acc_add: index without a running sum");
+    const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
+    rc = view_check(st, k, n_embd, "meank_acc_add");
+    if (rc) return rc;
+    if (n_keep == 0) return KVM_OK;
+    if ((uint64_t)tok0 + n_keep > (uint64_t)k->ne2) return kvm_fail(st, KVM_ERANGE, "meank_acc_add: tokens past the view");
+    KVM_HIP(st, hipSetDevice(st->device));
+    hipLaunchKernelGGL(k_meank_acc_add, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream,
+                       ix->acc + (uint64_t)il * n_embd, n_embd, view_of(k), tok0, n_keep);
+    KVM_LAUNCH_CHECK(st, "meank_acc_add");
+    return KVM_OK;
+}
+
+extern "C" int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
+                                   uint32_t n) {
+    int rc = meank_check(st, ix, il, "meank_acc_flush");
+    if (rc) return rc;
+    if (!ix->acc) return kvm_fail(st, KVM_EINVAL, "meank_acc_flush: index without a running sum");
+    if (n == 0) return KVM_OK;
+    const uint32_t bt = ix->block_tokens, bid = pos0 / bt, off = pos0 % bt;
+    const uint32_t take = n < bt - off ? n : bt - off;
+    if (bid >= ix->n_blocks) return kvm_fail(st, KVM_ERANGE, "meank_acc_flush: block %u >= capacity %u", bid, ix->n_blocks);
+    const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
+    KVM_HIP(st, hipSetDevice(st->device));
+    hipLaunchKernelGGL(k_meank_acc_flush, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream,
+                       ix->k_sum + (uint64_t)il * meank_layer_floats(ix),
+                       ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present,
+                       ix->acc + (uint64_t)il * n_embd, n_embd, bid, off, take);
+    KVM_LAUNCH_CHECK(st, "meank_acc_flush");
     return KVM_OK;
 }
 

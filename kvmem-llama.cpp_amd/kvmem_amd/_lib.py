@@ -41,7 +41,12 @@ class QueryAcc(C.Structure):
 class MeanKIndex(C.Structure):
     _fields_ = [("n_layer", C.c_uint32), ("n_blocks", C.c_uint32), ("n_head_kv", C.c_uint32),
                 ("head_dim", C.c_uint32), ("block_tokens", C.c_uint32), ("k_sum", C.c_void_p),
-                ("mean_tokens", C.c_void_p), ("present", C.c_void_p)]
+                ("mean_tokens", C.c_void_p), ("present", C.c_void_p), ("acc", C.c_void_p)]
+
+
+class View(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("type", C.c_int), ("ne0", C.c_int64), ("ne1", C.c_int64),
+                ("ne2", C.c_int64), ("nb0", C.c_size_t), ("nb1", C.c_size_t), ("nb2", C.c_size_t)]
 
 
 class SelectParams(C.Structure):
@@ -76,6 +81,10 @@ class StageinLane(C.Structure):
 class Lane(C.Structure):
     _fields_ = [("w", C.POINTER(Window)), ("q", C.c_void_p), ("q_pos", C.c_void_p),
                 ("out", C.c_void_p), ("n_tokens", C.c_uint32)]
+
+
+class RowRange(C.Structure):
+    _fields_ = [("begin", C.c_int32), ("end", C.c_int32)]
 
 
 class SnapshotInfo(C.Structure):
@@ -117,6 +126,11 @@ SIGNATURES = {
     "kvm_query_add": (C.c_int, [_P, C.POINTER(QueryAcc), _u32, _P, _u32]),
     "kvm_meank_k_sum_floats": (_sz, [C.POINTER(MeanKIndex)]),
     "kvm_meank_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32, _P]),
+    "kvm_query_add_view": (C.c_int, [_P, C.POINTER(QueryAcc), _u32, C.POINTER(View), _P]),
+    "kvm_meank_add_view": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, C.POINTER(View)]),
+    "kvm_meank_acc_zero": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32]),
+    "kvm_meank_acc_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, C.POINTER(View), _u32, _u32]),
+    "kvm_meank_acc_flush": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32]),
     "kvm_score_topk": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
                                  C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
     "kvm_score_topk_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), _u32]),
@@ -125,6 +139,8 @@ SIGNATURES = {
     "kvm_score_topk_stagein_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), C.POINTER(C.POINTER(History)), _u32,
                                                C.POINTER(RopeParams)]),
     "kvm_select_topk": (C.c_int, [_P, _P, C.POINTER(SelectParams), _PW, C.POINTER(Selection)]),
+    "kvm_retrieval_mandatory": (C.c_int, [_P, _P, _u32, C.POINTER(RowRange), _u32, _i32, _i32, _i32, _P, _u32,
+                                          C.POINTER(_u32)]),
     "kvm_stagein_selection": (C.c_int, [_P, C.POINTER(History), _PW, C.POINTER(Selection),
                                         C.POINTER(RopeParams)]),
     "kvm_stagein_selection_lanes": (C.c_int, [_P, C.POINTER(StageinLane), _u32, C.POINTER(RopeParams)]),

@@ -67,6 +67,17 @@ class State:
             pass
 
 
+_VIEW_TYPES = {torch.float32: L.T_F32, torch.float16: L.T_F16, torch.bfloat16: L.T_BF16}
+
+
+def view(t):
+    """The kvm_view of a 3-d device tensor [tokens][heads][dims] with its own strides."""
+    assert t.dim() == 3, "a view is [tokens][heads][dims]"
+    es = t.element_size()
+    return L.View(t.data_ptr(), _VIEW_TYPES[t.dtype], t.shape[2], t.shape[1], t.shape[0],
+                  t.stride(2) * es, t.stride(1) * es, t.stride(0) * es)
+
+
 class HostBuffer:
     """Pinned, device-mapped host memory (kvm_host_alloc) viewed as numpy."""
 
@@ -166,8 +177,10 @@ class MeanKIndex:
         self.k_sum = torch.zeros((n_layer, n_tiles, n_head_kv * head_dim, self.TILE), dtype=torch.float32, device=dev)
         self.mean_tokens = torch.zeros((n_layer, n_blocks), dtype=torch.int32, device=dev)
         self.present = torch.zeros((n_blocks,), dtype=torch.uint8, device=dev)
+        self.acc = torch.zeros((n_layer, n_head_kv * head_dim), dtype=torch.float32, device=dev)
         self.c = L.MeanKIndex(n_layer, n_blocks, n_head_kv, head_dim, block_tokens,
-                              self.k_sum.data_ptr(), self.mean_tokens.data_ptr(), self.present.data_ptr())
+                              self.k_sum.data_ptr(), self.mean_tokens.data_ptr(), self.present.data_ptr(),
+                              self.acc.data_ptr())
         assert self.k_sum.numel() == st.lib.kvm_meank_k_sum_floats(C.byref(self.c))
 
     def block_sums(self):
@@ -189,6 +202,19 @@ class MeanKIndex:
         self.st.check(self.st.lib.kvm_meank_add(self.st.h, C.byref(self.c), il, pos0,
                                                 k_rows.shape[0], _ptr(k_rows)))
 
+    def add_view(self, il, pos0, k):
+        """k: device tensor [tokens][heads][dims] (any strides) of fp32 / fp16 / bf16."""
+        self.st.check(self.st.lib.kvm_meank_add_view(self.st.h, C.byref(self.c), il, pos0, C.byref(view(k))))
+
+    def acc_zero(self, il):
+        self.st.check(self.st.lib.kvm_meank_acc_zero(self.st.h, C.byref(self.c), il))
+
+    def acc_add(self, il, k, tok0, n_keep):
+        self.st.check(self.st.lib.kvm_meank_acc_add(self.st.h, C.byref(self.c), il, C.byref(view(k)), tok0, n_keep))
+
+    def acc_flush(self, il, pos0, n):
+        self.st.check(self.st.lib.kvm_meank_acc_flush(self.st.h, C.byref(self.c), il, pos0, n))
+
 
 class QueryAcc:
     def __init__(self, st, n_layer, n_head, head_dim):
@@ -205,6 +231,13 @@ class QueryAcc:
         q_rows = q_rows.contiguous()
         self.st.check(self.st.lib.kvm_query_add(self.st.h, C.byref(self.c), il, _ptr(q_rows),
                                                 q_rows.shape[0]))
+
+    def add_view(self, il, q, keep=None):
+        """q: device tensor [tokens][heads][dims] (any strides) of fp32 / fp16 / bf16;
+        keep: host bool / uint8 array per token, or None for every token."""
+        kp = None if keep is None else np.ascontiguousarray(keep, np.uint8)
+        self.st.check(self.st.lib.kvm_query_add_view(self.st.h, C.byref(self.c), il, C.byref(view(q)),
+                                                     None if kp is None else kp.ctypes.data))
 
 
 class SelectionBuffers:
@@ -271,6 +304,21 @@ def select_topk(st, scores, n_tokens, budget_blocks, sink_blocks=1, recent_block
     st.check(st.lib.kvm_select_topk(st.h, C.c_void_p(scores.data_ptr()), C.byref(p),
                                     None if window is None else C.byref(window.c), C.byref(sel.c)))
     return sel
+
+
+def retrieval_mandatory(n_tokens, spans=(), query_begin=-1, query_end=0, force_pos=-1):
+    """Mandatory block ids of a retrieval (kvm_retrieval_mandatory): n_tokens is
+    the host per-block token count, spans (begin, end) row ranges."""
+    lib = L.load()
+    nt = np.ascontiguousarray(n_tokens, np.uint32)
+    arr = (L.RowRange * max(len(spans), 1))(*[L.RowRange(int(b), int(e)) for b, e in spans])
+    out = np.zeros(nt.size + 1, np.uint32)
+    n = L._u32(0)
+    rc = lib.kvm_retrieval_mandatory(None, nt.ctypes.data, nt.size, arr, len(spans), query_begin, query_end,
+                                     force_pos, out.ctypes.data, out.size, C.byref(n))
+    if rc:
+        raise L.KvmError(rc, "kvm_retrieval_mandatory")
+    return out[:n.value].astype(np.int64)
 
 
 def stagein_selection(st, history, window, sel, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):

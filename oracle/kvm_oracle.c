@@ -410,6 +410,54 @@ uint32_t oracle_window_layout(const uint32_t *sel, uint32_t n_sel, const uint32_
 }
 
 /* ------------------------------------------------------------------------- */
+/* Mandatory blocks of a retrieval (llama-memory-kvmem.cpp:4306-4325): the     */
+/* ranges are the explicit mandatory spans when given, else the query span     */
+/* [query_begin, query_end > 0 ? query_end : total) when query_begin >= 0;     */
+/* every block overlapping a range, once, in block order; then the block       */
+/* containing force_pos (KvMemStore::block_id_containing, kvmem_store.cpp:     */
+/* 158-177) when force_pos >= 0 and inside the store, appended even if listed. */
+/* Block b covers [sum_{i<b} n_tokens_i, + n_tokens_b).  Returns the count.    */
+/* ------------------------------------------------------------------------- */
+uint32_t oracle_retrieval_mandatory(const uint32_t *n_tokens, uint32_t n_blocks, const int32_t *ranges,
+                                    uint32_t n_ranges, int32_t query_begin, int32_t query_end,
+                                    int32_t force_pos, uint32_t *out) {
+    int64_t total = 0;
+    for (uint32_t b = 0; b < n_blocks; ++b) total += n_tokens[b];
+    int32_t qr[2];
+    const int32_t *rg = ranges;
+    uint32_t nr = n_ranges;
+    if (nr == 0 && query_begin >= 0) {
+        qr[0] = query_begin;
+        qr[1] = query_end > 0 ? query_end : (int32_t)total;
+        rg = qr;
+        nr = 1;
+    }
+    uint32_t n = 0;
+    int64_t start = 0;
+    for (uint32_t b = 0; b < n_blocks; ++b) {
+        const int64_t end = start + n_tokens[b];
+        for (uint32_t r = 0; r < nr; ++r) {
+            if (end > rg[2 * r] && start < rg[2 * r + 1]) {
+                out[n++] = b;
+                break;
+            }
+        }
+        start = end;
+    }
+    if (force_pos >= 0 && force_pos < total) {
+        start = 0;
+        for (uint32_t b = 0; b < n_blocks; ++b) {
+            if (force_pos >= start && force_pos < start + n_tokens[b]) {
+                out[n++] = b;
+                break;
+            }
+            start += n_tokens[b];
+        }
+    }
+    return n;
+}
+
+/* ------------------------------------------------------------------------- */
 /* Flash attention, ggml-CPU semantics (ggml-cpu/ops.cpp,                      */
 /* ggml_compute_forward_flash_attn_ext_f16_one_chunk, called from build_attn,  */
 /* patches/0002-attn-qk-capture-hook.patch:225 with kq_scale 1/sqrt(d) :256):  */

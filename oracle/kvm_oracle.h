@@ -97,6 +97,12 @@ uint32_t oracle_window_layout(const uint32_t *sel, uint32_t n_sel, const uint32_
                               uint32_t block_tokens, uint32_t n_slots, int32_t *to_base,
                               int32_t *cell_pos);
 
+/* ---- mandatory block ids from row ranges and force_pos (retrieval_mandatory) ----
+ * ranges: n_ranges pairs (begin, end); out holds n_blocks + 1 ids; returns the count. */
+uint32_t oracle_retrieval_mandatory(const uint32_t *n_tokens, uint32_t n_blocks, const int32_t *ranges,
+                                    uint32_t n_ranges, int32_t query_begin, int32_t query_end,
+                                    int32_t force_pos, uint32_t *out);
+
 /* ---- flash attention over a ggml-layout KV window ------------------------------
  * q        [n_tokens][n_head][head_dim] fp32
  * k, v     ggml rows [n_cells][n_head_kv * row(head_dim)] of k_type / v_type

@@ -53,6 +53,7 @@ def lib():
             "oracle_fa_ggml": (C.c_int, [C.c_int, C.c_int, P, P, P, P, P] + [C.c_int] * 5 + [f, P, C.c_int]),
             "oracle_fa_f64": (C.c_int, [C.c_int, C.c_int, P, P, P, P, P] + [C.c_int] * 5 + [d, P, C.c_int]),
             "oracle_quant_q8_0_rows": (None, [P, P, i64, i64]),
+            "oracle_retrieval_mandatory": (u32, [P, u32, P, u32, i32, i32, i32, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_o, name)
@@ -80,6 +81,8 @@ def ref():
         _r.ref_raw_snapshot.restype = C.c_longlong
         _r.ref_raw_snapshot.argtypes = [u32, u32, u32, u32, C.c_uint64, C.c_uint64, u32, u32, P, P, P, P,
                                         C.c_uint64]
+        _r.ref_block_layout.restype = C.c_int
+        _r.ref_block_layout.argtypes = [P, u32, u32, P, P, u32, P, u32, P]
         _r.ref_rope_neox.restype = None
         _r.ref_rope_neox.argtypes = [u32, u32, u32, f, f, P, u32, i32, P]
     return _r
@@ -224,6 +227,17 @@ def fa_f64(k_type, v_type, q, k_rows, v_rows, cell_pos, q_pos, n_head, n_head_kv
     return out
 
 
+def retrieval_mandatory(n_tokens, ranges=(), query_begin=-1, query_end=0, force_pos=-1):
+    """Mandatory block ids (llama-memory-kvmem.cpp:4306-4325) of a store whose
+    block b holds n_tokens[b] consecutive positions."""
+    nt = np.ascontiguousarray(n_tokens, np.uint32)
+    rg = np.ascontiguousarray(np.asarray(ranges, dtype=np.int32).reshape(-1, 2))
+    out = np.zeros(nt.size + 1, np.uint32)
+    n = lib().oracle_retrieval_mandatory(_p(nt), nt.size, _p(rg) if rg.size else None, rg.shape[0], query_begin,
+                                         query_end, force_pos, _p(out))
+    return out[:n].astype(np.int64)
+
+
 # ---- reference library (oracle/_ref) -----------------------------------------
 def ref_pick_topk(total_tokens, block_tokens, budget_tokens, sink_blocks, recent_blocks, scores, mandatory=()):
     scores = np.ascontiguousarray(scores, np.float64)
@@ -268,6 +282,20 @@ def ref_raw_snapshot(k_rows, k_f32, v_rows, n_embd_k, n_embd_v, block_tokens, ch
     out = np.zeros(n, np.uint8)
     assert ref().ref_raw_snapshot(*args, _p(out), n) == n
     return out.tobytes()
+
+
+def ref_block_layout(appends, block_tokens, positions):
+    """The reference store's blocks after register_append of each chunk in
+    `appends`: (orig_pos_start, n_tokens) per block, and block_id_containing of
+    each position."""
+    ap = np.ascontiguousarray(appends, np.uint32)
+    cap = int(ap.sum()) // block_tokens + len(ap) + 1
+    start, nt = np.zeros(cap, np.uint32), np.zeros(cap, np.uint32)
+    pos = np.ascontiguousarray(positions, np.int32)
+    cont = np.zeros(max(pos.size, 1), np.int32)
+    n = ref().ref_block_layout(_p(ap), ap.size, block_tokens, _p(start), _p(nt), cap, _p(pos), pos.size, _p(cont))
+    assert n >= 0
+    return start[:n].astype(np.int64), nt[:n].astype(np.int64), cont[:pos.size].astype(np.int64)
 
 
 def ref_mean_k(k, block_tokens, chunk):

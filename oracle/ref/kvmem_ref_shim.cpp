@@ -42,6 +42,31 @@ int ref_pick_topk(uint32_t total_tokens, uint32_t block_tokens, uint32_t budget_
     }
 }
 
+// Block bounds of a store filled by register_append in the given chunks
+// (kvmem_store.cpp:179-205): orig_pos_start and n_tokens per block; and
+// KvMemStore::block_id_containing (kvmem_store.cpp:158-177) of each position in
+// `pos`.  Returns #blocks or -1.
+int ref_block_layout(const uint32_t *appends, uint32_t n_appends, uint32_t block_tokens, uint32_t *start,
+                     uint32_t *n_tokens, uint32_t cap, const int32_t *pos, uint32_t n_pos, int32_t *containing) {
+    try {
+        kvmem::KvMemStoreConfig cfg;
+        cfg.block_tokens = block_tokens;
+        kvmem::KvMemStore s(cfg);
+        for (uint32_t i = 0; i < n_appends; ++i) s.register_append(appends[i]);
+        const auto &blocks = s.blocks();
+        if (blocks.size() > cap) return -1;
+        for (size_t i = 0; i < blocks.size(); ++i) {
+            start[i] = blocks[i].orig_pos_start;
+            n_tokens[i] = blocks[i].n_tokens;
+        }
+        for (uint32_t i = 0; i < n_pos; ++i)
+            containing[i] = pos[i] < 0 ? -1 : s.block_id_containing(static_cast<uint32_t>(pos[i]));
+        return static_cast<int>(blocks.size());
+    } catch (const std::exception &) {
+        return -1;
+    }
+}
+
 // One remap record as the executor sees it (kvmem_store.hpp:75-94).
 struct ref_remap {
     uint32_t block_id, n_tokens;

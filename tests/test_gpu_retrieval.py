@@ -279,3 +279,31 @@ def test_select_topk_maximum_size(kvm_state):
         assert np.array_equal(res["ids"], O.pick_topk(s, budget, 1, 2)), (kind, budget)
     with pytest.raises(L.KvmError):
         api.select_topk(kvm_state, dev(np.zeros(n + 1)), dev(np.full(n + 1, 128, np.int32)), 8, 1, 0)
+
+
+def test_topk_with_mandatory_blocks_from_row_ranges(kvm_state):
+    """The turn's mandatory spans and force_pos become block ids on the host
+    (kvm_retrieval_mandatory, llama-memory-kvmem.cpp:4306-4325) and the GPU
+    top-k keeps them within the budget, newest first, exactly as the oracle's
+    pick_topk_ungrouped restatement does; the query span stands in when the
+    turn has no explicit spans."""
+    rng = np.random.default_rng(17)
+    bt, n_blocks, budget = 128, 300, 24
+    nt = np.full(n_blocks, bt, np.int64)
+    nt[-1] = 61
+    total = int(nt.sum())
+    scores = rng.standard_normal(n_blocks)
+    cases = [([(1000, 1900), (30000, 30100)], -1, 0, 5000),     # explicit spans + force_pos
+             ([], 36000, 0, -1),                                 # query span to the store's end
+             ([(0, total)], -1, 0, 100),                         # every block mandatory: trimmed to the budget
+             ([], -1, 0, total - 1)]                             # force_pos alone, in the partial last block
+    for spans, qb, qe, fp in cases:
+        mand = api.retrieval_mandatory(nt, spans, qb, qe, fp)
+        want = O.pick_topk(scores, budget, 1, 2, mandatory=mand)
+        sel = api.select_topk(kvm_state, dev(scores), dev(nt.astype(np.int32)), budget, 1, 2,
+                              mandatory=dev(mand.astype(np.int32)))
+        r = sel.result()
+        assert r["status"] == 0 and np.array_equal(r["ids"], want), (spans, qb, fp)
+        kept = set(r["ids"].tolist())
+        if len(set(mand.tolist())) + 3 <= budget:
+            assert set(mand.tolist()) <= kept
