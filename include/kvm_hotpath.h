@@ -117,6 +117,37 @@ int kvm_window_export_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, u
                            void *k_rows, void *v_rows);
 
 /* ------------------------------------------------------------------------ */
+/* The slot seam of the reference runtime (kvmem::KvMemBackend,              */
+/* kvmem/include/kvmem/kvmem_backend.hpp:11-27, implemented by SlotBackend,  */
+/* src/adapter/llama-memory-kvmem.h:220-232).                                  */
+/* ------------------------------------------------------------------------ */
+/* A host free list of window slots (free_slots_, llama-memory-kvmem.cpp:
+ * 1018-1024, 1720-1741).  free_slots: caller memory of n_slots entries. */
+typedef struct kvm_slot_pool {
+    uint32_t n_slots;
+    uint32_t n_free;
+    int32_t *free_slots;
+} kvm_slot_pool;
+/* reset_slots: every slot free, pushed n_slots-1 .. 0 so that allocation
+ * yields 0, 1, 2, ... */
+int kvm_slot_pool_reset(kvm_slot_pool *p);
+/* alloc_gpu_slot / alloc_slot: the last freed slot, -1 when none is free. */
+int32_t kvm_slot_alloc(kvm_slot_pool *p);
+/* free_gpu_slot / free_slot: a negative slot is ignored; KVM_ERANGE for a slot
+ * outside the pool or a full list. */
+int kvm_slot_free(kvm_slot_pool *p, int32_t slot);
+/* copy_block_to_host / copy_block_from_host (copy_gpu_block_to_host /
+ * _from_host, llama-memory-kvmem.cpp:4073-4147): one slot's cells of every
+ * layer, in layer order: block_tokens ggml K rows, then block_tokens V rows.
+ * host may be pageable; both return once the copy is complete.  The reference
+ * stops silently when `bytes` runs out; here fewer bytes than the layers need
+ * is KVM_ERANGE and nothing is copied. */
+int kvm_slot_copy_to_host(kvm_state *st, const kvm_window *const *layers, uint32_t n_layers,
+                          int32_t slot, void *host, uint64_t bytes);
+int kvm_slot_copy_from_host(kvm_state *st, const kvm_window *const *layers, uint32_t n_layers,
+                            int32_t slot, const void *host, uint64_t bytes);
+
+/* ------------------------------------------------------------------------ */
 /* Row codecs (src/adapter/llama-kvmem-stagein.cu:133-234, ggml quantizers)  */
 /* ------------------------------------------------------------------------ */
 /* n_rows x n_per_row fp32 (device) -> ggml rows of type (Q8_0, Q4_0 or F16). */
@@ -212,6 +243,21 @@ int kvm_meank_acc_add(kvm_state *st, const kvm_meank_index *ix, uint32_t il, con
                       uint32_t tok0, uint32_t n_keep);
 int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
                         uint32_t n);
+
+/* Harvest of n generated tokens into the host history (harvest_gpu_v,
+ * llama-memory-kvmem.cpp:3583-3690, through the stage-out gather and one
+ * device-to-host copy, llama-kvmem-stagein.cu:879-969): the window cells
+ * [cell0, cell0+n) give their V rows (cache format, unchanged) and the view
+ * tokens tok0 .. tok0+n-1 of their captured pre-RoPE K give the history's
+ * unrotated K rows, quantised to q8_0 with ggml's formula (the rows the
+ * re-RoPE stage-in reads back); both are gathered on the device and copied to
+ * k_raw_rows / v_rows (host: the history rows of the tokens' positions).
+ * When ix is given the same K rows are added to its layer il at pos0
+ * (write_layer_mean_k).  q8_0 K windows; the copies are done when the state's
+ * stream reaches this point (kvm_state_sync). */
+int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
+                      const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,
+                      const kvm_meank_index *ix, uint32_t il, uint32_t pos0);
 
 /* ------------------------------------------------------------------------ */
 /* Retrieval: scoring + top-k + chronological window layout                 */

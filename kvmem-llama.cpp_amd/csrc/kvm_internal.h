@@ -300,3 +300,35 @@ __device__ __forceinline__ void kvm_quant_block_q4_0(const float (&x)[32], uint1
 }
 
 inline uint32_t kvm_cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Captured views (kvm_view): element (token t, head hh, dim d) at byte
+// t*nb2 + hh*nb1 + d*nb0, an fp32, fp16 or bf16 value, read as fp32.
+// ---------------------------------------------------------------------------
+struct view_args {
+    const uint8_t *data;
+    int type;
+    uint32_t ne0;                // dims per head; embedding e = hh * ne0 + d
+    size_t nb0, nb1, nb2;
+};
+
+__device__ inline float view_load(const view_args &v, uint32_t t, uint32_t e) {
+    const uint8_t *p = v.data + (size_t)t * v.nb2 + (size_t)(e / v.ne0) * v.nb1 + (size_t)(e % v.ne0) * v.nb0;
+    if (v.type == KVM_TYPE_F16) return kvm_h2f(*(const uint16_t *)p);
+    if (v.type == KVM_TYPE_BF16) return kvm_bf2f(*(const uint16_t *)p);
+    return *(const float *)p;
+}
+
+inline int view_check(kvm_state *st, const kvm_view *v, uint32_t n_embd, const char *what) {
+    if (!v || !v->data) return kvm_fail(st, KVM_EINVAL, "%s: null view", what);
+    if (v->type != KVM_TYPE_F32 && v->type != KVM_TYPE_F16 && v->type != KVM_TYPE_BF16)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "%s: view type %d", what, v->type);
+    if (v->ne0 <= 0 || v->ne1 <= 0 || v->ne2 < 0 || (uint64_t)v->ne0 * (uint64_t)v->ne1 != n_embd)
+        return kvm_fail(st, KVM_EINVAL, "%s: view of %lld x %lld values per token, expected %u", what,
+                        (long long)v->ne0, (long long)v->ne1, n_embd);
+    return KVM_OK;
+}
+
+inline view_args view_of(const kvm_view *v) {
+    return view_args{(const uint8_t *)v->data, v->type, (uint32_t)v->ne0, v->nb0, v->nb1, v->nb2};
+}

@@ -429,3 +429,166 @@ extern "C" int kvm_d2d_batched(kvm_state *st, const void *const *src, void *cons
     KVM_LAUNCH_CHECK(st, "d2d_batched");
     return KVM_OK;
 }
+
+// ---------------------------------------------------------------------------
+// The slot seam of the reference runtime (kvmem::KvMemBackend,
+// kvmem/include/kvmem/kvmem_backend.hpp:11-27, as SlotBackend implements it,
+// llama-memory-kvmem.h:220-232): a host free list of window slots and byte
+// copies of one slot's rows, every layer's K rows then V rows.
+// ---------------------------------------------------------------------------
+extern "C" int kvm_slot_pool_reset(kvm_slot_pool *p) {
+    if (!p || (p->n_slots && !p->free_slots)) return KVM_EINVAL;
+    // reset_slots (llama-memory-kvmem.cpp:1018-1024): pushed n-1 .. 0, so the
+    // first allocations return 0, 1, 2, ...
+    for (uint32_t i = 0; i < p->n_slots; ++i) p->free_slots[i] = (int32_t)(p->n_slots - 1 - i);
+    p->n_free = p->n_slots;
+    return KVM_OK;
+}
+
+extern "C" int32_t kvm_slot_alloc(kvm_slot_pool *p) {
+    if (!p || p->n_free == 0) return -1;                        // alloc_slot, 1720-1727
+    return p->free_slots[--p->n_free];
+}
+
+extern "C" int kvm_slot_free(kvm_slot_pool *p, int32_t slot) {
+    if (!p) return KVM_EINVAL;
+    if (slot < 0) return KVM_OK;                                // free_slot, 1729-1734
+    if ((uint32_t)slot >= p->n_slots || p->n_free >= p->n_slots) return KVM_ERANGE;
+    p->free_slots[p->n_free++] = slot;
+    return KVM_OK;
+}
+
+// Bytes per layer of one slot: block_tokens K rows, then block_tokens V rows.
+static uint64_t slot_span(const kvm_window *w, uint64_t *kspan) {
+    const uint64_t krow = (uint64_t)w->n_head_kv * (w->k_type == KVM_TYPE_Q8_0 ? w->head_dim / 32 * 34 : w->head_dim * 2);
+    const uint64_t vrow = (uint64_t)w->n_head_kv * (w->v_type == KVM_TYPE_Q4_0 ? w->head_dim / 32 * 18 : w->head_dim * 2);
+    *kspan = w->block_tokens * krow;
+    return *kspan + w->block_tokens * vrow;
+}
+
+static int slot_copy_check(kvm_state *st, const kvm_window *const *layers, uint32_t n_layers, int32_t slot,
+                           const void *host, uint64_t bytes, uint64_t *need, const char *what) {
+    if (!st || !layers || !host) return kvm_fail(st, KVM_EINVAL, "%s: null argument", what);
+    *need = 0;
+    for (uint32_t il = 0; il < n_layers; ++il) {
+        int rc = kvm_window_check(layers[il]);
+        if (rc) return kvm_fail(st, rc, "%s: layer %u: bad window", what, il);
+        if (slot < 0 || (uint64_t)(slot + 1) * layers[il]->block_tokens > layers[il]->n_cells)
+            return kvm_fail(st, KVM_ERANGE, "%s: slot %d outside layer %u's window", what, slot, il);
+        uint64_t kspan;
+        *need += slot_span(layers[il], &kspan);
+    }
+    if (bytes < *need) return kvm_fail(st, KVM_ERANGE, "%s: %llu bytes < %llu", what, (unsigned long long)bytes,
+                                       (unsigned long long)*need);
+    return KVM_OK;
+}
+
+extern "C" int kvm_slot_copy_to_host(kvm_state *st, const kvm_window *const *layers, uint32_t n_layers,
+                                     int32_t slot, void *host, uint64_t bytes) {
+    uint64_t need;
+    int rc = slot_copy_check(st, layers, n_layers, slot, host, bytes, &need, "slot_copy_to_host");
+    if (rc || need == 0) return rc;
+    uint8_t *stage = (uint8_t *)kvm_workspace(st, need);
+    if (!stage) return kvm_fail(st, KVM_ENOMEM, "slot_copy_to_host: staging of %llu bytes", (unsigned long long)need);
+    uint64_t off = 0;
+    for (uint32_t il = 0; il < n_layers; ++il) {
+        const kvm_window *w = layers[il];
+        uint64_t kspan;
+        const uint64_t span = slot_span(w, &kspan);
+        rc = kvm_window_export_rows(st, w, (uint32_t)slot * w->block_tokens, w->block_tokens, stage + off, stage + off + kspan);
+        if (rc) return rc;
+        off += span;
+    }
+    KVM_HIP(st, hipMemcpyAsync(host, stage, need, hipMemcpyDeviceToHost, st->stream));
+    KVM_HIP(st, hipStreamSynchronize(st->stream));
+    return KVM_OK;
+}
+
+extern "C" int kvm_slot_copy_from_host(kvm_state *st, const kvm_window *const *layers, uint32_t n_layers,
+                                       int32_t slot, const void *host, uint64_t bytes) {
+    uint64_t need;
+    int rc = slot_copy_check(st, layers, n_layers, slot, host, bytes, &need, "slot_copy_from_host");
+    if (rc || need == 0) return rc;
+    uint8_t *stage = (uint8_t *)kvm_workspace(st, need);
+    if (!stage) return kvm_fail(st, KVM_ENOMEM, "slot_copy_from_host: staging of %llu bytes", (unsigned long long)need);
+    KVM_HIP(st, hipMemcpyAsync(stage, host, need, hipMemcpyHostToDevice, st->stream));
+    uint64_t off = 0;
+    for (uint32_t il = 0; il < n_layers; ++il) {
+        const kvm_window *w = layers[il];
+        uint64_t kspan;
+        const uint64_t span = slot_span(w, &kspan);
+        rc = kvm_window_import_rows(st, w, (uint32_t)slot * w->block_tokens, w->block_tokens, stage + off,
+                                    stage + off + kspan, nullptr);
+        if (rc) return rc;
+        off += span;
+    }
+    KVM_HIP(st, hipStreamSynchronize(st->stream));
+    return KVM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Harvest of a block of generated tokens into the host history
+// (harvest_gpu_v, llama-memory-kvmem.cpp:3583-3690, through the stage-out
+// gather and one device-to-host copy, llama-kvmem-stagein.cu:879-969).  The
+// history keeps unrotated K (the stage-in re-applies RoPE), so the block's K
+// rows are the q8_0 rows of its captured pre-RoPE K, quantised here with the
+// ggml q8_0 formula; its V rows are the window's cache rows, unchanged.
+// ---------------------------------------------------------------------------
+__global__ void k_quant_view_q8(view_args v, uint32_t tok0, uint32_t n, uint32_t n_embd, uint8_t *dst) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;     // 32-value block
+    const uint32_t nb = n_embd / 32;
+    if (i >= (uint64_t)n * nb) return;
+    const uint32_t t = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
+    float x[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) x[j] = view_load(v, tok0 + t, 32 * b + j);
+    uint16_t d;
+    int8_t q[32];
+    kvm_quant_block_q8_0(x, &d, q);
+    uint8_t *o = dst + i * 34;
+    o[0] = (uint8_t)d;
+    o[1] = (uint8_t)(d >> 8);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)q[j];
+}
+
+extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
+                                 const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,
+                                 const kvm_meank_index *ix, uint32_t il, uint32_t pos0) {
+    if (!st) return KVM_EINVAL;
+    int rc = kvm_window_check(w);
+    if (rc) return kvm_fail(st, rc, "harvest: bad window");
+    if (w->k_type != KVM_TYPE_Q8_0) return kvm_fail(st, KVM_EUNSUPPORTED, "harvest: q8_0 K history only");
+    if ((uint64_t)cell0 + n > w->n_cells) return kvm_fail(st, KVM_ERANGE, "harvest: cells past the window");
+    const uint32_t n_embd = w->n_head_kv * w->head_dim;
+    rc = view_check(st, k_prerope, n_embd, "harvest");
+    if (rc) return rc;
+    if ((uint64_t)tok0 + n > (uint64_t)k_prerope->ne2) return kvm_fail(st, KVM_ERANGE, "harvest: tokens past the view");
+    if (!k_raw_rows || !v_rows) return kvm_fail(st, KVM_EINVAL, "harvest: null history rows");
+    if (n == 0) return KVM_OK;
+    const uint64_t krow = (uint64_t)n_embd / 32 * 34;
+    const uint64_t vrow = w->v_type == KVM_TYPE_Q4_0 ? (uint64_t)n_embd / 32 * 18 : (uint64_t)n_embd * 2;
+    const uint64_t kb = n * krow, vb = n * vrow;
+    uint8_t *stage = (uint8_t *)kvm_workspace(st, kb + vb);
+    if (!stage) return kvm_fail(st, KVM_ENOMEM, "harvest: staging of %llu bytes", (unsigned long long)(kb + vb));
+    KVM_HIP(st, hipSetDevice(st->device));
+    // the gather: K rows quantised from the view, V rows out of the tiles
+    const uint64_t nblk = (uint64_t)n * (n_embd / 32);
+    hipLaunchKernelGGL(k_quant_view_q8, dim3(kvm_cdiv(nblk, 256)), dim3(256), 0, st->stream, view_of(k_prerope),
+                       tok0, n, n_embd, stage);
+    KVM_LAUNCH_CHECK(st, "harvest");
+    rc = kvm_window_export_rows(st, w, cell0, n, nullptr, stage + kb);
+    if (rc) return rc;
+    if (ix) {
+        // the mean-K index from the same captured rows (write_layer_mean_k)
+        kvm_view part = *k_prerope;
+        part.data = (const uint8_t *)k_prerope->data + (size_t)tok0 * k_prerope->nb2;
+        part.ne2 = n;
+        rc = kvm_meank_add_view(st, ix, il, pos0, &part);
+        if (rc) return rc;
+    }
+    KVM_HIP(st, hipMemcpyAsync(k_raw_rows, stage, kb, hipMemcpyDeviceToHost, st->stream));
+    KVM_HIP(st, hipMemcpyAsync(v_rows, stage + kb, vb, hipMemcpyDeviceToHost, st->stream));
+    return KVM_OK;
+}
+

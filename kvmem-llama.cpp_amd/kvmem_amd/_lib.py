@@ -83,6 +83,10 @@ class Lane(C.Structure):
                 ("out", C.c_void_p), ("n_tokens", C.c_uint32)]
 
 
+class SlotPool(C.Structure):
+    _fields_ = [("n_slots", C.c_uint32), ("n_free", C.c_uint32), ("free_slots", C.c_void_p)]
+
+
 class RowRange(C.Structure):
     _fields_ = [("begin", C.c_int32), ("end", C.c_int32)]
 
@@ -120,6 +124,13 @@ SIGNATURES = {
     "kvm_window_reset": (C.c_int, [_P, _PW]),
     "kvm_window_import_rows": (C.c_int, [_P, _PW, _u32, _u32, _P, _P, _P]),
     "kvm_window_export_rows": (C.c_int, [_P, _PW, _u32, _u32, _P, _P]),
+    "kvm_slot_pool_reset": (C.c_int, [C.POINTER(SlotPool)]),
+    "kvm_slot_alloc": (_i32, [C.POINTER(SlotPool)]),
+    "kvm_slot_free": (C.c_int, [C.POINTER(SlotPool), _i32]),
+    "kvm_slot_copy_to_host": (C.c_int, [_P, C.POINTER(_PW), _u32, _i32, _P, C.c_uint64]),
+    "kvm_slot_copy_from_host": (C.c_int, [_P, C.POINTER(_PW), _u32, _i32, _P, C.c_uint64]),
+    "kvm_harvest_block": (C.c_int, [_P, _PW, _u32, _u32, C.POINTER(View), _u32, _P, _P, C.POINTER(MeanKIndex),
+                                    _u32, _u32]),
     "kvm_quantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_dequantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_query_reset": (C.c_int, [_P, C.POINTER(QueryAcc)]),

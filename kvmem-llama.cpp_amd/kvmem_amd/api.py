@@ -306,6 +306,59 @@ def select_topk(st, scores, n_tokens, budget_blocks, sink_blocks=1, recent_block
     return sel
 
 
+class SlotPool:
+    """Host free list of window slots (kvm_slot_pool: reset_slots / alloc_slot /
+    free_slot of the reference adapter)."""
+
+    def __init__(self, n_slots):
+        self.lib = L.load()
+        self.buf = np.zeros(max(n_slots, 1), np.int32)
+        self.c = L.SlotPool(n_slots, 0, self.buf.ctypes.data)
+        self.reset()
+
+    def reset(self):
+        rc = self.lib.kvm_slot_pool_reset(C.byref(self.c))
+        if rc:
+            raise L.KvmError(rc, "kvm_slot_pool_reset")
+
+    def alloc(self):
+        return self.lib.kvm_slot_alloc(C.byref(self.c))
+
+    def free(self, slot):
+        rc = self.lib.kvm_slot_free(C.byref(self.c), slot)
+        if rc:
+            raise L.KvmError(rc, "kvm_slot_free")
+
+
+def _layers(windows):
+    arr = (C.POINTER(L.Window) * len(windows))()
+    for i, w in enumerate(windows):
+        arr[i] = C.pointer(w.c)
+    return arr
+
+
+def slot_copy_to_host(st, windows, slot):
+    """One slot of every layer's window as bytes: per layer, block_tokens K rows then V rows."""
+    need = sum(w.block_tokens * (w.k_row_bytes() + w.v_row_bytes()) for w in windows)
+    out = np.zeros(need, np.uint8)
+    st.check(st.lib.kvm_slot_copy_to_host(st.h, _layers(windows), len(windows), slot, out.ctypes.data, need))
+    return out
+
+
+def slot_copy_from_host(st, windows, slot, data):
+    data = np.ascontiguousarray(data, np.uint8)
+    st.check(st.lib.kvm_slot_copy_from_host(st.h, _layers(windows), len(windows), slot, data.ctypes.data, data.nbytes))
+
+
+def harvest_block(st, window, cell0, n, k_prerope, tok0, k_raw_rows, v_rows, index=None, il=0, pos0=0):
+    """kvm_harvest_block: k_raw_rows / v_rows are numpy uint8 arrays (the history
+    rows of the tokens); returns after the copies are complete."""
+    st.check(st.lib.kvm_harvest_block(st.h, C.byref(window.c), cell0, n, C.byref(view(k_prerope)), tok0,
+                                      k_raw_rows.ctypes.data, v_rows.ctypes.data,
+                                      None if index is None else C.byref(index.c), il, pos0))
+    st.sync()
+
+
 def retrieval_mandatory(n_tokens, spans=(), query_begin=-1, query_end=0, force_pos=-1):
     """Mandatory block ids of a retrieval (kvm_retrieval_mandatory): n_tokens is
     the host per-block token count, spans (begin, end) row ranges."""

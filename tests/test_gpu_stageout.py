@@ -1,0 +1,96 @@
+"""Stage-out side of the window: the slot seam's byte copies (copy_block_to_host
+/ _from_host, llama-memory-kvmem.cpp:4073-4147) and the harvest of generated
+blocks into the host history (harvest_gpu_v, llama-memory-kvmem.cpp:3583-3690;
+stage-out gather + D2H, llama-kvmem-stagein.cu:879-969), then the cycle the
+runtime orders (stage-out before stage-in, kvmem_runtime.cpp:121-126, 225-249):
+a harvested block leaves the window and a later retrieval stages it back from
+the history, byte-equal to the oracle's stage-in of the harvested rows."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import dev, host, rand_rows
+from kvmem_amd import api, _lib as L
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("kt,vt,H,D", [(L.T_Q8_0, L.T_Q4_0, 4, 256), (L.T_F16, L.T_F16, 2, 128)])
+def test_slot_copies_round_trip(kvm_state, kt, vt, H, D):
+    rng = np.random.default_rng(31)
+    bt, n_cells = 128, 8 * 128
+    layers = []
+    for il in range(3):
+        w = api.KVWindow(kvm_state, n_cells, H, D, bt, kt, vt)
+        kr, vr = rand_rows(rng, n_cells, H, D, kt, vt)
+        w.import_rows(0, dev(kr), dev(vr), dev(np.arange(n_cells, dtype=np.int32)))
+        layers.append((w, kr, vr))
+    ws = [w for w, _, _ in layers]
+    blob = api.slot_copy_to_host(kvm_state, ws, 3)
+    off = 0
+    for w, kr, vr in layers:
+        kb, vb = bt * w.k_row_bytes(), bt * w.v_row_bytes()
+        assert np.array_equal(blob[off:off + kb], kr[3 * bt:4 * bt].reshape(-1))
+        assert np.array_equal(blob[off + kb:off + kb + vb], vr[3 * bt:4 * bt].reshape(-1))
+        off += kb + vb
+    assert off == blob.size
+    # into slot 6 of three empty windows: their rows now equal slot 3's
+    dst = [api.KVWindow(kvm_state, n_cells, H, D, bt, kt, vt) for _ in range(3)]
+    api.slot_copy_from_host(kvm_state, dst, 6, blob)
+    for w, (_, kr, vr) in zip(dst, layers):
+        ek, ev = w.export_rows(6 * bt, bt)
+        assert np.array_equal(host(ek), kr[3 * bt:4 * bt]) and np.array_equal(host(ev), vr[3 * bt:4 * bt])
+    with pytest.raises(L.KvmError):                         # too few bytes
+        api.slot_copy_from_host(kvm_state, dst, 6, blob[:-1])
+    with pytest.raises(L.KvmError):                         # slot past the window
+        api.slot_copy_to_host(kvm_state, ws, 8)
+
+
+def test_harvest_then_restage(kvm_state):
+    """Generated tokens occupy slot 5 of the window (window positions 640..767,
+    original positions 4*128.. of the history); the harvest writes their
+    q8_0-quantised captured pre-RoPE K and their window V rows as history
+    block 4 and adds the K to the mean-K index; a reselect that drops the block
+    reuses the slot, and a later one that picks it again stages it back from the
+    history exactly as the oracle stages the harvested rows."""
+    rng = np.random.default_rng(32)
+    H, D, bt, n_hist_blocks = 4, 256, 128, 8
+    n_hist = n_hist_blocks * bt
+    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    k_hist = np.zeros_like(kr)
+    v_hist = np.zeros_like(vr)
+    k_hist[:4 * bt], v_hist[:4 * bt] = kr[:4 * bt], vr[:4 * bt]     # blocks 4.. are not harvested yet
+    hist = api.History(k_hist, v_hist)
+    w = api.KVWindow(kvm_state, 6 * bt, H, D, bt)
+    # generated block: rotated K rows in the cache (any bytes), V rows, positions
+    gk, gv = rand_rows(rng, bt, H, D, L.T_Q8_0, L.T_Q4_0)
+    w.import_rows(5 * bt, dev(gk), dev(gv), dev(np.arange(5 * bt, 6 * bt, dtype=np.int32)))
+    cap = torch.from_numpy(rng.standard_normal((bt + 3, H, D)).astype(np.float32)).to(torch.bfloat16).cuda()
+    cap = cap.permute(1, 0, 2).contiguous().permute(1, 0, 2)          # the captured view, heads-major storage
+    ix = api.MeanKIndex(kvm_state, 1, n_hist_blocks, H, D, bt)
+    api.harvest_block(kvm_state, w, 5 * bt, bt, cap, 3, hist.kbuf.u8[4 * bt * w.k_row_bytes():].reshape(-1)[:bt * w.k_row_bytes()],
+                      hist.vbuf.u8[4 * bt * w.v_row_bytes():].reshape(-1)[:bt * w.v_row_bytes()], ix, 0, 4 * bt)
+    k32 = cap[3:].float().cpu().numpy().reshape(bt, -1)
+    want_k = O.quant(O.T_Q8_0, k32.reshape(-1)).reshape(bt, -1)
+    got_k = hist.kbuf.u8.reshape(n_hist, -1)[4 * bt:5 * bt]
+    assert np.array_equal(got_k, want_k)
+    assert np.array_equal(hist.vbuf.u8.reshape(n_hist, -1)[4 * bt:5 * bt], gv)
+    sums, mt = O.meank_sums(k32, bt)
+    assert np.array_equal(host(ix.block_sums())[0][4].view(np.uint32), sums[0].view(np.uint32))
+    assert int(host(ix.mean_tokens)[0][4]) == bt
+    # the window's slot map: slots 0..3 hold blocks 0..3; block 4 leaves and comes back
+    nt = dev(np.full(n_hist_blocks, bt, np.int32))
+    s = np.zeros(n_hist_blocks)
+    s[[1, 2, 3]] = [3, 2, 1]
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    s[3], s[4] = 0.0, 5.0                                              # block 4 (harvested) is picked
+    sel = api.select_topk(kvm_state, dev(s), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(kvm_state, hist, w, sel, 64, 1e7)
+    r = sel.result()
+    assert list(r["ids"]) == [0, 1, 2, 4] and r["status"] == 0
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, ev = w.export_rows(3 * bt, bt)
+    assert np.array_equal(host(ek).reshape(-1), O.stagein_k(want_k.reshape(-1), bt, H, D, 64, 256, 3 * bt, theta))
+    assert np.array_equal(host(ev), gv)
