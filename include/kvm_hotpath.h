@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 2
+#define KVM_ABI_VERSION 3
 
 enum kvm_status {
     KVM_OK = 0,
@@ -96,10 +96,23 @@ typedef struct kvm_window {
     int32_t *cell_pos;      /* device [n_cells]: position of the cell's token, -1 = empty */
     uint32_t *slot_block;   /* device [n_slots]: block id held by the slot, 0xffffffff = none */
     int32_t *slot_base;     /* device [n_slots]: position the slot's first cell is baked at */
+    /* Optional HBM shadow of the staged blocks' raw K (both NULL = none).  A
+     * stage-in writes every staged cell's unrotated q8_0 K row (the history's
+     * bytes) here and the slot's staged row count into shadow_rows; a later
+     * plan that moves a full block to another slot or base re-rotates it from
+     * the shadow and moves its V within HBM instead of reading the host
+     * history again (the reference reloads such blocks from the host, or moves
+     * them with kvmem_d2d_batched without re-rotation,
+     * llama-memory-kvmem.cpp:1958-2285).  Importing rows into a slot's cells
+     * and kvm_slot_copy_from_host void that slot's shadow (shadow_rows = 0). */
+    void *k_shadow;         /* device [n_cells][n_head_kv * row(head_dim)] of q8_0 */
+    uint32_t *shadow_rows;  /* device [n_slots]: rows of the slot the shadow holds */
 } kvm_window;
 
 size_t kvm_window_k_bytes(const kvm_window *w);
 size_t kvm_window_v_bytes(const kvm_window *w);
+/* Bytes of the optional K shadow (q8_0 windows; 0 otherwise). */
+size_t kvm_window_shadow_bytes(const kvm_window *w);
 /* Checks geometry; KVM_OK when the window is usable. */
 int kvm_window_check(const kvm_window *w);
 /* Empties every cell and slot (reset_slots + seq_rm of the pool,
@@ -281,6 +294,10 @@ typedef struct kvm_selection {
     int32_t *to_base;           /* device [cap], window position of each block */
     uint32_t *stage_slots;      /* device [cap], slots whose contents must be (re)staged */
     uint32_t *info;             /* device [4] */
+    /* device [cap] or NULL: for stage_slots[i], the slot whose shadow and V
+     * hold that block before the plan (a full block already in the window of a
+     * window with a shadow), else -1 = stage from the host history */
+    int32_t *stage_src;
 } kvm_selection;
 
 /* A half-open range [begin, end) of original token positions (llama_kvmem_row_range,
@@ -369,7 +386,11 @@ typedef struct kvm_history {
  * (llama-kvmem-stagein.cu:731-786 order) and writes the tiled window; V bytes
  * are moved unchanged (stagein.cu:733-744).  Updates cell_pos, slot_block and
  * slot_base.  Replaces write_block_to_gpu + kvmem_stagein_flush
- * (llama-memory-kvmem.cpp:4000-4071, stagein.cu:669-790) for one retrieval. */
+ * (llama-memory-kvmem.cpp:4000-4071, stagein.cu:669-790) for one retrieval.
+ * Entries with sel->stage_src[i] >= 0 (a window with a shadow) take their raw K
+ * rows from the shadow of that slot and their V from that slot's tiles, all
+ * gathered before any slot is written, so the window ends byte-equal to a
+ * stage-in of the whole plan from the host. */
 int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
                           const kvm_selection *sel, const kvm_rope_params *rope);
 

@@ -54,13 +54,18 @@ struct kvm_state {
     // device address of the fixed scratch array of the allocation-free entry
     // point on this state's device (kvm_noalloc_setup)
     void *scratch = nullptr;
-    // ticket counters of the decode attention's in-launch split merge (zero
-    // between launches; each launch leaves them zero), kvm_fa_sync_bytes()
+    // per-split arrival flags of the decode attention's in-launch split merge
+    // (each holds the epoch of the last launch that completed the split) and
+    // its status word, kvm_fa_sync_bytes()
     uint32_t *fa_sync = nullptr;
     // attention workspace (split partials), apart from `ws`, whose retrieval
     // outputs a decode step's attention must not overwrite
     void *fa_ws = nullptr;
     size_t fa_ws_bytes = 0;
+    // staging of the blocks a stage-in plan moves within the window (their
+    // shadow K rows and V rows, gathered before any slot is written)
+    void *mv_ws = nullptr;
+    size_t mv_ws_bytes = 0;
 };
 
 // error helpers ----------------------------------------------------------------
@@ -87,6 +92,8 @@ size_t kvm_fa_sync_bytes();
 void *kvm_workspace(kvm_state *st, size_t bytes);
 // The same for the attention workspace (kvm_state::fa_ws).
 void *kvm_fa_workspace(kvm_state *st, size_t bytes);
+// The same for the stage-in move staging (kvm_state::mv_ws).
+void *kvm_move_workspace(kvm_state *st, size_t bytes);
 // Ensures a device copy of `bytes` of descriptor data; returns the device pointer.
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes);
 // theta_i = powf(base, -2i/n_rot) * scale for i < n_rot/2 (kvmem/src/host/rope.cpp:19-22)

@@ -538,6 +538,9 @@ struct topk_args {
     uint32_t *stage_slots;
     uint32_t *info;
     uint32_t n, budget, sink, recent, n_mand, n_slots, cap, n_layer, ls_cap;
+    const uint32_t *shadow_rows;   // the window's shadow row counts, or null
+    int32_t *stage_src;            // per staged entry, the old slot it moves from (-1: host)
+    uint32_t bt;                   // the window's block_tokens
 };
 
 #define KVM_TOPK_THREADS 1024
@@ -631,14 +634,18 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_
     constexpr uint32_t SLT = KVM_TOPK_SLOTS / KVM_TOPK_THREADS;
     const uint32_t *sbp = a.slot_block ? a.slot_block : a.n_tokens;
     const int32_t *sbb = a.slot_base ? a.slot_base : (const int32_t *)a.n_tokens;
+    // blocks may move within the window (from the shadow of their old slot)
+    const bool moves = a.stage_src && a.shadow_rows && a.slot_block;
+    const uint32_t *srp = moves ? a.shadow_rows : a.n_tokens;
     const uint32_t nsl1 = n_sl_lds ? n_sl_lds - 1 : 0u, n1 = n ? n - 1 : 0u;
-    uint32_t sl_blk[SLT];
+    uint32_t sl_blk[SLT], sl_rows[SLT];
     int32_t sl_base[SLT];
 #pragma unroll
     for (uint32_t j = 0; j < SLT; ++j) {
         const uint32_t i = tid + j * KVM_TOPK_THREADS;
         sl_blk[j] = sbp[i < nsl1 ? i : nsl1];
         sl_base[j] = sbb[i < nsl1 ? i : nsl1];
+        sl_rows[j] = srp[i < nsl1 ? i : nsl1];
     }
     const uint32_t kpt = (n + KVM_TOPK_THREADS - 1) / KVM_TOPK_THREADS;
     const bool have_ls = a.layer_score != nullptr, have_pr = have_ls && a.present != nullptr;
@@ -948,6 +955,20 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_
             KVM_LDS_BARRIER();
         }
     }
+    // ---- the old slot of every block the window holds with a complete shadow
+    // (a full block), in the keys' buffer, which the selection no longer
+    // reads: s_inv[b] = slot, or -1 for a slot whose shadow is incomplete.
+    // Entries of blocks in no slot are not written; a lookup accepts slot j
+    // only where the slot map names the block, so stale entries are harmless.
+    int32_t *const s_inv = (int32_t *)s_big;
+    if (moves) {
+#pragma unroll
+        for (uint32_t j = 0; j < SLT; ++j) {
+            const uint32_t i = tid + j * KVM_TOPK_THREADS;
+            if (i < n_sl_lds && sl_blk[j] < n) s_inv[sl_blk[j]] = sl_rows[j] == a.bt ? (int32_t)i : -1;
+        }
+        KVM_LDS_BARRIER();
+    }
     // ---- ascending compaction with window positions: ranks and token
     // offsets of this thread's blocks come from one scan
     uint32_t local = 0, tok = 0;
@@ -983,7 +1004,19 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_
         uint32_t rank = rank0, k = 0;
         for (uint32_t i = i0; i < i1; ++i) {
             if (!s_kept[i]) continue;
-            if (need_mask >> k & 1u) a.stage_slots[pos++] = rank;
+            if (need_mask >> k & 1u) {
+                a.stage_slots[pos] = rank;
+                if (a.stage_src) {
+                    // a full block in a slot with a complete shadow moves from there
+                    int32_t src = -1;
+                    if (moves && s_ntok[i] == a.bt) {
+                        const int32_t j = s_inv[i];
+                        if (j >= 0 && (uint32_t)j < n_sl_lds && s_sblk[j] == i) src = j;
+                    }
+                    a.stage_src[pos] = src;
+                }
+                ++pos;
+            }
             ++rank;
             ++k;
         }
@@ -1001,6 +1034,11 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_
         const bool ok = fits && (n_sel <= a.n_slots || a.n_slots == 0);
         if (ok && n_stage > 0) {
             __syncthreads();                 // the plan is written; the selection's LDS is free
+            if (sa.moves) {
+                // blocks moving within the window: every source read before any slot is written
+                for (uint32_t si = 0; si < n_stage; ++si) stage_gather_entry<SD>(sa, si, tid, KVM_TOPK_THREADS);
+                __syncthreads();
+            }
             const uint32_t tps = sa.bt / 64;
             for (uint32_t item = 0; item < n_stage * tps; ++item) {
                 stagein_item<SD, KVM_TOPK_THREADS>(sa, s_big, item / tps, item % tps);
@@ -1034,7 +1072,8 @@ static int make_topk(kvm_state *st, const double *scores, const double *layer_sc
                     out->ids, out->to_base, out->stage_slots, out->info,
                     p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
                     w ? w->n_cells / w->block_tokens : 0u, out->cap,
-                    ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u};
+                    ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u,
+                    w ? w->shadow_rows : nullptr, w ? out->stage_src : nullptr, w ? w->block_tokens : 0u};
     return KVM_OK;
 }
 

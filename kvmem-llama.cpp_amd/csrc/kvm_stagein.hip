@@ -28,6 +28,15 @@ __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     }
 }
 
+// The gather of the entries moving within the window (stage_src >= 0), before
+// k_stagein writes any slot: one workgroup per plan entry and lane.
+template <int D>
+__global__ void __launch_bounds__(256) k_stage_gather(stage_lanes sl) {
+    const stage_args &a = sl.lane[blockIdx.y];
+    if (!a.moves || (a.info[3] & 3u) != 0) return;
+    const uint32_t n = a.info[2];
+    for (uint32_t si = blockIdx.x; si < n; si += gridDim.x) stage_gather_entry<D>(a, si, threadIdx.x, 256);
+}
 
 static int rope_ctx_for(kvm_state *st, const float *theta, uint32_t n_half, int32_t nrot,
                         uint32_t max_pos, rope_ctx *rc) {
@@ -84,9 +93,24 @@ static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window
     a->to_base = sel->to_base;
     a->stage_slots = sel->stage_slots;
     a->info = sel->info;
+    // the shadow is kept whenever the window has one; blocks move within the
+    // window when the plan also names their sources (moves: set by the caller)
+    a->k_shadow = (uint8_t *)w->k_shadow;
+    a->shadow_rows = w->shadow_rows;
+    a->stage_src = w->k_shadow ? sel->stage_src : nullptr;
+    a->moves = nullptr;
     const uint32_t max_slots = sel->cap < a->n_slots ? sel->cap : a->n_slots;
     *max_items = max_slots * (w->block_tokens / 64);
     return KVM_OK;
+}
+
+// Bytes of a lane's move staging: every plan entry may move (bt K rows and the
+// slot's V tiles each).
+static uint64_t move_bytes(const kvm_window *w, const kvm_selection *sel) {
+    if (!w->k_shadow || !sel->stage_src) return 0;
+    const uint32_t n_slots = w->n_cells / w->block_tokens, max_slots = sel->cap < n_slots ? sel->cap : n_slots;
+    const uint64_t NB = w->head_dim / 32;
+    return (uint64_t)max_slots * w->block_tokens * w->n_head_kv * NB * (34 + 18);
 }
 
 int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
@@ -120,6 +144,18 @@ int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_l
     if (rc) return rc;
     for (uint32_t i = 0; i < n_lanes; ++i) sl->lane[i].rc = rc0;
     *lds = (size_t)64 * max_h * (w0->head_dim / 32) * (34 + 18);
+    // the lanes' move staging regions, one after the other (256-byte aligned)
+    uint64_t mv_total = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) mv_total += (move_bytes(lanes[i].w, lanes[i].sel) + 255) & ~255ull;
+    if (mv_total) {
+        uint8_t *mv = (uint8_t *)kvm_move_workspace(st, mv_total);
+        if (!mv) return kvm_fail(st, KVM_ENOMEM, "stagein: move staging of %llu bytes", (unsigned long long)mv_total);
+        for (uint32_t i = 0; i < n_lanes; ++i) {
+            const uint64_t b = (move_bytes(lanes[i].w, lanes[i].sel) + 255) & ~255ull;
+            if (b) sl->lane[i].moves = mv;
+            mv += b;
+        }
+    }
     return KVM_OK;
 }
 
@@ -139,6 +175,21 @@ extern "C" int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane
     const uint32_t wgs = KVM_STAGEIN_WGS_PER_CU * st->n_cu, per_lane = (wgs + n_lanes - 1) / n_lanes;
     const dim3 grid(max_items < per_lane ? max_items : per_lane, n_lanes);
     if (grid.x == 0) return KVM_OK;
+    bool moves = false;
+    for (uint32_t i = 0; i < n_lanes; ++i) moves = moves || sl.lane[i].moves;
+    if (moves) {
+        // a workgroup per plan entry, up to about two per CU in all
+        uint32_t gx = 0;
+        for (uint32_t i = 0; i < n_lanes; ++i) {
+            const uint32_t ns = lanes[i].w->n_cells / lanes[i].w->block_tokens;
+            const uint32_t e = lanes[i].sel->cap < ns ? lanes[i].sel->cap : ns;
+            gx = e > gx ? e : gx;
+        }
+        const dim3 gg(gx < per_lane ? gx : per_lane, n_lanes);
+        if (lanes[0].w->head_dim == 256) hipLaunchKernelGGL(k_stage_gather<256>, gg, dim3(256), 0, st->stream, sl);
+        else hipLaunchKernelGGL(k_stage_gather<128>, gg, dim3(256), 0, st->stream, sl);
+        KVM_LAUNCH_CHECK(st, "stage_gather");
+    }
     if (lanes[0].w->head_dim == 256) {
         KVM_HIP(st, hipFuncSetAttribute((const void *)k_stagein<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(k_stagein<256>, grid, dim3(256), lds, st->stream, sl);

@@ -120,7 +120,42 @@ struct stage_args {
     const uint32_t *stage_slots;
     uint32_t *info;
     rope_ctx rc;
+    // HBM re-basing of resident blocks (all null without a shadow): the raw K
+    // rows of every staged cell, per plan entry the slot its block held before
+    // the plan (-1: from the host), and per plan entry a staging region of
+    // bt K rows then bt V rows that the gather fills before any slot is written
+    uint8_t *k_shadow;
+    uint32_t *shadow_rows;
+    const int32_t *stage_src;
+    uint8_t *moves;
 };
+
+// Row bytes of the history / shadow: q8_0 K and q4_0 V, all kv heads.
+__host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 34; }
+__host__ __device__ inline uint32_t stage_row_v(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 18; }
+
+// Gather of a plan entry whose block moves within the window (stage_src[si] =
+// src >= 0) into its staging region, by threads tid, tid + nth, ...: the bt raw
+// K rows from the shadow of slot src, then the slot's V tiles, [head][tile of
+// the slot].  Slots start on tile boundaries (block_tokens % 64 == 0), so a V
+// tile's bytes do not depend on where the slot lies and move as they are.
+// Only full blocks move (the top-k stages partly filled ones from the host).
+template <int D>
+__device__ inline void stage_gather_entry(const stage_args &a, uint32_t si, uint32_t tid, uint32_t nth) {
+    const int32_t src = a.stage_src[si];
+    if (src < 0) return;
+    const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
+    uint8_t *dk = a.moves + (uint64_t)si * a.bt * (rowK + rowV);
+    const uint4 *sk = (const uint4 *)(a.k_shadow + (uint64_t)src * a.bt * rowK);
+    for (uint32_t i = tid; i < a.bt * rowK / 16; i += nth) ((uint4 *)dk)[i] = sk[i];
+    const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
+    uint4 *dv = (uint4 *)(dk + (uint64_t)a.bt * rowK);
+    for (uint32_t i = tid; i < a.H * tps * per; i += nth) {
+        const uint32_t ht = i / per, h = ht / tps, q = ht % tps;
+        const uint4 *sv = (const uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps + q) * vtile);
+        dv[i] = sv[i % per];
+    }
+}
 
 
 // One (plan entry, IT-token run) item, staged by a workgroup of NTH threads
@@ -137,7 +172,8 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     // kvmem_store.cpp:179-205): block id covers [id*bt, min((id+1)*bt, h_tokens))
     const uint64_t first = (uint64_t)id * a.bt;
     const uint32_t tid = threadIdx.x;
-    if (first >= a.h_tokens) {
+    const int32_t src = a.moves ? a.stage_src[si] : -1;          // >= 0: rows from the gathered staging
+    if (src < 0 && first >= a.h_tokens) {
         // a block outside the history is not staged: report it, and empty the
         // slot's cells of this item (and, once, its slot map entry) so attention
         // never reads what the slot held before and the next plan restages it
@@ -146,18 +182,23 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         if (tt == 0 && tid == 0) {
             a.slot_block[slot] = 0xffffffffu;
             a.slot_base[slot] = -1;
+            if (a.shadow_rows) a.shadow_rows[slot] = 0u;
         }
         return;
     }
-    const uint32_t nt = a.h_tokens - first < a.bt ? (uint32_t)(a.h_tokens - first) : a.bt;
+    const uint32_t nt = src >= 0 ? a.bt : (a.h_tokens - first < a.bt ? (uint32_t)(a.h_tokens - first) : a.bt);
     const uint32_t t0 = tt * IT;
     const uint32_t count = nt > t0 ? (nt - t0 < IT ? nt - t0 : IT) : 0;
     const uint64_t htok0 = first + t0;
     const uint32_t rowK = a.H * NB * 34, rowV = a.H * NB * 18;
     uint8_t *lk = s_rows, *lv = s_rows + IT * rowK;
-    // bulk copy of `count` consecutive token rows of K and V (contiguous in host memory)
-    const uint8_t *gk = a.hk + htok0 * rowK, *gv = a.hv + htok0 * rowV;
-    const uint32_t nk = count * rowK, nv = count * rowV;
+    // bulk copy of `count` consecutive token rows of K and V (contiguous in host
+    // memory, or in the entry's staging region for a block moving in HBM)
+    const uint8_t *mk = src >= 0 ? a.moves + (uint64_t)si * a.bt * (rowK + rowV) : nullptr;
+    const uint8_t *gk = src >= 0 ? mk + (uint64_t)t0 * rowK : a.hk + htok0 * rowK;
+    const uint8_t *gv = src >= 0 ? mk : a.hv + htok0 * rowV;
+    // a moved block's V comes as whole tiles (below), not as rows
+    const uint32_t nk = count * rowK, nv = src >= 0 ? 0u : count * rowV;
     const bool al16 = (((uintptr_t)gk | (uintptr_t)gv | rowK | rowV) & 15u) == 0;
     if (al16) {
 #pragma unroll 4
@@ -169,6 +210,14 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         for (uint32_t i = tid; i < nv; i += NTH) lv[i] = gv[i];
     }
     __syncthreads();
+    // the raw K rows of the staged cells into the shadow (read when the block
+    // is later re-based within the window)
+    if (a.k_shadow) {
+        // 16-byte aligned: the item starts at a multiple of 32 rows, of an even size
+        uint8_t *sk = a.k_shadow + ((uint64_t)slot * a.bt + t0) * rowK;
+        for (uint32_t i = tid; i < nk / 16; i += NTH) ((uint4 *)sk)[i] = ((const uint4 *)lk)[i];
+        for (uint32_t i = nk / 16 * 16 + tid; i < nk; i += NTH) sk[i] = lk[i];
+    }
 
     const uint32_t tile = (slot * a.bt + t0) / 64, c0 = t0 % 64;   // c0: the item's first cell in the tile
     // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ...
@@ -178,31 +227,42 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         uint8_t *kt = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
         stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, c0 + j, base + (int32_t)(t0 + j), a.rc);
     }
-    // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
+    // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step;
+    // a moved block's words and scales are those of its gathered tiles
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
     constexpr uint32_t NKS = IT / 32;    // key halves of the tile this item fills
+    const uint8_t *mv = src >= 0 ? gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile : nullptr;
+    const uint64_t mv_head = (uint64_t)(a.bt / 64) * vtile;     // gathered tiles of one head
     for (uint32_t wi = tid; wi < a.H * D * 4 * NKS; wi += NTH) {
         const uint32_t h = wi / (D * 4 * NKS), r = wi % (D * 4 * NKS);
         const uint32_t X = r / NKS, ks = NKS == 2 ? (r & 1u) : c0 / 32;
         const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
         const uint32_t b = dd / 32, e = dd % 32;
         uint32_t word = 0;
+        if (src >= 0) {
+            word = *(const uint32_t *)(mv + h * mv_head + kvm_vq_word(dd, gg, ks));
+        } else {
 #pragma unroll
-        for (uint32_t j = 0; j < 8; ++j) {
-            const uint32_t cj = 32 * ks + 8 * gg + j - c0;    // key within the item
-            uint32_t nib = 0;
-            if (cj < count) {
-                const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
-                nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint32_t cj = 32 * ks + 8 * gg + j - c0;    // key within the item
+                uint32_t nib = 0;
+                if (cj < count) {
+                    const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
+                    nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
+                }
+                word |= nib << kvm_vq_nib_shift(j);
             }
-            word |= nib << kvm_vq_nib_shift(j);
         }
         *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
     }
     for (uint32_t si2 = tid; si2 < a.H * IT * NB; si2 += NTH) {
         const uint32_t h = si2 / (IT * NB), cj = (si2 / NB) % IT, b = si2 % NB;
         uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, c0 + cj, b);
-        if (cj < count) {
+        if (src >= 0) {
+            const uint8_t *md = mv + h * mv_head + kvm_vd_off(D, c0 + cj, b);
+            sd[0] = md[0];
+            sd[1] = md[1];
+        } else if (cj < count) {
             const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
             sd[0] = blk[0];
             sd[1] = blk[1];
@@ -215,6 +275,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     if (tt == 0 && tid == 0) {
         a.slot_block[slot] = id;
         a.slot_base[slot] = base;
+        if (a.shadow_rows) a.shadow_rows[slot] = nt;
     }
 }
 

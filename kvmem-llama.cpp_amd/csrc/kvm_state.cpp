@@ -38,7 +38,6 @@ extern "C" kvm_state *kvm_state_create(int device) {
         hipMemsetAsync(st->fa_sync, 0, kvm_fa_sync_bytes(), st->own_stream) != hipSuccess ||
         hipStreamSynchronize(st->own_stream) != hipSuccess) {
         if (st->fa_sync) (void)hipFree(st->fa_sync);
-    if (st->fa_ws) (void)hipFree(st->fa_ws);
         (void)hipEventDestroy(st->ev);
         (void)hipStreamDestroy(st->own_stream);
         delete st;
@@ -56,6 +55,7 @@ extern "C" void kvm_state_free(kvm_state *st) {
     if (st->desc) (void)hipFree(st->desc);
     if (st->fa_sync) (void)hipFree(st->fa_sync);
     if (st->fa_ws) (void)hipFree(st->fa_ws);
+    if (st->mv_ws) (void)hipFree(st->mv_ws);
     if (st->slab) (void)hipHostFree(st->slab);
     if (st->ev) (void)hipEventDestroy(st->ev);
     if (st->own_stream) (void)hipStreamDestroy(st->own_stream);
@@ -101,6 +101,8 @@ static void *grow(kvm_state *st, void **buf, size_t *have, size_t bytes) {
 void *kvm_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->ws, &st->ws_bytes, bytes); }
 
 void *kvm_fa_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->fa_ws, &st->fa_ws_bytes, bytes); }
+
+void *kvm_move_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->mv_ws, &st->mv_ws_bytes, bytes); }
 
 
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes) {

@@ -16,7 +16,15 @@ extern "C" int kvm_window_check(const kvm_window *w) {
     const bool h = w->k_type == KVM_TYPE_F16 && w->v_type == KVM_TYPE_F16;
     if (!q && !h) return KVM_EUNSUPPORTED;
     if (!w->k || !w->v || !w->cell_pos) return KVM_EINVAL;
+    // a shadow comes with its row counts and the slot map, and holds q8_0 rows
+    if (!w->k_shadow != !w->shadow_rows) return KVM_EINVAL;
+    if (w->k_shadow && (!q || !w->slot_block || !w->slot_base)) return KVM_EINVAL;
     return KVM_OK;
+}
+
+extern "C" size_t kvm_window_shadow_bytes(const kvm_window *w) {
+    if (!w || w->k_type != KVM_TYPE_Q8_0) return 0;
+    return (size_t)w->n_cells * w->n_head_kv * (w->head_dim / 32) * 34;
 }
 
 extern "C" size_t kvm_window_k_bytes(const kvm_window *w) {
@@ -48,6 +56,9 @@ extern "C" int kvm_window_reset(kvm_state *st, const kvm_window *w) {
     if (w->slot_base)
         hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
                            w->slot_base, -1, n_slots);
+    if (w->shadow_rows)
+        hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
+                           (int32_t *)w->shadow_rows, 0, n_slots);
     KVM_LAUNCH_CHECK(st, "window_reset");
     return KVM_OK;
 }
@@ -58,7 +69,15 @@ extern "C" int kvm_window_reset(kvm_state *st, const kvm_window *w) {
 struct win_geo {
     uint8_t *k, *v;
     uint32_t H, D, n_tiles, ktile, vtile;
+    uint32_t *shadow_rows;       // null, or the shadow row counts an import voids
+    uint32_t bt, n_slots;
 };
+
+// An import into cell `cell` voids its slot's shadow (the shadow holds only
+// what a stage-in wrote); called by the thread of the cell's first row block.
+__device__ inline void void_shadow(const win_geo &g, uint32_t cell) {
+    if (g.shadow_rows && cell / g.bt < g.n_slots) g.shadow_rows[cell / g.bt] = 0u;
+}
 
 static win_geo geo_of(const kvm_window *w) {
     win_geo g;
@@ -69,6 +88,9 @@ static win_geo geo_of(const kvm_window *w) {
     g.n_tiles = w->n_cells / KVM_TILE_CELLS;
     g.ktile = kvm_ktile_bytes(w->k_type, w->head_dim);
     g.vtile = kvm_vtile_bytes(w->v_type, w->head_dim);
+    g.shadow_rows = w->shadow_rows;
+    g.bt = w->block_tokens;
+    g.n_slots = w->n_cells / w->block_tokens;
     return g;
 }
 
@@ -90,6 +112,7 @@ __global__ void k_import_k_q8(win_geo g, uint32_t cell0, uint32_t n, const uint8
     uint8_t *sd = dst + kvm_kd_off(g.D, c, b);
     sd[0] = src[0];
     sd[1] = src[1];
+    if (b == 0 && h == 0) void_shadow(g, cell);
 }
 
 // f16 K rows: one thread per (cell, head, dim)
@@ -138,6 +161,7 @@ __global__ void k_import_v_q4_scales(win_geo g, uint32_t cell0, uint32_t n, cons
     uint8_t *dst = g.v + ((uint64_t)h * g.n_tiles + tile) * g.vtile + kvm_vd_off(g.D, c, b);
     dst[0] = blk[0];
     dst[1] = blk[1];
+    if (b == 0 && h == 0) void_shadow(g, cell);
 }
 
 __global__ void k_import_v_f16(win_geo g, uint32_t cell0, uint32_t n, const uint16_t *rows) {

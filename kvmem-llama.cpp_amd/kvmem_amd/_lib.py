@@ -30,7 +30,8 @@ class Window(C.Structure):
     _fields_ = [("n_cells", C.c_uint32), ("n_head_kv", C.c_uint32), ("head_dim", C.c_uint32),
                 ("block_tokens", C.c_uint32), ("k_type", C.c_int32), ("v_type", C.c_int32),
                 ("k", C.c_void_p), ("v", C.c_void_p), ("cell_pos", C.c_void_p),
-                ("slot_block", C.c_void_p), ("slot_base", C.c_void_p)]
+                ("slot_block", C.c_void_p), ("slot_base", C.c_void_p),
+                ("k_shadow", C.c_void_p), ("shadow_rows", C.c_void_p)]
 
 
 class QueryAcc(C.Structure):
@@ -57,7 +58,8 @@ class SelectParams(C.Structure):
 
 class Selection(C.Structure):
     _fields_ = [("cap", C.c_uint32), ("scores", C.c_void_p), ("ids", C.c_void_p),
-                ("to_base", C.c_void_p), ("stage_slots", C.c_void_p), ("info", C.c_void_p)]
+                ("to_base", C.c_void_p), ("stage_slots", C.c_void_p), ("info", C.c_void_p),
+                ("stage_src", C.c_void_p)]
 
 
 class RetrievalLane(C.Structure):
@@ -120,6 +122,7 @@ SIGNATURES = {
     "kvm_host_free": (None, [_P]),
     "kvm_window_k_bytes": (_sz, [_PW]),
     "kvm_window_v_bytes": (_sz, [_PW]),
+    "kvm_window_shadow_bytes": (_sz, [_PW]),
     "kvm_window_check": (C.c_int, [_PW]),
     "kvm_window_reset": (C.c_int, [_P, _PW]),
     "kvm_window_import_rows": (C.c_int, [_P, _PW, _u32, _u32, _P, _P, _P]),

@@ -1,7 +1,10 @@
 """The C ABI library loads without a GPU and exports every function that
 include/kvm_hotpath.h declares (no compute calls here)."""
 import ctypes
+import ctypes as C
+import os
 import re
+import subprocess
 
 from kvmem_amd import _lib as L
 
@@ -31,4 +34,38 @@ def test_binding_covers_header():
 
 
 def test_abi_version_without_gpu():
-    assert L.load().kvm_abi_version() == 2
+    assert L.load().kvm_abi_version() == 3
+
+
+# ctypes mirror -> C typedef of include/kvm_hotpath.h
+_STRUCTS = {
+    "Window": "kvm_window", "QueryAcc": "kvm_query_acc", "MeanKIndex": "kvm_meank_index", "View": "kvm_view",
+    "SelectParams": "kvm_select_params", "Selection": "kvm_selection", "RetrievalLane": "kvm_retrieval_lane",
+    "RopeParams": "kvm_rope_params", "History": "kvm_history", "StageinLane": "kvm_stagein_lane",
+    "Lane": "kvm_lane", "SlotPool": "kvm_slot_pool", "RowRange": "kvm_row_range",
+    "SnapshotInfo": "kvm_snapshot_info", "SnapshotLayer": "kvm_snapshot_layer",
+}
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every ctypes struct has the size and field offsets the C compiler gives
+    the header's struct (a C program compiled with gcc prints them)."""
+    src = open(L.HEADER_PATH).read()
+    declared = set(re.findall(r"typedef struct (kvm_[a-z0-9_]+) \{", src))
+    assert declared == set(_STRUCTS.values()), declared ^ set(_STRUCTS.values())
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "kvm_hotpath.h"', 'int main(void) {']
+    want = []
+    for py, c in sorted(_STRUCTS.items()):
+        cls = getattr(L, py)
+        lines.append(f'  printf("%zu\\n", sizeof({c}));')
+        want.append(C.sizeof(cls))
+        for name, *_ in cls._fields_:
+            lines.append(f'  printf("%zu\\n", offsetof({c}, {name}));')
+            want.append(getattr(cls, name).offset)
+    lines += ['  return 0;', '}']
+    (tmp_path / "layout.c").write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(L.HEADER_PATH),
+                    str(tmp_path / "layout.c"), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got == want
