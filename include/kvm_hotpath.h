@@ -407,16 +407,12 @@ typedef struct kvm_stagein_lane {
 int kvm_stagein_selection_lanes(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
                                 const kvm_rope_params *rope);
 
-/* Retrieval and stage-in in two launches instead of three: kvm_score_topk (or
- * its lanes form, hist[i] being lane i's history) whose top-k workgroups then
- * stage their own plans, with exactly kvm_stagein_selection's results.  The
- * reference retrieves (pick_topk_blocks, kvmem_store.cpp:357-623) and then
- * flushes the queued stage-in items (llama-kvmem-stagein.cu:669-790); here the
- * flush runs inside the selection's kernel.  For the per-token decode loop,
- * where plans are empty or a few blocks: one workgroup per lane stages the plan,
- * so a large plan (a new query's first retrieval) is staged faster by
- * kvm_score_topk + kvm_stagein_selection.  Windows whose staging rows exceed
- * the top-k's LDS fall back to those two calls inside this one. */
+/* Retrieval and stage-in in one call: kvm_score_topk (or its lanes form,
+ * hist[i] being lane i's history) then kvm_stagein_selection of every lane's
+ * plan, with every argument checked before the first launch.  The reference
+ * retrieves (pick_topk_blocks, kvmem_store.cpp:357-623) and then flushes the
+ * queued stage-in items (llama-kvmem-stagein.cu:669-790).  An empty plan (the
+ * decode loop's steady state) costs the stage-in one short launch. */
 int kvm_score_topk_stagein(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,
                            const kvm_select_params *p, const kvm_window *w, const kvm_selection *out,
                            const kvm_history *h, const kvm_rope_params *rope);

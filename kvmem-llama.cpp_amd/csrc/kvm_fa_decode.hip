@@ -51,10 +51,10 @@ struct fa_args {
     fa_lane lanes[KVM_MAX_LANES];
     float *ws;              // partial O  [lane][H][split][RMAX][D]
     float *ws_ml;           // partial m,l [lane][H][split][RMAX][2]
-    uint32_t *sync;         // [lane][H][split]: the epoch of the last launch that completed
+    uint32_t *sync;         // [lane][64][512] by (lane, head, split): the epoch of the last launch that completed
                             // the split's partials; sync[KVM_FA_SYNC_STATUS]: bit 0 = a
-                            // merge wait timed out
-    uint32_t epoch;         // this launch's epoch (nonzero, unlike any earlier launch's)
+                            // merge wait timed out; sync[KVM_FA_SYNC_EPOCH + lane * 64 + h]:
+                            // the (lane, head)'s epoch, one less than its next launch's
     uint32_t H, G, n_head, n_splits;
     float scale_log2;       // kq_scale * log2(e)
     int q_bf16;
@@ -62,7 +62,8 @@ struct fa_args {
 #define KVM_FA_MAX_HEADS 64
 #define KVM_MAX_SPLITS 512
 #define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)
-#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_STATUS + 64)
+#define KVM_FA_SYNC_EPOCH (KVM_FA_SYNC_STATUS + 64)
+#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_EPOCH + KVM_MAX_LANES * KVM_FA_MAX_HEADS)
 
 __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
     return bf16 ? kvm_bf2f(((const uint16_t *)q)[i]) : ((const float *)q)[i];
@@ -152,7 +153,7 @@ __device__ __forceinline__ float fa_load(const float *p) {
 #define KVM_FA_MERGE_BATCH 16
 template <int D, int RMAX>
 __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, uint32_t h, const uint32_t *flags,
-                                         uint32_t j, uint32_t nm, uint32_t dc, int R) {
+                                         uint32_t epoch, uint32_t j, uint32_t nm, uint32_t dc, int R) {
     __shared__ float s_w[KVM_MAX_SPLITS + 1];     // [KVM_MAX_SPLITS] stays 0: splits past the last
     __shared__ float s_red[2][8];
     __shared__ float s_acc[512];
@@ -163,7 +164,7 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
     uint32_t ok = 1;
     if (tid < S) {
         uint32_t it = 0;
-        while (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != a.epoch) {
+        while (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
             __builtin_amdgcn_s_sleep(2);
             if (++it > KVM_FA_MERGE_SPIN) {
                 __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -176,6 +177,11 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
     __syncthreads();
     if (!ok) s_ok = 0;
     __syncthreads();
+    // every split of the head has read the head's epoch (each raised its flag
+    // after reading it): the next launch may take the next one
+    if (j == 0 && tid == 0)
+        __hip_atomic_store(a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS + h, epoch, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t p0 = ((uint64_t)blockIdx.z * a.H + h) * S;
     const uint32_t UD = D / dc, SP = 512 / UD;
     if (s_ok) {
@@ -314,7 +320,13 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
         const int row = srow(rt);
         qpos_raw[rt] = ln.q_pos[(row < R ? row : 0) / a.G];
     }
+    // this launch's epoch for the (lane, head): one more than the stored one,
+    // which the head's first merging split advances once every split has read it
+    __shared__ uint32_t s_epoch;
+    const uint32_t ep = __hip_atomic_load(a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS + h,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid == 0) s_epoch = ep + 1;
     // (the scoring waves call it behind their K prologue, the P V waves ahead
     // of their V prologue; it ends with the barrier)
     auto quantise_q = [&]() {
@@ -711,8 +723,11 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     // units j = split, split + NM, ... once every flag of the head is up.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    uint32_t *flags = a.sync + ((uint64_t)blockIdx.z * a.H + h) * a.n_splits;
-    if (tid == 0) __hip_atomic_store(flags + split, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // flag slots are fixed per (lane, head, split), whatever the launch's head
+    // and split counts, so a slot only ever holds its own head's epochs
+    uint32_t *flags = a.sync + ((uint64_t)blockIdx.z * KVM_FA_MAX_HEADS + h) * KVM_MAX_SPLITS;
+    const uint32_t epoch = s_epoch;
+    if (tid == 0) __hip_atomic_store(flags + split, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // merge units: rows split into dc dim chunks (at least 64 dims) so that
     // about every split of the head merges one unit
     const uint32_t S = a.n_splits;
@@ -720,7 +735,7 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     while (dc < D / 64 && (uint32_t)R * dc * 2 <= S) dc *= 2;
     const uint32_t units = (uint32_t)R * dc, NM = units < S ? units : S;
     if (split >= NM) return;
-    fa_merge<D, RMAX>(a, ln, h, flags, split, NM, dc, R);
+    fa_merge<D, RMAX>(a, ln, h, flags, epoch, split, NM, dc, R);
 }
 
 static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
@@ -835,12 +850,10 @@ static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, in
     return KVM_OK;
 }
 
-// One launch on `stream`.  Every launch takes a new epoch: a split flag equals
-// it only once this launch has completed that split (flags start at 0, which
-// no launch uses).
+// One launch on `stream`.  Every launch of a (lane, head) takes the next epoch
+// from the device (a graph replay too): a split flag equals it only once this
+// launch has completed that split (flags and epochs start at 0).
 static int fa_launch(kvm_state *st, fa_plan &fp, hipStream_t stream) {
-    static std::atomic<uint32_t> g_epoch{0};
-    do fp.a.epoch = ++g_epoch; while (fp.a.epoch == 0);
     KVM_HIP(st, hipSetDevice(st->device));
     if (fp.D == 256) launch_decode_d<256>(fp.a, fp.n_lanes, fp.rows, fp.quant, stream);
     else launch_decode_d<128>(fp.a, fp.n_lanes, fp.rows, fp.quant, stream);

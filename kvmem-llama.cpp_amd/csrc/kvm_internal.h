@@ -66,7 +66,14 @@ struct kvm_state {
     // shadow K rows and V rows, gathered before any slot is written)
     void *mv_ws = nullptr;
     size_t mv_ws_bytes = 0;
+    // the stage-in's per-lane barrier words (epoch, go, failure, arrivals),
+    // KVM_STAGE_SYNC_BYTES, zero at creation
+    uint32_t *stage_sync = nullptr;
 };
+
+#define KVM_STAGE_MAX_WGS 1024                      // stage-in workgroups of one lane
+#define KVM_STAGE_SYNC_LANE (64 + KVM_STAGE_MAX_WGS) // words per lane
+#define KVM_STAGE_SYNC_BYTES (8 * KVM_STAGE_SYNC_LANE * 4)
 
 // error helpers ----------------------------------------------------------------
 int kvm_fail(kvm_state *st, int code, const char *fmt, ...);

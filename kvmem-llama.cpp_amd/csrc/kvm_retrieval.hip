@@ -599,11 +599,8 @@ struct topk_lanes {
     topk_args lane[KVM_RET_LANES];
 };
 
-// SD > 0: the workgroup then stages its own plan (head_dim SD) through the
-// LDS buffer s_big, which the selection no longer needs by then.
 #define KVM_TOPK_BIG (KVM_MAX_TOPK_BLOCKS * 13u + KVM_TOPK_SLOTS * 8u)   // bytes of s_big
-template <int SD>
-__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_lanes sl) {
+__global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     const topk_args a = tl.lane[blockIdx.x];     // one copy out of the argument segment
     // the largest arrays share one buffer: keys, token counts, kept flags, slot map
     __shared__ __align__(16) uint8_t s_big[KVM_TOPK_BIG];
@@ -1027,25 +1024,6 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl, stage_
         a.info[2] = n_stage;
         a.info[3] = fits ? (n_sel <= a.n_slots || a.n_slots == 0 ? 0u : 2u) : 1u;
     }
-    if constexpr (SD > 0) {
-        // stage the plan (kvm_stagein_selection's items, by this workgroup):
-        // only a plan that fits the window's slots, as the stage-in kernel does
-        const stage_args &sa = sl.lane[blockIdx.x];
-        const bool ok = fits && (n_sel <= a.n_slots || a.n_slots == 0);
-        if (ok && n_stage > 0) {
-            __syncthreads();                 // the plan is written; the selection's LDS is free
-            if (sa.moves) {
-                // blocks moving within the window: every source read before any slot is written
-                for (uint32_t si = 0; si < n_stage; ++si) stage_gather_entry<SD>(sa, si, tid, KVM_TOPK_THREADS);
-                __syncthreads();
-            }
-            const uint32_t tps = sa.bt / 64;
-            for (uint32_t item = 0; item < n_stage * tps; ++item) {
-                stagein_item<SD, KVM_TOPK_THREADS>(sa, s_big, item / tps, item % tps);
-                __syncthreads();             // LDS rows of this item read before the next overwrites them
-            }
-        }
-    }
 }
 
 static int make_topk(kvm_state *st, const double *scores, const double *layer_score,
@@ -1077,14 +1055,8 @@ static int make_topk(kvm_state *st, const double *scores, const double *layer_sc
     return KVM_OK;
 }
 
-// sd = head_dim of the windows when the top-k workgroups stage their plans
-// (sl filled by kvm_stage_prepare), 0 for the selection alone
-static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes, int sd = 0,
-                       const stage_lanes *sl = nullptr) {
-    static const stage_lanes none{};
-    if (sd == 256) hipLaunchKernelGGL(k_topk<256>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, *sl);
-    else if (sd == 128) hipLaunchKernelGGL(k_topk<128>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, *sl);
-    else hipLaunchKernelGGL(k_topk<0>, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl, none);
+static int launch_topk(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes) {
+    hipLaunchKernelGGL(k_topk, dim3(n_lanes), dim3(KVM_TOPK_THREADS), 0, st->stream, tl);
     KVM_LAUNCH_CHECK(st, "topk");
     return KVM_OK;
 }
@@ -1138,10 +1110,8 @@ static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
     return KVM_OK;
 }
 
-// Scoring grid + top-k for every lane; sd > 0: the top-k workgroups also
-// stage their plans (stage arguments from kvm_stage_prepare).
-static int score_topk_impl(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, int sd,
-                           const stage_lanes *stl) {
+// Scoring grid + top-k for every lane.
+static int score_topk_impl(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes) {
     if (!st) return KVM_EINVAL;
     if (!lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk: no lanes");
     if (n_lanes > KVM_RET_LANES) return kvm_fail(st, KVM_ERANGE, "score_topk: %u lanes > %d", n_lanes, KVM_RET_LANES);
@@ -1205,11 +1175,11 @@ static int score_topk_impl(kvm_state *st, const kvm_retrieval_lane *lanes, uint3
         }
         KVM_LAUNCH_CHECK(st, "score");
     }
-    return launch_topk(st, tl, n_lanes, sd, stl);
+    return launch_topk(st, tl, n_lanes);
 }
 
 extern "C" int kvm_score_topk_lanes(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes) {
-    return score_topk_impl(st, lanes, n_lanes, 0, nullptr);
+    return score_topk_impl(st, lanes, n_lanes);
 }
 
 extern "C" int kvm_score_topk_stagein_lanes(kvm_state *st, const kvm_retrieval_lane *lanes,
@@ -1220,17 +1190,15 @@ extern "C" int kvm_score_topk_stagein_lanes(kvm_state *st, const kvm_retrieval_l
     if (n_lanes > KVM_RET_LANES) return kvm_fail(st, KVM_ERANGE, "score_topk_stagein: %u lanes > %d", n_lanes, KVM_RET_LANES);
     kvm_stagein_lane sg[KVM_RET_LANES];
     for (uint32_t i = 0; i < n_lanes; ++i) sg[i] = kvm_stagein_lane{hist[i], lanes[i].w, lanes[i].out};
+    // the stage-in arguments are checked before anything is launched
     stage_lanes stl;
     uint32_t max_items = 0;
     size_t lds = 0;
     int rc = kvm_stage_prepare(st, sg, n_lanes, rope, &stl, &max_items, &lds);
     if (rc) return rc;
-    const uint32_t hd = lanes[0].w->head_dim;
-    if (lds <= KVM_TOPK_BIG && (hd == 128 || hd == 256)) return score_topk_impl(st, lanes, n_lanes, (int)hd, &stl);
-    // a rows buffer larger than the top-k's LDS: the selection, then the stage-in kernel
-    rc = score_topk_impl(st, lanes, n_lanes, 0, nullptr);
+    rc = score_topk_impl(st, lanes, n_lanes);
     if (rc) return rc;
-    return kvm_stagein_selection_lanes(st, sg, n_lanes, rope);
+    return kvm_stage_launch(st, stl, n_lanes, max_items, lds, lanes[0].w->head_dim);
 }
 
 extern "C" int kvm_score_topk_stagein(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *q,

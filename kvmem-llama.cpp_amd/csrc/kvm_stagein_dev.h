@@ -128,6 +128,7 @@ struct stage_args {
     uint32_t *shadow_rows;
     const int32_t *stage_src;
     uint8_t *moves;
+    uint32_t *sync;                  // the lane's barrier words (kvm_state::stage_sync)
 };
 
 // Row bytes of the history / shadow: q8_0 K and q4_0 V, all kv heads.
@@ -292,3 +293,6 @@ struct stage_lanes {
 // a lane, *lds = the rows buffer for the largest lane.
 int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_lanes,
                       const kvm_rope_params *rope, stage_lanes *sl, uint32_t *max_items, size_t *lds);
+// Launches the stage-in kernel over prepared lanes (kvm_stagein.hip).
+int kvm_stage_launch(kvm_state *st, const stage_lanes &sl, uint32_t n_lanes, uint32_t max_items, size_t lds,
+                     uint32_t head_dim);

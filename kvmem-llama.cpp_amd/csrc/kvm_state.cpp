@@ -36,8 +36,11 @@ extern "C" kvm_state *kvm_state_create(int device) {
         st->n_cu = (uint32_t)n_cu;
     if (kvm_noalloc_setup(st) != KVM_OK || hipMalloc((void **)&st->fa_sync, kvm_fa_sync_bytes()) != hipSuccess ||
         hipMemsetAsync(st->fa_sync, 0, kvm_fa_sync_bytes(), st->own_stream) != hipSuccess ||
+        hipMalloc((void **)&st->stage_sync, KVM_STAGE_SYNC_BYTES) != hipSuccess ||
+        hipMemsetAsync(st->stage_sync, 0, KVM_STAGE_SYNC_BYTES, st->own_stream) != hipSuccess ||
         hipStreamSynchronize(st->own_stream) != hipSuccess) {
         if (st->fa_sync) (void)hipFree(st->fa_sync);
+        if (st->stage_sync) (void)hipFree(st->stage_sync);
         (void)hipEventDestroy(st->ev);
         (void)hipStreamDestroy(st->own_stream);
         delete st;
@@ -56,6 +59,7 @@ extern "C" void kvm_state_free(kvm_state *st) {
     if (st->fa_sync) (void)hipFree(st->fa_sync);
     if (st->fa_ws) (void)hipFree(st->fa_ws);
     if (st->mv_ws) (void)hipFree(st->mv_ws);
+    if (st->stage_sync) (void)hipFree(st->stage_sync);
     if (st->slab) (void)hipHostFree(st->slab);
     if (st->ev) (void)hipEventDestroy(st->ev);
     if (st->own_stream) (void)hipStreamDestroy(st->own_stream);

@@ -64,3 +64,79 @@ def test_decode_step_graph_replays_equal_eager(kvm_state, fused):
         step()                               # eager work between the replays
         torch.cuda.synchronize()
         assert torch.equal(out, want_out), r
+
+
+def test_back_to_back_replays_follow_changing_inputs(kvm_state):
+    """Replays of one captured decode step with nothing of the library's in
+    between, while the inputs change: the query accumulator drifts (so plans
+    restage and move blocks within a window with a K shadow, through the
+    stage-in's in-launch barrier) and the attention query changes every
+    replay.  Each replay's window equals an eager retrieval + stage-in of the
+    same plans into a second window, and each replay's attention output equals
+    an eager attention over the replay's window: the launches' in-launch
+    flags take their epochs from the device, not from the captured arguments."""
+    st = kvm_state
+    rng = np.random.default_rng(23)
+    H, G, D, BT, n_blocks, budget = 4, 6, 256, 128, 48, 12
+    n_hist = n_blocks * BT
+    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    hist = api.History(kr, vr)
+    ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
+    ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
+    qa = api.QueryAcc(st, 1, H * G, D)
+    qa.reset()
+    qa.add(0, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
+    n_tokens = dev(np.full(n_blocks, BT, np.int32))
+    w = api.KVWindow(st, 16 * BT, H, D, BT, shadow=True)
+    sel = api.SelectionBuffers(st, n_blocks, budget)
+    wr = api.KVWindow(st, 16 * BT, H, D, BT)
+    selr = api.SelectionBuffers(st, n_blocks, budget)
+    q = dev(rng.standard_normal((4, H * G, D)).astype(np.float32))
+    q_pos = dev(np.arange(budget * BT - 4, budget * BT, dtype=np.int32))
+    out = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
+    retrieval = api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel, hist, 64, 1e7)
+    fa = api.prepare_fa_decode(st, w, q, q_pos, H * G, D ** -0.5, out)
+
+    def step():
+        retrieval()
+        fa()
+
+    step()
+    api.score_topk(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, None, wr, selr)
+    api.stagein_selection(st, hist, wr, selr, 64, 1e7)
+    torch.cuda.synchronize()
+    g = st.capture(step)
+    n_rep = 6
+    qs = [dev(rng.standard_normal((4, H * G, D)).astype(np.float32)) for _ in range(n_rep)]
+    drift = [dev((rng.standard_normal((1, H * G * D)) * 0.6).astype(np.float32)) for _ in range(n_rep)]
+    outs, moved = [], 0
+    for r in range(n_rep):
+        # the inputs change on the replay stream's side of the graph: torch work only
+        q.copy_(qs[r])
+        qa.q_sum.add_(drift[r].view_as(qa.q_sum))
+        g.replay()
+        outs.append(out.clone())
+        # the same plan eagerly, into the reference window (read after the replay)
+        api.score_topk(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, None, wr, selr)
+        api.stagein_selection(st, hist, wr, selr, 64, 1e7)
+        torch.cuda.synchronize()
+        ra, rb = sel.result(), selr.result()
+        assert np.array_equal(ra["ids"], rb["ids"]) and np.array_equal(ra["stage_slots"], rb["stage_slots"]), r
+        for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+            assert torch.equal(getattr(w, name), getattr(wr, name)), (r, name)
+        moved += int((ra["stage_src"] >= 0).sum())
+        # eager attention over the same window and query
+        ref = api.fa_decode(st, w, qs[r], q_pos, H * G, D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(outs[r], ref), r
+    assert moved > 0
+    # replays back to back with nothing of the library's between them: only the
+    # query changes (the plan stays put), every output still matches its query
+    outs = []
+    for r in range(n_rep):
+        q.copy_(qs[r])
+        g.replay()
+        outs.append(out.clone())
+    torch.cuda.synchronize()
+    for r in range(n_rep):
+        assert torch.equal(outs[r], api.fa_decode(st, w, qs[r], q_pos, H * G, D ** -0.5)), r

@@ -158,8 +158,7 @@ def _retrieval(st, seed, n_blocks, n_head):
 
 @pytest.mark.parametrize("n_lanes", [1, 3])
 def test_fused_retrieval_restages_from_shadow(kvm_state, n_lanes):
-    """kvm_score_topk_stagein(_lanes): the top-k workgroup gathers the moving
-    blocks and stages its plan.  Queries drift over six steps; each lane's
+    """kvm_score_topk_stagein(_lanes), one and three lanes.  Queries drift over six steps; each lane's
     window (with a shadow, the host rows of the blocks it holds poisoned during
     each plan) equals kvm_score_topk + kvm_stagein_selection from the clean
     history into a window without a shadow."""
@@ -256,3 +255,33 @@ def test_shadow_geometry_is_checked(kvm_state):
     assert lib.kvm_window_shadow_bytes(C.byref(wf.c)) == 0
     with pytest.raises(L.KvmError):
         api.KVWindow(kvm_state, 256, H, 128, BT, L.T_F16, L.T_F16, shadow=True)
+
+
+def test_churn_over_a_128_block_window(kvm_state):
+    """The decode workload's window shape: 128 blocks of 128 tokens from a
+    512-block history.  Each step drops the second-earliest block and adds one
+    past the last, or the reverse, so 126 blocks move a slot (504 staging items,
+    the stage-in's gather barrier over its full grid); the window equals a fresh
+    stage-in of the plan from the clean history."""
+    st = kvm_state
+    n_blocks, nsel = 512, 128
+    hp, hc, kr, vr, rng = _histories(0x5B00, n_blocks * BT)
+    nt = np.full(n_blocks, BT, np.int32)
+    sa = np.concatenate([[0], np.sort(rng.choice(np.arange(1, n_blocks - 1), nsel - 1, replace=False))])
+    late = next(b for b in range(n_blocks - 1, 0, -1) if b not in set(sa))
+    sb = np.sort(np.concatenate([np.setdiff1d(sa, [sa[1]]), [late]]))
+    w = api.KVWindow(st, nsel * BT, H, D, BT, shadow=True)
+    for step, chosen in enumerate((sa, sb, sa, sb)):
+        s = np.zeros(n_blocks)
+        s[chosen] = 1.0
+        held = _resident_full(w, nt)
+        _poison(hp, held, rng)
+        sel = api.select_topk(st, dev(s), dev(nt), nsel, 1, 0, None, window=w)
+        api.stagein_selection(st, hp, w, sel, 64, 1e7)
+        _restore(hp, held, kr, vr)
+        res = sel.result()
+        assert res["status"] == 0 and np.array_equal(res["ids"], chosen), step
+        n_moved = int((res["stage_src"] >= 0).sum())
+        assert (len(res["stage_slots"]), n_moved) == ((nsel, 0) if step == 0 else (nsel - 1, nsel - 2)), step
+        ref_w, _ = _fresh(st, hc, s, nt, nsel, nsel)
+        _same_window(w, ref_w, nsel * BT)

@@ -312,9 +312,8 @@ def _same_selection_and_window(sa, wa, sb, wb):
 
 @pytest.mark.parametrize("H,n_head", [(4, 24), (5, 10)])
 def test_score_topk_stagein_matches_two_calls(kvm_state, H, n_head):
-    """The fused retrieval + stage-in (the top-k workgroup stages its plan; at 5
-    kv heads the rows exceed its LDS and the call falls back to the stage-in
-    kernel) against kvm_score_topk + kvm_stagein_selection on a second window:
+    """The one-call retrieval + stage-in (at 4 and 5 kv heads) against
+    kvm_score_topk + kvm_stagein_selection on a second window:
     a fresh window (full plan), a changed query (some slots restaged) and the
     same query again (empty plan) give equal selections and equal windows."""
     D, bt, n_blocks, budget, slots = 256, 128, 40, 12, 16
