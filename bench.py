@@ -125,12 +125,13 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HI
 
 def prepare_decode(st, api, wl, out):
     """The two calls of a decode step for every layer replica, marshalled once:
-    retrieval + stage-in (kvm_score_topk_stagein: scoring, then a top-k
-    workgroup that stages its own plan) and FA decode."""
+    retrieval (kvm_score_topk: the scoring grid, then a top-k workgroup that
+    writes the plan) and stage-in + attention (kvm_stagein_fa_decode: the
+    attention's workgroups stage the plan, then attend)."""
     n_blocks = wl["hist_tokens"] // BT
-    return [(api.prepare_score_topk_stagein(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel,
-                                            wl["hist"], N_ROT, FREQ_BASE),
-             api.prepare_fa_decode(st, w, wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out))
+    return [(api.prepare_score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel),
+             api.prepare_stagein_fa_decode(st, wl["hist"], sel, w, wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out,
+                                           N_ROT, FREQ_BASE))
             for ix, w, sel in wl["reps"]]
 
 
@@ -458,8 +459,8 @@ def run_lanes(args, st, api, L, torch, np):
     """Four conversations, each with its own 32K-cell window, mean-K index and
     pinned host history (64K / 128K / 192K / 256K tokens), one bf16 query token
     each: retrieval for all lanes in one launch sequence (scoring grid over every
-    lane's blocks + one top-k workgroup per lane, which then stages the lane's
-    plan), attention for all lanes in one launch."""
+    lane's blocks + one top-k workgroup per lane), stage-in and attention for all
+    lanes in one launch."""
     n_rep = 2
     wls = []
     for i, ht in enumerate(LANE_HIST):
@@ -472,9 +473,10 @@ def run_lanes(args, st, api, L, torch, np):
         lanes = [dict(index=wl["reps"][r][0], query=wl["qa"], n_blocks=wl["hist_tokens"] // BT,
                       n_tokens=wl["n_tokens"], budget_blocks=RETRIEVED // BT, sink_blocks=1,
                       window=wl["reps"][r][1], sel=wl["reps"][r][2], history=wl["hist"]) for wl in wls]
-        preps.append((api.prepare_score_topk_stagein_lanes(st, lanes, N_ROT, FREQ_BASE),
-                      api.prepare_fa_decode_lanes(st, [wl["reps"][r][1] for wl in wls], [wl["q"] for wl in wls],
-                                                  [wl["q_pos"] for wl in wls], N_HEAD, scale, outs)))
+        fa_lanes = [dict(history=wl["hist"], sel=wl["reps"][r][2], window=wl["reps"][r][1], q=wl["q"],
+                         q_pos=wl["q_pos"], out=o) for wl, o in zip(wls, outs)]
+        preps.append((api.prepare_score_topk_lanes(st, lanes),
+                      api.prepare_stagein_fa_decode_lanes(st, fa_lanes, N_HEAD, scale, N_ROT, FREQ_BASE)))
 
     def step(i):
         retrieve, fa = preps[i % n_rep]
@@ -513,11 +515,12 @@ def run_lanes(args, st, api, L, torch, np):
         "data": "synthetic N(0,1), seeds 0xC0FFEE05 + lane, 16 planted blocks per lane",
         "config": {"workload": "4 lanes: histories of 65536/131072/196608/262144 tokens (pinned host q8_0 K / "
                                "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; score + top-k for all "
-                               "lanes in one launch sequence (the top-k workgroups stage the plans), FA decode for all lanes in one "
-                               "launch; 24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
+                               "lanes in one launch sequence, stage-in + FA decode for all lanes in one launch; "
+                               "24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
                    "lanes": len(wls), "step_bytes": step_bytes},
         "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode_lanes (k_fa_decode split-K + k_fa_combine)",
+        "roofline": {"bound": "hbm", "kernel": "kvm_stagein_fa_decode_lanes (k_fa_decode_staged: split-K "
+                                               "attention over every lane, splits merged in-launch)",
                      "achieved": round(fa_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "launch_us": round(fa_ms * 1e3, 3), "algorithmic_bytes": fa_bytes},
@@ -582,8 +585,8 @@ def main():
                     help="after the timed region, copy 256 MiB device-to-device once (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); multi-GPU sharding is designed "
-              "but not built in this round", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for {args.gpus}): the path is not sharded across GPUs",
+              file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -646,13 +649,15 @@ def main():
         "hbm_gbps": round(STEP_BYTES / (step_ms * 1e-3) / 1e9, 1),
         # the reference retrieves once per query (tools/llama-kvmem-server.cpp:1466):
         # the step above is the worst case (a retrieval every token); split into
-        # retrieval per event (score + top-k + stage plan + empty stage-in) and
+        # retrieval per event (score + top-k + stage plan) and
         # attention per token, from the step and the separately timed attention loop
         "per_event": {"retrieval_us": round(step_us - fa_ms * 1e3, 2),
                       "attention_us_per_token": round(fa_ms * 1e3, 3)},
         "step_bytes": STEP_BYTES,
         "roofline_step_us": round(STEP_BYTES / (HBM_PEAK_GBPS * 1e9) * 1e6, 3),
-        "roofline": {"bound": "hbm", "kernel": "kvm_fa_decode (k_fa_decode: split-K with the splits merged in-launch)",
+        "roofline": {"bound": "hbm", "kernel": "kvm_stagein_fa_decode (k_fa_decode_staged: the plan's stage-in, "
+                                               "empty in the steady state, then split-K attention with the splits "
+                                               "merged in-launch)",
                      "achieved": round(fa_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(fa_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),

@@ -459,6 +459,22 @@ typedef struct kvm_lane {
 int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
                         uint32_t n_head, float scale);
 
+/* A decode step's stage-in and attention in one launch: kvm_stagein_selection
+ * of (h, sel) into w, then kvm_fa_decode over w, with the results of those two
+ * calls.  The attention's workgroups stage the plan themselves and meet at an
+ * in-launch barrier before reading the window; with an empty plan (the decode
+ * loop's steady state) the step's stage-in launch disappears.  The reference
+ * stages in the memory module (write_block_to_gpu + kvmem_stagein_flush,
+ * llama-memory-kvmem.cpp:4000-4071) before the graph's flash attention runs
+ * (ggml_cuda_flash_attn_ext, ggml-cuda/fattn.cu:457).  q8_0 / q4_0 windows;
+ * in the lanes form stage[i].w must be lanes[i].w's window. */
+int kvm_stagein_fa_decode(kvm_state *st, const kvm_history *h, const kvm_selection *sel,
+                          const kvm_rope_params *rope, const kvm_window *w, const void *q, int q_type,
+                          const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale, float *out);
+int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, const kvm_lane *lanes,
+                                uint32_t n_lanes, const kvm_rope_params *rope, int q_type, uint32_t n_head,
+                                float scale);
+
 /* kvm_fa_decode without any allocation, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  It has no counterpart in the reference.  The split

@@ -27,7 +27,7 @@
 // with this launch's epoch; splits 0 .. NM-1 of a head then wait for the
 // head's flags and each merges whole rows (or row chunks) of the head, so no
 // combine launch follows.
-#include "kvm_internal.h"
+#include "kvm_stagein_dev.h"
 
 #include <cmath>
 #include <cstdlib>
@@ -35,6 +35,7 @@
 #include <mutex>
 
 #define KVM_MAX_LANES 8
+#define KVM_FA_STAGE_IT 32        // tokens per stage-in item of a staged launch
 
 struct fa_lane {
     const uint8_t *wk;
@@ -241,8 +242,24 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
     }
 }
 
-template <int D, int NRT, bool QUANT, bool PK>
-__global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
+// The lane's stage-in plan, carried out by the attention's own workgroups
+// before any of them reads the window: workgroup x = h * n_splits + split of
+// the lane's G = H * n_splits stages its share of the items (after the gather
+// of the blocks that move within the window, behind the plan's first
+// barrier), then every workgroup waits at a second barrier for the whole plan.
+template <int D>
+__device__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent) {
+    extern __shared__ __align__(16) uint8_t s_rows[];     // the staged launch's dynamic LDS
+    __shared__ uint32_t s_e;
+    if (threadIdx.x == 0) s_e = sync_load(sg.sync);
+    __syncthreads();
+    const uint32_t e = s_e, G = a.H * a.n_splits, x = blockIdx.y * a.n_splits + blockIdx.x;
+    stage_plan<D, 512, KVM_FA_STAGE_IT>(sg, s_rows, n_ent, x, G, e + 1, false);
+    if (!lane_barrier<512>(sg.sync, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
+}
+
+template <int D, int NRT, bool QUANT, bool PK, bool STAGE>
+__device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_args *stg) {
     constexpr int NB = D / 32;          // 32-dim blocks per row
     constexpr int NP = NB / 2;          // block pairs (packed row tile)
     constexpr int NG = QUANT ? NB / 4 : 1;   // 4-block scale groups
@@ -289,7 +306,13 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     __shared__ float s_l[4][RMAX];
     __shared__ __align__(16) _Float16 s_p[2][RMAX][PSTR];   // P of the tile (tile parity)
 
-    if (R == 0) return;                  // lane without query rows: no partials
+    if (R == 0) {                        // lane without query rows: no partials
+        if constexpr (STAGE) {
+            const uint32_t n_ent = stage_entries(stg[blockIdx.z]);
+            if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
+        }
+        return;
+    }
 
     // ---- query rows: item (row r = token r/G, query head h*G + r%G; block b),
     // four lanes per item, 8 dims each, quantised to q8_0 per 32 dims as
@@ -325,8 +348,15 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     __shared__ uint32_t s_epoch;
     const uint32_t ep = __hip_atomic_load(a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS + h,
                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // a staged launch reads the lane's plan length with the query (an empty
+    // plan, the decode loop's steady state, then costs no memory round trip)
+    uint32_t n_ent = 0;
+    if constexpr (STAGE) n_ent = stage_entries(stg[blockIdx.z]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (tid == 0) s_epoch = ep + 1;
+    if constexpr (STAGE) {
+        if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
+    }
     // (the scoring waves call it behind their K prologue, the P V waves ahead
     // of their V prologue; it ends with the barrier)
     auto quantise_q = [&]() {
@@ -738,6 +768,21 @@ __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
     fa_merge<D, RMAX>(a, ln, h, flags, epoch, split, NM, dc, R);
 }
 
+template <int D, int NRT, bool QUANT, bool PK>
+__global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
+    fa_decode_body<D, NRT, QUANT, PK, false>(a, nullptr);
+}
+
+// Decode attention that first stages its lanes' plans (q8_0 windows only).
+struct fa_staged_args {
+    fa_args a;
+    stage_args stage[KVM_MAX_LANES];
+};
+template <int D, int NRT, bool PK>
+__global__ void __launch_bounds__(512) k_fa_decode_staged(fa_staged_args sa) {
+    fa_decode_body<D, NRT, true, PK, true>(sa.a, sa.stage);
+}
+
 static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
     if (const char *e = getenv("KVM_FA_SPLITS")) {
         uint32_t v = (uint32_t)atoi(e);
@@ -784,7 +829,7 @@ struct fa_plan {
     bool quant;
 };
 static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type, uint32_t n_head,
-                      float scale, void *scratch, size_t scratch_cap, fa_plan *fp) {
+                      float scale, void *scratch, size_t scratch_cap, fa_plan *fp, uint32_t max_wgs = 0) {
     if (!st || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "fa_decode: no lanes");
     if (n_lanes > KVM_MAX_LANES) return kvm_fail(st, KVM_ERANGE, "fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
     if (q_type != KVM_TYPE_F32 && q_type != KVM_TYPE_BF16) return kvm_fail(st, KVM_EUNSUPPORTED, "fa_decode: q type %d", q_type);
@@ -820,6 +865,11 @@ static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, in
     a.G = n_head / H;
     a.n_head = n_head;
     a.n_splits = choose_splits(st->n_cu, n_lanes, H, max_tiles);
+    // a grid whose workgroups must all be resident at once (a staged launch)
+    if (max_wgs && a.n_splits * H * n_lanes > max_wgs) {
+        a.n_splits = max_wgs / (H * n_lanes);
+        if (a.n_splits == 0) return kvm_fail(st, KVM_ERANGE, "fa_decode: %u lanes x %u kv heads exceed the CUs", n_lanes, H);
+    }
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_type == KVM_TYPE_BF16;
     const bool quant = w0->k_type == KVM_TYPE_Q8_0;
@@ -881,6 +931,73 @@ extern "C" int kvm_fa_decode(kvm_state *st, const kvm_window *w, const void *q, 
 extern "C" int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type,
                                    uint32_t n_head, float scale) {
     return fa_decode_impl(st, lanes, n_lanes, q_type, n_head, scale);
+}
+
+// ---------------------------------------------------------------------------
+// Stage-in and decode attention in one launch
+// ---------------------------------------------------------------------------
+template <int D, int NRT, bool PK>
+static const void *staged_kernel() { return (const void *)k_fa_decode_staged<D, NRT, PK>; }
+
+static const void *staged_kernel_for(uint32_t D, uint32_t max_rows) {
+    const int NRT = max_rows <= 16 ? 1 : 2;
+    const bool pk = max_rows - 16u * (NRT - 1) <= 8u;
+    if (D == 256) return NRT == 1 ? (pk ? staged_kernel<256, 1, true>() : staged_kernel<256, 1, false>())
+                                  : (pk ? staged_kernel<256, 2, true>() : staged_kernel<256, 2, false>());
+    return NRT == 1 ? (pk ? staged_kernel<128, 1, true>() : staged_kernel<128, 1, false>())
+                    : (pk ? staged_kernel<128, 2, true>() : staged_kernel<128, 2, false>());
+}
+
+extern "C" int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, const kvm_lane *lanes,
+                                           uint32_t n_lanes, const kvm_rope_params *rope, int q_type,
+                                           uint32_t n_head, float scale) {
+    if (!st) return KVM_EINVAL;
+    if (!stage || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "stagein_fa_decode: no lanes");
+    if (n_lanes > KVM_MAX_LANES) return kvm_fail(st, KVM_ERANGE, "stagein_fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        if (!stage[i].w || !lanes[i].w) return kvm_fail(st, KVM_EINVAL, "stagein_fa_decode: lane %u: null window", i);
+        if (stage[i].w->k != lanes[i].w->k || stage[i].w->v != lanes[i].w->v || stage[i].w->cell_pos != lanes[i].w->cell_pos)
+            return kvm_fail(st, KVM_EINVAL, "stagein_fa_decode: lane %u stages another window than it attends", i);
+    }
+    fa_staged_args sa{};
+    stage_lanes stl;
+    uint32_t max_items = 0;
+    size_t lds = 0;
+    int rc = kvm_stage_prepare(st, stage, n_lanes, rope, &stl, &max_items, &lds);
+    if (rc) return rc;
+    lds = lds * KVM_FA_STAGE_IT / 64;                     // kvm_stage_prepare sizes 64-token items
+    // every workgroup resident at once: the plan's barriers wait for all of a lane's
+    uint32_t max_rows = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i)
+        if (lanes[i].w->n_head_kv && n_head % lanes[i].w->n_head_kv == 0) {
+            const uint32_t r = lanes[i].n_tokens * (n_head / lanes[i].w->n_head_kv);
+            max_rows = r > max_rows ? r : max_rows;
+        }
+    const void *fn = staged_kernel_for(lanes[0].w->head_dim, max_rows ? max_rows : 1u);
+    KVM_HIP(st, hipSetDevice(st->device));
+    int occ = 0;
+    rc = kvm_resident_blocks(st, fn, 512, lds, &occ);
+    if (rc) return rc;
+    fa_plan fp;
+    rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)occ * st->n_cu);
+    if (rc) return rc;
+    // no query rows at all: the plans alone
+    if (fp.rows == 0) return kvm_stage_launch(st, stl, n_lanes, max_items, lds * 64 / KVM_FA_STAGE_IT, lanes[0].w->head_dim);
+    if (!fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein_fa_decode: q8_0 windows only");
+    sa.a = fp.a;
+    for (uint32_t i = 0; i < n_lanes; ++i) sa.stage[i] = stl.lane[i];
+    void *kargs[] = {&sa};
+    KVM_HIP(st, hipLaunchKernel(fn, dim3(fp.a.n_splits, fp.a.H, n_lanes), dim3(512), kargs, lds, st->stream));
+    return KVM_OK;
+}
+
+extern "C" int kvm_stagein_fa_decode(kvm_state *st, const kvm_history *h, const kvm_selection *sel,
+                                     const kvm_rope_params *rope, const kvm_window *w, const void *q, int q_type,
+                                     const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                                     float *out) {
+    const kvm_stagein_lane sg{h, w, sel};
+    const kvm_lane lane{w, q, q_pos, out, n_tokens};
+    return kvm_stagein_fa_decode_lanes(st, &sg, &lane, 1, rope, q_type, n_head, scale);
 }
 
 // ---------------------------------------------------------------------------

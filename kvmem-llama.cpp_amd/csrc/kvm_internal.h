@@ -101,6 +101,10 @@ void *kvm_workspace(kvm_state *st, size_t bytes);
 void *kvm_fa_workspace(kvm_state *st, size_t bytes);
 // The same for the stage-in move staging (kvm_state::mv_ws).
 void *kvm_move_workspace(kvm_state *st, size_t bytes);
+// Workgroups of `threads` threads and `lds` bytes of dynamic LDS of kernel fn
+// that one CU holds at once (>= 1, or an error); also raises fn's dynamic LDS
+// limit to lds.  Cached per (kernel, threads, lds).
+int kvm_resident_blocks(kvm_state *st, const void *fn, int threads, size_t lds, int *blocks);
 // Ensures a device copy of `bytes` of descriptor data; returns the device pointer.
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes);
 // theta_i = powf(base, -2i/n_rot) * scale for i < n_rot/2 (kvmem/src/host/rope.cpp:19-22)
@@ -262,13 +266,26 @@ __device__ inline float kvm_bf2f(uint16_t b) { return __uint_as_float((uint32_t)
 
 // IEEE binary32 operations, round to nearest even.  Hardware add/sub/mul round
 // to nearest even; `/` and sqrtf are correctly rounded under
-// -fhip-fp32-correctly-rounded-divide-sqrt.  Files whose results must equal
-// host arithmetic bit for bit are compiled with -ffp-contract=off so no a*b+c
-// becomes an FMA.  (HIP's kvm_fsqrt is the approximate native sqrt.)
-__device__ __forceinline__ float kvm_fadd(float a, float b) { return a + b; }
-__device__ __forceinline__ float kvm_fsub(float a, float b) { return a - b; }
-__device__ __forceinline__ float kvm_fmul(float a, float b) { return a * b; }
-__device__ __forceinline__ float kvm_fdiv(float a, float b) { return a / b; }
+// -fhip-fp32-correctly-rounded-divide-sqrt.  Each one is its own rounding: no
+// a*b+c built from them becomes an FMA, whatever the file's -ffp-contract
+// (files whose results must equal host arithmetic bit for bit are also built
+// with -ffp-contract=off).  (HIP's kvm_fsqrt is the approximate native sqrt.)
+__device__ __forceinline__ float kvm_fadd(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float kvm_fsub(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+__device__ __forceinline__ float kvm_fmul(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float kvm_fdiv(float a, float b) {
+#pragma clang fp contract(off)
+    return a / b;
+}
 __device__ __forceinline__ float kvm_fsqrt(float a) { return sqrtf(a); }
 
 // q8_0 / q4_0 block quantisers with the reference kernels' exact arithmetic

@@ -653,7 +653,10 @@ __global__ void __launch_bounds__(KVM_TOPK_THREADS) k_topk(topk_lanes tl) {
     float sf[KVM_TOPK_LOAD];             // their scores rounded to fp32
     uint32_t nt[KVM_TOPK_LOAD];
     uint32_t pr[KVM_TOPK_LOAD];
-    const uint32_t qc0 = have_ls ? a.q_count[0] : 0u;
+    // (unconditional, through a stand-in pointer: a load under a branch would be
+    // waited for at the branch's join, ahead of the score loads)
+    const uint32_t *qcp = have_ls ? a.q_count : a.n_tokens;
+    const uint32_t qc0 = qcp[0];
 #pragma unroll
     for (uint32_t k = 0; k < KVM_TOPK_LOAD; ++k) {
         const uint32_t i = tid + k * KVM_TOPK_THREADS, ic = i < n1 ? i : n1;

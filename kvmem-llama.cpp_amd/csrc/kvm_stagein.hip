@@ -9,86 +9,7 @@
 
 #define KVM_STAGEIN_IT 32         // tokens per item: half a window tile
 #define KVM_STAGEIN_WGS_PER_CU 2  // workgroups per CU (a 32-token rows buffer takes a third of the LDS)
-// Longest wait at the gather barrier (s_sleep rounds of ~64 cycles, about
-// 0.1 s): every workgroup of the launch is resident (the grid never exceeds
-// what the CUs hold at once) and arrives without waiting on anything, so the
-// wait ends unless workgroups cannot be scheduled; past the limit the status
-// says so (bit 16) and the workgroup empties its items' cells instead.
-#define KVM_STAGE_SPIN (1u << 21)
 static_assert(KVM_STAGE_SYNC_BYTES == KVM_STAGEIN_LANES * KVM_STAGE_SYNC_LANE * 4, "stage-in sync words");
-
-__device__ __forceinline__ uint32_t sync_load(const uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void sync_store(uint32_t *p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool sync_wait(const uint32_t *p, uint32_t v) {
-    for (uint32_t it = 0; sync_load(p) != v; ++it) {
-        if (it > KVM_STAGE_SPIN) return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return true;
-}
-
-// A lane's gather of its moving entries (stage_src >= 0) into the staging
-// regions, then a barrier of the lane's workgroups, so that no slot is written
-// before every source has been read.  The lane's sync words (kvm_state::
-// stage_sync): [0] the epoch, [1] the go flag, [2] the failure flag, [64 + x]
-// workgroup x's arrival.  Every workgroup reads the epoch E before it arrives,
-// and workgroup 0 advances it only once all have arrived, so the flags of this
-// launch carry E + 1 and no earlier launch's flag (at most E) passes for one
-// of them, also when the launch is replayed from a captured graph.  Gathered
-// bytes are written back from the writer's L2 before its arrival (release)
-// and the readers' caches are invalidated after the go flag (acquire).
-template <int D>
-__device__ bool stage_gather_barrier(const stage_args &a, uint32_t n_ent) {
-    __shared__ uint32_t s_e, s_ok;
-    const uint32_t tid = threadIdx.x, G = gridDim.x, x = blockIdx.x;
-    uint32_t *sync = a.sync;
-    if (tid == 0) s_e = sync_load(sync);
-    __syncthreads();
-    const uint32_t E = s_e + 1;
-    for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, tid, 256);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        sync_store(sync + 64 + x, E);
-    }
-    uint32_t ok = 1;
-    if (x == 0) {
-        for (uint32_t t = tid; t < G; t += 256) ok &= sync_wait(sync + 64 + t, E);
-        ok = __syncthreads_and(ok);
-        if (tid == 0) {
-            if (!ok) sync_store(sync + 2, E);
-            sync_store(sync, E);                 // every workgroup has read the epoch
-            __threadfence();
-            sync_store(sync + 1, E);
-        }
-    } else if (tid == 0) {
-        ok = sync_wait(sync + 1, E) && sync_load(sync + 2) != E;
-        s_ok = ok;
-    }
-    __syncthreads();
-    if (x != 0) ok = s_ok;
-    __threadfence();
-    return ok != 0;
-}
-
-// An item whose plan could not be carried out: its cells are emptied and,
-// once, its slot's map entry and shadow count, so attention never reads what
-// the slot held before and the next plan restages it.
-__device__ void stage_void_item(const stage_args &a, uint32_t si, uint32_t tt) {
-    const uint32_t slot = a.stage_slots[si], tid = threadIdx.x;
-    if (tid < KVM_STAGEIN_IT) a.cell_pos[slot * a.bt + tt * KVM_STAGEIN_IT + tid] = -1;
-    if (tt == 0 && tid == 0) {
-        a.slot_block[slot] = 0xffffffffu;
-        a.slot_base[slot] = -1;
-        if (a.shadow_rows) a.shadow_rows[slot] = 0u;
-        atomicOr(&a.info[3], 16u);
-    }
-}
 
 // Up to two workgroups per CU walk the (plan entry, 32-token run) items, so
 // an empty plan (the steady state) costs one short launch; the plan length is
@@ -98,22 +19,13 @@ template <int D>
 __global__ void __launch_bounds__(256) k_stagein(stage_lanes sl) {
     extern __shared__ __align__(16) uint8_t s_rows[];
     const stage_args &a = sl.lane[blockIdx.y];
-    const uint32_t tps = a.bt / KVM_STAGEIN_IT;
-    // the plan bits of the status (1 = over capacity, 2 = more blocks than
-    // slots); bits 4 (a block past the history) and 16 are set by this kernel
-    const uint32_t n_ent = (a.info[3] & 3u) != 0 ? 0u : a.info[2], n_items = n_ent * tps;
-    if (n_items == 0) return;
-    bool ok = true;
-    if (a.moves) {
-        uint32_t any = 0;
-        for (uint32_t si = threadIdx.x; si < n_ent; si += 256) any |= a.stage_src[si] >= 0 ? 1u : 0u;
-        if (__syncthreads_or(any)) ok = stage_gather_barrier<D>(a, n_ent);
-    }
-    for (uint32_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-        if (ok) stagein_item<D, 256, KVM_STAGEIN_IT>(a, s_rows, item / tps, item % tps);
-        else stage_void_item(a, item / tps, item % tps);
-        __syncthreads();                 // LDS rows of this item read before the next overwrites them
-    }
+    const uint32_t n_ent = stage_entries(a);
+    if (n_ent == 0) return;
+    // one barrier at most (the gather's): it takes the epoch's next value
+    __shared__ uint32_t s_e;
+    if (threadIdx.x == 0) s_e = sync_load(a.sync);
+    __syncthreads();
+    stage_plan<D, 256, KVM_STAGEIN_IT>(a, s_rows, n_ent, blockIdx.x, gridDim.x, s_e + 1, true);
 }
 
 static int rope_ctx_for(kvm_state *st, const float *theta, uint32_t n_half, int32_t nrot,
@@ -248,12 +160,11 @@ int kvm_stage_launch(kvm_state *st, const stage_lanes &sl, uint32_t n_lanes, uin
     max_items *= 64 / KVM_STAGEIN_IT;
     lds = lds * KVM_STAGEIN_IT / 64;
     const void *fn = head_dim == 256 ? (const void *)k_stagein<256> : (const void *)k_stagein<128>;
-    KVM_HIP(st, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     // every workgroup resident at once (the gather barrier waits for all of a
     // lane's): at most what the CUs hold, two per CU at most
     int occ = 0;
-    KVM_HIP(st, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 256, lds));
-    if (occ < 1) return kvm_fail(st, KVM_ERANGE, "stagein: %zu bytes of rows do not fit a CU", lds);
+    int rc = kvm_resident_blocks(st, fn, 256, lds, &occ);
+    if (rc) return rc;
     if (occ > KVM_STAGEIN_WGS_PER_CU) occ = KVM_STAGEIN_WGS_PER_CU;
     uint32_t per_lane = (uint32_t)occ * st->n_cu / n_lanes;
     if (per_lane > KVM_STAGE_MAX_WGS) per_lane = KVM_STAGE_MAX_WGS;

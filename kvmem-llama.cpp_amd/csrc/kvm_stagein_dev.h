@@ -1,5 +1,5 @@
 // kvm_stagein_dev.h -- device side of the stage-in, shared by the stage-in
-// kernel and the top-k kernel that stages its own plan.
+// kernel and the decode attention kernel that stages its lanes' plans.
 //
 // K: dequant q8_0 -> NeoX RoPE at the window position -> normalised
 // Walsh-Hadamard -> q8_0, the order of llama-kvmem-stagein.cu:731-786, fused in
@@ -31,7 +31,7 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
     const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
     float x[DPL];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) x[i] = (float)(int8_t)blk[2 + e + i] * dsc;
+    for (int i = 0; i < DPL; ++i) x[i] = kvm_fmul((float)(int8_t)blk[2 + e + i], dsc);
 
     // NeoX RoPE: dims i and i + n_half rotate together for i < n_half.
     const int nh = (int)rc.n_half;
@@ -277,6 +277,116 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         a.slot_block[slot] = id;
         a.slot_base[slot] = base;
         if (a.shadow_rows) a.shadow_rows[slot] = nt;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A lane's plan staged by G workgroups x = 0 .. G-1 of one launch
+// ---------------------------------------------------------------------------
+// Longest wait at a lane barrier (s_sleep rounds of ~64 cycles, about 0.1 s):
+// every workgroup of the launch is resident (the grids never exceed what the
+// CUs hold at once) and arrives without waiting on anything, so the wait ends
+// unless workgroups cannot be scheduled; past the limit the status says so
+// (bit 16) and the workgroups empty their items' cells instead.
+#define KVM_STAGE_SPIN (1u << 21)
+
+__device__ __forceinline__ uint32_t sync_load(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void sync_store(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool sync_wait(const uint32_t *p, uint32_t v) {
+    for (uint32_t it = 0; sync_load(p) != v; ++it) {
+        if (it > KVM_STAGE_SPIN) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return true;
+}
+
+// Entries of the lane's plan to stage: none when the plan does not fit (status
+// bits 1, over capacity, and 2, more blocks than slots).
+__device__ inline uint32_t stage_entries(const stage_args &a) {
+    return (a.info[3] & 3u) != 0 ? 0u : a.info[2];
+}
+
+// Barrier of a lane's G workgroups (NTH threads each) at value v, through the
+// lane's sync words (kvm_state::stage_sync): [0] the epoch, [1] the go flag,
+// [2] the failure flag, [64 + x] workgroup x's arrival.  Every workgroup reads
+// the epoch e before its first arrival of the launch and the launch's barriers
+// take values e + 1, e + 2, ...; workgroup 0 stores the last one as the epoch
+// (`last`) once every workgroup has arrived there, so no flag of an earlier
+// launch (at most e) passes for one of this launch, also when the launch is
+// replayed from a captured graph.  The writes before the barrier are written
+// back from the writer's L2 before its arrival (release) and the caches are
+// invalidated after the go flag (acquire).  False: the wait timed out.
+template <int NTH>
+__device__ bool lane_barrier(uint32_t *sync, uint32_t v, uint32_t x, uint32_t G, bool last) {
+    __shared__ uint32_t s_ok;
+    const uint32_t tid = threadIdx.x;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        sync_store(sync + 64 + x, v);
+    }
+    uint32_t ok = 1;
+    if (x == 0) {
+        for (uint32_t t = tid; t < G; t += NTH) ok &= sync_wait(sync + 64 + t, v) ? 1u : 0u;
+        ok = __syncthreads_and(ok);
+        if (tid == 0) {
+            if (!ok) sync_store(sync + 2, v);
+            if (last) sync_store(sync, v);
+            __threadfence();
+            sync_store(sync + 1, v);
+        }
+    } else if (tid == 0) {
+        ok = sync_wait(sync + 1, v) && sync_load(sync + 2) != v;
+        s_ok = ok;
+    }
+    __syncthreads();
+    if (x != 0) ok = s_ok;
+    __threadfence();
+    return ok != 0;
+}
+
+// An item whose plan could not be carried out: its cells are emptied and,
+// once, its slot's map entry and shadow count, so attention never reads what
+// the slot held before and the next plan restages it.
+template <int IT>
+__device__ void stage_void_item(const stage_args &a, uint32_t si, uint32_t tt) {
+    const uint32_t slot = a.stage_slots[si], tid = threadIdx.x;
+    if (tid < IT) a.cell_pos[slot * a.bt + tt * IT + tid] = -1;
+    if (tt == 0 && tid == 0) {
+        a.slot_block[slot] = 0xffffffffu;
+        a.slot_base[slot] = -1;
+        if (a.shadow_rows) a.shadow_rows[slot] = 0u;
+        atomicOr(&a.info[3], 16u);
+    }
+}
+
+// The lane's n_ent plan entries staged by workgroup x of G: the gather of the
+// moving entries (x, x + G, ...) and a barrier at value v when any entry moves
+// within the window, then items x, x + G, ... of IT tokens.  `last`: the
+// gather barrier is the launch's last on these sync words.  No barrier
+// follows the items.
+template <int D, int NTH, int IT>
+__device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent, uint32_t x, uint32_t G,
+                           uint32_t v, bool last) {
+    const uint32_t tps = a.bt / IT, n_items = n_ent * tps;
+    bool ok = true;
+    if (a.moves) {
+        uint32_t any = 0;
+        for (uint32_t si = threadIdx.x; si < n_ent; si += NTH) any |= a.stage_src[si] >= 0 ? 1u : 0u;
+        if (__syncthreads_or(any)) {
+            for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
+            ok = lane_barrier<NTH>(a.sync, v, x, G, last);
+        }
+    }
+    for (uint32_t item = x; item < n_items; item += G) {
+        if (ok) stagein_item<D, NTH, IT>(a, s_rows, item / tps, item % tps);
+        else stage_void_item<IT>(a, item / tps, item % tps);
+        __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }
 }
 

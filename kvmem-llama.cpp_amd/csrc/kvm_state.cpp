@@ -2,6 +2,9 @@
 // host-generated RoPE cos/sin table.
 #include "kvm_internal.h"
 
+#include <mutex>
+#include <vector>
+
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -107,6 +110,35 @@ void *kvm_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->ws, &st-
 void *kvm_fa_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->fa_ws, &st->fa_ws_bytes, bytes); }
 
 void *kvm_move_workspace(kvm_state *st, size_t bytes) { return grow(st, &st->mv_ws, &st->mv_ws_bytes, bytes); }
+
+int kvm_resident_blocks(kvm_state *st, const void *fn, int threads, size_t lds, int *blocks) {
+    struct entry {
+        int device;
+        const void *fn;
+        int threads;
+        size_t lds;
+        int blocks;
+    };
+    static std::mutex mu;
+    static std::vector<entry> cache;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        for (const entry &e : cache)
+            if (e.device == st->device && e.fn == fn && e.threads == threads && e.lds == lds) {
+                *blocks = e.blocks;
+                return KVM_OK;
+            }
+    }
+    KVM_HIP(st, hipSetDevice(st->device));
+    KVM_HIP(st, hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    int n = 0;
+    KVM_HIP(st, hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds));
+    if (n < 1) return kvm_fail(st, KVM_ERANGE, "a workgroup of %d threads with %zu bytes of LDS does not fit a CU", threads, lds);
+    std::lock_guard<std::mutex> lk(mu);
+    cache.push_back(entry{st->device, fn, threads, lds, n});
+    *blocks = n;
+    return KVM_OK;
+}
 
 
 void *kvm_upload_desc(kvm_state *st, const void *host, size_t bytes) {

@@ -544,6 +544,42 @@ def prepare_fa_decode_lanes(st, windows, qs, q_poss, n_head, scale, outs):
                     (lanes, windows, qs, q_poss, outs))
 
 
+def prepare_stagein_fa_decode(st, history, sel, window, q, q_pos, n_head, scale, out, n_rot, freq_base,
+                              freq_scale=1.0, hadamard_nrot=-1):
+    """kvm_stagein_fa_decode: the selection's stage-in plan and the decode
+    attention over `window` in one launch."""
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_stagein_fa_decode,
+                    (st.h, C.byref(history.c), C.byref(sel.c), C.byref(r), C.byref(window.c), _ptr(q), qt,
+                     _ptr(q_pos), q.shape[0], n_head, float(scale), _ptr(out)),
+                    (r, history, sel, window, q, q_pos, out))
+
+
+def stagein_fa_decode(st, history, sel, window, q, q_pos, n_head, scale, n_rot, freq_base, freq_scale=1.0,
+                      hadamard_nrot=-1, out=None):
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty((q.shape[0], n_head, window.head_dim), dtype=torch.float32, device=q.device)
+    prepare_stagein_fa_decode(st, history, sel, window, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale,
+                              hadamard_nrot)()
+    return out
+
+
+def prepare_stagein_fa_decode_lanes(st, lanes, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    """lanes: dicts with history, sel, window, q, q_pos, out (kvm_stagein_fa_decode_lanes)."""
+    n = len(lanes)
+    sg, fl = (L.StageinLane * n)(), (L.Lane * n)()
+    for i, ln in enumerate(lanes):
+        sg[i] = L.StageinLane(C.pointer(ln["history"].c), C.pointer(ln["window"].c), C.pointer(ln["sel"].c))
+        fl[i] = L.Lane(C.pointer(ln["window"].c), ln["q"].data_ptr(), ln["q_pos"].data_ptr(), ln["out"].data_ptr(),
+                       ln["q"].shape[0])
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    qt = L.T_BF16 if lanes[0]["q"].dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_stagein_fa_decode_lanes, (st.h, sg, fl, n, C.byref(r), qt, n_head, float(scale)),
+                    (sg, fl, r, lanes))
+
+
 def quantize_rows(st, ty, x):
     """x: device fp32 [n_rows][n_per_row] -> uint8 ggml rows."""
     x = x.contiguous()

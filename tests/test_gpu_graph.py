@@ -66,7 +66,8 @@ def test_decode_step_graph_replays_equal_eager(kvm_state, fused):
         assert torch.equal(out, want_out), r
 
 
-def test_back_to_back_replays_follow_changing_inputs(kvm_state):
+@pytest.mark.parametrize("staged", [False, True])
+def test_back_to_back_replays_follow_changing_inputs(kvm_state, staged):
     """Replays of one captured decode step with nothing of the library's in
     between, while the inputs change: the query accumulator drifts (so plans
     restage and move blocks within a window with a K shadow, through the
@@ -74,7 +75,9 @@ def test_back_to_back_replays_follow_changing_inputs(kvm_state):
     replay.  Each replay's window equals an eager retrieval + stage-in of the
     same plans into a second window, and each replay's attention output equals
     an eager attention over the replay's window: the launches' in-launch
-    flags take their epochs from the device, not from the captured arguments."""
+    flags take their epochs from the device, not from the captured arguments.
+    staged: the step is kvm_score_topk + kvm_stagein_fa_decode (the attention
+    launch stages the plan) instead of kvm_score_topk_stagein + kvm_fa_decode."""
     st = kvm_state
     rng = np.random.default_rng(23)
     H, G, D, BT, n_blocks, budget = 4, 6, 256, 128, 48, 12
@@ -94,8 +97,13 @@ def test_back_to_back_replays_follow_changing_inputs(kvm_state):
     q = dev(rng.standard_normal((4, H * G, D)).astype(np.float32))
     q_pos = dev(np.arange(budget * BT - 4, budget * BT, dtype=np.int32))
     out = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
-    retrieval = api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel, hist, 64, 1e7)
-    fa = api.prepare_fa_decode(st, w, q, q_pos, H * G, D ** -0.5, out)
+    if staged:
+        retrieval = api.prepare_score_topk(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel)
+        fa = api.prepare_stagein_fa_decode(st, hist, sel, w, q, q_pos, H * G, D ** -0.5, out, 64, 1e7)
+    else:
+        retrieval = api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel, hist, 64,
+                                                   1e7)
+        fa = api.prepare_fa_decode(st, w, q, q_pos, H * G, D ** -0.5, out)
 
     def step():
         retrieval()
