@@ -451,6 +451,134 @@ def run_stagein(args, st, api, L, torch, np):
     print(json.dumps(rec), flush=True)
 
 
+# ---- churn: the decode step with one block swapped per step ------------------
+def pinned_history(st, api, L, torch, seed):
+    """A 262,144-token pinned host history of q8_0 K / q4_0 V rows of N(0,1) values."""
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    kbuf = api.HostBuffer(HIST_TOKENS * K_ROW)
+    vbuf = api.HostBuffer(HIST_TOKENS * V_ROW)
+    chunk = 16384
+    for t0 in range(0, HIST_TOKENS, chunk):
+        k = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
+        v = torch.randn((chunk, H_KV * D), generator=gen, device=dev)
+        torch.from_numpy(kbuf.u8[t0 * K_ROW:(t0 + chunk) * K_ROW]).copy_(api.quantize_rows(st, L.T_Q8_0, k).view(-1).cpu())
+        torch.from_numpy(vbuf.u8[t0 * V_ROW:(t0 + chunk) * V_ROW]).copy_(api.quantize_rows(st, L.T_Q4_0, v).view(-1).cpu())
+    hist = api.History.__new__(api.History)
+    hist.kbuf, hist.vbuf, hist.n_tokens = kbuf, vbuf, HIST_TOKENS
+    hist.c = L.History(kbuf.ptr, vbuf.ptr, HIST_TOKENS)
+    return hist
+
+
+def run_churn(args, st, api, L, torch, np):
+    """The headline decode step (256K history, 32K window, 4 bf16 query tokens)
+    when each step's selection differs from the previous one by one early block:
+    the second-oldest selected block leaves and one past the newest joins, or
+    the reverse, so the 126 blocks between move one slot and must be re-rotated
+    to their new window positions.  The mean-K index makes two alternating
+    queries select exactly those two sets.  Timed with a window that keeps a K
+    shadow (moved blocks re-based from HBM, one block read from the host) and
+    with one that does not (127 blocks restaged over PCIe), against the same
+    step with an unchanging query."""
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC0FFEE06)
+    n_blocks, nsel = HIST_TOKENS // BT, RETRIEVED // BT
+    hist = pinned_history(st, api, L, torch, 0xC0FFEE06)
+    rng = np.random.default_rng(0xC0FFEE06)
+    sa = np.concatenate([[0], np.sort(rng.choice(np.arange(1, n_blocks - 1), nsel - 1, replace=False))])
+    sb = np.sort(np.concatenate([np.setdiff1d(sa, [sa[1]]), [n_blocks - 1]]))
+    sums = torch.zeros((1, n_blocks, H_KV * D), device=dev)
+    sums[0, torch.from_numpy(sa).to(dev), 0] = float(BT)
+    sums[0, torch.from_numpy(sb).to(dev), 1] = float(BT)
+    ix = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT)
+    ix.set_block_sums(sums)
+    ix.mean_tokens[:, :n_blocks] = BT
+    ix.present[:n_blocks] = 1
+    qas = []
+    for dim in (0, 1):
+        qa = api.QueryAcc(st, 1, N_HEAD, D)
+        qa.q_sum.zero_()
+        qa.q_sum[0, dim] = 1.0
+        qa.q_count.fill_(1)
+        qas.append(qa)
+    n_tokens = torch.full((n_blocks,), BT, dtype=torch.int32, device=dev)
+    ng = WINDOW - RETRIEVED
+    gk = api.quantize_rows(st, L.T_Q8_0, torch.randn((ng, H_KV * D), generator=gen, device=dev))
+    gv = api.quantize_rows(st, L.T_Q4_0, torch.randn((ng, H_KV * D), generator=gen, device=dev))
+    gpos = torch.arange(RETRIEVED, WINDOW, dtype=torch.int32, device=dev)
+    q = torch.randn((MTP, N_HEAD, D), generator=gen, device=dev).to(torch.bfloat16)
+    q_pos = torch.arange(WINDOW - MTP, WINDOW, dtype=torch.int32, device=dev)
+    out = torch.empty((MTP, N_HEAD, D), dtype=torch.float32, device=dev)
+    res = {}
+    for shadow in (True, False):
+        w = api.KVWindow(st, WINDOW, H_KV, D, BT, shadow=shadow)
+        sel = api.SelectionBuffers(st, n_blocks, nsel)
+        w.import_rows(RETRIEVED, gk, gv, gpos)
+        calls = [(api.prepare_score_topk(st, ix, qa, n_blocks, n_tokens, nsel, 1, 0, w, sel),
+                  api.prepare_stagein_fa_decode(st, hist, sel, w, q, q_pos, N_HEAD, D ** -0.5, out, N_ROT, FREQ_BASE))
+                 for qa in qas]
+
+        def churn(i):
+            r, f = calls[i % 2]
+            r()
+            f()
+
+        def steady(i):
+            r, f = calls[0]
+            r()
+            f()
+
+        churn(0)
+        torch.cuda.synchronize()
+        assert np.array_equal(sel.result()["ids"], sa)
+        steady_ms, _ = time_steps(torch, steady, lambda i: None, args.steps, args.warmup)
+        churn_ms, _ = time_steps(torch, churn, lambda i: None, args.steps, args.warmup)
+        r = sel.result()
+        last = sb if (args.steps - 1) % 2 == 1 else sa            # the timed loop's last call
+        assert np.array_equal(r["ids"], last) and r["status"] == 0, r["status"]
+        moved = int((r["stage_src"] >= 0).sum())
+        assert len(r["stage_slots"]) == nsel - 1 and moved == (nsel - 2 if shadow else 0), (len(r["stage_slots"]), moved)
+        # the window equals a fresh stage-in of the last plan
+        wf = api.KVWindow(st, WINDOW, H_KV, D, BT)
+        sf = api.select_topk(st, sel.scores[:n_blocks].clone(), n_tokens, nsel, 1, 0, None, wf)
+        api.stagein_selection(st, hist, wf, sf, N_ROT, FREQ_BASE)
+        ka, va = w.export_rows(0, RETRIEVED)
+        kb, vb = wf.export_rows(0, RETRIEVED)
+        assert torch.equal(ka, kb) and torch.equal(va, vb), "churned window differs from a fresh stage-in"
+        res[shadow] = dict(churn_us=churn_ms * 1e3, steady_us=steady_ms * 1e3, moved=moved,
+                           host_blocks=len(r["stage_slots"]) - moved)
+        log("shadow=%s: steady %.2f us, churn %.2f us per step" % (shadow, steady_ms * 1e3, churn_ms * 1e3))
+        del w, sel, calls, wf, sf
+        torch.cuda.synchronize()
+    a, b = res[True], res[False]
+    # least HBM traffic of the shadow restage: a moved block's raw K read from the
+    # shadow and its K tile written, its V tiles read and written; the new block's
+    # rows cross the host link
+    hbm_min = a["moved"] * BT * 2 * (K_ROW + V_ROW)
+    rec = {
+        "metric": "decode step with one selected block swapped per step, µs/token @256K history, 32K window",
+        "value": round(a["churn_us"], 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(a["churn_us"] * 1e-3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0/q4_0 KV (int8 + fp16 MFMA), bf16 Q, fp32 softmax",
+        "data": "synthetic N(0,1) history and query, seed 0xC0FFEE06; mean-K index built for two alternating selections",
+        "config": {"workload": "decode step (score + top-k + stage-in + FA decode over a 32768-cell window, 4 bf16 "
+                               "query tokens) whose 128-block selection alternates between two sets differing in "
+                               "the second-oldest and the newest block: 127 slots restaged per step, 126 of them "
+                               "blocks already in the window that move one slot",
+                   "history_tokens": HIST_TOKENS, "window_cells": WINDOW},
+        "shadow": {"churn_us": round(a["churn_us"], 2), "steady_us": round(a["steady_us"], 2),
+                   "restage_us": round(a["churn_us"] - a["steady_us"], 2), "moved_blocks": a["moved"],
+                   "host_blocks": a["host_blocks"], "hbm_bytes_min": hbm_min,
+                   "h2d_bytes": a["host_blocks"] * BT * (K_ROW + V_ROW)},
+        "host_restage": {"churn_us": round(b["churn_us"], 2), "steady_us": round(b["steady_us"], 2),
+                         "restage_us": round(b["churn_us"] - b["steady_us"], 2), "host_blocks": b["host_blocks"],
+                         "h2d_bytes": b["host_blocks"] * BT * (K_ROW + V_ROW)},
+    }
+    print(json.dumps(rec), flush=True)
+
+
 # ---- multi-lane decode (4 conversations) -------------------------------------
 LANE_HIST = (65536, 131072, 196608, 262144)
 
@@ -572,10 +700,11 @@ def run_sweep(args, st, api, L, torch, np):
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="decode", choices=["decode", "prefill", "stagein", "lanes", "sweep"],
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "prefill", "stagein", "lanes", "sweep", "churn"],
                     help="decode: the headline decode step (default); prefill: chunked-prefill attention; "
                          "stagein: stage-in + RoPE of 128 blocks; lanes: 4-lane decode; sweep: decode step "
-                         "at 32K-256K histories")
+                         "at 32K-256K histories; churn: the decode step with one block swapped per step")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
@@ -601,6 +730,8 @@ def main():
         return run_lanes(args, st, api, L, torch, np)
     if args.workload == "sweep":
         return run_sweep(args, st, api, L, torch, np)
+    if args.workload == "churn":
+        return run_churn(args, st, api, L, torch, np)
     log("building workload (256K history, 32K window, %d replicas)" % args.replicas)
     t0 = time.time()
     wl = build_workload(st, api, L, torch, np, args.replicas)

@@ -65,8 +65,9 @@ static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window
     if (!h->k_raw || !h->v || !sel->ids || !sel->to_base || !sel->stage_slots || !sel->info)
         return kvm_fail(st, KVM_EINVAL, "stagein: null buffer");
     const uint32_t NB = w->head_dim / 32;
-    const size_t lds = (size_t)64 * w->n_head_kv * NB * (34 + 18);
-    if (lds > 150 * 1024) return kvm_fail(st, KVM_ERANGE, "stagein: %u kv heads x %u dims exceed the staging tile", w->n_head_kv, w->head_dim);
+    // a 32-token item's rows in LDS (the RoPE rows come on top)
+    const size_t lds = (size_t)32 * w->n_head_kv * NB * (34 + 18);
+    if (lds > 120 * 1024) return kvm_fail(st, KVM_ERANGE, "stagein: %u kv heads x %u dims exceed the staging tile", w->n_head_kv, w->head_dim);
     a->hk = (const uint8_t *)h->k_raw;
     a->hv = (const uint8_t *)h->v;
     a->h_tokens = h->n_tokens;
@@ -137,7 +138,8 @@ int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_l
         sl->lane[i].rc = rc0;
         sl->lane[i].sync = st->stage_sync + (size_t)i * KVM_STAGE_SYNC_LANE;
     }
-    *lds = (size_t)64 * max_h * (w0->head_dim / 32) * (34 + 18);
+    // 64-token items: K and V rows, then the (cos, sin) rows of their positions
+    *lds = (size_t)64 * (max_h * (w0->head_dim / 32) * (34 + 18) + (rope->n_rot / 2) * 8);
     // the lanes' move staging regions, one after the other (256-byte aligned)
     uint64_t mv_total = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) mv_total += (move_bytes(lanes[i].w, lanes[i].sel) + 255) & ~255ull;
@@ -222,7 +224,7 @@ __global__ void __launch_bounds__(256) k_stagein_items(const kitem_desc *items, 
     const uint32_t cell = it.cell0 + t;
     uint8_t *kt = it.wk + ((uint64_t)h * it.n_tiles + cell / 64) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
     stage_k_row<D>(it.src + (uint64_t)t * it.H * NB * 34 + h * NB * 34, kt, cell % 64,
-                   it.pos0 + (int32_t)t, rc);
+                   rc.tab + (uint64_t)(it.pos0 + (int32_t)t) * rc.n_half, rc);
     if ((threadIdx.x & 63) == 0 && h == 0) it.cell_pos[cell] = it.pos0 + (int32_t)t;
 }
 

@@ -18,42 +18,54 @@ struct rope_ctx {
     float hscale;          // 1 / sqrtf(nrot), computed on the host as the reference does
 };
 
-// One (token, head) row of D dims: src = NB q8_0 blocks (34 B each) readable by
-// every lane; writes the requantised row into K tile `kt` at cell c (0..63).
-template <int D>
-__device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, int32_t pos,
-                                   const rope_ctx &rc) {
+// NR (token, head) rows of D dims, interleaved so that their dependent shuffle
+// chains overlap: row r's src = NB q8_0 blocks (34 B each) readable by every
+// lane, requantised into K tile kt[r] at cell c[r] (0..63); cs[r] = the (cos,
+// sin) row of its window position, [n_half] (global memory or LDS).  Rows with
+// live[r] false are computed on their (valid) inputs but not written.
+template <int D, int NR>
+__device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *const (&kt)[NR],
+                                    const uint32_t (&c)[NR], const float2 *const (&cs_pos)[NR],
+                                    const bool (&live)[NR], const rope_ctx &rc) {
     constexpr int DPL = D / 64;
     const int L = threadIdx.x & 63;
     const int d0 = DPL * L;
     const int b = d0 >> 5, e = d0 & 31;
-    const uint8_t *blk = src + b * 34;
-    const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
-    float x[DPL];
+    float x[NR][DPL];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) x[i] = kvm_fmul((float)(int8_t)blk[2 + e + i], dsc);
+    for (int r = 0; r < NR; ++r) {
+        const uint8_t *blk = src[r] + b * 34;
+        const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) x[r][i] = kvm_fmul((float)(int8_t)blk[2 + e + i], dsc);
+    }
 
     // NeoX RoPE: dims i and i + n_half rotate together for i < n_half.
     const int nh = (int)rc.n_half;
     if (nh > 0) {
         const int pl = nh / DPL;                       // lane distance of the partner
         const bool lo = d0 < nh, hi = d0 >= nh && d0 < 2 * nh;
-        float y[DPL];
+        float y[NR][DPL];
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-            const float up = __shfl(x[i], (L + pl) & 63, 64);
-            const float dn = __shfl(x[i], (L - pl) & 63, 64);
-            y[i] = lo ? up : dn;
-        }
-        if (lo || hi) {
-            const float2 *cs = rc.tab + (size_t)pos * rc.n_half + (lo ? d0 : d0 - nh);
+        for (int r = 0; r < NR; ++r)
 #pragma unroll
             for (int i = 0; i < DPL; ++i) {
-                const float2 t = cs[i];
-                if (lo)   // x0' = x0 c - x1 s
-                    x[i] = kvm_fsub(kvm_fmul(x[i], t.x), kvm_fmul(y[i], t.y));
-                else      // x1' = x0 s + x1 c
-                    x[i] = kvm_fadd(kvm_fmul(y[i], t.y), kvm_fmul(x[i], t.x));
+                const float up = __shfl(x[r][i], (L + pl) & 63, 64);
+                const float dn = __shfl(x[r][i], (L - pl) & 63, 64);
+                y[r][i] = lo ? up : dn;
+            }
+        if (lo || hi) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const float2 *cs = cs_pos[r] + (lo ? d0 : d0 - nh);
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) {
+                    const float2 t = cs[i];
+                    if (lo)   // x0' = x0 c - x1 s
+                        x[r][i] = kvm_fsub(kvm_fmul(x[r][i], t.x), kvm_fmul(y[r][i], t.y));
+                    else      // x1' = x0 s + x1 c
+                        x[r][i] = kvm_fadd(kvm_fmul(y[r][i], t.y), kvm_fmul(x[r][i], t.x));
+                }
             }
         }
     }
@@ -62,46 +74,74 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
     // butterflies h = 1, 2, ..., nrot/2 (stagein.cu:105-131)
     if (rc.nrot > 0) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
+        for (int r = 0; r < NR; ++r)
 #pragma unroll
-        for (int h = 1; h < DPL; h <<= 1) {
+            for (int i = 0; i < DPL; ++i) x[r][i] = kvm_fmul(x[r][i], rc.hscale);
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                if (!(i & h)) {
-                    const float a = x[i], bb = x[i + h];
-                    x[i] = kvm_fadd(a, bb);
-                    x[i + h] = kvm_fsub(a, bb);
+        for (int h = 1; h < DPL; h <<= 1)
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) {
+                    if (!(i & h)) {
+                        const float a = x[r][i], bb = x[r][i + h];
+                        x[r][i] = kvm_fadd(a, bb);
+                        x[r][i + h] = kvm_fsub(a, bb);
+                    }
                 }
-            }
-        }
         for (int h = DPL; h < rc.nrot; h <<= 1) {
             const int lx = h / DPL;
             const bool first = (L & lx) == 0;
 #pragma unroll
-            for (int i = 0; i < DPL; ++i) {
-                const float o = __shfl_xor(x[i], lx, 64);
-                x[i] = first ? kvm_fadd(x[i], o) : kvm_fsub(o, x[i]);
-            }
+            for (int r = 0; r < NR; ++r)
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) {
+                    const float o = __shfl_xor(x[r][i], lx, 64);
+                    x[r][i] = first ? kvm_fadd(x[r][i], o) : kvm_fsub(o, x[r][i]);
+                }
         }
     }
 
     // q8_0 requantisation of each 32-dim block (32/DPL lanes per block)
-    float amax = 0.0f;
+    float amax[NR];
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    for (int r = 0; r < NR; ++r) {
+        amax[r] = 0.0f;
 #pragma unroll
-    for (int o = 1; o < 32 / DPL; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float d = kvm_fdiv(amax, 127.0f);
-    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
-    uint8_t *qd = kt + kvm_kq_off(D, c, d0);
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) qd[i] = (uint8_t)(int8_t)roundf(kvm_fmul(x[i], id));
-    if (e == 0) {
-        const uint16_t h16 = kvm_f2h(d);
-        uint8_t *sd = kt + kvm_kd_off(D, c, b);
-        sd[0] = (uint8_t)h16;
-        sd[1] = (uint8_t)(h16 >> 8);
+        for (int i = 0; i < DPL; ++i) amax[r] = fmaxf(amax[r], fabsf(x[r][i]));
     }
+#pragma unroll
+    for (int o = 1; o < 32 / DPL; o <<= 1)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) amax[r] = fmaxf(amax[r], __shfl_xor(amax[r], o, 64));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const float d = kvm_fdiv(amax[r], 127.0f);
+        const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+        // the lane's DPL quants are consecutive in the tile (8-byte runs of one
+        // block and lane group): one store of DPL bytes, aligned to DPL
+        uint32_t qw = 0;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) qw |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(x[r][i], id)) << (8 * i);
+        if (!live[r]) continue;
+        uint8_t *qd = kt[r] + kvm_kq_off(D, c[r], d0);
+        if constexpr (DPL == 4) *(uint32_t *)qd = qw;
+        else if constexpr (DPL == 2) *(uint16_t *)qd = (uint16_t)qw;
+        else *qd = (uint8_t)qw;
+        if (e == 0) *(uint16_t *)(kt[r] + kvm_kd_off(D, c[r], b)) = kvm_f2h(d);
+    }
+}
+
+// One row (stage_k_rows of one).
+template <int D>
+__device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, const float2 *cs_pos,
+                                   const rope_ctx &rc) {
+    const uint8_t *const s1[1] = {src};
+    uint8_t *const k1[1] = {kt};
+    const uint32_t c1[1] = {c};
+    const float2 *const t1[1] = {cs_pos};
+    const bool l1[1] = {true};
+    stage_k_rows<D, 1>(s1, k1, c1, t1, l1, rc);
 }
 
 // ---------------------------------------------------------------------------
@@ -131,6 +171,53 @@ struct stage_args {
     uint32_t *sync;                  // the lane's barrier words (kvm_state::stage_sync)
 };
 
+// dst[i] = src[i] for i = tid, tid + nth, ... < n (16-byte units, n >= 1, the
+// ranges disjoint): eight loads in flight before their stores (a load-store
+// pair per step would wait for each load in turn); loads past n re-read n - 1.
+__device__ inline void copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, uint32_t n, uint32_t tid,
+                              uint32_t nth) {
+    constexpr uint32_t B = 8;
+    for (uint32_t i0 = tid; i0 < n; i0 += B * nth) {
+        uint4 r[B];
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth;
+            r[j] = src[i < n ? i : n - 1];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth;
+            if (i < n) dst[i] = r[j];
+        }
+    }
+}
+
+// An item's LDS fill: n0, n1, n2 16-byte units from s0, s1, s2 to d0, d1, d2,
+// as one stream of loads, eight in flight per thread before their stores.
+__device__ inline void stage_fill(uint8_t *d0, const uint8_t *__restrict__ s0, uint32_t n0, uint8_t *d1,
+                                  const uint8_t *__restrict__ s1, uint32_t n1, uint8_t *d2,
+                                  const uint8_t *__restrict__ s2, uint32_t n2, uint32_t tid, uint32_t nth) {
+    constexpr uint32_t B = 8;
+    const uint32_t n01 = n0 + n1, n = n01 + n2;
+    for (uint32_t i0 = tid; i0 < n; i0 += B * nth) {
+        uint4 r[B];
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth, ic = i < n ? i : n - 1;
+            const uint8_t *p = ic < n0 ? s0 + 16u * ic : ic < n01 ? s1 + 16u * (ic - n0) : s2 + 16u * (ic - n01);
+            r[j] = *(const uint4 *)p;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth;
+            if (i < n) {
+                uint8_t *p = i < n0 ? d0 + 16u * i : i < n01 ? d1 + 16u * (i - n0) : d2 + 16u * (i - n01);
+                *(uint4 *)p = r[j];
+            }
+        }
+    }
+}
+
 // Row bytes of the history / shadow: q8_0 K and q4_0 V, all kv heads.
 __host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 34; }
 __host__ __device__ inline uint32_t stage_row_v(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 18; }
@@ -147,15 +234,12 @@ __device__ inline void stage_gather_entry(const stage_args &a, uint32_t si, uint
     if (src < 0) return;
     const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
     uint8_t *dk = a.moves + (uint64_t)si * a.bt * (rowK + rowV);
-    const uint4 *sk = (const uint4 *)(a.k_shadow + (uint64_t)src * a.bt * rowK);
-    for (uint32_t i = tid; i < a.bt * rowK / 16; i += nth) ((uint4 *)dk)[i] = sk[i];
+    copy16((uint4 *)dk, (const uint4 *)(a.k_shadow + (uint64_t)src * a.bt * rowK), a.bt * rowK / 16, tid, nth);
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
     uint4 *dv = (uint4 *)(dk + (uint64_t)a.bt * rowK);
-    for (uint32_t i = tid; i < a.H * tps * per; i += nth) {
-        const uint32_t ht = i / per, h = ht / tps, q = ht % tps;
-        const uint4 *sv = (const uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps + q) * vtile);
-        dv[i] = sv[i % per];
-    }
+    for (uint32_t h = 0; h < a.H; ++h)     // a slot's tiles of one head are consecutive
+        copy16(dv + (uint64_t)h * tps * per, (const uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile),
+               tps * per, tid, nth);
 }
 
 
@@ -192,7 +276,9 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint32_t count = nt > t0 ? (nt - t0 < IT ? nt - t0 : IT) : 0;
     const uint64_t htok0 = first + t0;
     const uint32_t rowK = a.H * NB * 34, rowV = a.H * NB * 18;
+    // LDS: the item's K rows, V rows, and the (cos, sin) rows of its positions
     uint8_t *lk = s_rows, *lv = s_rows + IT * rowK;
+    float2 *lt = (float2 *)(s_rows + IT * (rowK + rowV));
     // bulk copy of `count` consecutive token rows of K and V (contiguous in host
     // memory, or in the entry's staging region for a block moving in HBM)
     const uint8_t *mk = src >= 0 ? a.moves + (uint64_t)si * a.bt * (rowK + rowV) : nullptr;
@@ -200,13 +286,14 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint8_t *gv = src >= 0 ? mk : a.hv + htok0 * rowV;
     // a moved block's V comes as whole tiles (below), not as rows
     const uint32_t nk = count * rowK, nv = src >= 0 ? 0u : count * rowV;
+    // the table rows are contiguous ([position][n_half] float2, n_half a multiple of 4)
+    const uint32_t nh = a.rc.n_half, ntab = count * nh * 8;
+    const uint8_t *gt = (const uint8_t *)(a.rc.tab + (uint64_t)(base + (int32_t)t0) * nh);
     const bool al16 = (((uintptr_t)gk | (uintptr_t)gv | rowK | rowV) & 15u) == 0;
     if (al16) {
-#pragma unroll 4
-        for (uint32_t i = tid; i < nk / 16; i += NTH) ((uint4 *)lk)[i] = ((const uint4 *)gk)[i];
-#pragma unroll 4
-        for (uint32_t i = tid; i < nv / 16; i += NTH) ((uint4 *)lv)[i] = ((const uint4 *)gv)[i];
+        stage_fill(lk, gk, nk / 16, lv, gv, nv / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
     } else {
+        stage_fill(lk, gk, 0, lv, gv, 0, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
         for (uint32_t i = tid; i < nk; i += NTH) lk[i] = gk[i];
         for (uint32_t i = tid; i < nv; i += NTH) lv[i] = gv[i];
     }
@@ -221,28 +308,48 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     }
 
     const uint32_t tile = (slot * a.bt + t0) / 64, c0 = t0 % 64;   // c0: the item's first cell in the tile
-    // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ...
-    const uint32_t wave = tid >> 6;
-    for (uint32_t r = wave; r < count * a.H; r += NTH / 64) {
-        const uint32_t j = r / a.H, h = r % a.H;
-        uint8_t *kt = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
-        stage_k_row<D>(lk + j * rowK + h * NB * 34, kt, c0 + j, base + (int32_t)(t0 + j), a.rc);
+    // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time
+    const uint32_t wave = tid >> 6, nrow = count * a.H;
+    constexpr uint32_t W = NTH / 64, NR = 4;
+    for (uint32_t r0 = wave; r0 < nrow; r0 += NR * W) {
+        const uint8_t *src[NR];
+        uint8_t *kt[NR];
+        uint32_t cc[NR];
+        const float2 *cs[NR];
+        bool live[NR];
+#pragma unroll
+        for (uint32_t k = 0; k < NR; ++k) {
+            const uint32_t r = r0 + k * W < nrow ? r0 + k * W : r0;    // past the rows: recompute r0, unwritten
+            const uint32_t j = r / a.H, h = r % a.H;
+            src[k] = lk + j * rowK + h * NB * 34;
+            kt[k] = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
+            cc[k] = c0 + j;
+            cs[k] = lt + j * nh;
+            live[k] = r0 + k * W < nrow;
+        }
+        stage_k_rows<D, NR>(src, kt, cc, cs, live, a.rc);
     }
-    // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step;
-    // a moved block's words and scales are those of its gathered tiles
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
-    constexpr uint32_t NKS = IT / 32;    // key halves of the tile this item fills
-    const uint8_t *mv = src >= 0 ? gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile : nullptr;
-    const uint64_t mv_head = (uint64_t)(a.bt / 64) * vtile;     // gathered tiles of one head
-    for (uint32_t wi = tid; wi < a.H * D * 4 * NKS; wi += NTH) {
-        const uint32_t h = wi / (D * 4 * NKS), r = wi % (D * 4 * NKS);
-        const uint32_t X = r / NKS, ks = NKS == 2 ? (r & 1u) : c0 / 32;
-        const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
-        const uint32_t b = dd / 32, e = dd % 32;
-        uint32_t word = 0;
-        if (src >= 0) {
-            word = *(const uint32_t *)(mv + h * mv_head + kvm_vq_word(dd, gg, ks));
-        } else {
+    if (src >= 0) {
+        // a moved block's V: its gathered tiles, whole, by the first item of each
+        // tile (an item of 32 tokens fills half a tile; the other half's item
+        // skips V, its bytes come with this copy)
+        if (c0 == 0) {
+            const uint32_t per = vtile / 16;
+            const uint4 *mv = (const uint4 *)(gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile);
+            for (uint32_t h = 0; h < a.H; ++h)
+                copy16((uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile), mv + (uint64_t)h * (a.bt / 64) * per,
+                       per, tid, NTH);
+        }
+    } else {
+        // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
+        constexpr uint32_t NKS = IT / 32;    // key halves of the tile this item fills
+        for (uint32_t wi = tid; wi < a.H * D * 4 * NKS; wi += NTH) {
+            const uint32_t h = wi / (D * 4 * NKS), r = wi % (D * 4 * NKS);
+            const uint32_t X = r / NKS, ks = NKS == 2 ? (r & 1u) : c0 / 32;
+            const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
+            const uint32_t b = dd / 32, e = dd % 32;
+            uint32_t word = 0;
 #pragma unroll
             for (uint32_t j = 0; j < 8; ++j) {
                 const uint32_t cj = 32 * ks + 8 * gg + j - c0;    // key within the item
@@ -253,23 +360,19 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
                 }
                 word |= nib << kvm_vq_nib_shift(j);
             }
+            *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
         }
-        *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
-    }
-    for (uint32_t si2 = tid; si2 < a.H * IT * NB; si2 += NTH) {
-        const uint32_t h = si2 / (IT * NB), cj = (si2 / NB) % IT, b = si2 % NB;
-        uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, c0 + cj, b);
-        if (src >= 0) {
-            const uint8_t *md = mv + h * mv_head + kvm_vd_off(D, c0 + cj, b);
-            sd[0] = md[0];
-            sd[1] = md[1];
-        } else if (cj < count) {
-            const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
-            sd[0] = blk[0];
-            sd[1] = blk[1];
-        } else {
-            sd[0] = 0;
-            sd[1] = 0;
+        for (uint32_t si2 = tid; si2 < a.H * IT * NB; si2 += NTH) {
+            const uint32_t h = si2 / (IT * NB), cj = (si2 / NB) % IT, b = si2 % NB;
+            uint8_t *sd = a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vd_off(D, c0 + cj, b);
+            if (cj < count) {
+                const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
+                sd[0] = blk[0];
+                sd[1] = blk[1];
+            } else {
+                sd[0] = 0;
+                sd[1] = 0;
+            }
         }
     }
     if (tid < IT) a.cell_pos[slot * a.bt + t0 + tid] = tid < count ? base + (int32_t)(t0 + tid) : -1;
