@@ -69,3 +69,12 @@ def test_struct_layouts_match_the_header(tmp_path):
                     str(tmp_path / "layout.c"), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     assert got == want
+
+
+def test_c_caller_builds(tmp_path):
+    """tests/c/kvm_abi_decode.c, a C99 caller of the library, compiles against the
+    header and links against the library (run on the GPU by test_gpu_c_abi.py)."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    exe = tmp_path / "kvm_abi_decode"
+    subprocess.run(["sh", os.path.join(here, "c", "build.sh"), str(exe)], check=True)
+    assert exe.exists()
