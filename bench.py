@@ -124,23 +124,29 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HI
 
 
 def prepare_decode(st, api, wl, out):
-    """The two calls of a decode step for every layer replica, marshalled once:
-    retrieval (kvm_score_topk: the scoring grid, then a top-k workgroup that
-    writes the plan) and stage-in + attention (kvm_stagein_fa_decode: the
-    attention's workgroups stage the plan, then attend)."""
+    """A decode step for every layer replica, marshalled once, as
+    (step, retrieval, attention): the step is one call in two launches
+    (kvm_score_topk_stagein_fa_decode: the scoring grid, then one launch whose
+    selector workgroup picks the blocks while the attention workgroups attend,
+    staging the plan and attending again when it stages anything); retrieval
+    (kvm_score_topk: scoring grid + top-k workgroup) and attention
+    (kvm_stagein_fa_decode: the attention's workgroups stage the plan, then
+    attend) are the same step as three launches."""
     n_blocks = wl["hist_tokens"] // BT
-    return [(api.prepare_score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel),
+    return [(api.prepare_decode_step(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel,
+                                     wl["hist"], wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out, N_ROT, FREQ_BASE),
+             api.prepare_score_topk(st, ix, wl["qa"], n_blocks, wl["n_tokens"], RETRIEVED // BT, 1, 0, w, sel),
              api.prepare_stagein_fa_decode(st, wl["hist"], sel, w, wl["q"], wl["q_pos"], N_HEAD, D ** -0.5, out,
                                            N_ROT, FREQ_BASE))
             for ix, w, sel in wl["reps"]]
 
 
-def time_steps(torch, step, fa, steps, warmup):
-    """Eager (ms per step, ms per attention launch), each from one pair of
-    events around a loop: an event recorded between two launches would itself
-    open a gap of several microseconds in the stream.  `step(i)` runs step i;
-    `fa(i)` runs only the attention launch of step i (back to back over the
-    replicas, so every launch streams its window from HBM)."""
+def time_steps(torch, step, fa, steps, warmup, *more):
+    """Eager ms per call of each loop, each from one pair of events around
+    the loop: an event recorded between two launches would itself open a gap
+    of several microseconds in the stream.  `step(i)` runs step i; `fa(i)` runs
+    only the attention launch of step i (back to back over the replicas, so
+    every launch streams its window from HBM); `more`: further loops."""
     def timed(fn):
         for i in range(warmup):
             fn(i)
@@ -152,7 +158,7 @@ def time_steps(torch, step, fa, steps, warmup):
         stop.record()
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps
-    return timed(step), timed(fa)
+    return tuple(timed(fn) for fn in (step, fa) + more)
 
 
 def check_full_size(st, api, L, torch, np, wl):
@@ -670,12 +676,8 @@ def run_sweep(args, st, api, L, torch, np):
         wl = build_workload(st, api, L, torch, np, args.replicas, hist_tokens=ht)
         preps = prepare_decode(st, api, wl, out)
 
-        def step(i):
-            retrieve, fa = preps[i % len(preps)]
-            retrieve()
-            fa()
-
-        ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][1](), args.steps, args.warmup)
+        ms, fa_ms = time_steps(torch, lambda i: preps[i % len(preps)][0](), lambda i: preps[i % len(preps)][2](),
+                               args.steps, args.warmup)
         nb = ht // BT
         step_bytes = nb * (H_KV * D * 4 + 8) + FA_KV_BYTES + QO_BYTES
         rows.append({"history_tokens": ht, "blocks": nb, "us_per_token": round(ms * 1e3, 2),
@@ -742,12 +744,14 @@ def main():
     out = torch.empty((MTP, N_HEAD, D), dtype=torch.float32, device="cuda")
     preps = prepare_decode(st, api, wl, out)
 
-    def step(i):
-        retrieve, fa = preps[i % len(preps)]
+    def three_launch(i):
+        _, retrieve, fa = preps[i % len(preps)]
         retrieve()
         fa()
 
-    step_ms, fa_ms = time_steps(torch, step, lambda i: preps[i % len(preps)][1](), args.steps, args.warmup)
+    step_ms, fa_ms, three_ms = time_steps(torch, lambda i: preps[i % len(preps)][0](),
+                                          lambda i: preps[i % len(preps)][2](), args.steps, args.warmup,
+                                          three_launch)
     out_gpu = out.cpu().numpy()
     if args.calibrate_copy:
         a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -775,12 +779,15 @@ def main():
                                "q8_0 K / q4_0 V) -> score + top-k(128 blocks incl. sink) + stage plan + "
                                "stage-in + FA decode over a 32768-cell q8_0/q4_0 window; 4 bf16 query tokens "
                                "(MTP verify), 24 q heads / 4 kv heads / head_dim 256; 1 layer per step, "
-                               f"{args.replicas} layer replicas cycled",
+                               f"{args.replicas} layer replicas cycled; two launches "
+                               "(kvm_score_topk_stagein_fa_decode)",
                    "history_tokens": HIST_TOKENS, "window_cells": WINDOW, "query_tokens": MTP},
         "hbm_gbps": round(STEP_BYTES / (step_ms * 1e-3) / 1e9, 1),
+        # the same step as three launches (kvm_score_topk, then kvm_stagein_fa_decode)
+        "three_launch_step_us": round(three_ms * 1e3, 2),
         # the reference retrieves once per query (tools/llama-kvmem-server.cpp:1466):
         # the step above is the worst case (a retrieval every token); split into
-        # retrieval per event (score + top-k + stage plan) and
+        # what retrieval adds per event (score + top-k + stage plan) and
         # attention per token, from the step and the separately timed attention loop
         "per_event": {"retrieval_us": round(step_us - fa_ms * 1e3, 2),
                       "attention_us_per_token": round(fa_ms * 1e3, 3)},

@@ -475,6 +475,30 @@ int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, co
                                 uint32_t n_lanes, const kvm_rope_params *rope, int q_type, uint32_t n_head,
                                 float scale);
 
+/* A whole decode step: kvm_score_topk of (ix, qa, p) into sel for window w,
+ * then kvm_stagein_fa_decode of (h, sel) and the query into w, with the
+ * results of those calls.  Two launches: the scoring grid, then one launch in
+ * which one workgroup per lane selects the blocks while the lane's attention
+ * workgroups attend over w as it is; a lane whose plan stages anything is
+ * staged by those workgroups, which then attend again.  The reference
+ * selects (prepare_reselect -> pick_topk_blocks, kvmem_runtime.cpp:112-119,
+ * kvmem_store.cpp:357-623),
+ * stages the plan (llama-memory-kvmem.cpp:4000-4071, llama-kvmem-stagein.cu:669-790)
+ * and then runs the graph's flash attention (ggml-cuda/fattn.cu:457), one
+ * after the other.  Steps with more than 4,096 blocks in a lane, a lane
+ * without query tokens or a window that is not q8_0 / q4_0 run as three
+ * launches (kvm_score_topk, then kvm_stagein_fa_decode) with the same results.
+ * In the lanes form ret[i].w must be lanes[i].w's window and hist[i] is lane
+ * i's history; every argument is checked before the first launch. */
+int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *qa,
+                                     const kvm_select_params *p, const kvm_window *w, const kvm_selection *sel,
+                                     const kvm_history *h, const kvm_rope_params *rope, const void *q, int q_type,
+                                     const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                                     float *out);
+int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_retrieval_lane *ret,
+                                           const kvm_history *const *hist, const kvm_lane *lanes, uint32_t n_lanes,
+                                           const kvm_rope_params *rope, int q_type, uint32_t n_head, float scale);
+
 /* kvm_fa_decode without any allocation, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  It has no counterpart in the reference.  The split

@@ -28,6 +28,7 @@
 // head's flags and each merges whole rows (or row chunks) of the head, so no
 // combine launch follows.
 #include "kvm_stagein_dev.h"
+#include "kvm_topk_dev.h"
 
 #include <cmath>
 #include <cstdlib>
@@ -54,8 +55,11 @@ struct fa_args {
     float *ws_ml;           // partial m,l [lane][H][split][RMAX][2]
     uint32_t *sync;         // [lane][64][512] by (lane, head, split): the epoch of the last launch that completed
                             // the split's partials; sync[KVM_FA_SYNC_STATUS]: bit 0 = a
-                            // merge wait timed out; sync[KVM_FA_SYNC_EPOCH + lane * 64 + h]:
-                            // the (lane, head)'s epoch, one less than its next launch's
+                            // merge wait timed out, bit 1 = a wait for the plan timed out;
+                            // sync[KVM_FA_SYNC_EPOCH + lane * 64 + h]: the (lane, head)'s
+                            // epoch, one less than its next launch's; 64-bit words from
+                            // KVM_FA_SYNC_PLAN, [lane * 64 + h]: the plan a selecting launch
+                            // published to the head (epoch, entries to stage)
     uint32_t H, G, n_head, n_splits;
     float scale_log2;       // kq_scale * log2(e)
     int q_bf16;
@@ -64,7 +68,9 @@ struct fa_args {
 #define KVM_MAX_SPLITS 512
 #define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)
 #define KVM_FA_SYNC_EPOCH (KVM_FA_SYNC_STATUS + 64)
-#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_EPOCH + KVM_MAX_LANES * KVM_FA_MAX_HEADS)
+#define KVM_FA_SYNC_PLAN (KVM_FA_SYNC_EPOCH + KVM_MAX_LANES * KVM_FA_MAX_HEADS)
+#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_PLAN + 2 * KVM_MAX_LANES * KVM_FA_MAX_HEADS)
+static_assert(KVM_FA_SYNC_PLAN % 2 == 0, "64-bit plan words");
 
 __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
     return bf16 ? kvm_bf2f(((const uint16_t *)q)[i]) : ((const float *)q)[i];
@@ -248,7 +254,7 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
 // of the blocks that move within the window, behind the plan's first
 // barrier), then every workgroup waits at a second barrier for the whole plan.
 template <int D>
-__device__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent) {
+__device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent) {
     extern __shared__ __align__(16) uint8_t s_rows[];     // the staged launch's dynamic LDS
     __shared__ uint32_t s_e;
     if (threadIdx.x == 0) s_e = sync_load(sg.sync);
@@ -258,8 +264,78 @@ __device__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n
     if (!lane_barrier<512>(sg.sync, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
 }
 
-template <int D, int NRT, bool QUANT, bool PK, bool STAGE>
-__device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_args *stg) {
+// A selecting launch: workgroup (n_splits, 0) of each lane runs the lane's
+// top-k and layout (kvm_topk_dev.h, 512 threads, at most KVM_SEL_MAXB blocks),
+// while the lane's attention workgroups attend over the window as it is.
+#define KVM_SEL_MAXB 4096
+typedef topk_lds<512, KVM_SEL_MAXB, 1024> sel_lds;
+
+// Longest wait of an attention workgroup for its lane's plan (s_sleep rounds
+// of ~128 cycles, about 0.2 s): the selector is resident with it (the grid
+// never exceeds what the CUs hold at once) and waits on nothing; past the
+// limit the status word says so (bit 1) and the workgroup keeps its pass
+// over the window as it was.
+#define KVM_FA_PLAN_SPIN (1u << 21)
+
+// The selector publishes the plan to each of the lane's heads: one 64-bit
+// word per (lane, head) = the head's epoch of this launch | the entries to
+// stage << 32, after the selection's stores are written back (release).  It
+// reads the epochs before the selection, and no split of a head raises its
+// flag before it has seen the head's word, so the head's merger cannot have
+// advanced the epoch yet.
+__device__ void fa_select_lane(const fa_args &a, const topk_args &t) {
+    extern __shared__ __align__(16) uint8_t s_rows[];     // the launch's dynamic LDS
+    __shared__ uint32_t s_ep[KVM_FA_MAX_HEADS];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t *ep = a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS;
+    // (issued with the selection's loads: every lane loads, tid < H keeps it)
+    const uint32_t my_ep = sync_load(ep + (tid < a.H ? tid : 0u));
+    const uint32_t n_ent = topk_body(t, *reinterpret_cast<sel_lds *>(s_rows));
+    if (tid < a.H) s_ep[tid] = my_ep;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        uint64_t *plan = (uint64_t *)(a.sync + KVM_FA_SYNC_PLAN) + blockIdx.z * KVM_FA_MAX_HEADS;
+        for (uint32_t h = 0; h < a.H; ++h)
+            __hip_atomic_store(plan + h, (uint64_t)(s_ep[h] + 1u) | (uint64_t)n_ent << 32, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// An attention workgroup's wait for its lane's plan (thread 0 polls the
+// head's word for this launch's epoch): the entries to stage, 0 when the plan
+// is empty or the wait timed out.
+__device__ uint32_t fa_await_plan(const fa_args &a, uint32_t h, uint32_t epoch) {
+    __shared__ uint32_t s_n;
+    if (threadIdx.x == 0) {
+        const uint64_t *pw = (const uint64_t *)(a.sync + KVM_FA_SYNC_PLAN) + blockIdx.z * KVM_FA_MAX_HEADS + h;
+        uint32_t n = 0;
+        for (uint32_t it = 0;; ++it) {
+            const uint64_t v = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)v == epoch) {
+                n = (uint32_t)(v >> 32);
+                break;
+            }
+            if (it > KVM_FA_PLAN_SPIN) {
+                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        s_n = n;
+    }
+    __syncthreads();
+    return s_n;
+}
+
+// STAGE: the launch first carries out its lanes' stage-in plans.  SELECT
+// (with STAGE): the plans come from the launch's selectors; the attention
+// workgroups attend over the window as it is, then wait for the lane's plan,
+// and only when it stages anything stage it and attend again.
+template <int D, int NRT, bool QUANT, bool PK, bool STAGE, bool SELECT>
+__device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_args *stg, const topk_args *sel) {
+    static_assert(!SELECT || STAGE, "a selecting launch stages its plans");
     constexpr int NB = D / 32;          // 32-dim blocks per row
     constexpr int NP = NB / 2;          // block pairs (packed row tile)
     constexpr int NG = QUANT ? NB / 4 : 1;   // 4-block scale groups
@@ -306,8 +382,19 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     __shared__ float s_l[4][RMAX];
     __shared__ __align__(16) _Float16 s_p[2][RMAX][PSTR];   // P of the tile (tile parity)
 
-    if (R == 0) {                        // lane without query rows: no partials
-        if constexpr (STAGE) {
+    if constexpr (SELECT) {
+        if (split == a.n_splits) {           // the lane's selector column
+            if (h == 0) {
+                const topk_args t = sel[blockIdx.z];     // one copy out of the argument segment
+                fa_select_lane(a, t);
+            }
+            return;
+        }
+    }
+    // lane without query rows: no partials (a selecting launch has none: its
+    // workgroups could not tell this launch's plan from an earlier one)
+    if (R == 0) {
+        if constexpr (STAGE && !SELECT) {
             const uint32_t n_ent = stage_entries(stg[blockIdx.z]);
             if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
         }
@@ -351,12 +438,26 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     // a staged launch reads the lane's plan length with the query (an empty
     // plan, the decode loop's steady state, then costs no memory round trip)
     uint32_t n_ent = 0;
-    if constexpr (STAGE) n_ent = stage_entries(stg[blockIdx.z]);
+    if constexpr (STAGE && !SELECT) n_ent = stage_entries(stg[blockIdx.z]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (tid == 0) s_epoch = ep + 1;
-    if constexpr (STAGE) {
+    if constexpr (STAGE && !SELECT) {
         if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
     }
+    // SELECT, after the first pass over the window (both roles, at the same
+    // barrier): true when the lane's plan staged anything, so the pass is redone
+    auto restaged = [&](uint32_t pass) -> bool {
+        if constexpr (!SELECT) {
+            return false;
+        } else {
+            if (pass) return false;
+            const uint32_t n = fa_await_plan(a, h, ep + 1);
+            if (!n) return false;
+            __threadfence();                 // acquire: the selection's stores
+            fa_stage_lane<D>(a, stg[blockIdx.z], n);
+            return true;
+        }
+    };
     // (the scoring waves call it behind their K prologue, the P V waves ahead
     // of their V prologue; it ends with the barrier)
     auto quantise_q = [&]() {
@@ -449,184 +550,192 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             rg.cp = *(const kvm_u32x4 *)((const uint8_t *)(ln.cell_pos + (uint64_t)T * 64) + cp_off);
         };
         KRegs kb[KVM_FA_NBUF];
+        auto prologue = [&]() {
 #pragma unroll
-        for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_k(kb[j], tile_index(j));
+            for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_k(kb[j], tile_index(j));
+        };
+        prologue();
         quantise_q();
+        for (uint32_t pass = 0;; ++pass) {
+            if (pass) prologue();
 
-        // B operands (Q^T) of every row tile: lane (row 16rt+m, k-group g)
-        long qop_i[QUANT ? NRT : 1][QUANT ? NB : 1];
-        kvm_i32x4 qop_p[NP];                 // packed row tile: [even block | odd block] per pair
-        kvm_f16x8 qop_h[QUANT ? 1 : NRT][QUANT ? 1 : NB];
-        float dqo[NRT][NG];                  // scale MFMA B operand: dq * kq_scale * log2(e)
-        float dqp[2];                        // packed row tile: even-block / odd-block columns
-        uint32_t qlim[NRT];                  // cell visible iff (uint)cell_pos < qlim (= q_pos + 1; 0 for padding)
-        float m_run[NRT], l_run[NRT];        // row 16rt + m (16rt + m % 8 packed) over this lane's keys
-        // B operands from the workgroup's quantised query in LDS
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            const int row = srow(rt);
-            if (is_pk(rt)) {
-                const bool odd = m >= 8;
-#pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    kvm_u32x2 v;
-                    __builtin_memcpy(&v, &s_qq[row][32 * (2 * p + odd) + 8 * g], 8);
-                    qop_p[p] = odd ? kvm_i32x4{0, 0, (int)v[0], (int)v[1]} : kvm_i32x4{(int)v[0], (int)v[1], 0, 0};
-                }
-                dqp[0] = !odd && g < NP ? s_dq[row][2 * g] * a.scale_log2 : 0.0f;
-                dqp[1] = odd && g < NP ? s_dq[row][2 * g + 1] * a.scale_log2 : 0.0f;
-            } else {
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    if constexpr (QUANT) __builtin_memcpy(&qop_i[rt][b], &s_qq[row][32 * b + 8 * g], 8);
-                    else qop_h[rt][b] = *(const kvm_f16x8 *)&s_qh[row][32 * b + 8 * g];
-                }
-#pragma unroll
-                for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
-            }
-            qlim[rt] = row < R && qpos_raw[rt] >= 0 ? (uint32_t)qpos_raw[rt] + 1u : 0u;
-            m_run[rt] = KVM_M_NONE;
-            l_run[rt] = 0.0f;
-        }
-        int par = 0;                         // tile parity: P and flag buffers
-
-        auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
-            load_k(nx, tile_index(inext));
-            // ---- scores of keys 16kq + 4g + i, rows 16rt + m (log2 domain; q8_0:
-            // kq_scale * log2(e) is folded into the query scales), masked
-            float s[NRT][4];
+            // B operands (Q^T) of every row tile: lane (row 16rt+m, k-group g)
+            long qop_i[QUANT ? NRT : 1][QUANT ? NB : 1];
+            kvm_i32x4 qop_p[NP];                 // packed row tile: [even block | odd block] per pair
+            kvm_f16x8 qop_h[QUANT ? 1 : NRT][QUANT ? 1 : NB];
+            float dqo[NRT][NG];                  // scale MFMA B operand: dq * kq_scale * log2(e)
+            float dqp[2];                        // packed row tile: even-block / odd-block columns
+            uint32_t qlim[NRT];                  // cell visible iff (uint)cell_pos < qlim (= q_pos + 1; 0 for padding)
+            float m_run[NRT], l_run[NRT];        // row 16rt + m (16rt + m % 8 packed) over this lane's keys
+            // B operands from the workgroup's quantised query in LDS
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
-                if constexpr (QUANT) {
-                    if (is_pk(rt)) {
-                        // d_k * d_q of (key 4g+i, column m) for the four pairs: the
-                        // even-block product in columns m < 8, the odd one in m >= 8
-                        kvm_f32x16 dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[0]), dqp[0],
-                                                                            kvm_f32x16{}, 0, 0, 0);
-                        dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[1]), dqp[1], dd, 0, 0, 0);
+                const int row = srow(rt);
+                if (is_pk(rt)) {
+                    const bool odd = m >= 8;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
-#pragma unroll
-                        for (int p = 0; p < NP; ++p) {
-                            kvm_i32x4 kw;
-                            __builtin_memcpy(&kw, &rg.k[p], 16);
-                            const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw, qop_p[p], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[4 * p + i], s[rt][i]);
-                        }
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) s[rt][i] += kvm_ror8_f32(s[rt][i]);
-                    } else {
-                        // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
-                        kvm_f32x16 dd[NG];
-#pragma unroll
-                        for (int gi = 0; gi < NG; ++gi)
-                            dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[rt][gi],
-                                                                           kvm_f32x16{}, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
-#pragma unroll
-                        for (int b = 0; b < NB; ++b) {
-                            const kvm_u32x4 kw = rg.k[b >> 1];
-                            const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
-                            const long av = (long)(lo32 | (hi32 << 32));
-                            const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[rt][i]);
-                        }
+                    for (int p = 0; p < NP; ++p) {
+                        kvm_u32x2 v;
+                        __builtin_memcpy(&v, &s_qq[row][32 * (2 * p + odd) + 8 * g], 8);
+                        qop_p[p] = odd ? kvm_i32x4{0, 0, (int)v[0], (int)v[1]} : kvm_i32x4{(int)v[0], (int)v[1], 0, 0};
                     }
+                    dqp[0] = !odd && g < NP ? s_dq[row][2 * g] * a.scale_log2 : 0.0f;
+                    dqp[1] = odd && g < NP ? s_dq[row][2 * g + 1] * a.scale_log2 : 0.0f;
                 } else {
-                    kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int ks = 0; ks < NB; ++ks) {
-                        kvm_f16x8 av;
-                        __builtin_memcpy(&av, &rg.k[ks], 16);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[rt][ks], acc, 0, 0, 0);
+                    for (int b = 0; b < NB; ++b) {
+                        if constexpr (QUANT) __builtin_memcpy(&qop_i[rt][b], &s_qq[row][32 * b + 8 * g], 8);
+                        else qop_h[rt][b] = *(const kvm_f16x8 *)&s_qh[row][32 * b + 8 * g];
                     }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) s[rt][i] = acc[i] * a.scale_log2;
+                    for (int gi = 0; gi < NG; ++gi) dqo[rt][gi] = QUANT ? s_dq[row][4 * gi + g] * a.scale_log2 : 0.0f;
                 }
+                qlim[rt] = row < R && qpos_raw[rt] >= 0 ? (uint32_t)qpos_raw[rt] + 1u : 0u;
+                m_run[rt] = KVM_M_NONE;
+                l_run[rt] = 0.0f;
             }
-            // ---- mask; per lane maxima; P against the current maxima.  A wave
-            // with a row whose maximum moves by more than 2^KVM_LAZY_MAX says so,
-            // and then (rarely) the scoring waves take the row maxima from LDS
-            // and redo P.  Before a row's first visible key m_run is KVM_M_NONE,
-            // which every finite score moves.
-            bool up_w = false;
-            float psum[NRT];
-            auto make_p = [&](int rt, float mn) {
-                _Float16 ph[4];
-                psum[rt] = 0.0f;
+            int par = 0;                         // tile parity: P and flag buffers
+
+            auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
+                load_k(nx, tile_index(inext));
+                // ---- scores of keys 16kq + 4g + i, rows 16rt + m (log2 domain; q8_0:
+                // kq_scale * log2(e) is folded into the query scales), masked
+                float s[NRT][4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const _Float16 p16 = (_Float16)__builtin_amdgcn_exp2f(s[rt][i] - mn);
-                    ph[i] = p16;
-                    psum[rt] += (float)p16;
+                for (int rt = 0; rt < NRT; ++rt) {
+                    if constexpr (QUANT) {
+                        if (is_pk(rt)) {
+                            // d_k * d_q of (key 4g+i, column m) for the four pairs: the
+                            // even-block product in columns m < 8, the odd one in m >= 8
+                            kvm_f32x16 dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[0]), dqp[0],
+                                                                                kvm_f32x16{}, 0, 0, 0);
+                            dd = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dkp[1]), dqp[1], dd, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+#pragma unroll
+                            for (int p = 0; p < NP; ++p) {
+                                kvm_i32x4 kw;
+                                __builtin_memcpy(&kw, &rg.k[p], 16);
+                                const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(kw, qop_p[p], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[4 * p + i], s[rt][i]);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) s[rt][i] += kvm_ror8_f32(s[rt][i]);
+                        } else {
+                            // d_k * d_q of (key 4g+i, row m) for four blocks per MFMA
+                            kvm_f32x16 dd[NG];
+#pragma unroll
+                            for (int gi = 0; gi < NG; ++gi)
+                                dd[gi] = __builtin_amdgcn_mfma_f32_16x16x1f32(kvm_h2f((uint16_t)rg.dk[gi]), dqo[rt][gi],
+                                                                               kvm_f32x16{}, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) s[rt][i] = 0.0f;
+#pragma unroll
+                            for (int b = 0; b < NB; ++b) {
+                                const kvm_u32x4 kw = rg.k[b >> 1];
+                                const uint64_t lo32 = kw[(b & 1) * 2], hi32 = kw[(b & 1) * 2 + 1];
+                                const long av = (long)(lo32 | (hi32 << 32));
+                                const kvm_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qop_i[rt][b], kvm_i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) s[rt][i] = fmaf((float)c[i], dd[b >> 2][4 * (b & 3) + i], s[rt][i]);
+                            }
+                        }
+                    } else {
+                        kvm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < NB; ++ks) {
+                            kvm_f16x8 av;
+                            __builtin_memcpy(&av, &rg.k[ks], 16);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop_h[rt][ks], acc, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s[rt][i] = acc[i] * a.scale_log2;
+                    }
                 }
-                __builtin_memcpy(&s_p[par][16 * rt + m][16 * kq + 4 * g], ph, 8);
+                // ---- mask; per lane maxima; P against the current maxima.  A wave
+                // with a row whose maximum moves by more than 2^KVM_LAZY_MAX says so,
+                // and then (rarely) the scoring waves take the row maxima from LDS
+                // and redo P.  Before a row's first visible key m_run is KVM_M_NONE,
+                // which every finite score moves.
+                bool up_w = false;
+                float psum[NRT];
+                auto make_p = [&](int rt, float mn) {
+                    _Float16 ph[4];
+                    psum[rt] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const _Float16 p16 = (_Float16)__builtin_amdgcn_exp2f(s[rt][i] - mn);
+                        ph[i] = p16;
+                        psum[rt] += (float)p16;
+                    }
+                    __builtin_memcpy(&s_p[par][16 * rt + m][16 * kq + 4 * g], ph, 8);
+                };
+#pragma unroll
+                for (int rt = 0; rt < NRT; ++rt) {
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (!(rg.cp[i] < qlim[rt])) s[rt][i] = -INFINITY;    // empty (-1) or after the row
+                        mx = fmaxf(mx, s[rt][i]);
+                    }
+                    s_max[kq][g][16 * rt + m] = mx;
+                    up_w = up_w || mx > m_run[rt] + KVM_LAZY_MAX;
+                    make_p(rt, m_run[rt]);
+                }
+                const bool wave_up = __builtin_amdgcn_ballot_w64(up_w) != 0;
+                if (l == 0) s_up[par][kq] = wave_up;
+                KVM_LDS_BARRIER();
+                if (*(const uint32_t *)&s_up[par][0] != 0) {
+                    asm volatile("" ::: "memory");      // keep this (rare) path a branch
+#pragma unroll
+                    for (int rt = 0; rt < NRT; ++rt) {
+                        const int row = 16 * rt + m;
+                        float tm = s_max[0][0][row];
+#pragma unroll
+                        for (int j = 1; j < 16; ++j) tm = fmaxf(tm, s_max[j >> 2][j & 3][row]);
+                        const bool up = tm > m_run[rt] + KVM_LAZY_MAX;
+                        const float mn = up ? tm : m_run[rt];
+                        const float alpha = up ? __builtin_amdgcn_exp2f(m_run[rt] - mn) : 1.0f;
+                        make_p(rt, mn);
+                        l_run[rt] = l_run[rt] * alpha + psum[rt];
+                        m_run[rt] = mn;
+                        if (kq == 0) {
+                            if (g == 0) s_alpha[row] = alpha;
+                            const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
+                            if (l == 0) s_rescale[rt] = any;
+                        }
+                    }
+                    KVM_LDS_BARRIER();
+                } else {
+#pragma unroll
+                    for (int rt = 0; rt < NRT; ++rt) l_run[rt] += psum[rt];
+                }
+                par ^= 1;
             };
+            run_tiles(kb, score);
+            if (restaged(pass)) continue;
+
+            // ---- (m, l) of this split's rows (a packed row tile: the lanes m >= 8
+            // repeat the rows of lanes m - 8 and are left out of the sum)
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
-                float mx = -INFINITY;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (!(rg.cp[i] < qlim[rt])) s[rt][i] = -INFINITY;    // empty (-1) or after the row
-                    mx = fmaxf(mx, s[rt][i]);
-                }
-                s_max[kq][g][16 * rt + m] = mx;
-                up_w = up_w || mx > m_run[rt] + KVM_LAZY_MAX;
-                make_p(rt, m_run[rt]);
+                float lr = is_pk(rt) && m >= 8 ? 0.0f : l_run[rt];
+                lr = kvm_add_xor32(kvm_add_xor16(lr));
+                if (g == 0) s_l[kq][16 * rt + m] = lr;
             }
-            const bool wave_up = __builtin_amdgcn_ballot_w64(up_w) != 0;
-            if (l == 0) s_up[par][kq] = wave_up;
-            KVM_LDS_BARRIER();
-            if (*(const uint32_t *)&s_up[par][0] != 0) {
-                asm volatile("" ::: "memory");      // keep this (rare) path a branch
+            __syncthreads();
+            if (kq == 0 && g == 0) {
 #pragma unroll
                 for (int rt = 0; rt < NRT; ++rt) {
                     const int row = 16 * rt + m;
-                    float tm = s_max[0][0][row];
-#pragma unroll
-                    for (int j = 1; j < 16; ++j) tm = fmaxf(tm, s_max[j >> 2][j & 3][row]);
-                    const bool up = tm > m_run[rt] + KVM_LAZY_MAX;
-                    const float mn = up ? tm : m_run[rt];
-                    const float alpha = up ? __builtin_amdgcn_exp2f(m_run[rt] - mn) : 1.0f;
-                    make_p(rt, mn);
-                    l_run[rt] = l_run[rt] * alpha + psum[rt];
-                    m_run[rt] = mn;
-                    if (kq == 0) {
-                        if (g == 0) s_alpha[row] = alpha;
-                        const bool any = __builtin_amdgcn_ballot_w64(up) != 0;
-                        if (l == 0) s_rescale[rt] = any;
+                    if (row < R) {
+                        fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 0], m_run[rt] == KVM_M_NONE ? -INFINITY : m_run[rt]);
+                        fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 1], s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row]);
                     }
                 }
-                KVM_LDS_BARRIER();
-            } else {
-#pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) l_run[rt] += psum[rt];
             }
-            par ^= 1;
-        };
-        run_tiles(kb, score);
-
-        // ---- (m, l) of this split's rows (a packed row tile: the lanes m >= 8
-        // repeat the rows of lanes m - 8 and are left out of the sum)
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-            float lr = is_pk(rt) && m >= 8 ? 0.0f : l_run[rt];
-            lr = kvm_add_xor32(kvm_add_xor16(lr));
-            if (g == 0) s_l[kq][16 * rt + m] = lr;
-        }
-        __syncthreads();
-        if (kq == 0 && g == 0) {
-#pragma unroll
-            for (int rt = 0; rt < NRT; ++rt) {
-                const int row = 16 * rt + m;
-                if (row < R) {
-                    fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 0], m_run[rt] == KVM_M_NONE ? -INFINITY : m_run[rt]);
-                    fa_store(&a.ws_ml[(pidx * RMAX + row) * 2 + 1], s_l[0][row] + s_l[1][row] + s_l[2][row] + s_l[3][row]);
-                }
-            }
+            break;
         }
     } else {
         // ================= P V waves: O[:, dims DW*dq ..] += P V ============
@@ -653,98 +762,102 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
         };
         quantise_q();                            // V is needed a tile later than K
         VRegs vbuf[KVM_FA_NBUF];
+        for (uint32_t pass = 0;; ++pass) {
 #pragma unroll
-        for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_v(vbuf[j], tile_index(j));
+            for (int j = 0; j < KVM_FA_NBUF - 1; ++j) load_v(vbuf[j], tile_index(j));
 
-        kvm_f32x4 O[NRT][NT];
-        // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and
-        // Oc P * dv * 8 * 2^-24 per row and 32-dim V block; (O - Oc) * 2^24 is P V
-        kvm_f32x4 Oc[NRT][NBW];
+            kvm_f32x4 O[NRT][NT];
+            // q8_0/q4_0: O accumulates P * dv * n * 2^-24 (V as fp16 denormals) and
+            // Oc P * dv * 8 * 2^-24 per row and 32-dim V block; (O - Oc) * 2^24 is P V
+            kvm_f32x4 Oc[NRT][NBW];
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
+            for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
+                for (int nt = 0; nt < NT; ++nt) O[rt][nt] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int bw = 0; bw < NBW; ++bw) Oc[rt][bw] = {0.f, 0.f, 0.f, 0.f};
-        }
-        const kvm_f16x8 eight_den = {(_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f,
-                                     (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f};
-        int par = 0;
-
-        auto accumulate = [&](const VRegs &rg, VRegs &nx, uint32_t inext) {
-            load_v(nx, tile_index(inext));
-            KVM_LDS_BARRIER();                   // P of this tile is in LDS
-            if (*(const uint32_t *)&s_up[par][0] != 0) {
-                asm volatile("" ::: "memory");
-                KVM_LDS_BARRIER();               // ... redone against the moved maxima
-#pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) {
-                    if (s_rescale[rt]) {
-                        float ar[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
-#pragma unroll
-                        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
-#pragma unroll
-                        for (int bw = 0; bw < NBW; ++bw)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) Oc[rt][bw][r] *= ar[r];
-                    }
-                }
+                for (int bw = 0; bw < NBW; ++bw) Oc[rt][bw] = {0.f, 0.f, 0.f, 0.f};
             }
-            kvm_f16x8 pa[2][NRT];
+            const kvm_f16x8 eight_den = {(_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f,
+                                         (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f, (_Float16)0x1p-21f};
+            int par = 0;
+
+            auto accumulate = [&](const VRegs &rg, VRegs &nx, uint32_t inext) {
+                load_v(nx, tile_index(inext));
+                KVM_LDS_BARRIER();                   // P of this tile is in LDS
+                if (*(const uint32_t *)&s_up[par][0] != 0) {
+                    asm volatile("" ::: "memory");
+                    KVM_LDS_BARRIER();               // ... redone against the moved maxima
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
+                    for (int rt = 0; rt < NRT; ++rt) {
+                        if (s_rescale[rt]) {
+                            float ar[4];
 #pragma unroll
-                for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[par][16 * rt + m][32 * ks + 8 * g];
+                            for (int r = 0; r < 4; ++r) ar[r] = s_alpha[16 * rt + 4 * g + r];
 #pragma unroll
-            for (int bw = 0; bw < NBW; ++bw) {
-                kvm_f16x8 pp[2][NRT];
-                if constexpr (QUANT) {
+                            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        kvm_f16x8 dv;
-                        __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
+                                for (int r = 0; r < 4; ++r) O[rt][nt][r] *= ar[r];
 #pragma unroll
-                        for (int rt = 0; rt < NRT; ++rt) {
-                            pp[ks][rt] = pa[ks][rt] * dv;
-                            Oc[rt][bw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], eight_den, Oc[rt][bw], 0, 0, 0);
+                            for (int bw = 0; bw < NBW; ++bw)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) Oc[rt][bw][r] *= ar[r];
                         }
                     }
                 }
+                kvm_f16x8 pa[2][NRT];
 #pragma unroll
-                for (int ntb = 0; ntb < NTB; ++ntb) {
-                    const int nt = bw * NTB + ntb;
+                for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        kvm_f16x8 vb;
-                        if constexpr (QUANT) vb = nib8_to_f16den(rg.vq[nt][ks]);
-                        else __builtin_memcpy(&vb, &rg.vh[nt][ks], 16);
+                    for (int rt = 0; rt < NRT; ++rt) pa[ks][rt] = *(const kvm_f16x8 *)&s_p[par][16 * rt + m][32 * ks + 8 * g];
 #pragma unroll
-                        for (int rt = 0; rt < NRT; ++rt)
-                            O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(QUANT ? pp[ks][rt] : pa[ks][rt], vb, O[rt][nt], 0, 0, 0);
+                for (int bw = 0; bw < NBW; ++bw) {
+                    kvm_f16x8 pp[2][NRT];
+                    if constexpr (QUANT) {
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            kvm_f16x8 dv;
+                            __builtin_memcpy(&dv, &rg.vs[bw][ks], 16);
+#pragma unroll
+                            for (int rt = 0; rt < NRT; ++rt) {
+                                pp[ks][rt] = pa[ks][rt] * dv;
+                                Oc[rt][bw] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pp[ks][rt], eight_den, Oc[rt][bw], 0, 0, 0);
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int ntb = 0; ntb < NTB; ++ntb) {
+                        const int nt = bw * NTB + ntb;
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            kvm_f16x8 vb;
+                            if constexpr (QUANT) vb = nib8_to_f16den(rg.vq[nt][ks]);
+                            else __builtin_memcpy(&vb, &rg.vh[nt][ks], 16);
+#pragma unroll
+                            for (int rt = 0; rt < NRT; ++rt)
+                                O[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(QUANT ? pp[ks][rt] : pa[ks][rt], vb, O[rt][nt], 0, 0, 0);
+                        }
                     }
                 }
-            }
-            par ^= 1;
-        };
-        run_tiles(vbuf, accumulate);
+                par ^= 1;
+            };
+            run_tiles(vbuf, accumulate);
+            if (restaged(pass)) continue;
 
-        __syncthreads();                          // pairs with the scoring waves' (m, l) exchange
-        float *po = a.ws + pidx * RMAX * D;
+            __syncthreads();                          // pairs with the scoring waves' (m, l) exchange
+            float *po = a.ws + pidx * RMAX * D;
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
+            for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+                for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = 16 * rt + 4 * g + r;
-                    if (row < R)
-                        fa_store(&po[row * D + DW * dq + 16 * nt + m],
-                                 QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r]);
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = 16 * rt + 4 * g + r;
+                        if (row < R)
+                            fa_store(&po[row * D + DW * dq + 16 * nt + m],
+                                     QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r]);
+                    }
+            break;
+        }
     }
 
     // ---- arrival: the partials of this split are complete at device scope
@@ -770,7 +883,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
 
 template <int D, int NRT, bool QUANT, bool PK>
 __global__ void __launch_bounds__(512) k_fa_decode(fa_args a) {
-    fa_decode_body<D, NRT, QUANT, PK, false>(a, nullptr);
+    fa_decode_body<D, NRT, QUANT, PK, false, false>(a, nullptr, nullptr);
 }
 
 // Decode attention that first stages its lanes' plans (q8_0 windows only).
@@ -780,7 +893,20 @@ struct fa_staged_args {
 };
 template <int D, int NRT, bool PK>
 __global__ void __launch_bounds__(512) k_fa_decode_staged(fa_staged_args sa) {
-    fa_decode_body<D, NRT, true, PK, true>(sa.a, sa.stage);
+    fa_decode_body<D, NRT, true, PK, true, false>(sa.a, sa.stage, nullptr);
+}
+
+// Decode attention whose launch also selects its lanes' plans (grid
+// (n_splits + 1, H, lanes): column n_splits holds the selectors).
+struct fa_select_args {
+    fa_args a;
+    stage_args stage[KVM_MAX_LANES];
+    topk_args sel[KVM_MAX_LANES];
+};
+static_assert(sizeof(fa_select_args) <= 4096, "kernel argument segment");
+template <int D, int NRT, bool PK>
+__global__ void __launch_bounds__(512) k_fa_decode_select(fa_select_args sa) {
+    fa_decode_body<D, NRT, true, PK, true, true>(sa.a, sa.stage, sa.sel);
 }
 
 static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
@@ -978,8 +1104,11 @@ extern "C" int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane
     int occ = 0;
     rc = kvm_resident_blocks(st, fn, 512, lds, &occ);
     if (rc) return rc;
+    // (and no lane with more workgroups than its barrier words count)
+    uint64_t cap = (uint64_t)occ * st->n_cu;
+    if (cap > (uint64_t)KVM_STAGE_MAX_WGS * n_lanes) cap = (uint64_t)KVM_STAGE_MAX_WGS * n_lanes;
     fa_plan fp;
-    rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)occ * st->n_cu);
+    rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)cap);
     if (rc) return rc;
     // no query rows at all: the plans alone
     if (fp.rows == 0) return kvm_stage_launch(st, stl, n_lanes, max_items, lds * 64 / KVM_FA_STAGE_IT, lanes[0].w->head_dim);
@@ -998,6 +1127,115 @@ extern "C" int kvm_stagein_fa_decode(kvm_state *st, const kvm_history *h, const 
     const kvm_stagein_lane sg{h, w, sel};
     const kvm_lane lane{w, q, q_pos, out, n_tokens};
     return kvm_stagein_fa_decode_lanes(st, &sg, &lane, 1, rope, q_type, n_head, scale);
+}
+
+// ---------------------------------------------------------------------------
+// A whole decode step in two launches: the scoring grid, then one launch whose
+// selector workgroups pick each lane's blocks while its attention workgroups
+// attend over the window as it is; a lane whose plan stages anything is staged
+// by its attention workgroups, which then attend again.
+// ---------------------------------------------------------------------------
+template <int D, int NRT, bool PK>
+static const void *select_kernel() { return (const void *)k_fa_decode_select<D, NRT, PK>; }
+
+static const void *select_kernel_for(uint32_t D, uint32_t max_rows) {
+    const int NRT = max_rows <= 16 ? 1 : 2;
+    const bool pk = max_rows - 16u * (NRT - 1) <= 8u;
+    if (D == 256) return NRT == 1 ? (pk ? select_kernel<256, 1, true>() : select_kernel<256, 1, false>())
+                                  : (pk ? select_kernel<256, 2, true>() : select_kernel<256, 2, false>());
+    return NRT == 1 ? (pk ? select_kernel<128, 1, true>() : select_kernel<128, 1, false>())
+                    : (pk ? select_kernel<128, 2, true>() : select_kernel<128, 2, false>());
+}
+
+extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_retrieval_lane *ret,
+                                                      const kvm_history *const *hist, const kvm_lane *lanes,
+                                                      uint32_t n_lanes, const kvm_rope_params *rope, int q_type,
+                                                      uint32_t n_head, float scale) {
+    if (!st) return KVM_EINVAL;
+    if (!ret || !hist || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: no lanes");
+    if (n_lanes > KVM_MAX_LANES)
+        return kvm_fail(st, KVM_ERANGE, "score_topk_stagein_fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
+    kvm_stagein_lane sg[KVM_MAX_LANES];
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        const kvm_window *w = ret[i].w;
+        if (!w || !lanes[i].w) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: lane %u: null window", i);
+        if (w->k != lanes[i].w->k || w->v != lanes[i].w->v || w->cell_pos != lanes[i].w->cell_pos)
+            return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: lane %u selects for another window than it attends", i);
+        sg[i] = kvm_stagein_lane{hist[i], w, ret[i].out};
+    }
+    // every argument is checked before the first launch
+    stage_lanes stl;
+    uint32_t max_items = 0;
+    size_t lds = 0;
+    int rc = kvm_stage_prepare(st, sg, n_lanes, rope, &stl, &max_items, &lds);
+    if (rc) return rc;
+    topk_lanes tl;
+    rc = kvm_retrieval_prepare(st, ret, n_lanes, &tl);
+    if (rc) return rc;
+    // the selecting launch takes lanes that all have query rows, at most
+    // KVM_SEL_MAXB blocks each and q8_0 windows; other steps take the
+    // three-launch path (scoring, top-k, stage-in + attention)
+    bool fuse = lanes[0].w->k_type == KVM_TYPE_Q8_0;
+    uint32_t max_rows = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        const kvm_window *w = lanes[i].w;
+        const uint32_t r = w->n_head_kv && n_head % w->n_head_kv == 0 ? lanes[i].n_tokens * (n_head / w->n_head_kv) : 0u;
+        fuse = fuse && r > 0 && ret[i].p->n_blocks <= KVM_SEL_MAXB;
+        max_rows = r > max_rows ? r : max_rows;
+    }
+    size_t lds_sel = lds * KVM_FA_STAGE_IT / 64;           // kvm_stage_prepare sizes 64-token items
+    if (lds_sel < sizeof(sel_lds)) lds_sel = sizeof(sel_lds);
+    const void *fn = nullptr;
+    fa_plan fp;
+    if (fuse) {
+        fn = select_kernel_for(lanes[0].w->head_dim, max_rows);
+        KVM_HIP(st, hipSetDevice(st->device));
+        int occ = 0;
+        rc = kvm_resident_blocks(st, fn, 512, lds_sel, &occ);
+        if (rc) return rc;
+        // every workgroup resident at once, the selector column included (and
+        // no lane with more attention workgroups than its barrier words count)
+        const uint64_t cap = (uint64_t)occ * st->n_cu, sel_wgs = (uint64_t)lanes[0].w->n_head_kv * n_lanes;
+        fuse = cap > 2 * sel_wgs;
+        if (fuse) {
+            uint64_t att = cap - sel_wgs;
+            if (att > (uint64_t)KVM_STAGE_MAX_WGS * n_lanes) att = (uint64_t)KVM_STAGE_MAX_WGS * n_lanes;
+            rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)att);
+            if (rc) return rc;
+        }
+    }
+    if (!fuse) {
+        rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp);
+        if (rc) return rc;
+        if (fp.rows && !fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk_stagein_fa_decode: q8_0 windows only");
+        rc = kvm_retrieval_score(st, ret, n_lanes, tl);
+        if (rc) return rc;
+        rc = kvm_topk_launch(st, tl, n_lanes);
+        if (rc) return rc;
+        return kvm_stagein_fa_decode_lanes(st, sg, lanes, n_lanes, rope, q_type, n_head, scale);
+    }
+    rc = kvm_retrieval_score(st, ret, n_lanes, tl);
+    if (rc) return rc;
+    fa_select_args sa{};
+    sa.a = fp.a;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        sa.stage[i] = stl.lane[i];
+        sa.sel[i] = tl.lane[i];
+    }
+    void *kargs[] = {&sa};
+    KVM_HIP(st, hipLaunchKernel(fn, dim3(fp.a.n_splits + 1, fp.a.H, n_lanes), dim3(512), kargs, lds_sel, st->stream));
+    return KVM_OK;
+}
+
+extern "C" int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *qa,
+                                                const kvm_select_params *p, const kvm_window *w,
+                                                const kvm_selection *sel, const kvm_history *h,
+                                                const kvm_rope_params *rope, const void *q, int q_type,
+                                                const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head,
+                                                float scale, float *out) {
+    const kvm_retrieval_lane ret{ix, qa, p, w, sel};
+    const kvm_lane lane{w, q, q_pos, out, n_tokens};
+    return kvm_score_topk_stagein_fa_decode_lanes(st, &ret, &h, &lane, 1, rope, q_type, n_head, scale);
 }
 
 // ---------------------------------------------------------------------------

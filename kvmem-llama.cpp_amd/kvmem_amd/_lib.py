@@ -169,6 +169,13 @@ SIGNATURES = {
                                         C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_stagein_fa_decode_lanes": (C.c_int, [_P, C.POINTER(StageinLane), C.POINTER(Lane), _u32,
                                               C.POINTER(RopeParams), C.c_int, _u32, _f]),
+    "kvm_score_topk_stagein_fa_decode": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
+                                                   C.POINTER(SelectParams), _PW, C.POINTER(Selection),
+                                                   C.POINTER(History), C.POINTER(RopeParams), _P, C.c_int, _P,
+                                                   _u32, _u32, _f, _P]),
+    "kvm_score_topk_stagein_fa_decode_lanes": (C.c_int, [_P, C.POINTER(RetrievalLane), C.POINTER(C.POINTER(History)),
+                                                         C.POINTER(Lane), _u32, C.POINTER(RopeParams), C.c_int,
+                                                         _u32, _f]),
     "kvm_fa_prefill": (C.c_int, [_P, _PW, _P, C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_d2d_batched": (C.c_int, [_P, C.POINTER(_P), C.POINTER(_P), C.POINTER(_sz), C.c_int]),
     "kvm_snapshot_info_read": (C.c_int, [_P, _P, _sz, C.POINTER(SnapshotInfo)]),

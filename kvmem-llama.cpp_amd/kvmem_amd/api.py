@@ -580,6 +580,53 @@ def prepare_stagein_fa_decode_lanes(st, lanes, n_head, scale, n_rot, freq_base, 
                     (sg, fl, r, lanes))
 
 
+def prepare_decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window,
+                        sel, history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale=1.0,
+                        hadamard_nrot=-1):
+    """kvm_score_topk_stagein_fa_decode: a whole decode step (scoring, top-k,
+    stage-in of the plan into `window`, decode attention over it) in two
+    launches."""
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks, None, 0, n_tokens.data_ptr())
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_score_topk_stagein_fa_decode,
+                    (st.h, C.byref(index.c), C.byref(query.c), C.byref(p), C.byref(window.c), C.byref(sel.c),
+                     C.byref(history.c), C.byref(r), _ptr(q), qt, _ptr(q_pos), q.shape[0], n_head, float(scale),
+                     _ptr(out)),
+                    (p, r, index, query, window, sel, n_tokens, history, q, q_pos, out))
+
+
+def decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window, sel,
+                history, q, q_pos, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1, out=None):
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty((q.shape[0], n_head, window.head_dim), dtype=torch.float32, device=q.device)
+    prepare_decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window,
+                        sel, history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale, hadamard_nrot)()
+    return out
+
+
+def prepare_decode_step_lanes(st, lanes, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
+    """lanes: score_topk_lanes dicts with history, q, q_pos, out as well
+    (kvm_score_topk_stagein_fa_decode_lanes)."""
+    n = len(lanes)
+    keep, arr = [], (L.RetrievalLane * n)()
+    hists, fl = (C.POINTER(L.History) * n)(), (L.Lane * n)()
+    for i, ln in enumerate(lanes):
+        p = L.SelectParams(ln["n_blocks"], ln["budget_blocks"], ln.get("sink_blocks", 1), ln.get("recent_blocks", 0),
+                           None, 0, ln["n_tokens"].data_ptr())
+        keep += [p, ln]
+        arr[i] = L.RetrievalLane(C.pointer(ln["index"].c), C.pointer(ln["query"].c), C.pointer(p),
+                                 C.pointer(ln["window"].c), C.pointer(ln["sel"].c))
+        hists[i] = C.pointer(ln["history"].c)
+        fl[i] = L.Lane(C.pointer(ln["window"].c), ln["q"].data_ptr(), ln["q_pos"].data_ptr(), ln["out"].data_ptr(),
+                       ln["q"].shape[0])
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    qt = L.T_BF16 if lanes[0]["q"].dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_score_topk_stagein_fa_decode_lanes,
+                    (st.h, arr, hists, fl, n, C.byref(r), qt, n_head, float(scale)), (keep, arr, hists, fl, r))
+
+
 def quantize_rows(st, ty, x):
     """x: device fp32 [n_rows][n_per_row] -> uint8 ggml rows."""
     x = x.contiguous()

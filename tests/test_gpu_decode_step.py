@@ -1,0 +1,223 @@
+"""kvm_score_topk_stagein_fa_decode(_lanes): a whole decode step in two
+launches (the scoring grid, then one launch whose selector workgroup picks the
+blocks while the attention workgroups attend, stage a non-empty plan and attend
+again) against the same step as separate calls on a second window:
+kvm_score_topk, kvm_stagein_selection, kvm_fa_decode.  Selections equal
+(scores, ids, layout, stage plan), windows equal byte for byte, attention
+outputs bit-equal where both split the keys alike (KVM_FA_SPLITS), else within
+the attention tolerance; one output also against the oracle."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import check_attention, dev, host, rand_rows
+from kvmem_amd import api, _lib as L
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+H, G, D, BT = 4, 6, 256, 128
+K_ROW, V_ROW = H * D // 32 * 34, H * D // 32 * 18
+
+
+def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4):
+    rng = np.random.default_rng(seed)
+    n_hist = n_blocks * BT - 40                         # the last block partly filled
+    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
+    ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
+    qa = api.QueryAcc(st, 1, H * G, D)
+    qa.reset()
+    qa.add(0, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
+    nt = dev(np.array([min(BT, n_hist - b * BT) for b in range(n_blocks)], np.int32))
+    mk = lambda sh: dict(window=api.KVWindow(st, slots * BT, H, D, BT, shadow=sh),
+                         sel=api.SelectionBuffers(st, n_blocks, budget), history=api.History(kr, vr))
+    return dict(rng=rng, kr=kr, vr=vr, ix=ix, qa=qa, nt=nt, n_blocks=n_blocks, budget=budget, n_hist=n_hist,
+                q_pos=dev(np.arange(budget * BT - max(n_tok_q, 1), budget * BT, dtype=np.int32)), n_tok_q=n_tok_q,
+                a=mk(True), b=mk(False))
+
+
+def _step_dict(ln):
+    a = ln["a"]
+    return dict(index=ln["ix"], query=ln["qa"], n_blocks=ln["n_blocks"], n_tokens=ln["nt"],
+                budget_blocks=ln["budget"], sink_blocks=1, recent_blocks=0, window=a["window"], sel=a["sel"],
+                history=a["history"], q=ln["q"], q_pos=ln["q_pos"], out=ln["out"])
+
+
+def _resident_full(w, nt_host):
+    return sorted({int(b) for b in host(w.slot_block) if 0 <= int(b) < len(nt_host) and nt_host[int(b)] == BT})
+
+
+def _set_rows(hist, blocks, rows_k, rows_v):
+    torch.cuda.synchronize()
+    k = hist.kbuf.u8.reshape(hist.n_tokens, K_ROW)
+    v = hist.vbuf.u8.reshape(hist.n_tokens, V_ROW)
+    for b in blocks:
+        k[b * BT:(b + 1) * BT] = rows_k(b)
+        v[b * BT:(b + 1) * BT] = rows_v(b)
+
+
+def _reference_step(st, ln):
+    b = ln["b"]
+    api.score_topk(st, ln["ix"], ln["qa"], ln["n_blocks"], ln["nt"], ln["budget"], 1, 0, None, b["window"], b["sel"])
+    api.stagein_selection(st, b["history"], b["window"], b["sel"], 64, 1e7)
+    return api.fa_decode(st, b["window"], ln["q"], ln["q_pos"], H * G, D ** -0.5)
+
+
+def _compare(ln, ref, bit_equal, tag):
+    ra, rb = ln["a"]["sel"].result(), ln["b"]["sel"].result()
+    assert ra["status"] == rb["status"] == 0, tag
+    assert ra["total"] == rb["total"], tag
+    for key in ("ids", "to_base", "stage_slots"):
+        assert np.array_equal(ra[key], rb[key]), (tag, key)
+    n = ln["n_blocks"]
+    assert torch.equal(ln["a"]["sel"].scores[:n], ln["b"]["sel"].scores[:n]), tag
+    for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+        assert torch.equal(getattr(ln["a"]["window"], name), getattr(ln["b"]["window"], name)), (tag, name)
+    if bit_equal:
+        assert torch.equal(ln["out"], ref), tag
+    else:
+        check_attention(host(ln["out"]), host(ref))
+    return int((ra["stage_src"] >= 0).sum())
+
+
+@pytest.mark.parametrize("n_lanes,splits", [(1, None), (1, 32), (3, None)])
+def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, splits):
+    """Queries drift over six steps, so plans restage and move blocks within
+    windows that carry a K shadow (the host rows of the full blocks a window
+    holds are poisoned while its step runs: a moved block must come from the
+    shadow).  splits: both attention paths take that many key splits, so the
+    outputs are bit-equal (the same code over the same bytes); otherwise the
+    step's launch takes one split fewer per head than kvm_fa_decode (the
+    selectors' column) and the outputs agree within the attention tolerance."""
+    if splits:
+        monkeypatch.setenv("KVM_FA_SPLITS", str(splits))
+    st = kvm_state
+    lanes = [_lane(st, 0x5D00 + i, 40 + 6 * i, 12, 16) for i in range(n_lanes)]
+    moved = staged = 0
+    for step in range(6):
+        for ln in lanes:
+            if step:
+                ln["qa"].q_sum.add_(dev((ln["rng"].standard_normal((1, H * G * D)) * 0.6).astype(np.float32)))
+            ln["q"] = dev(ln["rng"].standard_normal((ln["n_tok_q"], H * G, D)).astype(np.float32)).to(torch.bfloat16)
+            ln["out"] = torch.empty((ln["n_tok_q"], H * G, D), dtype=torch.float32, device="cuda")
+        nts = [host(ln["nt"]) for ln in lanes]
+        held = [_resident_full(ln["a"]["window"], nt) for ln, nt in zip(lanes, nts)]
+        for ln, hb in zip(lanes, held):
+            _set_rows(ln["a"]["history"], hb, lambda b, r=ln["rng"]: r.integers(0, 256, (BT, K_ROW), dtype=np.uint8),
+                      lambda b, r=ln["rng"]: r.integers(0, 256, (BT, V_ROW), dtype=np.uint8))
+        if n_lanes == 1:
+            d = _step_dict(lanes[0])
+            api.decode_step(st, d["index"], d["query"], d["n_blocks"], d["n_tokens"], d["budget_blocks"], 1, 0,
+                            d["window"], d["sel"], d["history"], d["q"], d["q_pos"], H * G, D ** -0.5, 64, 1e7,
+                            out=d["out"])
+        else:
+            api.prepare_decode_step_lanes(st, [_step_dict(ln) for ln in lanes], H * G, D ** -0.5, 64, 1e7)()
+        for ln, hb in zip(lanes, held):
+            _set_rows(ln["a"]["history"], hb, lambda b, ln=ln: ln["kr"][b * BT:(b + 1) * BT],
+                      lambda b, ln=ln: ln["vr"][b * BT:(b + 1) * BT])
+        for i, ln in enumerate(lanes):
+            ref = _reference_step(st, ln)
+            torch.cuda.synchronize()
+            staged += len(ln["a"]["sel"].result()["stage_slots"])
+            moved += _compare(ln, ref, splits is not None, (step, i))
+    assert moved > 0 and staged > moved
+    # the oracle on the last step of lane 0 (ggml semantics over the window's bytes)
+    ln = lanes[0]
+    w = ln["b"]["window"]
+    ek, ev = w.export_rows(0, w.n_cells)
+    ref = O.fa_ggml(O.T_Q8_0, O.T_Q4_0, ln["q"].float().cpu().numpy(), host(ek), host(ev), host(w.cell_pos),
+                    host(ln["q_pos"]), H * G, H, D, D ** -0.5)
+    check_attention(host(ln["out"]), ref)
+
+
+def test_decode_step_steady_state(kvm_state, monkeypatch):
+    """The same query accumulator twice: the second step's plan is empty (the
+    attention workgroups keep their first pass), its selection and window equal
+    the first's and its output equals kvm_fa_decode's over the window."""
+    monkeypatch.setenv("KVM_FA_SPLITS", "48")
+    st = kvm_state
+    ln = _lane(st, 0x5D10, 32, 10, 12)
+    ln["q"] = dev(ln["rng"].standard_normal((4, H * G, D)).astype(np.float32))
+    ln["out"] = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
+    d = _step_dict(ln)
+    step = api.prepare_decode_step(st, d["index"], d["query"], d["n_blocks"], d["n_tokens"], d["budget_blocks"], 1, 0,
+                                   d["window"], d["sel"], d["history"], d["q"], d["q_pos"], H * G, D ** -0.5,
+                                   d["out"], 64, 1e7)
+    step()
+    torch.cuda.synchronize()
+    first = ln["a"]["sel"].result()
+    assert len(first["stage_slots"]) > 0
+    k0 = ln["a"]["window"].k.clone()
+    ln["out"].zero_()
+    step()
+    torch.cuda.synchronize()
+    second = ln["a"]["sel"].result()
+    assert len(second["stage_slots"]) == 0 and second["status"] == 0
+    assert np.array_equal(first["ids"], second["ids"]) and np.array_equal(first["to_base"], second["to_base"])
+    assert torch.equal(ln["a"]["window"].k, k0)
+    ref = api.fa_decode(st, ln["a"]["window"], ln["q"], ln["q_pos"], H * G, D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(ln["out"], ref)
+
+
+def test_decode_step_three_launch_path(kvm_state):
+    """A step with a lane that has no query token takes the three-launch path
+    (kvm_score_topk + kvm_stagein_fa_decode) with the same results: the other
+    lane's selection, window and output as the separate calls give them, the
+    empty lane's plan staged and its output untouched."""
+    st = kvm_state
+    lanes = [_lane(st, 0x5D20 + i, 24, 8, 10, n_tok_q=(4, 0)[i]) for i in range(2)]
+    for ln in lanes:
+        ln["q"] = dev(ln["rng"].standard_normal((max(ln["n_tok_q"], 1), H * G, D)).astype(np.float32))
+        ln["q"] = ln["q"][:ln["n_tok_q"]] if ln["n_tok_q"] else ln["q"]
+        ln["out"] = torch.full((max(ln["n_tok_q"], 1), H * G, D), 7.0, dtype=torch.float32, device="cuda")
+    steps = [_step_dict(ln) for ln in lanes]
+    n = len(steps)
+    arr, hists, fl = (L.RetrievalLane * n)(), (C.POINTER(L.History) * n)(), (L.Lane * n)()
+    keep = []
+    for i, (ln, d) in enumerate(zip(lanes, steps)):
+        p = L.SelectParams(d["n_blocks"], d["budget_blocks"], 1, 0, None, 0, d["n_tokens"].data_ptr())
+        keep.append(p)
+        arr[i] = L.RetrievalLane(C.pointer(d["index"].c), C.pointer(d["query"].c), C.pointer(p),
+                                 C.pointer(d["window"].c), C.pointer(d["sel"].c))
+        hists[i] = C.pointer(d["history"].c)
+        fl[i] = L.Lane(C.pointer(d["window"].c), d["q"].data_ptr(), d["q_pos"].data_ptr(), d["out"].data_ptr(),
+                       ln["n_tok_q"])
+    st.check(st.lib.kvm_score_topk_stagein_fa_decode_lanes(st.h, arr, hists, fl, n, C.byref(L.RopeParams(64, 1e7, 1.0, -1)),
+                                                           L.T_F32, H * G, D ** -0.5))
+    torch.cuda.synchronize()
+    ref = _reference_step(st, lanes[0])
+    torch.cuda.synchronize()
+    _compare(lanes[0], ref, False, "lane 0")
+    ln = lanes[1]
+    b = ln["b"]
+    api.score_topk(st, ln["ix"], ln["qa"], ln["n_blocks"], ln["nt"], ln["budget"], 1, 0, None, b["window"], b["sel"])
+    api.stagein_selection(st, b["history"], b["window"], b["sel"], 64, 1e7)
+    torch.cuda.synchronize()
+    for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+        assert torch.equal(getattr(ln["a"]["window"], name), getattr(b["window"], name)), name
+    assert bool((ln["out"] == 7.0).all())
+
+
+def test_decode_step_bad_arguments(kvm_state):
+    """A lane that selects for one window and attends another is refused
+    before anything is launched."""
+    st = kvm_state
+    ln = _lane(st, 0x5D30, 16, 6, 8)
+    q = dev(ln["rng"].standard_normal((4, H * G, D)).astype(np.float32))
+    out = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
+    p = L.SelectParams(ln["n_blocks"], ln["budget"], 1, 0, None, 0, ln["nt"].data_ptr())
+    a, b = ln["a"], ln["b"]
+    arr = (L.RetrievalLane * 1)(L.RetrievalLane(C.pointer(ln["ix"].c), C.pointer(ln["qa"].c), C.pointer(p),
+                                                C.pointer(a["window"].c), C.pointer(a["sel"].c)))
+    hists = (C.POINTER(L.History) * 1)(C.pointer(a["history"].c))
+    fl = (L.Lane * 1)(L.Lane(C.pointer(b["window"].c), q.data_ptr(), ln["q_pos"].data_ptr(), out.data_ptr(), 4))
+    info0 = a["sel"].info.clone()
+    rc = st.lib.kvm_score_topk_stagein_fa_decode_lanes(st.h, arr, hists, fl, 1, C.byref(L.RopeParams(64, 1e7, 1.0, -1)),
+                                                       L.T_F32, H * G, D ** -0.5)
+    assert rc == L.KVM_EINVAL
+    torch.cuda.synchronize()
+    assert torch.equal(a["sel"].info, info0)

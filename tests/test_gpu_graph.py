@@ -66,8 +66,8 @@ def test_decode_step_graph_replays_equal_eager(kvm_state, fused):
         assert torch.equal(out, want_out), r
 
 
-@pytest.mark.parametrize("staged", [False, True])
-def test_back_to_back_replays_follow_changing_inputs(kvm_state, staged):
+@pytest.mark.parametrize("mode", ["retrieval_stagein", "staged", "step"])
+def test_back_to_back_replays_follow_changing_inputs(kvm_state, monkeypatch, mode):
     """Replays of one captured decode step with nothing of the library's in
     between, while the inputs change: the query accumulator drifts (so plans
     restage and move blocks within a window with a K shadow, through the
@@ -76,8 +76,11 @@ def test_back_to_back_replays_follow_changing_inputs(kvm_state, staged):
     same plans into a second window, and each replay's attention output equals
     an eager attention over the replay's window: the launches' in-launch
     flags take their epochs from the device, not from the captured arguments.
-    staged: the step is kvm_score_topk + kvm_stagein_fa_decode (the attention
-    launch stages the plan) instead of kvm_score_topk_stagein + kvm_fa_decode."""
+    mode: kvm_score_topk_stagein + kvm_fa_decode ("retrieval_stagein"),
+    kvm_score_topk + kvm_stagein_fa_decode (the attention launch stages the
+    plan, "staged"), or kvm_score_topk_stagein_fa_decode (the attention launch
+    also selects, "step"; both attention paths take 32 key splits)."""
+    monkeypatch.setenv("KVM_FA_SPLITS", "32")
     st = kvm_state
     rng = np.random.default_rng(23)
     H, G, D, BT, n_blocks, budget = 4, 6, 256, 128, 48, 12
@@ -97,9 +100,13 @@ def test_back_to_back_replays_follow_changing_inputs(kvm_state, staged):
     q = dev(rng.standard_normal((4, H * G, D)).astype(np.float32))
     q_pos = dev(np.arange(budget * BT - 4, budget * BT, dtype=np.int32))
     out = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
-    if staged:
+    if mode == "staged":
         retrieval = api.prepare_score_topk(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel)
         fa = api.prepare_stagein_fa_decode(st, hist, sel, w, q, q_pos, H * G, D ** -0.5, out, 64, 1e7)
+    elif mode == "step":
+        retrieval = api.prepare_decode_step(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel, hist, q, q_pos,
+                                            H * G, D ** -0.5, out, 64, 1e7)
+        fa = lambda: None
     else:
         retrieval = api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, budget, 1, 0, w, sel, hist, 64,
                                                    1e7)
