@@ -486,7 +486,9 @@ def run_churn(args, st, api, L, torch, np):
     queries select exactly those two sets.  Timed with a window that keeps a K
     shadow (moved blocks re-based from HBM, one block read from the host) and
     with one that does not (127 blocks restaged over PCIe), against the same
-    step with an unchanging query."""
+    step with an unchanging query; the step as three launches (value) and as
+    two (kvm_score_topk_stagein_fa_decode: a changed plan is staged after a
+    pass of the attention over the window as it was, which then runs again)."""
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0xC0FFEE06)
@@ -536,9 +538,17 @@ def run_churn(args, st, api, L, torch, np):
             r()
             f()
 
+        # the same steps in two launches (kvm_score_topk_stagein_fa_decode): the
+        # attention runs over the window as it was, then the plan is staged and
+        # the attention runs again
+        steps2 = [api.prepare_decode_step(st, ix, qa, n_blocks, n_tokens, nsel, 1, 0, w, sel, hist, q, q_pos, N_HEAD,
+                                          D ** -0.5, out, N_ROT, FREQ_BASE) for qa in qas]
         churn(0)
         torch.cuda.synchronize()
         assert np.array_equal(sel.result()["ids"], sa)
+        steady2_ms, churn2_ms = time_steps(torch, lambda i: steps2[0](), lambda i: steps2[i % 2](), args.steps,
+                                           args.warmup)
+        churn(0)
         steady_ms, _ = time_steps(torch, steady, lambda i: None, args.steps, args.warmup)
         churn_ms, _ = time_steps(torch, churn, lambda i: None, args.steps, args.warmup)
         r = sel.result()
@@ -554,9 +564,10 @@ def run_churn(args, st, api, L, torch, np):
         kb, vb = wf.export_rows(0, RETRIEVED)
         assert torch.equal(ka, kb) and torch.equal(va, vb), "churned window differs from a fresh stage-in"
         res[shadow] = dict(churn_us=churn_ms * 1e3, steady_us=steady_ms * 1e3, moved=moved,
-                           host_blocks=len(r["stage_slots"]) - moved)
+                           host_blocks=len(r["stage_slots"]) - moved, churn2_us=churn2_ms * 1e3,
+                           steady2_us=steady2_ms * 1e3)
         log("shadow=%s: steady %.2f us, churn %.2f us per step" % (shadow, steady_ms * 1e3, churn_ms * 1e3))
-        del w, sel, calls, wf, sf
+        del w, sel, calls, steps2, wf, sf
         torch.cuda.synchronize()
     a, b = res[True], res[False]
     # least HBM traffic of the shadow restage: a moved block's raw K read from the
@@ -577,10 +588,13 @@ def run_churn(args, st, api, L, torch, np):
         "shadow": {"churn_us": round(a["churn_us"], 2), "steady_us": round(a["steady_us"], 2),
                    "restage_us": round(a["churn_us"] - a["steady_us"], 2), "moved_blocks": a["moved"],
                    "host_blocks": a["host_blocks"], "hbm_bytes_min": hbm_min,
-                   "h2d_bytes": a["host_blocks"] * BT * (K_ROW + V_ROW)},
+                   "h2d_bytes": a["host_blocks"] * BT * (K_ROW + V_ROW),
+                   "two_launch_churn_us": round(a["churn2_us"], 2), "two_launch_steady_us": round(a["steady2_us"], 2)},
         "host_restage": {"churn_us": round(b["churn_us"], 2), "steady_us": round(b["steady_us"], 2),
                          "restage_us": round(b["churn_us"] - b["steady_us"], 2), "host_blocks": b["host_blocks"],
-                         "h2d_bytes": b["host_blocks"] * BT * (K_ROW + V_ROW)},
+                         "h2d_bytes": b["host_blocks"] * BT * (K_ROW + V_ROW),
+                         "two_launch_churn_us": round(b["churn2_us"], 2),
+                         "two_launch_steady_us": round(b["steady2_us"], 2)},
     }
     print(json.dumps(rec), flush=True)
 
@@ -592,9 +606,13 @@ LANE_HIST = (65536, 131072, 196608, 262144)
 def run_lanes(args, st, api, L, torch, np):
     """Four conversations, each with its own 32K-cell window, mean-K index and
     pinned host history (64K / 128K / 192K / 256K tokens), one bf16 query token
-    each: retrieval for all lanes in one launch sequence (scoring grid over every
-    lane's blocks + one top-k workgroup per lane), stage-in and attention for all
-    lanes in one launch."""
+    each.  A step is two launches for all lanes
+    (kvm_score_topk_stagein_fa_decode_lanes: the scoring grid over every lane's
+    blocks, then one launch whose selector workgroup per lane picks the blocks
+    while the lanes' attention workgroups attend); the same step as three
+    launches (retrieval for all lanes: scoring grid + one top-k workgroup per
+    lane; then stage-in and attention for all lanes in one launch) is timed
+    beside it."""
     n_rep = 2
     wls = []
     for i, ht in enumerate(LANE_HIST):
@@ -609,15 +627,18 @@ def run_lanes(args, st, api, L, torch, np):
                       window=wl["reps"][r][1], sel=wl["reps"][r][2], history=wl["hist"]) for wl in wls]
         fa_lanes = [dict(history=wl["hist"], sel=wl["reps"][r][2], window=wl["reps"][r][1], q=wl["q"],
                          q_pos=wl["q_pos"], out=o) for wl, o in zip(wls, outs)]
-        preps.append((api.prepare_score_topk_lanes(st, lanes),
+        steps = [dict(ln, q=fl["q"], q_pos=fl["q_pos"], out=fl["out"]) for ln, fl in zip(lanes, fa_lanes)]
+        preps.append((api.prepare_decode_step_lanes(st, steps, N_HEAD, scale, N_ROT, FREQ_BASE),
+                      api.prepare_score_topk_lanes(st, lanes),
                       api.prepare_stagein_fa_decode_lanes(st, fa_lanes, N_HEAD, scale, N_ROT, FREQ_BASE)))
 
-    def step(i):
-        retrieve, fa = preps[i % n_rep]
+    def three_launch(i):
+        _, retrieve, fa = preps[i % n_rep]
         retrieve()
         fa()
 
-    ms, fa_ms = time_steps(torch, step, lambda i: preps[i % n_rep][1](), args.steps, args.warmup)
+    ms, fa_ms, three_ms = time_steps(torch, lambda i: preps[i % n_rep][0](), lambda i: preps[i % n_rep][2](),
+                                     args.steps, args.warmup, three_launch)
     # checks: each lane's selection equals its single-lane one, nothing to restage,
     # and its attention equals the single-lane kernel's and the oracle's
     r = (args.steps - 1) % n_rep
@@ -648,10 +669,12 @@ def run_lanes(args, st, api, L, torch, np):
         "vs_baseline": None, "dtype": "q8_0/q4_0 KV (int8 + fp16 MFMA), bf16 Q, fp32 softmax",
         "data": "synthetic N(0,1), seeds 0xC0FFEE05 + lane, 16 planted blocks per lane",
         "config": {"workload": "4 lanes: histories of 65536/131072/196608/262144 tokens (pinned host q8_0 K / "
-                               "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; score + top-k for all "
-                               "lanes in one launch sequence, stage-in + FA decode for all lanes in one launch; "
-                               "24 q heads / 4 kv heads / head_dim 256; 2 replicas cycled",
+                               "q4_0 V), 32768-cell windows, 1 bf16 query token per lane; the scoring grid for all "
+                               "lanes, then one launch that selects, stages and attends for all lanes "
+                               "(kvm_score_topk_stagein_fa_decode_lanes); 24 q heads / 4 kv heads / head_dim 256; "
+                               "2 replicas cycled",
                    "lanes": len(wls), "step_bytes": step_bytes},
+        "three_launch_ms_per_step": round(three_ms, 5),
         "hbm_gbps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "kernel": "kvm_stagein_fa_decode_lanes (k_fa_decode_staged: split-K "
                                                "attention over every lane, splits merged in-launch)",
