@@ -200,7 +200,7 @@ class MeanKIndex:
         """Store sums [n_layer][n][e] (device tensor) for blocks first .. first+n-1."""
         Lr, T, E, W = self.k_sum.shape
         n = sums.shape[1]
-        view = self.k_sum.permute(0, 1, 3, 2).reshape(Lr, T * W, E)
+        view = self.k_sum.permute(0, 1, 3, 2).reshape(Lr, T * W, E).clone()   # (a copy even where reshape can view)
         view[:, first:first + n] = sums
         self.k_sum.copy_(view.reshape(Lr, T, W, E).permute(0, 1, 3, 2))
 
@@ -582,27 +582,31 @@ def prepare_stagein_fa_decode_lanes(st, lanes, n_head, scale, n_rot, freq_base, 
 
 def prepare_decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window,
                         sel, history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale=1.0,
-                        hadamard_nrot=-1):
+                        hadamard_nrot=-1, mandatory=None):
     """kvm_score_topk_stagein_fa_decode: a whole decode step (scoring, top-k,
     stage-in of the plan into `window`, decode attention over it) in two
-    launches."""
-    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks, None, 0, n_tokens.data_ptr())
+    launches.  mandatory: device int32 block ids (newest last) or None."""
+    p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks,
+                       None if mandatory is None else mandatory.data_ptr(),
+                       0 if mandatory is None else mandatory.numel(), n_tokens.data_ptr())
     r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
     qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
     return Prepared(st, st.lib.kvm_score_topk_stagein_fa_decode,
                     (st.h, C.byref(index.c), C.byref(query.c), C.byref(p), C.byref(window.c), C.byref(sel.c),
                      C.byref(history.c), C.byref(r), _ptr(q), qt, _ptr(q_pos), q.shape[0], n_head, float(scale),
                      _ptr(out)),
-                    (p, r, index, query, window, sel, n_tokens, history, q, q_pos, out))
+                    (p, r, index, query, window, sel, n_tokens, history, q, q_pos, out, mandatory))
 
 
 def decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window, sel,
-                history, q, q_pos, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1, out=None):
+                history, q, q_pos, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1, out=None,
+                mandatory=None):
     q = q.contiguous()
     if out is None:
         out = torch.empty((q.shape[0], n_head, window.head_dim), dtype=torch.float32, device=q.device)
     prepare_decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window,
-                        sel, history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale, hadamard_nrot)()
+                        sel, history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale, hadamard_nrot,
+                        mandatory)()
     return out
 
 

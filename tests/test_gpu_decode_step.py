@@ -221,3 +221,116 @@ def test_decode_step_bad_arguments(kvm_state):
     assert rc == L.KVM_EINVAL
     torch.cuda.synchronize()
     assert torch.equal(a["sel"].info, info0)
+
+
+def _rows(rng, n, h, d):
+    """Valid q8_0 K / q4_0 V rows without an fp32 source: fp16 scales in
+    [2^-8, 2^-4), random quants."""
+    nb = h * d // 32
+    k = np.zeros((n, nb, 34), np.uint8)
+    k[:, :, :2] = (rng.uniform(2 ** -8, 2 ** -4, (n, nb)).astype(np.float16)).view(np.uint8).reshape(n, nb, 2)
+    k[:, :, 2:] = rng.integers(-127, 128, (n, nb, 32), dtype=np.int8).view(np.uint8)
+    v = np.zeros((n, nb, 18), np.uint8)
+    v[:, :, :2] = (rng.uniform(2 ** -6, 2 ** -2, (n, nb)).astype(np.float16)).view(np.uint8).reshape(n, nb, 2)
+    v[:, :, 2:] = rng.integers(0, 256, (n, nb, 16), dtype=np.uint8)
+    return k.reshape(n, -1), v.reshape(n, -1)
+
+
+def _small_lane(st, seed, n_blocks, bt, budget, slots, h=1, g=8, d=128):
+    rng = np.random.default_rng(seed)
+    n_hist = n_blocks * bt
+    kr, vr = _rows(rng, n_hist, h, d)
+    ix = api.MeanKIndex(st, 1, n_blocks, h, d, bt)
+    ix.set_block_sums(dev(rng.standard_normal((1, n_blocks, h * d)).astype(np.float32)))
+    ix.mean_tokens[:, :n_blocks] = bt
+    ix.present[:n_blocks] = 1
+    qa = api.QueryAcc(st, 1, h * g, d)
+    qa.reset()
+    qa.add(0, dev(rng.standard_normal((2, h * g * d)).astype(np.float32)))
+    nt = dev(np.full(n_blocks, bt, np.int32))
+    mk = lambda: dict(window=api.KVWindow(st, slots * bt, h, d, bt), sel=api.SelectionBuffers(st, n_blocks, budget),
+                      history=api.History(kr, vr))
+    q = dev(rng.standard_normal((1, h * g, d)).astype(np.float32))
+    q_pos = dev(np.array([budget * bt - 1], np.int32))
+    return dict(rng=rng, ix=ix, qa=qa, nt=nt, n_blocks=n_blocks, bt=bt, budget=budget, h=h, g=g, d=d, q=q,
+                q_pos=q_pos, a=mk(), b=mk())
+
+
+def _check_small(st, ln, sink, recent, mandatory=None):
+    h, g, d = ln["h"], ln["g"], ln["d"]
+    a, b = ln["a"], ln["b"]
+    out = api.decode_step(st, ln["ix"], ln["qa"], ln["n_blocks"], ln["nt"], ln["budget"], sink, recent,
+                          a["window"], a["sel"], a["history"], ln["q"], ln["q_pos"], h * g, d ** -0.5, 64, 1e7,
+                          mandatory=mandatory)
+    api.score_topk(st, ln["ix"], ln["qa"], ln["n_blocks"], ln["nt"], ln["budget"], sink, recent, mandatory,
+                   b["window"], b["sel"])
+    api.stagein_selection(st, b["history"], b["window"], b["sel"], 64, 1e7)
+    ref = api.fa_decode(st, b["window"], ln["q"], ln["q_pos"], h * g, d ** -0.5)
+    torch.cuda.synchronize()
+    ra, rb = a["sel"].result(), b["sel"].result()
+    assert ra["status"] == rb["status"] == 0
+    for key in ("ids", "to_base", "stage_slots"):
+        assert np.array_equal(ra[key], rb[key]), key
+    assert torch.equal(a["sel"].scores[:ln["n_blocks"]], b["sel"].scores[:ln["n_blocks"]])
+    for name in ("k", "v", "cell_pos", "slot_block", "slot_base"):
+        assert torch.equal(getattr(a["window"], name), getattr(b["window"], name)), name
+    check_attention(host(out), host(ref))
+    return ra
+
+
+@pytest.mark.parametrize("n_blocks", [4096, 4097])
+def test_decode_step_at_the_selector_capacity(kvm_state, n_blocks):
+    """4,096 blocks (the selector workgroup's capacity: eight keys per thread)
+    take the two-launch step, one block more the three-launch path; 1,100
+    selected blocks in 1,100 slots (past the 1,024 slot-map entries the
+    selector keeps in LDS), over two steps whose query drifts.  Both equal the
+    separate calls (scores, selection, window bytes, attention)."""
+    st = kvm_state
+    ln = _small_lane(st, 0x5D40 + n_blocks, n_blocks, 64, 1100, 1100)
+    r = _check_small(st, ln, 1, 0)
+    assert len(r["ids"]) == 1100 and r["ids"][0] == 0 and len(r["stage_slots"]) == 1100
+    ln["qa"].q_sum.add_(dev((ln["rng"].standard_normal((1, ln["h"] * ln["g"] * ln["d"])) * 0.5).astype(np.float32)))
+    r = _check_small(st, ln, 1, 0)
+    assert 0 < len(r["stage_slots"]) < 1100
+
+
+def test_decode_step_mandatory_and_recent(kvm_state):
+    """Mandatory ids (newest last, trimmed by the budget newest first) and a
+    recent tail go through the selector's serial pass as through the top-k
+    kernel's."""
+    ln = _small_lane(kvm_state, 0x5D50, 300, 64, 10, 12)
+    mand = dev(np.array([7, 250, 31, 123, 250], np.int32))
+    r = _check_small(kvm_state, ln, 2, 3, mandatory=mand)
+    ids = set(r["ids"].tolist())
+    assert {0, 1, 297, 298, 299, 7, 31, 123, 250} <= ids
+
+
+def test_decode_step_lane_without_blocks(kvm_state):
+    """A lane whose history holds no block yet selects nothing, stages nothing
+    and attends over what its window holds, beside a lane that retrieves."""
+    st = kvm_state
+    H1, G1, D1, bt = 1, 8, 128, 64
+    full = _small_lane(st, 0x5D60, 40, bt, 8, 10)
+    empty = _small_lane(st, 0x5D61, 1, bt, 8, 10)
+    lanes = []
+    for ln, nb in ((full, 40), (empty, 0)):
+        ln["out"] = torch.empty((1, H1 * G1, D1), dtype=torch.float32, device="cuda")
+        lanes.append(dict(index=ln["ix"], query=ln["qa"], n_blocks=nb, n_tokens=ln["nt"], budget_blocks=8,
+                          sink_blocks=1, recent_blocks=0, window=ln["a"]["window"], sel=ln["a"]["sel"],
+                          history=ln["a"]["history"], q=ln["q"], q_pos=ln["q_pos"], out=ln["out"]))
+    api.prepare_decode_step_lanes(st, lanes, H1 * G1, D1 ** -0.5, 64, 1e7)()
+    torch.cuda.synchronize()
+    r = empty["a"]["sel"].result()
+    assert r["status"] == 0 and len(r["ids"]) == 0 and len(r["stage_slots"]) == 0
+    # nothing staged: every cell of the empty lane's window is still empty, so
+    # its token sees no cell and gets zeros
+    assert bool((empty["a"]["window"].cell_pos == -1).all())
+    assert bool((empty["out"] == 0).all())
+    b = full["b"]
+    api.score_topk(st, full["ix"], full["qa"], 40, full["nt"], 8, 1, 0, None, b["window"], b["sel"])
+    api.stagein_selection(st, b["history"], b["window"], b["sel"], 64, 1e7)
+    ref = api.fa_decode(st, b["window"], full["q"], full["q_pos"], H1 * G1, D1 ** -0.5)
+    torch.cuda.synchronize()
+    assert np.array_equal(full["a"]["sel"].result()["ids"], b["sel"].result()["ids"])
+    assert torch.equal(full["a"]["window"].k, b["window"].k)
+    check_attention(host(full["out"]), host(ref))
