@@ -27,6 +27,13 @@
 // with this launch's epoch; splits 0 .. NM-1 of a head then wait for the
 // head's flags and each merges whole rows (or row chunks) of the head, so no
 // combine launch follows.
+//
+// Two further forms of the same launch: the staged one first carries out the
+// lanes' stage-in plans (its workgroups meet at in-launch barriers before any
+// reads the window), and the selecting one adds a column of workgroups whose
+// first runs the lane's top-k and layout while the others attend over the
+// window as it is, then stage the plan and attend again only if it changed
+// anything.  With the scoring grid before it, a decode step is two launches.
 #include "kvm_stagein_dev.h"
 #include "kvm_topk_dev.h"
 
