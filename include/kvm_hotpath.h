@@ -485,11 +485,15 @@ int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, co
  * kvmem_store.cpp:357-623),
  * stages the plan (llama-memory-kvmem.cpp:4000-4071, llama-kvmem-stagein.cu:669-790)
  * and then runs the graph's flash attention (ggml-cuda/fattn.cu:457), one
- * after the other.  Steps with more than 4,096 blocks in a lane, a lane
- * without query tokens or a window that is not q8_0 / q4_0 run as three
- * launches (kvm_score_topk, then kvm_stagein_fa_decode) with the same results.
- * In the lanes form ret[i].w must be lanes[i].w's window and hist[i] is lane
- * i's history; every argument is checked before the first launch. */
+ * after the other.  Steps with more than 4,096 blocks in a lane or a lane
+ * without query tokens run as three launches (kvm_score_topk, then
+ * kvm_stagein_fa_decode) with the same results; a window that is not
+ * q8_0 / q4_0 is refused (KVM_EUNSUPPORTED), as kvm_stagein_fa_decode refuses
+ * it.  A step whose plan stages anything pays for the attention's first pass:
+ * where a plan change is expected (the first retrieval after a new query) the
+ * three-launch calls are faster.  In the lanes form ret[i].w must be
+ * lanes[i].w's window and hist[i] is lane i's history; every argument is
+ * checked before the first launch. */
 int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *qa,
                                      const kvm_select_params *p, const kvm_window *w, const kvm_selection *sel,
                                      const kvm_history *h, const kvm_rope_params *rope, const void *q, int q_type,
