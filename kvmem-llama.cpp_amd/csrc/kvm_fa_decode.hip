@@ -167,16 +167,18 @@ __device__ __forceinline__ float fa_load(const float *p) {
 #define KVM_FA_MERGE_BATCH 16
 template <int D, int RMAX>
 __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, uint32_t h, const uint32_t *flags,
-                                         uint32_t epoch, uint32_t j, uint32_t nm, uint32_t dc, int R) {
+                                         uint32_t n_flags, uint32_t epoch, uint32_t j, uint32_t nm, uint32_t dc,
+                                         int R) {
     __shared__ float s_w[KVM_MAX_SPLITS + 1];     // [KVM_MAX_SPLITS] stays 0: splits past the last
     __shared__ float s_red[2][8];
     __shared__ float s_acc[512];
     __shared__ uint32_t s_ok;
     const uint32_t tid = threadIdx.x, S = a.n_splits;
-    // thread t < S waits for split t's flag (device-coherent polling, no cache
+    // thread t < n_flags waits for flag t (the splits', and in a selecting
+    // launch the selector column's at S; device-coherent polling, no cache
     // invalidation); the partials are then read device-coherently as well
     uint32_t ok = 1;
-    if (tid < S) {
+    if (tid < n_flags) {
         uint32_t it = 0;
         while (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
             __builtin_amdgcn_s_sleep(2);
@@ -191,8 +193,8 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
     __syncthreads();
     if (!ok) s_ok = 0;
     __syncthreads();
-    // every split of the head has read the head's epoch (each raised its flag
-    // after reading it): the next launch may take the next one
+    // every workgroup of the head has read the head's epoch (each raised its
+    // flag after reading it): the next launch may take the next one
     if (j == 0 && tid == 0)
         __hip_atomic_store(a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS + h, epoch, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -256,17 +258,18 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
 }
 
 // The lane's stage-in plan, carried out by the attention's own workgroups
-// before any of them reads the window: workgroup x = h * n_splits + split of
-// the lane's G = H * n_splits stages its share of the items (after the gather
-// of the blocks that move within the window, behind the plan's first
-// barrier), then every workgroup waits at a second barrier for the whole plan.
+// before any of them reads the window: workgroup x = h * cols + column of the
+// lane's G = H * cols stages its share of the items (after the gather of the
+// blocks that move within the window, behind the plan's first barrier), then
+// every workgroup waits at a second barrier for the whole plan.
 template <int D>
-__device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent) {
+// In a selecting launch (cols = n_splits + 1) the selector column stages too.
+__device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent, uint32_t cols) {
     extern __shared__ __align__(16) uint8_t s_rows[];     // the staged launch's dynamic LDS
     __shared__ uint32_t s_e;
     if (threadIdx.x == 0) s_e = sync_load(sg.sync);
     __syncthreads();
-    const uint32_t e = s_e, G = a.H * a.n_splits, x = blockIdx.y * a.n_splits + blockIdx.x;
+    const uint32_t e = s_e, G = a.H * cols, x = blockIdx.y * cols + blockIdx.x;
     stage_plan<D, 512, KVM_FA_STAGE_IT>(sg, s_rows, n_ent, x, G, e + 1, false);
     if (!lane_barrier<512>(sg.sync, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
 }
@@ -391,10 +394,25 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
 
     if constexpr (SELECT) {
         if (split == a.n_splits) {           // the lane's selector column
+            // the head's epoch, read before this workgroup raises its flag (the
+            // head's merger waits for it, so the epoch cannot move before)
+            const uint32_t ep_c = __hip_atomic_load(a.sync + KVM_FA_SYNC_EPOCH + blockIdx.z * KVM_FA_MAX_HEADS + h,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (h == 0) {
                 const topk_args t = sel[blockIdx.z];     // one copy out of the argument segment
                 fa_select_lane(a, t);
             }
+            // the column takes part in staging a plan that stages anything, so
+            // that the items spread over every workgroup the CUs hold
+            const uint32_t n = fa_await_plan(a, h, ep_c + 1);
+            if (n) {
+                __threadfence();             // acquire: the selection's stores
+                fa_stage_lane<D>(a, stg[blockIdx.z], n, a.n_splits + 1);
+            }
+            __syncthreads();
+            if (tid == 0)
+                __hip_atomic_store(a.sync + ((uint64_t)blockIdx.z * KVM_FA_MAX_HEADS + h) * KVM_MAX_SPLITS + a.n_splits,
+                                   ep_c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return;
         }
     }
@@ -403,7 +421,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     if (R == 0) {
         if constexpr (STAGE && !SELECT) {
             const uint32_t n_ent = stage_entries(stg[blockIdx.z]);
-            if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
+            if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent, a.n_splits);
         }
         return;
     }
@@ -449,7 +467,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (tid == 0) s_epoch = ep + 1;
     if constexpr (STAGE && !SELECT) {
-        if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent);
+        if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent, a.n_splits);
     }
     // SELECT, after the first pass over the window (both roles, at the same
     // barrier): true when the lane's plan staged anything, so the pass is redone
@@ -461,7 +479,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             const uint32_t n = fa_await_plan(a, h, ep + 1);
             if (!n) return false;
             __threadfence();                 // acquire: the selection's stores
-            fa_stage_lane<D>(a, stg[blockIdx.z], n);
+            fa_stage_lane<D>(a, stg[blockIdx.z], n, a.n_splits + 1);
             return true;
         }
     };
@@ -885,7 +903,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     while (dc < D / 64 && (uint32_t)R * dc * 2 <= S) dc *= 2;
     const uint32_t units = (uint32_t)R * dc, NM = units < S ? units : S;
     if (split >= NM) return;
-    fa_merge<D, RMAX>(a, ln, h, flags, epoch, split, NM, dc, R);
+    fa_merge<D, RMAX>(a, ln, h, flags, SELECT ? S + 1 : S, epoch, split, NM, dc, R);
 }
 
 template <int D, int NRT, bool QUANT, bool PK>
@@ -1201,12 +1219,14 @@ extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_r
         rc = kvm_resident_blocks(st, fn, 512, lds_sel, &occ);
         if (rc) return rc;
         // every workgroup resident at once, the selector column included (and
-        // no lane with more attention workgroups than its barrier words count)
+        // no lane with more workgroups than its barrier words count: the
+        // column stages too)
         const uint64_t cap = (uint64_t)occ * st->n_cu, sel_wgs = (uint64_t)lanes[0].w->n_head_kv * n_lanes;
         fuse = cap > 2 * sel_wgs;
         if (fuse) {
             uint64_t att = cap - sel_wgs;
-            if (att > (uint64_t)KVM_STAGE_MAX_WGS * n_lanes) att = (uint64_t)KVM_STAGE_MAX_WGS * n_lanes;
+            const uint64_t bar = (uint64_t)(KVM_STAGE_MAX_WGS - lanes[0].w->n_head_kv) * n_lanes;
+            if (att > bar) att = bar;
             rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)att);
             if (rc) return rc;
         }
