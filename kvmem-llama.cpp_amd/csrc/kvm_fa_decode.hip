@@ -158,19 +158,21 @@ __device__ __forceinline__ float fa_load(const float *p) {
 // Merge units j, j + nm, ... of (lane blockIdx.z, head h): unit u is row
 // u / dc, dims (u % dc) * D / dc .. + D / dc, over the S split partials:
 // M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s
-// (zeros when no split saw a visible cell).  512 threads: one thread per
-// split loads (m, l); thread t accumulates dim t % UD of the unit (UD = D / dc)
-// over the splits s = t / UD (mod 512 / UD), whose partial outputs it loads in
-// batches of KVM_FA_MERGE_BATCH before using any (the first batch in flight
-// together with (m, l): one memory round trip per unit); the 512 / UD sums are
-// then added in split-phase order.
+// (zeros when no split saw a visible cell).  512 threads: thread t accumulates
+// dim t % UD of the unit (UD = D / dc) over the splits s = t / UD (mod 512 /
+// UD), whose partial outputs it loads in batches of KVM_FA_MERGE_BATCH before
+// using any.  Wave 0 loads (m, l) of splits t, t + 64, ... ahead of its first
+// batch, reduces them within the wave and publishes the weights and
+// 1 / sum_s w_s l_s while the other waves' partial outputs are still in flight
+// (one memory round trip per unit, two barriers after it); the 512 / UD sums
+// are then added in split-phase order.
 #define KVM_FA_MERGE_BATCH 16
 template <int D, int RMAX>
 __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, uint32_t h, const uint32_t *flags,
                                          uint32_t n_flags, uint32_t epoch, uint32_t j, uint32_t nm, uint32_t dc,
                                          int R) {
     __shared__ float s_w[KVM_MAX_SPLITS + 1];     // [KVM_MAX_SPLITS] stays 0: splits past the last
-    __shared__ float s_red[2][8];
+    __shared__ float s_inv;
     __shared__ float s_acc[512];
     __shared__ uint32_t s_ok;
     const uint32_t tid = threadIdx.x, S = a.n_splits;
@@ -189,7 +191,10 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
             }
         }
     }
-    if (tid == 0) s_ok = 1;
+    if (tid == 0) {
+        s_ok = 1;
+        s_w[KVM_MAX_SPLITS] = 0.0f;
+    }
     __syncthreads();
     if (!ok) s_ok = 0;
     __syncthreads();
@@ -204,40 +209,49 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
         const uint32_t dd = tid % UD, sp = tid / UD;
         for (uint32_t u = j; u < (uint32_t)R * dc; u += nm) {
             const uint32_t row = u / dc, d = (u % dc) * UD + dd;
-            // every load unconditional (a conditional load makes the compiler
-            // wait for all loads in flight at the join): splits past S re-read
-            // split S - 1 and get weight 0
+            const float *ml = a.ws_ml + (p0 * RMAX + row) * 2;
+            // every load unconditional within its wave (a conditional load makes
+            // the compiler wait for all loads in flight at the join): splits
+            // past S re-read split S - 1 and get weight 0
             const float *po = a.ws + (p0 * RMAX + row) * D + d;
             auto ld = [&](uint32_t s) { return fa_load(po + (uint64_t)(s < S ? s : S - 1) * RMAX * D); };
+            float m0 = 0.0f, l0 = 0.0f;
+            if (tid < 64) {
+                const uint32_t sc = tid < S ? tid : S - 1;
+                m0 = fa_load(ml + (uint64_t)sc * RMAX * 2);
+                l0 = fa_load(ml + (uint64_t)sc * RMAX * 2 + 1);
+            }
             float v[KVM_FA_MERGE_BATCH];
 #pragma unroll
             for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) v[i] = ld(sp + SP * i);
-            const uint32_t tc = tid < S ? tid : S - 1;
-            float m_t = fa_load(&a.ws_ml[((p0 + tc) * RMAX + row) * 2]);
-            float l_t = fa_load(&a.ws_ml[((p0 + tc) * RMAX + row) * 2 + 1]);
-            m_t = tid < S ? m_t : -INFINITY;
-            l_t = tid < S ? l_t : 0.0f;
-            float M = kvm_wave_max_f32(m_t);
-            if ((tid & 63) == 0) s_red[0][tid >> 6] = M;
+            if (tid < 64) {
+                // the lane's splits tid, tid + 64, ...: running maximum and sum,
+                // the maxima kept in s_w until the weights replace them
+                float m_l = tid < S ? m0 : -INFINITY, l_l = tid < S ? l0 : 0.0f;
+                s_w[tid] = m_l;
+                for (uint32_t s = tid + 64; s < S; s += 64) {
+                    const float ms = fa_load(ml + (uint64_t)s * RMAX * 2), ls = fa_load(ml + (uint64_t)s * RMAX * 2 + 1);
+                    s_w[s] = ms;
+                    const float mn = fmaxf(m_l, ms);
+                    l_l = (m_l == -INFINITY ? 0.0f : l_l * __builtin_amdgcn_exp2f(m_l - mn)) +
+                          (ms == -INFINITY ? 0.0f : ls * __builtin_amdgcn_exp2f(ms - mn));
+                    m_l = mn;
+                }
+                const float M = kvm_wave_max_f32(m_l);
+                const float L = kvm_wave_sum_f32(m_l == -INFINITY ? 0.0f : l_l * __builtin_amdgcn_exp2f(m_l - M));
+                for (uint32_t s = tid; s < S; s += 64) {
+                    const float ms = s_w[s];
+                    s_w[s] = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+                }
+                if (tid == 0) s_inv = M == -INFINITY || !(L > 0.0f) ? 0.0f : 1.0f / L;
+            }
             __syncthreads();
-            M = s_red[0][0];
-#pragma unroll
-            for (int i = 1; i < 8; ++i) M = fmaxf(M, s_red[0][i]);
-            const float wt = m_t == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_t - M);
-            s_w[tid] = wt;                       // 0 for tid >= S
-            if (tid == 0) s_w[KVM_MAX_SPLITS] = 0.0f;
-            float L = kvm_wave_sum_f32(l_t * wt);
-            if ((tid & 63) == 0) s_red[1][tid >> 6] = L;
-            __syncthreads();
-            L = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) L += s_red[1][i];
             float acc = 0.0f;
             for (uint32_t s0 = sp;; ) {
 #pragma unroll
                 for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) {
                     const uint32_t si = s0 + SP * i;
-                    acc += s_w[si < KVM_MAX_SPLITS ? si : KVM_MAX_SPLITS] * v[i];
+                    acc += s_w[si < S ? si : KVM_MAX_SPLITS] * v[i];
                 }
                 s0 += SP * KVM_FA_MERGE_BATCH;
                 if (s0 >= S) break;
@@ -250,9 +264,9 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
                 float o = acc;
                 for (uint32_t i = 1; i < SP; ++i) o += s_acc[i * UD + dd];
                 const uint32_t t = row / a.G, qh = h * a.G + row % a.G;
-                ln.out[((uint64_t)t * a.n_head + qh) * D + d] = M == -INFINITY || !(L > 0.0f) ? 0.0f : o / L;
+                ln.out[((uint64_t)t * a.n_head + qh) * D + d] = o * s_inv;
             }
-            __syncthreads();
+            if (u + nm < (uint32_t)R * dc) __syncthreads();   // s_w and s_acc are reused by the next unit
         }
     }
 }
