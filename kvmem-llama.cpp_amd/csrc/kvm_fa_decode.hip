@@ -154,27 +154,33 @@ __device__ __forceinline__ float fa_load(const float *p) {
 // waiting on anything, so the wait ends unless workgroups cannot be scheduled;
 // past the limit the status word says so and the rows are left unmerged.
 #define KVM_FA_MERGE_SPIN (1u << 21)
+#define KVM_FA_POLL_WORDS 2048
 
 // Merge units j, j + nm, ... of (lane blockIdx.z, head h): unit u is row
 // u / dc, dims (u % dc) * D / dc .. + D / dc, over the S split partials:
 // M = max_s m_s, w_s = exp2(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s
 // (zeros when no split saw a visible cell).  512 threads: thread t accumulates
 // dim t % UD of the unit (UD = D / dc) over the splits s = t / UD (mod 512 /
-// UD), whose partial outputs it loads in batches of KVM_FA_MERGE_BATCH before
-// using any.  Wave 0 loads (m, l) of splits t, t + 64, ... ahead of its first
+// UD), whose partial outputs it loads in batches of NBAT before using any
+// (NBAT: the smallest of 4, 8, 16, 32 that covers the thread's splits, so one
+// batch, one memory round trip, serves the usual shapes).  Wave 0 loads (m, l) of splits t, t + 64, ... ahead of its first
 // batch, reduces them within the wave and publishes the weights and
 // 1 / sum_s w_s l_s while the other waves' partial outputs are still in flight
 // (one memory round trip per unit, two barriers after it); the 512 / UD sums
 // are then added in split-phase order.
-#define KVM_FA_MERGE_BATCH 16
-template <int D, int RMAX>
+struct fa_merge_lds {
+    float w[KVM_MAX_SPLITS + 1];          // weights; [KVM_MAX_SPLITS] stays 0: splits past the last
+    float acc[512];
+    float inv;
+    uint32_t ok;
+};
+template <int D, int RMAX, int NBAT>
 __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, uint32_t h, const uint32_t *flags,
                                          uint32_t n_flags, uint32_t epoch, uint32_t j, uint32_t nm, uint32_t dc,
-                                         int R) {
-    __shared__ float s_w[KVM_MAX_SPLITS + 1];     // [KVM_MAX_SPLITS] stays 0: splits past the last
-    __shared__ float s_inv;
-    __shared__ float s_acc[512];
-    __shared__ uint32_t s_ok;
+                                         int R, fa_merge_lds &L_) {
+    float *const s_w = L_.w, *const s_acc = L_.acc;
+    float &s_inv = L_.inv;
+    uint32_t &s_ok = L_.ok;
     const uint32_t tid = threadIdx.x, S = a.n_splits;
     // thread t < n_flags waits for flag t (the splits', and in a selecting
     // launch the selector column's at S; device-coherent polling, no cache
@@ -221,9 +227,9 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
                 m0 = fa_load(ml + (uint64_t)sc * RMAX * 2);
                 l0 = fa_load(ml + (uint64_t)sc * RMAX * 2 + 1);
             }
-            float v[KVM_FA_MERGE_BATCH];
+            float v[NBAT];
 #pragma unroll
-            for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) v[i] = ld(sp + SP * i);
+            for (int i = 0; i < NBAT; ++i) v[i] = ld(sp + SP * i);
             if (tid < 64) {
                 // the lane's splits tid, tid + 64, ...: running maximum and sum,
                 // the maxima kept in s_w until the weights replace them
@@ -249,14 +255,14 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
             float acc = 0.0f;
             for (uint32_t s0 = sp;; ) {
 #pragma unroll
-                for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) {
+                for (int i = 0; i < NBAT; ++i) {
                     const uint32_t si = s0 + SP * i;
                     acc += s_w[si < S ? si : KVM_MAX_SPLITS] * v[i];
                 }
-                s0 += SP * KVM_FA_MERGE_BATCH;
+                s0 += SP * NBAT;
                 if (s0 >= S) break;
 #pragma unroll
-                for (int i = 0; i < KVM_FA_MERGE_BATCH; ++i) v[i] = ld(s0 + SP * i);
+                for (int i = 0; i < NBAT; ++i) v[i] = ld(s0 + SP * i);
             }
             s_acc[tid] = acc;
             __syncthreads();
@@ -910,14 +916,23 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     uint32_t *flags = a.sync + ((uint64_t)blockIdx.z * KVM_FA_MAX_HEADS + h) * KVM_MAX_SPLITS;
     const uint32_t epoch = s_epoch;
     if (tid == 0) __hip_atomic_store(flags + split, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // merge units: rows split into dc dim chunks (at least 64 dims) so that
-    // about every split of the head merges one unit
+    // merge units: rows split into dc dim chunks (at least 64 dims) while at
+    // most about half the splits merge and the head's mergers, each polling
+    // every flag of the head, poll at most KVM_FA_POLL_WORDS flag words per
+    // round (the head's flags share a few cache lines, and more pollers only
+    // queue behind each other there)
     const uint32_t S = a.n_splits;
     uint32_t dc = 1;
-    while (dc < D / 64 && (uint32_t)R * dc * 2 <= S) dc *= 2;
+    while (dc < D / 64 && (uint32_t)R * dc * 2 <= S && (uint32_t)R * dc * 2 * S <= KVM_FA_POLL_WORDS) dc *= 2;
     const uint32_t units = (uint32_t)R * dc, NM = units < S ? units : S;
     if (split >= NM) return;
-    fa_merge<D, RMAX>(a, ln, h, flags, SELECT ? S + 1 : S, epoch, split, NM, dc, R);
+    __shared__ fa_merge_lds s_mg;
+    const uint32_t per = (S + 512 * dc / D - 1) / (512 * dc / D);     // splits per merging thread
+    const uint32_t nf = SELECT ? S + 1 : S;
+    if (per > 16) fa_merge<D, RMAX, 32>(a, ln, h, flags, nf, epoch, split, NM, dc, R, s_mg);
+    else if (per > 8) fa_merge<D, RMAX, 16>(a, ln, h, flags, nf, epoch, split, NM, dc, R, s_mg);
+    else if (per > 4) fa_merge<D, RMAX, 8>(a, ln, h, flags, nf, epoch, split, NM, dc, R, s_mg);
+    else fa_merge<D, RMAX, 4>(a, ln, h, flags, nf, epoch, split, NM, dc, R, s_mg);
 }
 
 template <int D, int NRT, bool QUANT, bool PK>
