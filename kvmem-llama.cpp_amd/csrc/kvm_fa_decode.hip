@@ -639,6 +639,15 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
                 m_run[rt] = KVM_M_NONE;
                 l_run[rt] = 0.0f;
             }
+            // the smallest limit of a real row: keys below it are visible to
+            // every row, and a tile whose keys all are needs no masking (the
+            // padding rows then score unmasked keys, which only their own,
+            // never stored, outputs see)
+            uint32_t qmin = 0xffffffffu;
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt)
+                if (srow(rt) < R) qmin = qlim[rt] < qmin ? qlim[rt] : qmin;
+            qmin = kvm_wave_min_u32(qmin);
             int par = 0;                         // tile parity: P and flag buffers
 
             auto score = [&](const KRegs &rg, KRegs &nx, uint32_t inext) {
@@ -705,25 +714,34 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
                 // which every finite score moves.
                 bool up_w = false;
                 float psum[NRT];
-                auto make_p = [&](int rt, float mn) {
-                    _Float16 ph[4];
-                    psum[rt] = 0.0f;
+                uint32_t cmax = rg.cp[0] > rg.cp[1] ? rg.cp[0] : rg.cp[1];
+                cmax = cmax > rg.cp[2] ? cmax : rg.cp[2];
+                cmax = cmax > rg.cp[3] ? cmax : rg.cp[3];
+                if (__builtin_amdgcn_ballot_w64(!(cmax < qmin)) != 0) {
+                    asm volatile("" ::: "memory");      // keep the masking a branch: most tiles skip it
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const _Float16 p16 = (_Float16)__builtin_amdgcn_exp2f(s[rt][i] - mn);
-                        ph[i] = p16;
-                        psum[rt] += (float)p16;
-                    }
+                    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (!(rg.cp[i] < qlim[rt])) s[rt][i] = -INFINITY;    // empty (-1) or after the row
+                }
+                // (the sum of a lane's four fp16 probabilities in fp32 by two
+                // v_dot2_f32_f16 against ones, from the pairs packed for LDS)
+                auto make_p = [&](int rt, float mn) {
+                    const kvm_f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
+                    kvm_f16x2 ph[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        ph[i] = kvm_f16x2{(_Float16)__builtin_amdgcn_exp2f(s[rt][2 * i] - mn),
+                                          (_Float16)__builtin_amdgcn_exp2f(s[rt][2 * i + 1] - mn)};
+                    psum[rt] = __builtin_amdgcn_fdot2(ph[1], one2, __builtin_amdgcn_fdot2(ph[0], one2, 0.0f, false), false);
                     __builtin_memcpy(&s_p[par][16 * rt + m][16 * kq + 4 * g], ph, 8);
                 };
 #pragma unroll
                 for (int rt = 0; rt < NRT; ++rt) {
                     float mx = -INFINITY;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (!(rg.cp[i] < qlim[rt])) s[rt][i] = -INFINITY;    // empty (-1) or after the row
-                        mx = fmaxf(mx, s[rt][i]);
-                    }
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[rt][i]);
                     s_max[kq][g][16 * rt + m] = mx;
                     up_w = up_w || mx > m_run[rt] + KVM_LAZY_MAX;
                     make_p(rt, m_run[rt]);

@@ -229,6 +229,18 @@ KVM_WAVE_REDUCE_F32(kvm_wave_max_f32, fmaxf, -INFINITY)
 KVM_WAVE_REDUCE_F32(kvm_wave_min_f32, fminf, INFINITY)
 KVM_WAVE_REDUCE_F32(kvm_wave_sum_f32, kvm_add_f32, 0.0f)
 #undef KVM_WAVE_REDUCE_F32
+// Unsigned minimum over the wave, the same way.
+__device__ inline uint32_t kvm_wave_min_u32(uint32_t x) {
+    const int id = -1;                    // 0xffffffff, the identity
+    auto mn = [](uint32_t a, int b) { return a < (uint32_t)b ? a : (uint32_t)b; };
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x111, 0xf, 0xf, false));
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x112, 0xf, 0xf, false));
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x114, 0xf, 0xf, false));
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x118, 0xf, 0xf, false));
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x142, 0xa, 0xf, false));
+    x = mn(x, __builtin_amdgcn_update_dpp(id, (int)x, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
 // Max / sum with lane l ^ 16 or l ^ 32 without LDS: v_permlane16_swap /
 // v_permlane32_swap with both operands x hand each lane the pair {x[l],
 // x[l ^ 16 or 32]} (order unspecified; max and + do not care).
