@@ -907,6 +907,11 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             if (restaged(pass)) continue;
 
             __syncthreads();                          // pairs with the scoring waves' (m, l) exchange
+            // a padding row (row >= R, so R < RMAX) is stored into row RMAX - 1,
+            // itself padding and never read by the merge: the stores need no
+            // guard (a guard puts each store behind a branch of its own in a
+            // half-used row tile) and the padding lanes of a store share one
+            // segment instead of writing their own
             float *po = a.ws + pidx * RMAX * D;
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt)
@@ -915,9 +920,8 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int row = 16 * rt + 4 * g + r;
-                        if (row < R)
-                            fa_store(&po[row * D + DW * dq + 16 * nt + m],
-                                     QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r]);
+                        fa_store(&po[(row < R ? row : RMAX - 1) * D + DW * dq + 16 * nt + m],
+                                 QUANT ? (O[rt][nt][r] - Oc[rt][nt / NTB][r]) * 0x1p24f : O[rt][nt][r]);
                     }
             break;
         }
