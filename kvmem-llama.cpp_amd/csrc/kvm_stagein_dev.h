@@ -89,15 +89,17 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
                         x[r][i + h] = kvm_fsub(a, bb);
                     }
                 }
+        // across lanes: x + o in the lane whose bit lx is clear, o - x in its
+        // partner, both as fma(x, +-1, o): the same single IEEE rounding
         for (int h = DPL; h < rc.nrot; h <<= 1) {
             const int lx = h / DPL;
-            const bool first = (L & lx) == 0;
+            const float sg = (L & lx) == 0 ? 1.0f : -1.0f;
 #pragma unroll
             for (int r = 0; r < NR; ++r)
 #pragma unroll
                 for (int i = 0; i < DPL; ++i) {
                     const float o = __shfl_xor(x[r][i], lx, 64);
-                    x[r][i] = first ? kvm_fadd(x[r][i], o) : kvm_fsub(o, x[r][i]);
+                    x[r][i] = __builtin_fmaf(x[r][i], sg, o);
                 }
         }
     }
