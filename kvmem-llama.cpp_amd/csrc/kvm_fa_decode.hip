@@ -532,12 +532,12 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
 #pragma unroll
                 for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qx[j]));
                 amax = kvm_max_xor32(kvm_max_xor16(amax));
-                const float d = kvm_fdiv(amax, 127.0f);
-                const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+                const float d = kvm_div127(amax);
+                const float id = kvm_recip_or0(d);
                 uint32_t q01[2] = {0u, 0u};
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    q01[j >> 2] |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(qx[j], id)) << (8 * (j & 3));
+                    q01[j >> 2] |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(qx[j], id)) << (8 * (j & 3));
                 *(kvm_u32x2 *)&s_qq[r][32 * b + 8 * g] = kvm_u32x2{q01[0], q01[1]};
                 if (g == 0) s_dq[r][b] = kvm_h2f(kvm_f2h(d));
             } else {

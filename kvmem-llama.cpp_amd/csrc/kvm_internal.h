@@ -300,16 +300,49 @@ __device__ __forceinline__ float kvm_fdiv(float a, float b) {
 }
 __device__ __forceinline__ float kvm_fsqrt(float a) { return sqrtf(a); }
 
+// a / 127 rounded as the IEEE quotient, without the division sequence: q =
+// a * RN(1/127) is within an ulp, the residual a - 127 q is exact in one fma,
+// and q + residual * RN(1/127) in a second fma rounds to the quotient.  Equal
+// to IEEE a / 127.0f for every finite float a but -0, which gives +0 (an amax
+// is never -0); checked exhaustively.
+__device__ __forceinline__ float kvm_div127(float a) {
+    constexpr float C = 1.0f / 127.0f;
+    const float q = kvm_fmul(a, C);
+    return __builtin_fmaf(__builtin_fmaf(-q, 127.0f, a), C, q);
+}
+// d != 0 ? 1 / d : 0 with IEEE rounding.  For 2^-126 <= |d| < 2^126 one
+// Newton step from v_rcp_f32 (y + y (1 - |d| y), both fma) equals the IEEE
+// quotient: checked on gfx950 against the division for every float in that
+// range.  Subnormal and huge |d| take the division itself.
+__device__ __forceinline__ float kvm_recip_or0(float d) {
+    const float a = fabsf(d);
+    if (__builtin_expect(a >= 0x1p-126f && a < 0x1p126f, 1)) {
+        const float y = __builtin_amdgcn_rcpf(a);
+        return copysignf(__builtin_fmaf(__builtin_fmaf(-a, y, 1.0f), y, y), d);
+    }
+    return d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+}
+// (int)roundf(y) (halves away from zero) for |y| < 2^23: |y| + 0.5 is exact
+// there, and truncating it rounds |y|, except for the largest float below one
+// half, whose sum rounds up to 1.0.  Equal to roundf for every such y (checked
+// exhaustively).
+__device__ __forceinline__ int kvm_round_away(float y) {
+    const float a = fabsf(y);
+    const float t = a == 0x1.fffffep-2f ? 0.0f : kvm_fadd(a, 0.5f);
+    return (int)copysignf(t, y);
+}
+
 // q8_0 / q4_0 block quantisers with the reference kernels' exact arithmetic
 // (llama-kvmem-stagein.cu:181-234): fp32 amax, d = amax/127 (q8) or vmax/-8
 // (q4), id = d ? 1/d : 0, fp16 d with RNE, roundf (ties away) / (int)(x*id+8.5).
-// Division and reciprocal are correctly rounded (kvm_fdiv) to match host IEEE.
+// Division and reciprocal round as host IEEE division does (kvm_div127,
+// kvm_recip_or0; vmax * -0.125 is vmax / -8 exactly).
 __device__ __forceinline__ void kvm_quant_block_q8_0(const float (&x)[32], uint16_t *d_out, int8_t *q) {
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
-    const float d = kvm_fdiv(amax, 127.0f);
-    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+    const float d = kvm_div127(amax);
+    const float id = kvm_recip_or0(d);
     *d_out = kvm_f2h(d);
     uint32_t packed[8];
 #pragma unroll
@@ -317,7 +350,7 @@ __device__ __forceinline__ void kvm_quant_block_q8_0(const float (&x)[32], uint1
         uint32_t wv = 0;
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            wv |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(x[4 * j + k], id)) << (8 * k);
+            wv |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[4 * j + k], id)) << (8 * k);
         packed[j] = wv;
     }
     __builtin_memcpy(q, packed, 32);
@@ -329,8 +362,8 @@ __device__ __forceinline__ void kvm_quant_block_q4_0(const float (&x)[32], uint1
         const float a = fabsf(x[j]);
         if (amax < a) { amax = a; vmax = x[j]; }
     }
-    const float d = kvm_fdiv(vmax, -8.0f);
-    const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+    const float d = kvm_fmul(vmax, -0.125f);
+    const float id = kvm_recip_or0(d);
     *d_out = kvm_f2h(d);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {

@@ -45,29 +45,36 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
     if (nh > 0) {
         const int pl = nh / DPL;                       // lane distance of the partner
         const bool lo = d0 < nh, hi = d0 >= nh && d0 < 2 * nh;
+        // each lane reads its partner only: lane + pl below n_half, lane - pl
+        // above (lanes past 2 n_half read a value they do not use)
+        const int pa = ((lo ? L + pl : L - pl) & 63) << 2;
         float y[NR][DPL];
 #pragma unroll
         for (int r = 0; r < NR; ++r)
 #pragma unroll
+            for (int i = 0; i < DPL; ++i)
+                y[r][i] = __int_as_float(__builtin_amdgcn_ds_bpermute(pa, __float_as_int(x[r][i])));
+        // x0' = x0 c - x1 s below n_half, x1' = x0 s + x1 c above, both as
+        // RN(RN(x c) + RN(y s')) with s' = -s below (the same roundings, no
+        // branch); lanes past 2 n_half read row entry 0 and keep x
+        const bool act = lo || hi;
+        const int ci = lo ? d0 : hi ? d0 - nh : 0;
+        const uint32_t sm = lo ? 0x80000000u : 0u;
+        // every table entry loaded before the first product (source order is
+        // what the compiler keeps where registers are scarce)
+        float2 t[NR][DPL];
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) t[r][i] = cs_pos[r][ci + (act ? i : 0)];
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
             for (int i = 0; i < DPL; ++i) {
-                const float up = __shfl(x[r][i], (L + pl) & 63, 64);
-                const float dn = __shfl(x[r][i], (L - pl) & 63, 64);
-                y[r][i] = lo ? up : dn;
+                const float v = kvm_fadd(kvm_fmul(x[r][i], t[r][i].x),
+                                         kvm_fmul(y[r][i], __uint_as_float(__float_as_uint(t[r][i].y) ^ sm)));
+                x[r][i] = act ? v : x[r][i];
             }
-        if (lo || hi) {
-#pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                const float2 *cs = cs_pos[r] + (lo ? d0 : d0 - nh);
-#pragma unroll
-                for (int i = 0; i < DPL; ++i) {
-                    const float2 t = cs[i];
-                    if (lo)   // x0' = x0 c - x1 s
-                        x[r][i] = kvm_fsub(kvm_fmul(x[r][i], t.x), kvm_fmul(y[r][i], t.y));
-                    else      // x1' = x0 s + x1 c
-                        x[r][i] = kvm_fadd(kvm_fmul(y[r][i], t.y), kvm_fmul(x[r][i], t.x));
-                }
-            }
-        }
     }
 
     // normalised Walsh-Hadamard over nrot-wide chunks: pre-scale, then
@@ -89,22 +96,35 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
                         x[r][i + h] = kvm_fsub(a, bb);
                     }
                 }
-        // across lanes: x + o in the lane whose bit lx is clear, o - x in its
-        // partner, both as fma(x, +-1, o): the same single IEEE rounding
+        // across lanes, with the partner's value o: a lane whose bit lx is
+        // clear needs x + o, its partner o - x.  Both compute fma(o, +-1, x),
+        // the same single rounding, the partner getting -(o - x): its register
+        // holds the value negated from then on.  A lane's sign is the parity of
+        // its bits below lx; that holds for its partner too, so every stage
+        // reads like the first, and x is the fma's addend, updated in place.
         for (int h = DPL; h < rc.nrot; h <<= 1) {
             const int lx = h / DPL;
+            const int pa = (L ^ lx) << 2;
             const float sg = (L & lx) == 0 ? 1.0f : -1.0f;
+            // all of the stage's shuffles in flight before its first fma
+            float o[NR][DPL];
 #pragma unroll
             for (int r = 0; r < NR; ++r)
 #pragma unroll
-                for (int i = 0; i < DPL; ++i) {
-                    const float o = __shfl_xor(x[r][i], lx, 64);
-                    x[r][i] = __builtin_fmaf(x[r][i], sg, o);
-                }
+                for (int i = 0; i < DPL; ++i)
+                    o[r][i] = __int_as_float(__builtin_amdgcn_ds_bpermute(pa, __float_as_int(x[r][i])));
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+#pragma unroll
+                for (int i = 0; i < DPL; ++i) x[r][i] = __builtin_fmaf(o[r][i], sg, x[r][i]);
         }
     }
+    // the sign the lane's registers carry (bit 31), undone by the requantiser's
+    // 1/d (|x| is unaffected, and x * -id is -x * id exactly)
+    const uint32_t xs = rc.nrot > DPL && (__popc((uint32_t)L & (uint32_t)(rc.nrot / DPL - 1)) & 1) ? 0x80000000u : 0u;
 
     // q8_0 requantisation of each 32-dim block (32/DPL lanes per block)
+    const uint32_t lq = kvm_kq_off(D, 0, d0);
     float amax[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -118,19 +138,21 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
         for (int r = 0; r < NR; ++r) amax[r] = fmaxf(amax[r], __shfl_xor(amax[r], o, 64));
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const float d = kvm_fdiv(amax[r], 127.0f);
-        const float id = d != 0.0f ? kvm_fdiv(1.0f, d) : 0.0f;
+        const float d = kvm_div127(amax[r]);
+        const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ xs);
         // the lane's DPL quants are consecutive in the tile (8-byte runs of one
         // block and lane group): one store of DPL bytes, aligned to DPL
         uint32_t qw = 0;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) qw |= (uint32_t)(uint8_t)(int8_t)roundf(kvm_fmul(x[r][i], id)) << (8 * i);
+        for (int i = 0; i < DPL; ++i) qw |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[r][i], id)) << (8 * i);
         if (!live[r]) continue;
-        uint8_t *qd = kt[r] + kvm_kq_off(D, c[r], d0);
+        // tile offsets split into the row's cell part and the lane's dim part
+        uint8_t *row = kt[r] + kvm_kq_off(D, c[r], 0);
+        uint8_t *qd = row + lq;
         if constexpr (DPL == 4) *(uint32_t *)qd = qw;
         else if constexpr (DPL == 2) *(uint16_t *)qd = (uint16_t)qw;
         else *qd = (uint8_t)qw;
-        if (e == 0) *(uint16_t *)(kt[r] + kvm_kd_off(D, c[r], b)) = kvm_f2h(d);
+        if (e == 0) *(uint16_t *)(kt[r] + kvm_kd_off(D, c[r], 0) + 32u * b) = kvm_f2h(d);
     }
 }
 
@@ -311,7 +333,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
 
     const uint32_t tile = (slot * a.bt + t0) / 64, c0 = t0 % 64;   // c0: the item's first cell in the tile
     // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time
-    const uint32_t wave = tid >> 6, nrow = count * a.H;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), nrow = count * a.H;
     constexpr uint32_t W = NTH / 64, NR = 4;
     for (uint32_t r0 = wave; r0 < nrow; r0 += NR * W) {
         const uint8_t *src[NR];
