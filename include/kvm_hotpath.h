@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 3
+#define KVM_ABI_VERSION 4
 
 enum kvm_status {
     KVM_OK = 0,
@@ -34,7 +34,17 @@ enum kvm_status {
     KVM_EHIP = -2,         /* HIP runtime error */
     KVM_ENOMEM = -3,       /* allocation failed */
     KVM_ERANGE = -4,       /* size beyond a documented maximum */
-    KVM_EUNSUPPORTED = -5  /* type combination not implemented */
+    KVM_EUNSUPPORTED = -5, /* type combination not implemented */
+    KVM_ETIMEOUT = -6      /* an in-launch wait gave up (kvm_state_sync, kvm_state_status) */
+};
+
+/* Waits inside a launch that gave up, as kvm_state_status reports them. */
+enum kvm_wait_status {
+    KVM_WAIT_MERGE = 1,    /* the attention's split merge: some output rows were not written */
+    KVM_WAIT_PLAN = 2,     /* a selecting launch's plan: the attention used the window as it was
+                            * and the plan was not staged (the slot map is unchanged) */
+    KVM_WAIT_STAGE = 4     /* a stage-in barrier: the plan's items were emptied (selection
+                            * info[3] bit 16), so the next plan restages them */
 };
 
 /* ggml type ids (ggml.h enum ggml_type) for the types this path handles. */
@@ -66,8 +76,25 @@ void kvm_state_free(kvm_state *st);
  * stream.  Replaces the per-execution stream (llama-kvmem-stagein.cu:334-343). */
 int kvm_state_set_stream(kvm_state *st, void *hip_stream);
 void *kvm_state_stream(kvm_state *st);
-/* Replaces kvmem_stagein_sync (src/adapter/llama-kvmem-stagein.h:31). */
+/* Replaces kvmem_stagein_sync (src/adapter/llama-kvmem-stagein.h:31): waits
+ * for the state's stream.  Returns KVM_ETIMEOUT when a wait inside one of the
+ * state's launches gave up since the last kvm_state_sync / kvm_state_status
+ * (the reference's stage-in returns false there and the caller falls back,
+ * llama-kvmem-stagein.cu:93-99, llama-memory-kvmem.cpp:4032-4038); the message
+ * names the waits.  Reporting clears the status and resets the state's
+ * in-launch sync words, so the next launch starts clean: after KVM_ETIMEOUT
+ * the results of the launches since the previous sync are not to be used. */
 int kvm_state_sync(kvm_state *st);
+/* kvm_state_sync that hands back the KVM_WAIT_* bits of the waits that gave up
+ * (0 = none) in *status and returns KVM_OK for them. */
+int kvm_state_status(kvm_state *st, uint32_t *status);
+/* Polls of an in-launch wait (split merge, plan, stage-in barrier) before it
+ * gives up; the default (about 0.1-0.2 s of waiting) is restored by
+ * KVM_WAIT_POLLS_DEFAULT.  0 makes every such wait give up at once, without a
+ * look at its flag: a host-side way to drive the failure paths, under which
+ * every kernel still runs to its end.  No counterpart in the reference. */
+#define KVM_WAIT_POLLS_DEFAULT (1u << 21)
+int kvm_state_set_wait_polls(kvm_state *st, uint32_t polls);
 const char *kvm_state_last_error(const kvm_state *st);
 int kvm_abi_version(void);
 /* Pinned, device-mapped host memory for histories and staging buffers

@@ -42,7 +42,6 @@
 #include <atomic>
 #include <mutex>
 
-#define KVM_MAX_LANES 8
 #define KVM_FA_STAGE_IT 32        // tokens per stage-in item of a staged launch
 
 struct fa_lane {
@@ -61,23 +60,17 @@ struct fa_args {
     float *ws;              // partial O  [lane][H][split][RMAX][D]
     float *ws_ml;           // partial m,l [lane][H][split][RMAX][2]
     uint32_t *sync;         // [lane][64][512] by (lane, head, split): the epoch of the last launch that completed
-                            // the split's partials; sync[KVM_FA_SYNC_STATUS]: bit 0 = a
-                            // merge wait timed out, bit 1 = a wait for the plan timed out;
+                            // the split's partials; sync[KVM_FA_SYNC_STATUS]: KVM_WAIT_MERGE =
+                            // a merge wait gave up, KVM_WAIT_PLAN = a wait for the plan gave up;
                             // sync[KVM_FA_SYNC_EPOCH + lane * 64 + h]: the (lane, head)'s
                             // epoch, one less than its next launch's; 64-bit words from
                             // KVM_FA_SYNC_PLAN, [lane * 64 + h]: the plan a selecting launch
                             // published to the head (epoch, entries to stage)
     uint32_t H, G, n_head, n_splits;
+    uint32_t spin;          // polls of a wait before it gives up (0: at once, without a look)
     float scale_log2;       // kq_scale * log2(e)
     int q_bf16;
 };
-#define KVM_FA_MAX_HEADS 64
-#define KVM_MAX_SPLITS 512
-#define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)
-#define KVM_FA_SYNC_EPOCH (KVM_FA_SYNC_STATUS + 64)
-#define KVM_FA_SYNC_PLAN (KVM_FA_SYNC_EPOCH + KVM_MAX_LANES * KVM_FA_MAX_HEADS)
-#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_PLAN + 2 * KVM_MAX_LANES * KVM_FA_MAX_HEADS)
-static_assert(KVM_FA_SYNC_PLAN % 2 == 0, "64-bit plan words");
 
 __device__ inline float load_q(const void *q, uint64_t i, int bf16) {
     return bf16 ? kvm_bf2f(((const uint16_t *)q)[i]) : ((const float *)q)[i];
@@ -148,12 +141,11 @@ __device__ __forceinline__ void fa_store(float *p, float v) {
 __device__ __forceinline__ float fa_load(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-// Longest wait of a merging workgroup for the other splits' flags (s_sleep
-// rounds of ~128 cycles each, about 0.2 s): every split raises its flag without
-// waiting on anything, so the wait ends unless workgroups cannot be scheduled;
-// past the limit the status word says so and the rows are left unmerged.
-#define KVM_FA_MERGE_SPIN (1u << 21)
+// A merging workgroup waits for the other splits' flags for at most a.spin
+// polls (s_sleep rounds of ~128 cycles each; about 0.2 s by default): every
+// split raises its flag without waiting on anything, so the wait ends unless
+// workgroups cannot be scheduled; past the limit the status word says so
+// (KVM_WAIT_MERGE) and the rows are left unmerged.
 #define KVM_FA_POLL_WORDS 2048
 
 // Merge units j, j + nm, ... of (lane blockIdx.z, head h): unit u is row
@@ -187,14 +179,15 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
     // invalidation); the partials are then read device-coherently as well
     uint32_t ok = 1;
     if (tid < n_flags) {
-        uint32_t it = 0;
-        while (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
-            __builtin_amdgcn_s_sleep(2);
-            if (++it > KVM_FA_MERGE_SPIN) {
-                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (uint32_t it = 0;; ++it) {
+            if (it >= a.spin) {
+                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, (uint32_t)KVM_WAIT_MERGE, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
                 ok = 0;
                 break;
             }
+            if (__hip_atomic_load(flags + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch) break;
+            __builtin_amdgcn_s_sleep(2);
         }
     }
     if (tid == 0) {
@@ -291,7 +284,7 @@ __device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args
     __syncthreads();
     const uint32_t e = s_e, G = a.H * cols, x = blockIdx.y * cols + blockIdx.x;
     stage_plan<D, 512, KVM_FA_STAGE_IT>(sg, s_rows, n_ent, x, G, e + 1, false);
-    if (!lane_barrier<512>(sg.sync, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
+    if (!lane_barrier<512>(sg.sync, sg.status, sg.spin, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
 }
 
 // A selecting launch: workgroup (n_splits, 0) of each lane runs the lane's
@@ -300,20 +293,13 @@ __device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args
 #define KVM_SEL_MAXB 4096
 typedef topk_lds<512, KVM_SEL_MAXB, 1024> sel_lds;
 
-// Longest wait of an attention workgroup for its lane's plan (s_sleep rounds
-// of ~128 cycles, about 0.2 s): the selector is resident with it (the grid
-// never exceeds what the CUs hold at once) and waits on nothing; past the
-// limit the status word says so (bit 1) and the workgroup keeps its pass
-// over the window as it was.
-#define KVM_FA_PLAN_SPIN (1u << 21)
-
 // The selector publishes the plan to each of the lane's heads: one 64-bit
 // word per (lane, head) = the head's epoch of this launch | the entries to
 // stage << 32, after the selection's stores are written back (release).  It
 // reads the epochs before the selection, and no split of a head raises its
 // flag before it has seen the head's word, so the head's merger cannot have
 // advanced the epoch yet.
-__device__ void fa_select_lane(const fa_args &a, const topk_args &t) {
+__device__ __forceinline__ void fa_select_lane(const fa_args &a, const topk_args &t) {
     extern __shared__ __align__(16) uint8_t s_rows[];     // the launch's dynamic LDS
     __shared__ uint32_t s_ep[KVM_FA_MAX_HEADS];
     const uint32_t tid = threadIdx.x;
@@ -335,20 +321,25 @@ __device__ void fa_select_lane(const fa_args &a, const topk_args &t) {
 
 // An attention workgroup's wait for its lane's plan (thread 0 polls the
 // head's word for this launch's epoch): the entries to stage, 0 when the plan
-// is empty or the wait timed out.
-__device__ uint32_t fa_await_plan(const fa_args &a, uint32_t h, uint32_t epoch) {
+// is empty or the wait gave up.  At most a.spin polls (s_sleep rounds of ~128
+// cycles, about 0.2 s by default): the selector is resident with it (the grid
+// never exceeds what the CUs hold at once) and waits on nothing; past the
+// limit the status word says so (KVM_WAIT_PLAN) and the workgroup keeps its
+// pass over the window as it was.
+__device__ __forceinline__ uint32_t fa_await_plan(const fa_args &a, uint32_t h, uint32_t epoch) {
     __shared__ uint32_t s_n;
     if (threadIdx.x == 0) {
         const uint64_t *pw = (const uint64_t *)(a.sync + KVM_FA_SYNC_PLAN) + blockIdx.z * KVM_FA_MAX_HEADS + h;
         uint32_t n = 0;
         for (uint32_t it = 0;; ++it) {
+            if (it >= a.spin) {
+                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, (uint32_t)KVM_WAIT_PLAN, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             const uint64_t v = __hip_atomic_load(pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if ((uint32_t)v == epoch) {
                 n = (uint32_t)(v >> 32);
-                break;
-            }
-            if (it > KVM_FA_PLAN_SPIN) {
-                __hip_atomic_fetch_or(a.sync + KVM_FA_SYNC_STATUS, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
@@ -1031,7 +1022,8 @@ struct fa_plan {
     bool quant;
 };
 static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, int q_type, uint32_t n_head,
-                      float scale, void *scratch, size_t scratch_cap, fa_plan *fp, uint32_t max_wgs = 0) {
+                      float scale, void *scratch, size_t scratch_cap, fa_plan *fp, uint32_t max_wgs = 0,
+                      uint32_t max_splits = KVM_MAX_SPLITS) {
     if (!st || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "fa_decode: no lanes");
     if (n_lanes > KVM_MAX_LANES) return kvm_fail(st, KVM_ERANGE, "fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
     if (q_type != KVM_TYPE_F32 && q_type != KVM_TYPE_BF16) return kvm_fail(st, KVM_EUNSUPPORTED, "fa_decode: q type %d", q_type);
@@ -1067,6 +1059,8 @@ static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, in
     a.G = n_head / H;
     a.n_head = n_head;
     a.n_splits = choose_splits(st->n_cu, n_lanes, H, max_tiles);
+    if (a.n_splits > max_splits) a.n_splits = max_splits;
+    a.spin = st->wait_polls;
     // a grid whose workgroups must all be resident at once (a staged launch)
     if (max_wgs && a.n_splits * H * n_lanes > max_wgs) {
         a.n_splits = max_wgs / (H * n_lanes);
@@ -1278,7 +1272,10 @@ extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_r
             uint64_t att = cap - sel_wgs;
             const uint64_t bar = (uint64_t)(KVM_STAGE_MAX_WGS - lanes[0].w->n_head_kv) * n_lanes;
             if (att > bar) att = bar;
-            rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)att);
+            // (the selector column's flag takes slot n_splits of the head's
+            // KVM_MAX_SPLITS, and the merge polls n_splits + 1 flags)
+            rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp, (uint32_t)att,
+                            KVM_MAX_SPLITS - 1);
             if (rc) return rc;
         }
     }
@@ -1350,6 +1347,7 @@ extern "C" int kvm_fa_decode_noalloc(kvm_state *st, const kvm_window *w, const v
     if (!st) return KVM_EINVAL;
     if (!st->scratch) return kvm_fail(st, KVM_EHIP, "fa_decode_noalloc: scratch not set up on device %d", st->device);
     kvm_lane lane{w, q, q_pos, out, n_tokens};
+    st->used_scratch = true;
     return fa_decode_impl(st, &lane, 1, q_type, n_head, scale, st->scratch, KVM_NOALLOC_SCRATCH_BYTES);
 }
 

@@ -27,6 +27,21 @@ struct kvm_stage_item {          // one queued enqueue_k / enqueue_v
     int32_t nrot;                // Hadamard width, 0 = off (K)
 };
 
+// Device sync words of the decode attention (kvm_state::fa_sync, or the head of
+// the allocation-free entry point's scratch array), in 32-bit words:
+//   [lane][head][split]          the epoch of the last launch that completed the split
+//   KVM_FA_SYNC_STATUS           sticky status of the waits that gave up (KVM_WAIT_*)
+//   KVM_FA_SYNC_EPOCH + lane*64+h  the (lane, head)'s epoch
+//   KVM_FA_SYNC_PLAN, 64-bit [lane*64+h]  the plan a selecting launch published
+#define KVM_MAX_LANES 8
+#define KVM_FA_MAX_HEADS 64
+#define KVM_MAX_SPLITS 512
+#define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)
+#define KVM_FA_SYNC_EPOCH (KVM_FA_SYNC_STATUS + 64)
+#define KVM_FA_SYNC_PLAN (KVM_FA_SYNC_EPOCH + KVM_MAX_LANES * KVM_FA_MAX_HEADS)
+#define KVM_FA_SYNC_WORDS (KVM_FA_SYNC_PLAN + 2 * KVM_MAX_LANES * KVM_FA_MAX_HEADS)
+static_assert(KVM_FA_SYNC_PLAN % 2 == 0, "64-bit plan words");
+
 struct kvm_state {
     int device = 0;
     uint32_t n_cu = 256;         // compute units of the device (launch sizing)
@@ -69,6 +84,12 @@ struct kvm_state {
     // the stage-in's per-lane barrier words (epoch, go, failure, arrivals),
     // KVM_STAGE_SYNC_BYTES, zero at creation
     uint32_t *stage_sync = nullptr;
+    // polls of an in-launch wait before it gives up (kvm_state_set_wait_polls;
+    // 0: every such wait gives up at once)
+    uint32_t wait_polls = KVM_WAIT_POLLS_DEFAULT;
+    // the allocation-free entry point ran on this state (its sync words and
+    // status word live in the device's scratch array)
+    bool used_scratch = false;
 };
 
 #define KVM_STAGE_MAX_WGS 1024                      // stage-in workgroups of one lane

@@ -5,6 +5,7 @@
 // same fp32 operation order, each operation one IEEE rounding (this file is
 // compiled with -ffp-contract=off and correctly rounded `/` and sqrtf), and the
 // per-head/per-layer accumulation in double in the same order.
+#include "kvm_score_dev.h"
 #include "kvm_stagein_dev.h"
 #include "kvm_topk_dev.h"
 
@@ -106,8 +107,6 @@ extern "C" int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t i
 // embedding index e fastest after the block-in-tile): a tile's sums for all
 // heads are one contiguous slab, which the scorer streams whole.
 // ---------------------------------------------------------------------------
-#define KVM_MEANK_TILE 8u
-
 __host__ __device__ inline uint64_t kvm_meank_off(uint32_t n_embd, uint32_t e, uint32_t b) {
     return ((uint64_t)(b / KVM_MEANK_TILE) * n_embd + e) * KVM_MEANK_TILE + b % KVM_MEANK_TILE;
 }
@@ -272,249 +271,38 @@ extern "C" int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uin
 }
 
 // ---------------------------------------------------------------------------
-// Scoring.  Workgroup = (8-block tile t, layer il), four waves; chain lane
-// (hh, bi) = 8*hh + bi owns block 8t + bi under head 8c + hh of head chunk c
-// (up to 8 heads per chunk).  Per chunk:
-//   1. the tile's slab of mean-K sums (8 blocks x the chunk's heads x D,
-//      contiguous) is loaded in one round trip, turned into
-//      kh = k_sum * (1/mean_tokens) (+0.0 for a block without tokens, the
-//      reference's zeroed mean) and written to LDS as [dim][lane], while each
-//      wave builds qv = qh * invq of two of the chunk's heads;
-//   2. wave 0 runs the sequential fp32 dot chains, wave 1 the nk chains and
-//      wave 2 the block-independent nq chains (lane hh), in the reference's
-//      operation order;
-//   3. wave 0 forms the cosines.
-// Lanes bi of wave 0 then sum each block's cosines over the heads in double
-// in head order and write the layer's contribution layer/H to a workspace
-// [layer][block] that the top-k kernel averages over layers.
+// Scoring (kvm_score_dev.h).  Workgroup = (8-block tile, layer, lane), four
+// waves, one kv head per wave (heads w, w + 4, ... for more than four): the
+// wave's reads (the head's 8 KB slab of the tile, its query group's rows, the
+// token counts) are issued first, then every lane forms the products of its 4
+// dims and 17 lanes sum one product row each in the reference's order (dot of
+// blocks 0-7, their nk, and nq), without a workgroup barrier; one barrier
+// before wave 0 sums each block's cosines over the heads in double in head
+// order and writes the layer's contribution layer / H to [layer][block],
+// which the top-k averages over layers.
 // ---------------------------------------------------------------------------
-struct score_args {
-    const float *q_sum;
-    const uint32_t *q_count;
-    const float *k_sum;
-    const uint32_t *mean_tokens;
-    double *layer_score;    // [n_layer][cap]
-    uint32_t n_blocks, cap, n_tiles, n_layer, n_head, H;
-    uint32_t n_tiles_used;  // tiles holding the first n_blocks blocks
-};
-
-#define KVM_SCORE_GMAX 16   // largest query group (n_head / n_head_kv)
-#define KVM_SCORE_HMAX 16   // largest n_head_kv
-
-// One head chunk of NT consecutive tiles (HC = 8 / NT heads, so NT tiles x HC
-// heads x 8 blocks = 64 (tile, head, block) rows): the chunk's slabs (every
-// load issued first) go into LDS as kh, row (t HC + head) 8 + block, then one
-// wave per chain (dot, nk, nq) walks the dims in order.  UPB = 16-byte slab
-// units per thread and 32-dim batch (1 for a single tile of <= 4 heads).
-template <int D, int UPB, int NT>
-__device__ __forceinline__ void score_chunk(const score_args &a, uint32_t il, uint32_t tile0, uint32_t c,
-                                            uint32_t nh, uint32_t g, uint32_t qc, float (*s_k)[D + 4],
-                                            float (*s_qv)[D + 4], float *s_nq, float *s_nk,
-                                            float (*s_cos)[KVM_MEANK_TILE * 8], float *dot_out) {
-    constexpr uint32_t TW = KVM_MEANK_TILE, HC = 8 / NT, NBAT = D / 32;
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t HD = a.H * D;
-    // ---- all loads first: query gathers, token counts, slab batches.  Query
-    // item u = tid + 256x is (head u / (D/4), dims 4(u % (D/4)) .. +3); its
-    // group's rows come in 16 bytes at a time.
-    constexpr uint32_t NQI = (HC * (D / 4) + 255) / 256;
-    kvm_f32x4 qg[NQI][8];
-#pragma unroll
-    for (uint32_t x = 0; x < NQI; ++x) {
-        const uint32_t u = tid + 256u * x, hl = u / (D / 4), d4 = u % (D / 4);
-        const uint32_t h = c * HC + (hl < nh ? hl : 0u);
-#pragma unroll
-        for (int gi = 0; gi < 8; ++gi) {
-            const uint32_t gc = (uint32_t)gi < g ? (uint32_t)gi : 0u;
-            qg[x][gi] = *(const kvm_f32x4 *)&a.q_sum[((uint64_t)il * a.n_head + h * g + gc) * D + 4 * d4];
-        }
-    }
-    const uint32_t quad = tid % (TW / 4);
-    // unit tid + 256x of batch k: hu = unit/64 = (tile t, head) = (hu / HC, hu % HC)
-    // (wave-uniform), dim 32k + (unit%64)/2, blocks 4 quad .. +3
-    const kvm_f32x4 *slab[UPB];
-    uint32_t mt4[UPB][4];
-    bool unit_live[UPB];
-#pragma unroll
-    for (int x = 0; x < UPB; ++x) {
-        const uint32_t hu = (tid >> 6) + 4u * x, t = hu / HC, head = hu % HC;
-        const uint32_t tile = tile0 + t < a.n_tiles_used ? tile0 + t : a.n_tiles_used - 1;
-        unit_live[x] = head < nh;
-        slab[x] = (const kvm_f32x4 *)(a.k_sum + (((uint64_t)il * a.n_tiles + tile) * HD +
-                                                 ((uint64_t)c * HC + (head < nh ? head : 0u)) * D) * TW);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t b = tile * TW + 4 * quad + j;
-            mt4[x][j] = a.mean_tokens[(uint64_t)il * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
-        }
-    }
-    kvm_f32x4 kv[NBAT][UPB];
-#pragma unroll
-    for (uint32_t k = 0; k < NBAT; ++k)
-#pragma unroll
-        for (int x = 0; x < UPB; ++x) {
-            const uint32_t r = (tid % 64) / 2;
-            kv[k][x] = __builtin_nontemporal_load(slab[x] + (32 * k + r) * (TW / 4) + quad);
-        }
-    if (qc == 0) return;                 // layer without queries: skipped by the reduction
-    // ---- qv of the chunk's heads (the group's q rows summed in order, scaled)
-    const float invq = kvm_fdiv(1.0f, (float)(qc * (g > 1u ? g : 1u)));
-#pragma unroll
-    for (uint32_t x = 0; x < NQI; ++x) {
-        const uint32_t u = tid + 256u * x, hl = u / (D / 4), d4 = u % (D / 4);
-        if (hl < nh) {
-            const uint32_t h = c * HC + hl;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float qh = 0.0f;
-#pragma unroll
-                for (int gi = 0; gi < 8; ++gi)
-                    if ((uint32_t)gi < g) qh = kvm_fadd(qh, qg[x][gi][e]);
-                for (uint32_t g0 = 8; g0 < g; ++g0)              // groups above 8 (rare)
-                    qh = kvm_fadd(qh, a.q_sum[((uint64_t)il * a.n_head + h * g + g0) * D + 4 * d4 + e]);
-                s_qv[hl][4 * d4 + e] = kvm_fmul(qh, invq);
-            }
-        }
-    }
-    float inv4[UPB][4];
-    uint32_t keep4[UPB][4];
-#pragma unroll
-    for (int x = 0; x < UPB; ++x)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            inv4[x][j] = mt4[x][j] ? kvm_fdiv(1.0f, (float)mt4[x][j]) : 0.0f;
-            keep4[x][j] = mt4[x][j] ? 0xffffffffu : 0u;
-        }
-    // ---- kh for all dims into LDS (one barrier), then the chains run straight
-    // through the D dims in the reference's order
-    const uint32_t hh = (lane / TW) % HC, tl = lane / (TW * HC);   // the chain's head and tile
-    const float *qrow = s_qv[hh < nh ? hh : 0u];
-    const float *nqrow = s_qv[lane < nh ? lane : 0u];
-    float chain = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < NBAT; ++k) {
-#pragma unroll
-        for (int x = 0; x < UPB; ++x) {
-            const uint32_t u = tid + 256u * x, hu = u / 64, r = (u % 64) / 2;
-            if (unit_live[x]) {
-                float4 kh;
-                kh.x = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][0], inv4[x][0])) & keep4[x][0]);
-                kh.y = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][1], inv4[x][1])) & keep4[x][1]);
-                kh.z = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][2], inv4[x][2])) & keep4[x][2]);
-                kh.w = __uint_as_float(__float_as_uint(kvm_fmul(kv[k][x][3], inv4[x][3])) & keep4[x][3]);
-                float *col = &s_k[hu * TW + 4 * quad][32 * k + r];
-                col[0] = kh.x;
-                col[D + 4] = kh.y;
-                col[2 * (D + 4)] = kh.z;
-                col[3 * (D + 4)] = kh.w;
-            }
-        }
-    }
-    KVM_LDS_BARRIER();
-    // Each chain reads 32 dims ahead (16-byte LDS reads into a second register
-    // buffer, kept ahead of the arithmetic by a scheduling barrier), so the
-    // dependent adds never wait on LDS.
-    const float *krow = s_k[lane];
-    constexpr int CH = 8;                // float4 per 32-dim chunk
-    auto chain_over = [&](auto &&ld, auto &&step) {
-        float4 buf[2][2][CH];
-        ld(buf[0], 0);
-#pragma unroll
-        for (int c = 0; c < D / (4 * CH); ++c) {
-            if (c + 1 < D / (4 * CH)) ld(buf[(c + 1) & 1], c + 1);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < CH; ++j) step(buf[c & 1][0][j], buf[c & 1][1][j]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    if (w == 0) {
-        chain_over([&](float4 (&b)[2][CH], int c) {
-#pragma unroll
-                       for (int j = 0; j < CH; ++j) {
-                           b[0][j] = *(const float4 *)&qrow[4 * (CH * c + j)];
-                           b[1][j] = *(const float4 *)&krow[4 * (CH * c + j)];
-                       }
-                   },
-                   [&](const float4 &q4, const float4 &k4) {
-                       chain = kvm_fadd(chain, kvm_fmul(q4.x, k4.x));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.y, k4.y));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.z, k4.z));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.w, k4.w));
-                   });
-    } else if (w == 1) {
-        chain_over([&](float4 (&b)[2][CH], int c) {
-#pragma unroll
-                       for (int j = 0; j < CH; ++j) b[1][j] = *(const float4 *)&krow[4 * (CH * c + j)];
-                   },
-                   [&](const float4 &, const float4 &k4) {
-                       chain = kvm_fadd(chain, kvm_fmul(k4.x, k4.x));
-                       chain = kvm_fadd(chain, kvm_fmul(k4.y, k4.y));
-                       chain = kvm_fadd(chain, kvm_fmul(k4.z, k4.z));
-                       chain = kvm_fadd(chain, kvm_fmul(k4.w, k4.w));
-                   });
-    } else if (w == 2) {
-        chain_over([&](float4 (&b)[2][CH], int c) {
-#pragma unroll
-                       for (int j = 0; j < CH; ++j) b[0][j] = *(const float4 *)&nqrow[4 * (CH * c + j)];
-                   },
-                   [&](const float4 &q4, const float4 &) {
-                       chain = kvm_fadd(chain, kvm_fmul(q4.x, q4.x));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.y, q4.y));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.z, q4.z));
-                       chain = kvm_fadd(chain, kvm_fmul(q4.w, q4.w));
-                   });
-    }
-    if (w == 1) s_nk[lane] = chain;
-    if (w == 2 && lane < nh) s_nq[lane] = chain;
-    KVM_LDS_BARRIER();
-    // ---- cosines of the chunk
-    const uint32_t bi = lane % TW, b = (tile0 + tl) * TW + bi;
-    if (w == 0 && hh < nh && b < a.n_blocks) {
-        const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(s_nq[hh]), kvm_fsqrt(s_nk[lane])), 1e-6f);
-        s_cos[c * HC + hh][tl * TW + bi] = kvm_fdiv(chain, den);
-    }
-    *dot_out = chain;
-    KVM_LDS_BARRIER();                   // chunk c's LDS reads done before chunk c+1 writes
-}
-
 // Independent retrievals (conversation lanes) in one launch: lane = blockIdx.z.
 struct score_lanes {
     score_args lane[KVM_RET_LANES];
 };
 
-// Workgroup = NT consecutive tiles of one layer: NT = 8 / HC tiles for head
-// chunks of HC heads, so that a chunk fills the 64 chain lanes (NT = 2 at 4 kv
-// heads: 16 blocks per workgroup).
-template <int D, int NT>
+template <int D>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     const score_args &a = sl.lane[blockIdx.z];
-    if (blockIdx.x * NT >= a.n_tiles_used || blockIdx.y >= a.n_layer) return;
-    constexpr uint32_t TW = KVM_MEANK_TILE;       // blocks per tile
-    constexpr uint32_t HC = 8 / NT;               // heads per chunk
-    __shared__ __align__(16) float s_k[64][D + 4];   // kh as [lane][dim], rows padded against bank conflicts
-    __shared__ __align__(16) float s_qv[HC][D + 4];
-    __shared__ float s_nq[HC];
-    __shared__ float s_nk[64];
-    __shared__ float s_cos[KVM_SCORE_HMAX][TW * 8];
-    const uint32_t tile = blockIdx.x * NT, il = blockIdx.y;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t qc = a.q_count[il];
-    const uint32_t g = a.n_head / a.H;
-    for (uint32_t c = 0; c * HC < a.H; ++c) {
-        const uint32_t nh = a.H - c * HC < HC ? a.H - c * HC : HC;
-        float dot;
-        if (NT == 1 && nh <= 4) score_chunk<D, 1, NT>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
-        else score_chunk<D, 2, NT>(a, il, tile, c, nh, g, qc, s_k, s_qv, s_nq, s_nk, s_cos, &dot);
-        if (qc == 0) return;
+    const uint32_t tile = blockIdx.x, il = blockIdx.y;
+    if (tile >= a.n_tiles_used || il >= a.n_layer) return;
+    __shared__ __align__(16) score_wg_lds<D, 4> L;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t g = a.n_head / a.H, qc = a.q_count[il];
+    score_regs r;
+    if ((uint32_t)w < a.H) score_tile_load<D>(a, il, tile, (uint32_t)w, g, r);
+    if (qc == 0) return;                 // a layer without queries: skipped by the reduction
+    for (uint32_t hh = (uint32_t)w; hh < a.H; hh += 4u) {
+        if (hh != (uint32_t)w) score_tile_load<D>(a, il, tile, hh, g, r);
+        score_tile_compute<D>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
     }
-    if (w == 0 && lane < TW * NT && tile * TW + lane < a.n_blocks) {
-        double layer = 0.0;
-        for (uint32_t h = 0; h < a.H; ++h) layer += (double)s_cos[h][lane];
-        a.layer_score[(uint64_t)il * a.cap + tile * TW + lane] = layer / (double)(a.H > 1 ? a.H : 1);
-    }
+    __syncthreads();
+    if (w == 0) score_tile_store(a, il, tile, L.cos);
 }
 
 // ---------------------------------------------------------------------------
@@ -588,12 +376,6 @@ extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_se
     return kvm_topk_launch(st, tl, 1);
 }
 
-template <int NT>
-static void launch_score(bool d256, dim3 grid, dim3 block, hipStream_t stream, const score_lanes &sl) {
-    if (d256) hipLaunchKernelGGL((k_score<256, NT>), grid, block, 0, stream, sl);
-    else hipLaunchKernelGGL((k_score<128, NT>), grid, block, 0, stream, sl);
-}
-
 static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
     const kvm_meank_index *ix = r.ix;
     const kvm_query_acc *q = r.q;
@@ -648,48 +430,31 @@ int kvm_retrieval_prepare(kvm_state *st, const kvm_retrieval_lane *lanes, uint32
 
 // The scoring grid of prepared lanes: every lane's layer contributions into
 // the buffer its top-k arguments read.
-int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl) {
-    score_lanes sl{};
-    uint32_t max_tiles = 0, max_layer = 0;
+void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl,
+                              score_args *out) {
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_retrieval_lane &r = lanes[i];
         const kvm_meank_index *ix = r.ix;
         const uint32_t used = r.p->n_blocks ? kvm_cdiv(r.p->n_blocks, KVM_MEANK_TILE) : 0u;
-        sl.lane[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, (double *)tl.lane[i].layer_score,
-                                r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
-                                r.q->n_head, ix->n_head_kv, used};
-        max_tiles = used > max_tiles ? used : max_tiles;
-        max_layer = ix->n_layer > max_layer ? ix->n_layer : max_layer;
+        out[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, (double *)tl.lane[i].layer_score,
+                            r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
+                            r.q->n_head, ix->n_head_kv, used};
+    }
+}
+
+int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl) {
+    score_lanes sl{};
+    kvm_retrieval_score_args(lanes, n_lanes, tl, sl.lane);
+    uint32_t max_tiles = 0, max_layer = 0;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        max_tiles = sl.lane[i].n_tiles_used > max_tiles ? sl.lane[i].n_tiles_used : max_tiles;
+        max_layer = sl.lane[i].n_layer > max_layer ? sl.lane[i].n_layer : max_layer;
     }
     if (max_tiles == 0) return KVM_OK;
     KVM_HIP(st, hipSetDevice(st->device));
-    // tiles per workgroup: head chunks of HC = 8 / NT heads fill the 64 chain
-    // lanes; lanes with different kv-head counts share the largest chunk
-    uint32_t max_h = 0;
-    for (uint32_t i = 0; i < n_lanes; ++i) max_h = lanes[i].ix->n_head_kv > max_h ? lanes[i].ix->n_head_kv : max_h;
-    int nt = max_h > 4 ? 1 : max_h > 2 ? 2 : max_h == 2 ? 4 : 8;
-    // fewer tiles per workgroup (some chain lanes idle) while the scoring
-    // workgroups still all run at once, two per CU: one memory round trip and
-    // one chain per workgroup either way, so more of them finish sooner (a
-    // 256K-token lane at 4 kv heads: 256 workgroups of 8 blocks score and
-    // select in 15.8 us against 16.8 with 128 of 16)
-    while (nt > 1) {
-        uint64_t wgs = 0;
-        for (uint32_t i = 0; i < n_lanes; ++i) {
-            const uint32_t used = lanes[i].p->n_blocks ? kvm_cdiv(lanes[i].p->n_blocks, KVM_MEANK_TILE) : 0u;
-            wgs += (uint64_t)kvm_cdiv(used, (uint32_t)nt / 2) * lanes[i].ix->n_layer;
-        }
-        if (wgs > 2ull * st->n_cu) break;
-        nt /= 2;
-    }
-    const dim3 grid(kvm_cdiv(max_tiles, (uint32_t)nt), max_layer, n_lanes), block(256);
-    const bool d256 = lanes[0].ix->head_dim == 256;
-    switch (nt) {
-    case 1: launch_score<1>(d256, grid, block, st->stream, sl); break;
-    case 2: launch_score<2>(d256, grid, block, st->stream, sl); break;
-    case 4: launch_score<4>(d256, grid, block, st->stream, sl); break;
-    default: launch_score<8>(d256, grid, block, st->stream, sl); break;
-    }
+    const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
+    if (lanes[0].ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sl);
+    else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sl);
     KVM_LAUNCH_CHECK(st, "score");
     return KVM_OK;
 }

@@ -137,6 +137,8 @@ int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_l
     for (uint32_t i = 0; i < n_lanes; ++i) {
         sl->lane[i].rc = rc0;
         sl->lane[i].sync = st->stage_sync + (size_t)i * KVM_STAGE_SYNC_LANE;
+        sl->lane[i].status = st->fa_sync + KVM_FA_SYNC_STATUS;
+        sl->lane[i].spin = st->wait_polls;
     }
     // 64-token items: K and V rows, then the (cos, sin) rows of their positions
     *lds = (size_t)64 * (max_h * (w0->head_dim / 32) * (34 + 18) + (rope->n_rot / 2) * 8);

@@ -193,6 +193,8 @@ struct stage_args {
     const int32_t *stage_src;
     uint8_t *moves;
     uint32_t *sync;                  // the lane's barrier words (kvm_state::stage_sync)
+    uint32_t *status;                // the state's sticky wait status (KVM_WAIT_STAGE when a barrier gives up)
+    uint32_t spin;                   // polls of a barrier wait before it gives up (0: at once)
 };
 
 // dst[i] = src[i] for i = tid, tid + nth, ... < n (16-byte units, n >= 1, the
@@ -410,12 +412,13 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
 // ---------------------------------------------------------------------------
 // A lane's plan staged by G workgroups x = 0 .. G-1 of one launch
 // ---------------------------------------------------------------------------
-// Longest wait at a lane barrier (s_sleep rounds of ~64 cycles, about 0.1 s):
-// every workgroup of the launch is resident (the grids never exceed what the
-// CUs hold at once) and arrives without waiting on anything, so the wait ends
-// unless workgroups cannot be scheduled; past the limit the status says so
-// (bit 16) and the workgroups empty their items' cells instead.
-#define KVM_STAGE_SPIN (1u << 21)
+// A wait at a lane barrier polls at most `spin` times (s_sleep rounds of ~64
+// cycles, about 0.1 s by default): every workgroup of the launch is resident
+// (the grids never exceed what the CUs hold at once) and arrives without
+// waiting on anything, so the wait ends unless workgroups cannot be scheduled;
+// past the limit the selection's status says so (info[3] bit 16, and the
+// state's status word KVM_WAIT_STAGE) and the workgroups empty their items'
+// cells instead.
 
 __device__ __forceinline__ uint32_t sync_load(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -423,12 +426,12 @@ __device__ __forceinline__ uint32_t sync_load(const uint32_t *p) {
 __device__ __forceinline__ void sync_store(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool sync_wait(const uint32_t *p, uint32_t v) {
-    for (uint32_t it = 0; sync_load(p) != v; ++it) {
-        if (it > KVM_STAGE_SPIN) return false;
+__device__ __forceinline__ bool sync_wait(const uint32_t *p, uint32_t v, uint32_t spin) {
+    for (uint32_t it = 0;; ++it) {
+        if (it >= spin) return false;
+        if (sync_load(p) == v) return true;
         __builtin_amdgcn_s_sleep(1);
     }
-    return true;
 }
 
 // Entries of the lane's plan to stage: none when the plan does not fit (status
@@ -448,7 +451,8 @@ __device__ inline uint32_t stage_entries(const stage_args &a) {
 // back from the writer's L2 before its arrival (release) and the caches are
 // invalidated after the go flag (acquire).  False: the wait timed out.
 template <int NTH>
-__device__ bool lane_barrier(uint32_t *sync, uint32_t v, uint32_t x, uint32_t G, bool last) {
+__device__ bool lane_barrier(uint32_t *sync, uint32_t *status, uint32_t spin, uint32_t v, uint32_t x, uint32_t G,
+                             bool last) {
     __shared__ uint32_t s_ok;
     const uint32_t tid = threadIdx.x;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -459,7 +463,7 @@ __device__ bool lane_barrier(uint32_t *sync, uint32_t v, uint32_t x, uint32_t G,
     }
     uint32_t ok = 1;
     if (x == 0) {
-        for (uint32_t t = tid; t < G; t += NTH) ok &= sync_wait(sync + 64 + t, v) ? 1u : 0u;
+        for (uint32_t t = tid; t < G; t += NTH) ok &= sync_wait(sync + 64 + t, v, spin) ? 1u : 0u;
         ok = __syncthreads_and(ok);
         if (tid == 0) {
             if (!ok) sync_store(sync + 2, v);
@@ -468,11 +472,12 @@ __device__ bool lane_barrier(uint32_t *sync, uint32_t v, uint32_t x, uint32_t G,
             sync_store(sync + 1, v);
         }
     } else if (tid == 0) {
-        ok = sync_wait(sync + 1, v) && sync_load(sync + 2) != v;
+        ok = sync_wait(sync + 1, v, spin) && sync_load(sync + 2) != v;
         s_ok = ok;
     }
     __syncthreads();
     if (x != 0) ok = s_ok;
+    if (!ok && tid == 0) atomicOr(status, (uint32_t)KVM_WAIT_STAGE);
     __threadfence();
     return ok != 0;
 }
@@ -507,7 +512,7 @@ __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent,
         for (uint32_t si = threadIdx.x; si < n_ent; si += NTH) any |= a.stage_src[si] >= 0 ? 1u : 0u;
         if (__syncthreads_or(any)) {
             for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
-            ok = lane_barrier<NTH>(a.sync, v, x, G, last);
+            ok = lane_barrier<NTH>(a.sync, a.status, a.spin, v, x, G, last);
         }
     }
     for (uint32_t item = x; item < n_items; item += G) {

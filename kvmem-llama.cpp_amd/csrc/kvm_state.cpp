@@ -77,9 +77,53 @@ extern "C" int kvm_state_set_stream(kvm_state *st, void *hip_stream) {
 
 extern "C" void *kvm_state_stream(kvm_state *st) { return st ? (void *)st->stream : nullptr; }
 
+// Waits for the stream, then reads and clears the sticky wait status of the
+// state's sync words (and of the scratch array's, when the allocation-free
+// entry point ran on the state).  A wait that gave up may have left flags,
+// epochs or a plan word that a workgroup of that launch wrote after its
+// head's or lane's epoch had moved on; with the stream idle, every sync word
+// is zeroed, so the next launch's epochs start from a clean slate.
+static int read_status(kvm_state *st, uint32_t *status) {
+    *status = 0;
+    KVM_HIP(st, hipSetDevice(st->device));
+    KVM_HIP(st, hipStreamSynchronize(st->stream));
+    uint32_t v[2] = {0u, 0u};
+    KVM_HIP(st, hipMemcpy(&v[0], st->fa_sync + KVM_FA_SYNC_STATUS, 4, hipMemcpyDeviceToHost));
+    if (st->used_scratch && st->scratch)
+        KVM_HIP(st, hipMemcpy(&v[1], (uint32_t *)st->scratch + KVM_FA_SYNC_STATUS, 4, hipMemcpyDeviceToHost));
+    *status = v[0] | v[1];
+    if (*status) {
+        KVM_HIP(st, hipMemsetAsync(st->fa_sync, 0, kvm_fa_sync_bytes(), st->stream));
+        KVM_HIP(st, hipMemsetAsync(st->stage_sync, 0, KVM_STAGE_SYNC_BYTES, st->stream));
+        if (st->used_scratch && st->scratch)
+            KVM_HIP(st, hipMemsetAsync(st->scratch, 0, kvm_fa_sync_bytes(), st->stream));
+        KVM_HIP(st, hipStreamSynchronize(st->stream));
+    }
+    return KVM_OK;
+}
+
 extern "C" int kvm_state_sync(kvm_state *st) {
     if (!st) return KVM_EINVAL;
-    KVM_HIP(st, hipStreamSynchronize(st->stream));
+    uint32_t status = 0;
+    int rc = read_status(st, &status);
+    if (rc) return rc;
+    if (status)
+        return kvm_fail(st, KVM_ETIMEOUT, "in-launch waits gave up:%s%s%s (status 0x%x)",
+                        status & KVM_WAIT_MERGE ? " split merge (output rows not written)" : "",
+                        status & KVM_WAIT_PLAN ? " selected plan (not staged, window unchanged)" : "",
+                        status & KVM_WAIT_STAGE ? " stage-in barrier (plan items emptied)" : "", status);
+    return KVM_OK;
+}
+
+extern "C" int kvm_state_status(kvm_state *st, uint32_t *status) {
+    if (!st) return KVM_EINVAL;
+    if (!status) return kvm_fail(st, KVM_EINVAL, "state_status: null output");
+    return read_status(st, status);
+}
+
+extern "C" int kvm_state_set_wait_polls(kvm_state *st, uint32_t polls) {
+    if (!st) return KVM_EINVAL;
+    st->wait_polls = polls;
     return KVM_OK;
 }
 

@@ -9,7 +9,7 @@
 // ... for loading and the contiguous range [t*per, (t+1)*per) for compaction.
 // Every global read is issued before any use; barriers order LDS only.
 #pragma once
-#include "kvm_internal.h"
+#include "kvm_score_dev.h"
 
 struct topk_args {
     const double *scores_in;   // caller's scores (kvm_select_topk), or null
@@ -148,7 +148,9 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
     const int32_t *sbb = a.slot_base ? a.slot_base : (const int32_t *)a.n_tokens;
     // blocks may move within the window (from the shadow of their old slot)
     const bool moves = a.stage_src && a.shadow_rows && a.slot_block;
-    const uint32_t *srp = moves ? a.shadow_rows : a.n_tokens;
+    // (without moves the shadow counts are unused: the stand-in is the slot
+    // map itself, which holds as many entries as the loop below reads)
+    const uint32_t *srp = moves ? a.shadow_rows : sbp;
     const uint32_t nsl1 = n_sl_lds ? n_sl_lds - 1 : 0u, n1 = n ? n - 1 : 0u;
     uint32_t sl_blk[SLT], sl_rows[SLT];
     int32_t sl_base[SLT];
@@ -175,7 +177,7 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
 #pragma unroll
     for (uint32_t k = 0; k < LOAD; ++k) {
         const uint32_t i = tid + k * NTH, ic = i < n1 ? i : n1;
-        sv[k] = scp[ic];
+        sv[k] = kvm_ld_f64_dev(scp + ic);
         nt[k] = a.n_tokens[ic];
         pr[k] = prp[ic];
     }
@@ -221,7 +223,7 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
                 uint32_t nlay = 0;
                 if (qc0) { acc += sc; nlay++; }
                 for (uint32_t il = 1; il < a.n_layer; ++il)
-                    if (a.q_count[il]) { acc += a.layer_score[(uint64_t)il * a.ls_cap + i]; nlay++; }
+                    if (a.q_count[il]) { acc += kvm_ld_f64_dev(a.layer_score + (uint64_t)il * a.ls_cap + i); nlay++; }
                 sc = nlay ? acc / (double)nlay : 0.0;
                 if (!pr[k]) sc = 0.0;
                 a.scores_out[i] = sc;
@@ -552,4 +554,8 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
 // kernel over them.
 int kvm_retrieval_prepare(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, topk_lanes *tl);
 int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl);
+// The scoring grid's arguments of prepared lanes (what kvm_retrieval_score
+// launches), for a launch that scores them itself.
+void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl,
+                              score_args *out);
 int kvm_topk_launch(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes);

@@ -11,13 +11,15 @@ PKG_DIR = os.path.dirname(_HERE)
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libkvm_hotpath.so")
 HEADER_PATH = os.path.join(os.path.dirname(PKG_DIR), "include", "kvm_hotpath.h")
 
-KVM_OK, KVM_EINVAL, KVM_EHIP, KVM_ENOMEM, KVM_ERANGE, KVM_EUNSUPPORTED = 0, -1, -2, -3, -4, -5
+KVM_OK, KVM_EINVAL, KVM_EHIP, KVM_ENOMEM, KVM_ERANGE, KVM_EUNSUPPORTED, KVM_ETIMEOUT = 0, -1, -2, -3, -4, -5, -6
+WAIT_MERGE, WAIT_PLAN, WAIT_STAGE = 1, 2, 4
+WAIT_POLLS_DEFAULT = 1 << 21
 T_F32, T_F16, T_Q4_0, T_Q8_0, T_BF16 = 0, 1, 2, 8, 30
 TILE_CELLS = 64
 MAX_TOPK_BLOCKS = 8192
 NOALLOC_SCRATCH_BYTES = 16 << 20
 STATUS_NAMES = {0: "KVM_OK", -1: "KVM_EINVAL", -2: "KVM_EHIP", -3: "KVM_ENOMEM",
-                -4: "KVM_ERANGE", -5: "KVM_EUNSUPPORTED"}
+                -4: "KVM_ERANGE", -5: "KVM_EUNSUPPORTED", -6: "KVM_ETIMEOUT"}
 
 
 class KvmError(RuntimeError):
@@ -117,6 +119,8 @@ SIGNATURES = {
     "kvm_state_set_stream": (C.c_int, [_P, _P]),
     "kvm_state_stream": (_P, [_P]),
     "kvm_state_sync": (C.c_int, [_P]),
+    "kvm_state_status": (C.c_int, [_P, C.POINTER(_u32)]),
+    "kvm_state_set_wait_polls": (C.c_int, [_P, _u32]),
     "kvm_state_last_error": (C.c_char_p, [_P]),
     "kvm_host_alloc": (_P, [_sz]),
     "kvm_host_free": (None, [_P]),

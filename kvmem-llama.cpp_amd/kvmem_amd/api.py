@@ -36,7 +36,20 @@ class State:
         return rc
 
     def sync(self):
+        """Waits for the state's stream; raises KvmError(KVM_ETIMEOUT) when an
+        in-launch wait gave up since the last sync."""
         self.check(self.lib.kvm_state_sync(self.h))
+
+    def status(self):
+        """Waits for the stream and returns (and clears) the KVM_WAIT_* bits of
+        the in-launch waits that gave up since the last sync / status."""
+        v = C.c_uint32(0)
+        self.check(self.lib.kvm_state_status(self.h, C.byref(v)))
+        return v.value
+
+    def set_wait_polls(self, polls):
+        """Polls of an in-launch wait before it gives up (0: every wait gives up at once)."""
+        self.check(self.lib.kvm_state_set_wait_polls(self.h, int(polls)))
 
     def capture(self, fns):
         """Capture the library calls made by fns() (one HIP graph, replayed with
