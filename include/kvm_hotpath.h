@@ -134,6 +134,14 @@ typedef struct kvm_window {
      * and kvm_slot_copy_from_host void that slot's shadow (shadow_rows = 0). */
     void *k_shadow;         /* device [n_cells][n_head_kv * row(head_dim)] of q8_0 */
     uint32_t *shadow_rows;  /* device [n_slots]: rows of the slot the shadow holds */
+    /* Optional (NULL = not tracked): per slot the rows imported into its cells
+     * (generated tokens, kvm_window_import_rows) that no kvm_harvest_block has
+     * taken into the host history since.  A plan that would overwrite such a
+     * slot is refused (kvm_selection info[3] bit 2): the reference harvests
+     * the outgoing blocks' generated rows before it spills them and admits
+     * the stage-in (apply_plan_to_kv, llama-memory-kvmem.cpp:1811-1857,
+     * KvMemRuntime::spill_outgoing / admit_incoming, kvmem_runtime.cpp:225-249). */
+    uint32_t *pending_rows; /* device [n_slots] */
 } kvm_window;
 
 size_t kvm_window_k_bytes(const kvm_window *w);
@@ -148,7 +156,8 @@ int kvm_window_reset(kvm_state *st, const kvm_window *w);
 /* Copies ggml cache rows for cells [cell0, cell0+n) into the tiled window and
  * sets their positions (pos: device int32[n], NULL = leave cell_pos alone).
  * k_rows / v_rows: device (or pinned host) rows of w->k_type / w->v_type.
- * This is the cpy of new K/V rows into cache cells (llama-kvmem-batch.cpp:42-50). */
+ * This is the cpy of new K/V rows into cache cells (llama-kvmem-batch.cpp:42-50).
+ * With w->pending_rows, every slot the cells touch counts the rows written. */
 int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                            const void *k_rows, const void *v_rows, const int32_t *pos);
 /* Inverse of import: ggml rows of cells [cell0, cell0+n).  Used by stage-out
@@ -294,7 +303,8 @@ int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, u
  * k_raw_rows / v_rows (host: the history rows of the tokens' positions).
  * When ix is given the same K rows are added to its layer il at pos0
  * (write_layer_mean_k).  q8_0 K windows; the copies are done when the state's
- * stream reaches this point (kvm_state_sync). */
+ * stream reaches this point (kvm_state_sync).  With w->pending_rows, the
+ * slots the cells touch count n fewer unharvested rows (not below zero). */
 int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                       const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,
                       const kvm_meank_index *ix, uint32_t il, uint32_t pos0);
@@ -313,18 +323,27 @@ typedef struct kvm_select_params {
 } kvm_select_params;
 
 /* Device outputs of one retrieval.  info[0] = selected blocks, info[1] = total
- * window tokens, info[2] = slots that need stage-in, info[3] = status (0 ok). */
+ * window tokens, info[2] = slots that need stage-in, info[3] = status (0 ok;
+ * bit 0: more selected blocks than `cap`, bit 1: more than the window's slots,
+ * bit 2: the plan would overwrite a slot with pending rows and was not staged,
+ * bit 4: a stage-in barrier gave up and the plan's items were emptied),
+ * info[4] = blocks in stage_out; info[5..7] are zero. */
 typedef struct kvm_selection {
     uint32_t cap;               /* capacity of ids / to_base / stage_slots */
     double *scores;             /* device [n_blocks] (score_retrieval output) */
     uint32_t *ids;              /* device [cap], ascending block ids */
     int32_t *to_base;           /* device [cap], window position of each block */
     uint32_t *stage_slots;      /* device [cap], slots whose contents must be (re)staged */
-    uint32_t *info;             /* device [4] */
+    uint32_t *info;             /* device [8] */
     /* device [cap] or NULL: for stage_slots[i], the slot whose shadow and V
      * hold that block before the plan (a full block already in the window of a
      * window with a shadow), else -1 = stage from the host history */
     int32_t *stage_src;
+    /* device [cap] or NULL: the blocks the window's slots hold before the plan
+     * that the new selection does not keep, ascending (the plan's stage_out,
+     * KvMemStore::set_selection, kvmem/src/host/kvmem_store.cpp:789-795);
+     * a window with pending_rows needs them harvested before the plan stages */
+    uint32_t *stage_out;
 } kvm_selection;
 
 /* A half-open range [begin, end) of original token positions (llama_kvmem_row_range,

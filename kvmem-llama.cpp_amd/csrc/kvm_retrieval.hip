@@ -342,7 +342,8 @@ static int make_topk(kvm_state *st, const double *scores, const double *layer_sc
                     p->n_blocks, p->budget_blocks, p->sink_blocks, p->recent_blocks, p->n_mandatory,
                     w ? w->n_cells / w->block_tokens : 0u, out->cap,
                     ix ? ix->n_layer : 0u, ix ? ix->n_blocks : 0u,
-                    w ? w->shadow_rows : nullptr, w ? out->stage_src : nullptr, w ? w->block_tokens : 0u};
+                    w ? w->shadow_rows : nullptr, w ? out->stage_src : nullptr, w ? w->block_tokens : 0u,
+                    w ? w->pending_rows : nullptr, w ? out->stage_out : nullptr};
     return KVM_OK;
 }
 

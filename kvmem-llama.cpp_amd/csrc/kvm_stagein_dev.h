@@ -435,9 +435,10 @@ __device__ __forceinline__ bool sync_wait(const uint32_t *p, uint32_t v, uint32_
 }
 
 // Entries of the lane's plan to stage: none when the plan does not fit (status
-// bits 1, over capacity, and 2, more blocks than slots).
+// bits 0, over capacity, and 1, more blocks than slots) or was refused (bit 2:
+// it would overwrite a slot's unharvested rows).
 __device__ inline uint32_t stage_entries(const stage_args &a) {
-    return (a.info[3] & 3u) != 0 ? 0u : a.info[2];
+    return (a.info[3] & 7u) != 0 ? 0u : a.info[2];
 }
 
 // Barrier of a lane's G workgroups (NTH threads each) at value v, through the

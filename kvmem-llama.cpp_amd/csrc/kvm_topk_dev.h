@@ -29,6 +29,8 @@ struct topk_args {
     const uint32_t *shadow_rows;   // the window's shadow row counts, or null
     int32_t *stage_src;            // per staged entry, the old slot it moves from (-1: host)
     uint32_t bt;                   // the window's block_tokens
+    const uint32_t *pending_rows;  // the window's unharvested rows per slot, or null
+    uint32_t *stage_out;           // the blocks leaving the plan's slots, or null
 };
 
 // Independent retrievals (conversation lanes) in one launch.
@@ -95,6 +97,7 @@ struct topk_lds {
     uint32_t ntok[MAXB];
     uint32_t sblk[SLOTS];
     int32_t sbase[SLOTS];
+    uint32_t spend[SLOTS];        // unharvested rows per slot (0 without tracking)
     uint32_t hist[2][256];
     uint32_t tmp[2][2 * NW];      // block_scan2 buffers, used alternately
     float wmm[2][NW];
@@ -152,7 +155,8 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
     // map itself, which holds as many entries as the loop below reads)
     const uint32_t *srp = moves ? a.shadow_rows : sbp;
     const uint32_t nsl1 = n_sl_lds ? n_sl_lds - 1 : 0u, n1 = n ? n - 1 : 0u;
-    uint32_t sl_blk[SLT], sl_rows[SLT];
+    const uint32_t *spp = a.pending_rows && a.slot_block ? a.pending_rows : sbp;
+    uint32_t sl_blk[SLT], sl_rows[SLT], sl_pend[SLT];
     int32_t sl_base[SLT];
 #pragma unroll
     for (uint32_t j = 0; j < SLT; ++j) {
@@ -160,6 +164,7 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
         sl_blk[j] = sbp[i < nsl1 ? i : nsl1];
         sl_base[j] = sbb[i < nsl1 ? i : nsl1];
         sl_rows[j] = srp[i < nsl1 ? i : nsl1];
+        sl_pend[j] = spp[i < nsl1 ? i : nsl1];
     }
     const uint32_t kpt = (n + NTH - 1) / NTH;
     const bool have_ls = a.layer_score != nullptr, have_pr = have_ls && a.present != nullptr;
@@ -189,6 +194,7 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
         if (i < n_sl_lds) {
             s_sblk[i] = sl_blk[j];
             s_sbase[i] = sl_base[j];
+            T.spend[i] = a.pending_rows ? sl_pend[j] : 0u;
         }
     }
     if (tid < 256) s_hist[0][tid] = 0;
@@ -495,8 +501,9 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
     block_scan2<NTH>(local, tok, s_tmp[0], rank0, base0, n_sel, total);
     const bool fits = n_sel <= a.cap;
     const uint32_t ns = fits ? (n_sel < a.n_slots ? n_sel : a.n_slots) : 0;
-    // slots whose (block, base) differ from the new layout
-    uint32_t need_mask = 0, need_local = 0;
+    // slots whose (block, base) differ from the new layout; a plan that would
+    // overwrite a slot holding unharvested rows is refused
+    uint32_t need_mask = 0, need_local = 0, refuse = 0;
     if (fits) {
         uint32_t rank = rank0, base = base0, k = 0;
         for (uint32_t i = i0; i < i1; ++i) {
@@ -509,14 +516,35 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
                               (in_lds ? s_sbase[rank] : a.slot_base[rank]) != (int32_t)base)) {
                 need_mask |= 1u << k;
                 ++need_local;
+                if (a.pending_rows && a.slot_block && (in_lds ? T.spend[rank] : a.pending_rows[rank]) != 0u) refuse = 1;
             }
             base += s_ntok[i];
             ++rank;
             ++k;
         }
     }
-    uint32_t pos, n_stage, z2, z3;
-    block_scan2<NTH>(need_local, 0u, s_tmp[1], pos, z2, n_stage, z3);
+    // stage-out: the blocks of slots [tid * SLT, ...) of the plan's first
+    // n_sl_lds slots that the selection does not keep, in slot order (the
+    // chronological layout keeps blocks ascending)
+    uint32_t out_local = 0;
+    const uint32_t so0 = tid * SLT;
+#pragma unroll
+    for (uint32_t j = 0; j < SLT; ++j) {
+        const uint32_t sl = so0 + j;
+        const uint32_t b = sl < n_sl_lds ? s_sblk[sl] : 0xffffffffu;
+        out_local += b < n && !s_kept[b] ? 1u : 0u;
+    }
+    uint32_t pos, out_pos, n_stage, n_out;
+    block_scan2<NTH>(need_local, out_local, s_tmp[1], pos, out_pos, n_stage, n_out);
+    if (a.stage_out && out_local) {
+#pragma unroll
+        for (uint32_t j = 0; j < SLT; ++j) {
+            const uint32_t sl = so0 + j;
+            const uint32_t b = sl < n_sl_lds ? s_sblk[sl] : 0xffffffffu;
+            if (b < n && !s_kept[b] && out_pos < a.cap) a.stage_out[out_pos++] = b;
+        }
+    }
+    refuse = __syncthreads_or(refuse) ? 1u : 0u;
     if (need_mask) {
         uint32_t rank = rank0, k = 0;
         for (uint32_t i = i0; i < i1; ++i) {
@@ -538,12 +566,16 @@ __device__ __forceinline__ uint32_t topk_body(const topk_args &a, topk_lds<NTH, 
             ++k;
         }
     }
-    const uint32_t status = fits ? (n_sel <= a.n_slots || a.n_slots == 0 ? 0u : 2u) : 1u;
+    const uint32_t status = (fits ? (n_sel <= a.n_slots || a.n_slots == 0 ? 0u : 2u) : 1u) | (refuse ? 4u : 0u);
     if (tid == 0) {
         a.info[0] = n_sel;
         a.info[1] = total;
         a.info[2] = n_stage;
         a.info[3] = status;
+        a.info[4] = a.stage_out ? (n_out < a.cap ? n_out : a.cap) : 0u;
+        a.info[5] = 0u;
+        a.info[6] = 0u;
+        a.info[7] = 0u;
     }
     return status ? 0u : n_stage;
 }

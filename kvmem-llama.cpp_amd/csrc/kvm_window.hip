@@ -59,6 +59,9 @@ extern "C" int kvm_window_reset(kvm_state *st, const kvm_window *w) {
     if (w->shadow_rows)
         hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
                            (int32_t *)w->shadow_rows, 0, n_slots);
+    if (w->pending_rows)
+        hipLaunchKernelGGL(k_fill_i32, dim3(kvm_cdiv(n_slots, 256)), dim3(256), 0, st->stream,
+                           (int32_t *)w->pending_rows, 0, n_slots);
     KVM_LAUNCH_CHECK(st, "window_reset");
     return KVM_OK;
 }
@@ -178,6 +181,27 @@ __global__ void k_copy_i32(int32_t *dst, const int32_t *src, uint32_t n) {
     if (i < n) dst[i] = src[i];
 }
 
+// The unharvested-row count of every slot that cells [cell0, cell0 + n) touch:
+// raised by the rows an import writes there (add), lowered by the rows a
+// harvest takes into the host history (sub, not below zero).  One thread per
+// slot.
+__global__ void k_pending_rows(uint32_t *pending, uint32_t bt, uint32_t n_slots, uint32_t cell0, uint32_t n,
+                               int add) {
+    const uint32_t slot = cell0 / bt + blockIdx.x * blockDim.x + threadIdx.x;
+    if (slot >= n_slots || slot * bt >= cell0 + n) return;
+    const uint32_t lo = slot * bt > cell0 ? slot * bt : cell0;
+    const uint32_t hi = (slot + 1) * bt < cell0 + n ? (slot + 1) * bt : cell0 + n;
+    const uint32_t cnt = hi - lo, cur = pending[slot];
+    pending[slot] = add ? cur + cnt : (cur > cnt ? cur - cnt : 0u);
+}
+
+static void pending_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n, bool add) {
+    const uint32_t bt = w->block_tokens, n_slots = w->n_cells / bt;
+    const uint32_t touched = (cell0 + n - 1) / bt - cell0 / bt + 1;
+    hipLaunchKernelGGL(k_pending_rows, dim3(kvm_cdiv(touched, 256)), dim3(256), 0, st->stream, w->pending_rows,
+                       bt, n_slots, cell0, n, add ? 1 : 0);
+}
+
 extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0,
                                       uint32_t n, const void *k_rows, const void *v_rows,
                                       const int32_t *pos) {
@@ -218,6 +242,7 @@ extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32
     if (pos)
         hipLaunchKernelGGL(k_copy_i32, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream,
                            w->cell_pos + cell0, pos, n);
+    if (w->pending_rows && (k_rows || v_rows)) pending_rows(st, w, cell0, n, true);
     KVM_LAUNCH_CHECK(st, "import_rows");
     return KVM_OK;
 }
@@ -613,6 +638,12 @@ extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t ce
     }
     KVM_HIP(st, hipMemcpyAsync(k_raw_rows, stage, kb, hipMemcpyDeviceToHost, st->stream));
     KVM_HIP(st, hipMemcpyAsync(v_rows, stage + kb, vb, hipMemcpyDeviceToHost, st->stream));
+    // the rows are in the host history once the copies are done (stream
+    // order): later plans on this stream may overwrite their slots
+    if (w->pending_rows) {
+        pending_rows(st, w, cell0, n, false);
+        KVM_LAUNCH_CHECK(st, "harvest");
+    }
     return KVM_OK;
 }
 

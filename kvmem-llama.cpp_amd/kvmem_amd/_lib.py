@@ -33,7 +33,7 @@ class Window(C.Structure):
                 ("block_tokens", C.c_uint32), ("k_type", C.c_int32), ("v_type", C.c_int32),
                 ("k", C.c_void_p), ("v", C.c_void_p), ("cell_pos", C.c_void_p),
                 ("slot_block", C.c_void_p), ("slot_base", C.c_void_p),
-                ("k_shadow", C.c_void_p), ("shadow_rows", C.c_void_p)]
+                ("k_shadow", C.c_void_p), ("shadow_rows", C.c_void_p), ("pending_rows", C.c_void_p)]
 
 
 class QueryAcc(C.Structure):
@@ -61,7 +61,7 @@ class SelectParams(C.Structure):
 class Selection(C.Structure):
     _fields_ = [("cap", C.c_uint32), ("scores", C.c_void_p), ("ids", C.c_void_p),
                 ("to_base", C.c_void_p), ("stage_slots", C.c_void_p), ("info", C.c_void_p),
-                ("stage_src", C.c_void_p)]
+                ("stage_src", C.c_void_p), ("stage_out", C.c_void_p)]
 
 
 class RetrievalLane(C.Structure):

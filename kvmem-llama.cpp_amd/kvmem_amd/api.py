@@ -123,9 +123,11 @@ class KVWindow:
     """Bounded GPU window of one attention layer in the library's tiled layout."""
 
     def __init__(self, st, n_cells, n_head_kv, head_dim, block_tokens=128,
-                 k_type=L.T_Q8_0, v_type=L.T_Q4_0, shadow=False):
+                 k_type=L.T_Q8_0, v_type=L.T_Q4_0, shadow=False, pending=False):
         """shadow: keep an HBM copy of the staged blocks' raw K rows, so that a
-        later plan re-bases resident blocks from HBM instead of the host."""
+        later plan re-bases resident blocks from HBM instead of the host.
+        pending: count each slot's imported rows not yet harvested, so that a
+        plan that would overwrite them is refused."""
         self.st = st
         dev = torch.device("cuda", st.device)
         self.c = L.Window(n_cells, n_head_kv, head_dim, block_tokens, k_type, v_type)
@@ -149,6 +151,10 @@ class KVWindow:
             self.shadow_rows = torch.zeros((n_slots,), dtype=torch.int32, device=dev)
             self.c.k_shadow = self.k_shadow.data_ptr()
             self.c.shadow_rows = self.shadow_rows.data_ptr()
+        self.pending_rows = None
+        if pending:
+            self.pending_rows = torch.zeros((n_slots,), dtype=torch.int32, device=dev)
+            self.c.pending_rows = self.pending_rows.data_ptr()
         st.check(st.lib.kvm_window_check(C.byref(self.c)))
         self.n_cells, self.n_head_kv, self.head_dim = n_cells, n_head_kv, head_dim
         self.block_tokens, self.k_type, self.v_type = block_tokens, k_type, v_type
@@ -270,10 +276,12 @@ class SelectionBuffers:
         self.ids = torch.zeros((cap,), dtype=torch.int32, device=dev)
         self.to_base = torch.zeros((cap,), dtype=torch.int32, device=dev)
         self.stage_slots = torch.zeros((cap,), dtype=torch.int32, device=dev)
-        self.info = torch.zeros((4,), dtype=torch.int32, device=dev)
+        self.info = torch.zeros((8,), dtype=torch.int32, device=dev)
         self.stage_src = torch.full((cap,), -1, dtype=torch.int32, device=dev)
+        self.stage_out = torch.full((cap,), -1, dtype=torch.int32, device=dev)
         self.c = L.Selection(cap, self.scores.data_ptr(), self.ids.data_ptr(), self.to_base.data_ptr(),
-                             self.stage_slots.data_ptr(), self.info.data_ptr(), self.stage_src.data_ptr())
+                             self.stage_slots.data_ptr(), self.info.data_ptr(), self.stage_src.data_ptr(),
+                             self.stage_out.data_ptr())
 
     def result(self):
         info = self.info.cpu().numpy().astype(np.int64)
@@ -282,6 +290,7 @@ class SelectionBuffers:
                 "to_base": self.to_base[:n].cpu().numpy().astype(np.int64),
                 "total": int(info[1]), "stage_slots": self.stage_slots[:int(info[2])].cpu().numpy(),
                 "stage_src": self.stage_src[:int(info[2])].cpu().numpy(),
+                "stage_out": self.stage_out[:int(info[4])].cpu().numpy().astype(np.int64),
                 "status": int(info[3])}
 
 

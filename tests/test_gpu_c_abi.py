@@ -19,4 +19,4 @@ def test_c_caller_decodes_through_the_abi(tmp_path):
         subprocess.run(["sh", os.path.join(HERE, "c", "build.sh"), exe], check=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
-    assert r.stdout.startswith("ok "), r.stdout
+    assert r.stdout.startswith("ok ") and "ok step on the caller's stream" in r.stdout, r.stdout

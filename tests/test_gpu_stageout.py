@@ -94,3 +94,96 @@ def test_harvest_then_restage(kvm_state):
     ek, ev = w.export_rows(3 * bt, bt)
     assert np.array_equal(host(ek).reshape(-1), O.stagein_k(want_k.reshape(-1), bt, H, D, 64, 256, 3 * bt, theta))
     assert np.array_equal(host(ev), gv)
+
+
+def test_plan_refuses_to_overwrite_unharvested_rows(kvm_state):
+    """Stage-out before stage-in (apply_plan_to_kv: harvest_gpu_v of every
+    stage_out block, then spill_outgoing and admit_incoming,
+    llama-memory-kvmem.cpp:1811-1857, kvmem_runtime.cpp:225-249): a window that
+    counts its unharvested rows refuses a plan that would overwrite a slot
+    holding generated rows (info[3] bit 2, window untouched, stage_out still
+    listing the blocks that leave); after the harvest the same selection
+    stages, byte-equal to a fresh stage-in into a window without tracking."""
+    st = kvm_state
+    rng = np.random.default_rng(33)
+    H, D, bt, n_blocks = 4, 256, 128, 12
+    kr, vr = rand_rows(rng, n_blocks * bt, H, D, L.T_Q8_0, L.T_Q4_0)
+    hist = api.History(kr, vr)
+    nt = dev(np.full(n_blocks, bt, np.int32))
+    w = api.KVWindow(st, 6 * bt, H, D, bt, pending=True)
+
+    def scores(chosen):
+        s = np.zeros(n_blocks)
+        s[list(chosen)] = 1.0 + np.arange(len(chosen))
+        return dev(s)
+    # the first plan: blocks 0 (sink), 3, 5, 7 in slots 0..3
+    sel = api.select_topk(st, scores([3, 5, 7]), nt, 4, 1, 0, None, window=w)
+    api.stagein_selection(st, hist, w, sel, 64, 1e7)
+    r = sel.result()
+    assert list(r["ids"]) == [0, 3, 5, 7] and r["status"] == 0 and len(r["stage_out"]) == 0
+    # a generated block's rows in slot 4 (window positions 512..639), not harvested
+    gk, gv = rand_rows(rng, bt, H, D, L.T_Q8_0, L.T_Q4_0)
+    w.import_rows(4 * bt, dev(gk), dev(gv), dev(np.arange(4 * bt, 5 * bt, dtype=np.int32)))
+    assert host(w.pending_rows).tolist() == [0, 0, 0, 0, bt, 0]
+    before = {k: getattr(w, k).clone() for k in ("k", "v", "cell_pos", "slot_block", "slot_base")}
+    # a plan of five blocks: block 3 leaves, and slot 4 would be overwritten
+    want = [0, 5, 7, 9, 11]
+    sel = api.select_topk(st, scores([5, 7, 9, 11]), nt, 5, 1, 0, None, window=w)
+    api.stagein_selection(st, hist, w, sel, 64, 1e7)
+    r = sel.result()
+    assert list(r["ids"]) == want
+    assert r["status"] & 4, r["status"]
+    assert list(r["stage_out"]) == [3]
+    for k, v in before.items():
+        assert torch.equal(getattr(w, k), v), k
+    # the harvest takes the generated rows into the host history (as block 11
+    # here, whose rows the test then restores), and the plan stages
+    cap = torch.from_numpy(rng.standard_normal((bt, H, D)).astype(np.float32)).cuda()
+    hk = np.zeros((bt, w.k_row_bytes()), np.uint8)
+    hv = np.zeros((bt, w.v_row_bytes()), np.uint8)
+    hk_buf, hv_buf = api.HostBuffer(hk.nbytes), api.HostBuffer(hv.nbytes)
+    api.harvest_block(st, w, 4 * bt, bt, cap, 0, hk_buf.u8, hv_buf.u8)
+    st.sync()
+    assert host(w.pending_rows).tolist() == [0] * 6
+    assert np.array_equal(hv_buf.u8.reshape(bt, -1), gv)
+    sel = api.select_topk(st, scores([5, 7, 9, 11]), nt, 5, 1, 0, None, window=w)
+    api.stagein_selection(st, hist, w, sel, 64, 1e7)
+    r = sel.result()
+    assert list(r["ids"]) == want and r["status"] == 0 and list(r["stage_out"]) == [3]
+    fresh = api.KVWindow(st, 6 * bt, H, D, bt)
+    sf = api.select_topk(st, scores([5, 7, 9, 11]), nt, 5, 1, 0, None, window=fresh)
+    api.stagein_selection(st, hist, fresh, sf, 64, 1e7)
+    st.sync()
+    for k in ("cell_pos", "slot_block", "slot_base"):
+        assert torch.equal(getattr(w, k)[:5 * bt if k == "cell_pos" else 5], getattr(fresh, k)[:5 * bt if k == "cell_pos" else 5]), k
+    ka, va = w.export_rows(0, 5 * bt)
+    kb, vb = fresh.export_rows(0, 5 * bt)
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+def test_stage_out_lists_the_blocks_that_leave(kvm_state):
+    """stage_out = the blocks the plan's slots held that the new selection
+    drops, ascending (KvMemStore::set_selection's stage_out for GPU-resident
+    blocks, kvmem_store.cpp:789-795), against the set difference."""
+    st = kvm_state
+    rng = np.random.default_rng(34)
+    n_blocks, budget, bt = 40, 12, 128
+    nt = dev(np.full(n_blocks, bt, np.int32))
+    w = api.KVWindow(st, 16 * bt, 2, 128, bt, L.T_F16, L.T_F16)
+    prev = None
+    for step in range(6):
+        s = rng.standard_normal(n_blocks)
+        sel = api.select_topk(st, dev(s), nt, budget, 1, 1, None, window=w)
+        r = sel.result()
+        held = [int(b) for b in host(w.slot_block)[:budget] if 0 <= int(b) < n_blocks]
+        want = sorted(set(held) - set(int(i) for i in r["ids"]))
+        assert list(r["stage_out"]) == want, (step, list(r["stage_out"]), want)
+        # the window takes the plan's layout as a stage-in would (slot map only)
+        ids, tb = r["ids"], r["to_base"]
+        sb = np.full(16, -1, np.int32)
+        sbase = np.full(16, -1, np.int32)
+        sb[:len(ids)], sbase[:len(ids)] = ids, tb
+        w.slot_block.copy_(dev(sb))
+        w.slot_base.copy_(dev(sbase))
+        prev = r
+    assert prev is not None
