@@ -134,10 +134,14 @@ typedef struct kvm_window {
      * and kvm_slot_copy_from_host void that slot's shadow (shadow_rows = 0). */
     void *k_shadow;         /* device [n_cells][n_head_kv * row(head_dim)] of q8_0 */
     uint32_t *shadow_rows;  /* device [n_slots]: rows of the slot the shadow holds */
-    /* Optional (NULL = not tracked): per slot the rows imported into its cells
-     * (generated tokens, kvm_window_import_rows) that no kvm_harvest_block has
-     * taken into the host history since.  A plan that would overwrite such a
-     * slot is refused (kvm_selection info[3] bit 2): the reference harvests
+    /* Optional (NULL = not tracked): per slot the end, in rows from the slot's
+     * first cell, of the rows imported into its cells (generated tokens,
+     * kvm_window_import_rows) that no kvm_harvest_block has taken into the
+     * host history since; 0 = none.  An import raises it to the end of its
+     * rows in the slot (importing the same cells again adds nothing), a
+     * harvest whose cells reach it clears it, and so does
+     * kvm_slot_copy_from_host.  A plan that would overwrite a slot with a
+     * nonzero count is refused (kvm_selection info[3] bit 2): the reference harvests
      * the outgoing blocks' generated rows before it spills them and admits
      * the stage-in (apply_plan_to_kv, llama-memory-kvmem.cpp:1811-1857,
      * KvMemRuntime::spill_outgoing / admit_incoming, kvmem_runtime.cpp:225-249). */
@@ -157,7 +161,8 @@ int kvm_window_reset(kvm_state *st, const kvm_window *w);
  * sets their positions (pos: device int32[n], NULL = leave cell_pos alone).
  * k_rows / v_rows: device (or pinned host) rows of w->k_type / w->v_type.
  * This is the cpy of new K/V rows into cache cells (llama-kvmem-batch.cpp:42-50).
- * With w->pending_rows, every slot the cells touch counts the rows written. */
+ * With w->pending_rows, every slot the cells touch records the end of the rows
+ * written (see kvm_window.pending_rows). */
 int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                            const void *k_rows, const void *v_rows, const int32_t *pos);
 /* Inverse of import: ggml rows of cells [cell0, cell0+n).  Used by stage-out
@@ -303,8 +308,8 @@ int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, u
  * k_raw_rows / v_rows (host: the history rows of the tokens' positions).
  * When ix is given the same K rows are added to its layer il at pos0
  * (write_layer_mean_k).  q8_0 K windows; the copies are done when the state's
- * stream reaches this point (kvm_state_sync).  With w->pending_rows, the
- * slots the cells touch count n fewer unharvested rows (not below zero). */
+ * stream reaches this point (kvm_state_sync).  With w->pending_rows, a slot
+ * whose recorded end the cells reach is clear again. */
 int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                       const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,
                       const kvm_meank_index *ix, uint32_t il, uint32_t pos0);
@@ -355,9 +360,10 @@ typedef struct kvm_row_range {
 
 /* llama_memory_kvmem::retrieval_mandatory (llama-memory-kvmem.cpp:4306-4325): the
  * block ids a retrieval must keep, for kvm_select_params.mandatory.  The ranges
- * are the turn's explicit mandatory spans when n_spans > 0, else the query span
- * [query_begin, query_end > 0 ? query_end : store end) when query_begin >= 0,
- * else none; every block overlapping a range is listed once, in block order;
+ * are the turn's explicit mandatory spans when spans is not NULL (the turn set
+ * its spans, explicit_spans_; n_spans may be 0: then no range), else the query
+ * span [query_begin, query_end > 0 ? query_end : store end) when
+ * query_begin >= 0, else none; every block overlapping a range is listed once, in block order;
  * then the block containing force_pos (KvMemStore::block_id_containing,
  * kvmem/src/host/kvmem_store.cpp:158-177) is appended when force_pos >= 0 lies
  * inside the store, even if already listed (the top-k counts each id once).

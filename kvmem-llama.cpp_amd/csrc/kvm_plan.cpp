@@ -17,11 +17,12 @@ extern "C" int kvm_retrieval_mandatory(kvm_state *st, const uint32_t *n_tokens, 
     *n_ids = 0;
     int64_t total = 0;
     for (uint32_t b = 0; b < n_blocks; ++b) total += n_tokens[b];
-    // the explicit mandatory spans when the turn has them, else the query span
+    // the turn's explicit mandatory spans (spans != NULL, possibly none), else
+    // the query span (the reference's explicit_spans_ test)
     kvm_row_range query{query_begin, query_end > 0 ? query_end : (int32_t)(total < INT32_MAX ? total : INT32_MAX)};
     const kvm_row_range *rg = spans;
-    uint32_t nr = n_spans;
-    if (nr == 0 && query_begin >= 0) {
+    uint32_t nr = spans ? n_spans : 0u;
+    if (!spans && query_begin >= 0) {
         rg = &query;
         nr = 1;
     }

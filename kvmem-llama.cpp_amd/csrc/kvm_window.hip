@@ -185,21 +185,29 @@ __global__ void k_copy_i32(int32_t *dst, const int32_t *src, uint32_t n) {
 // raised by the rows an import writes there (add), lowered by the rows a
 // harvest takes into the host history (sub, not below zero).  One thread per
 // slot.
+// Per touched slot: the end (rows from the slot's first cell) of the rows
+// imported since the last harvest that reached them.  An import raises it to
+// the end of its rows in the slot (a re-import of the same cells, e.g. after
+// rejected draft tokens, adds nothing); a harvest whose cells reach that end
+// clears it; a copy of the slot from the host clears it.
+enum pending_op { PENDING_IMPORT = 0, PENDING_HARVEST = 1, PENDING_CLEAR = 2 };
 __global__ void k_pending_rows(uint32_t *pending, uint32_t bt, uint32_t n_slots, uint32_t cell0, uint32_t n,
-                               int add) {
+                               int op) {
     const uint32_t slot = cell0 / bt + blockIdx.x * blockDim.x + threadIdx.x;
     if (slot >= n_slots || slot * bt >= cell0 + n) return;
-    const uint32_t lo = slot * bt > cell0 ? slot * bt : cell0;
     const uint32_t hi = (slot + 1) * bt < cell0 + n ? (slot + 1) * bt : cell0 + n;
-    const uint32_t cnt = hi - lo, cur = pending[slot];
-    pending[slot] = add ? cur + cnt : (cur > cnt ? cur - cnt : 0u);
+    const uint32_t end = hi - slot * bt, cur = pending[slot];
+    if (op == PENDING_IMPORT)
+        pending[slot] = end > cur ? end : cur;
+    else if (op == PENDING_CLEAR || end >= cur)
+        pending[slot] = 0u;
 }
 
-static void pending_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n, bool add) {
+static void pending_rows(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n, pending_op op) {
     const uint32_t bt = w->block_tokens, n_slots = w->n_cells / bt;
     const uint32_t touched = (cell0 + n - 1) / bt - cell0 / bt + 1;
     hipLaunchKernelGGL(k_pending_rows, dim3(kvm_cdiv(touched, 256)), dim3(256), 0, st->stream, w->pending_rows,
-                       bt, n_slots, cell0, n, add ? 1 : 0);
+                       bt, n_slots, cell0, n, (int)op);
 }
 
 extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32_t cell0,
@@ -242,7 +250,7 @@ extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32
     if (pos)
         hipLaunchKernelGGL(k_copy_i32, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream,
                            w->cell_pos + cell0, pos, n);
-    if (w->pending_rows && (k_rows || v_rows)) pending_rows(st, w, cell0, n, true);
+    if (w->pending_rows && (k_rows || v_rows)) pending_rows(st, w, cell0, n, PENDING_IMPORT);
     KVM_LAUNCH_CHECK(st, "import_rows");
     return KVM_OK;
 }
@@ -569,6 +577,8 @@ extern "C" int kvm_slot_copy_from_host(kvm_state *st, const kvm_window *const *l
         rc = kvm_window_import_rows(st, w, (uint32_t)slot * w->block_tokens, w->block_tokens, stage + off,
                                     stage + off + kspan, nullptr);
         if (rc) return rc;
+        if (w->pending_rows)   // the slot now equals its host copy: nothing to harvest
+            pending_rows(st, w, (uint32_t)slot * w->block_tokens, w->block_tokens, PENDING_CLEAR);
         off += span;
     }
     KVM_HIP(st, hipStreamSynchronize(st->stream));
@@ -641,7 +651,7 @@ extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t ce
     // the rows are in the host history once the copies are done (stream
     // order): later plans on this stream may overwrite their slots
     if (w->pending_rows) {
-        pending_rows(st, w, cell0, n, false);
+        pending_rows(st, w, cell0, n, PENDING_HARVEST);
         KVM_LAUNCH_CHECK(st, "harvest");
     }
     return KVM_OK;

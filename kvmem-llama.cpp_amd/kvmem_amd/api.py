@@ -391,16 +391,18 @@ def harvest_block(st, window, cell0, n, k_prerope, tok0, k_raw_rows, v_rows, ind
     st.sync()
 
 
-def retrieval_mandatory(n_tokens, spans=(), query_begin=-1, query_end=0, force_pos=-1):
+def retrieval_mandatory(n_tokens, spans=None, query_begin=-1, query_end=0, force_pos=-1):
     """Mandatory block ids of a retrieval (kvm_retrieval_mandatory): n_tokens is
-    the host per-block token count, spans (begin, end) row ranges."""
+    the host per-block token count, spans the turn's explicit (begin, end) row
+    ranges (None = the turn set none: the query span applies; [] = explicit and
+    empty)."""
     lib = L.load()
     nt = np.ascontiguousarray(n_tokens, np.uint32)
-    arr = (L.RowRange * max(len(spans), 1))(*[L.RowRange(int(b), int(e)) for b, e in spans])
+    arr = None if spans is None else (L.RowRange * max(len(spans), 1))(*[L.RowRange(int(b), int(e)) for b, e in spans])
     out = np.zeros(nt.size + 1, np.uint32)
     n = L._u32(0)
-    rc = lib.kvm_retrieval_mandatory(None, nt.ctypes.data, nt.size, arr, len(spans), query_begin, query_end,
-                                     force_pos, out.ctypes.data, out.size, C.byref(n))
+    rc = lib.kvm_retrieval_mandatory(None, nt.ctypes.data, nt.size, arr, 0 if spans is None else len(spans),
+                                     query_begin, query_end, force_pos, out.ctypes.data, out.size, C.byref(n))
     if rc:
         raise L.KvmError(rc, "kvm_retrieval_mandatory")
     return out[:n.value].astype(np.int64)

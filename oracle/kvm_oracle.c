@@ -411,7 +411,8 @@ uint32_t oracle_window_layout(const uint32_t *sel, uint32_t n_sel, const uint32_
 
 /* ------------------------------------------------------------------------- */
 /* Mandatory blocks of a retrieval (llama-memory-kvmem.cpp:4306-4325): the     */
-/* ranges are the explicit mandatory spans when given, else the query span     */
+/* ranges are the explicit mandatory spans when explicit_spans (even none),    */
+/* else the query span                                                          */
 /* [query_begin, query_end > 0 ? query_end : total) when query_begin >= 0;     */
 /* every block overlapping a range, once, in block order; then the block       */
 /* containing force_pos (KvMemStore::block_id_containing, kvmem_store.cpp:     */
@@ -419,14 +420,14 @@ uint32_t oracle_window_layout(const uint32_t *sel, uint32_t n_sel, const uint32_
 /* Block b covers [sum_{i<b} n_tokens_i, + n_tokens_b).  Returns the count.    */
 /* ------------------------------------------------------------------------- */
 uint32_t oracle_retrieval_mandatory(const uint32_t *n_tokens, uint32_t n_blocks, const int32_t *ranges,
-                                    uint32_t n_ranges, int32_t query_begin, int32_t query_end,
-                                    int32_t force_pos, uint32_t *out) {
+                                    uint32_t n_ranges, int explicit_spans, int32_t query_begin,
+                                    int32_t query_end, int32_t force_pos, uint32_t *out) {
     int64_t total = 0;
     for (uint32_t b = 0; b < n_blocks; ++b) total += n_tokens[b];
     int32_t qr[2];
     const int32_t *rg = ranges;
-    uint32_t nr = n_ranges;
-    if (nr == 0 && query_begin >= 0) {
+    uint32_t nr = explicit_spans ? n_ranges : 0u;
+    if (!explicit_spans && query_begin >= 0) {
         qr[0] = query_begin;
         qr[1] = query_end > 0 ? query_end : (int32_t)total;
         rg = qr;

@@ -98,10 +98,12 @@ uint32_t oracle_window_layout(const uint32_t *sel, uint32_t n_sel, const uint32_
                               int32_t *cell_pos);
 
 /* ---- mandatory block ids from row ranges and force_pos (retrieval_mandatory) ----
- * ranges: n_ranges pairs (begin, end); out holds n_blocks + 1 ids; returns the count. */
+ * ranges: n_ranges pairs (begin, end), used when explicit_spans (the turn set its
+ * spans; none is then no range), else the query span; out holds n_blocks + 1 ids;
+ * returns the count. */
 uint32_t oracle_retrieval_mandatory(const uint32_t *n_tokens, uint32_t n_blocks, const int32_t *ranges,
-                                    uint32_t n_ranges, int32_t query_begin, int32_t query_end,
-                                    int32_t force_pos, uint32_t *out);
+                                    uint32_t n_ranges, int explicit_spans, int32_t query_begin,
+                                    int32_t query_end, int32_t force_pos, uint32_t *out);
 
 /* ---- flash attention over a ggml-layout KV window ------------------------------
  * q        [n_tokens][n_head][head_dim] fp32

@@ -53,7 +53,7 @@ def lib():
             "oracle_fa_ggml": (C.c_int, [C.c_int, C.c_int, P, P, P, P, P] + [C.c_int] * 5 + [f, P, C.c_int]),
             "oracle_fa_f64": (C.c_int, [C.c_int, C.c_int, P, P, P, P, P] + [C.c_int] * 5 + [d, P, C.c_int]),
             "oracle_quant_q8_0_rows": (None, [P, P, i64, i64]),
-            "oracle_retrieval_mandatory": (u32, [P, u32, P, u32, i32, i32, i32, P]),
+            "oracle_retrieval_mandatory": (u32, [P, u32, P, u32, i32, i32, i32, i32, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_o, name)
@@ -227,14 +227,15 @@ def fa_f64(k_type, v_type, q, k_rows, v_rows, cell_pos, q_pos, n_head, n_head_kv
     return out
 
 
-def retrieval_mandatory(n_tokens, ranges=(), query_begin=-1, query_end=0, force_pos=-1):
+def retrieval_mandatory(n_tokens, ranges=None, query_begin=-1, query_end=0, force_pos=-1):
     """Mandatory block ids (llama-memory-kvmem.cpp:4306-4325) of a store whose
-    block b holds n_tokens[b] consecutive positions."""
+    block b holds n_tokens[b] consecutive positions; ranges None = the turn set
+    no explicit spans (the query span applies), [] = explicit and empty."""
     nt = np.ascontiguousarray(n_tokens, np.uint32)
-    rg = np.ascontiguousarray(np.asarray(ranges, dtype=np.int32).reshape(-1, 2))
+    rg = np.ascontiguousarray(np.asarray([] if ranges is None else ranges, dtype=np.int32).reshape(-1, 2))
     out = np.zeros(nt.size + 1, np.uint32)
-    n = lib().oracle_retrieval_mandatory(_p(nt), nt.size, _p(rg) if rg.size else None, rg.shape[0], query_begin,
-                                         query_end, force_pos, _p(out))
+    n = lib().oracle_retrieval_mandatory(_p(nt), nt.size, _p(rg) if rg.size else None, rg.shape[0],
+                                         0 if ranges is None else 1, query_begin, query_end, force_pos, _p(out))
     return out[:n].astype(np.int64)
 
 

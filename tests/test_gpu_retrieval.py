@@ -294,9 +294,9 @@ def test_topk_with_mandatory_blocks_from_row_ranges(kvm_state):
     total = int(nt.sum())
     scores = rng.standard_normal(n_blocks)
     cases = [([(1000, 1900), (30000, 30100)], -1, 0, 5000),     # explicit spans + force_pos
-             ([], 36000, 0, -1),                                 # query span to the store's end
+             (None, 36000, 0, -1),                               # query span to the store's end
              ([(0, total)], -1, 0, 100),                         # every block mandatory: trimmed to the budget
-             ([], -1, 0, total - 1)]                             # force_pos alone, in the partial last block
+             ([], 36000, 0, total - 1)]                          # explicit, empty spans: force_pos alone
     for spans, qb, qe, fp in cases:
         mand = api.retrieval_mandatory(nt, spans, qb, qe, fp)
         want = O.pick_topk(scores, budget, 1, 2, mandatory=mand)

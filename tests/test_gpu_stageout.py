@@ -161,6 +161,41 @@ def test_plan_refuses_to_overwrite_unharvested_rows(kvm_state):
     assert torch.equal(ka, kb) and torch.equal(va, vb)
 
 
+def test_pending_rows_record_the_end_of_the_imported_rows(kvm_state):
+    """A slot's pending count is the end of its unharvested imported rows: a
+    re-import of the same cells (rows rewritten after rejected draft tokens)
+    adds nothing, a harvest that stops short of the end leaves it, one that
+    reaches it clears it, and a copy of the slot from the host clears it."""
+    st = kvm_state
+    rng = np.random.default_rng(35)
+    H, D, bt = 4, 256, 128
+    w = api.KVWindow(st, 4 * bt, H, D, bt, pending=True)
+
+    def imp(c0, n):
+        kr, vr = rand_rows(rng, n, H, D, L.T_Q8_0, L.T_Q4_0)
+        w.import_rows(c0, dev(kr), dev(vr), dev(np.arange(c0, c0 + n, dtype=np.int32)))
+
+    def harvest(c0, n):
+        cap = torch.from_numpy(rng.standard_normal((n, H, D)).astype(np.float32)).cuda()
+        hk, hv = api.HostBuffer(n * w.k_row_bytes()), api.HostBuffer(n * w.v_row_bytes())
+        api.harvest_block(st, w, c0, n, cap, 0, hk.u8, hv.u8)
+
+    pend = lambda: host(w.pending_rows).tolist()
+    imp(bt + 2, 3)
+    assert pend() == [0, 5, 0, 0]
+    imp(bt + 2, 3)
+    assert pend() == [0, 5, 0, 0]
+    imp(bt - 3, 15)                        # across the slot boundary
+    assert pend() == [bt, 12, 0, 0]
+    harvest(bt, 5)                         # stops short of row 12
+    assert pend() == [bt, 12, 0, 0]
+    harvest(bt + 5, 7)
+    assert pend() == [bt, 0, 0, 0]
+    blob = api.slot_copy_to_host(st, [w], 0)
+    api.slot_copy_from_host(st, [w], 0, blob)
+    assert pend() == [0, 0, 0, 0]
+
+
 def test_stage_out_lists_the_blocks_that_leave(kvm_state):
     """stage_out = the blocks the plan's slots held that the new selection
     drops, ascending (KvMemStore::set_selection's stage_out for GPU-resident

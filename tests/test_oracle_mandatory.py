@@ -15,8 +15,8 @@ def _brute(n_tokens, spans, query_begin, query_end, force_pos):
     """Position by position: a block is mandatory if any position it holds lies in a range."""
     starts = np.concatenate([[0], np.cumsum(n_tokens)[:-1]]).astype(np.int64)
     total = int(np.sum(n_tokens))
-    ranges = list(spans) if spans else ([(query_begin, query_end if query_end > 0 else total)]
-                                       if query_begin >= 0 else [])
+    ranges = list(spans) if spans is not None else ([(query_begin, query_end if query_end > 0 else total)]
+                                                    if query_begin >= 0 else [])
     ids = [b for b, (s, n) in enumerate(zip(starts, n_tokens))
            if any(any(r0 <= p < r1 for r0, r1 in ranges) for p in range(s, s + n))]
     if 0 <= force_pos < total:
@@ -27,15 +27,20 @@ def _brute(n_tokens, spans, query_begin, query_end, force_pos):
 KATS = [
     # (n_tokens, spans, query_begin, query_end, force_pos, expected)
     ([128] * 10 + [77], [(200, 300)], -1, 0, 1000, [1, 2, 7]),
-    ([128] * 10 + [77], [], 1200, 0, -1, [9, 10]),              # query span to the store's end
-    ([128] * 10 + [77], [], 1200, 1290, 5, [9, 10, 0]),
+    ([128] * 10 + [77], None, 1200, 0, -1, [9, 10]),            # query span to the store's end
+    ([128] * 10 + [77], None, 1200, 1290, 5, [9, 10, 0]),
     ([128] * 10 + [77], [(0, 1), (1279, 1290)], -1, 0, 5000, [0, 9, 10]),   # force_pos past the end: none
     ([128] * 4, [(128, 128)], 5, 0, 130, [1]),                  # empty span; spans override the query span
     ([128] * 4, [(100, 140)], -1, 0, 130, [0, 1, 1]),           # force_pos block listed again
     ([], [(0, 10)], 0, 0, 0, []),
     # an inverted query span: the reference's overlap test (block end > begin and
     # block start < end) still keeps the block that straddles it
-    ([128] * 10, [], 950, 930, -1, [7]),
+    ([128] * 10, None, 950, 930, -1, [7]),
+    # the turn set explicit spans, none of them mandatory: the query span does
+    # not stand in (explicit_spans_ with an empty turn_spans_.mandatory), only
+    # the force_pos block is kept
+    ([128] * 4, [], 5, 0, 130, [1]),
+    ([128] * 4, [], 5, 0, -1, []),
 ]
 
 
@@ -57,9 +62,10 @@ def test_oracle_on_the_reference_store_layout():
         starts, nt, containing = O.ref_block_layout(appends, 128, pos)
         assert np.array_equal(starts, np.concatenate([[0], np.cumsum(nt)[:-1]]))
         for p, c in zip(pos, containing):                       # force_pos alone
-            got = O.retrieval_mandatory(nt, [], -1, 0, int(p))
+            got = O.retrieval_mandatory(nt, None, -1, 0, int(p))
             assert list(got) == ([] if c < 0 else [c])
         spans = [tuple(sorted(rng.integers(-3, int(appends.sum()) + 3, 2))) for _ in range(rng.integers(0, 4))]
+        spans = None if not spans and rng.random() < 0.5 else spans
         qb, fp = int(rng.integers(-1, 300)), int(pos[0])
         qe = int(rng.integers(qb, 600)) if qb >= 0 and rng.random() < 0.7 else 0
         assert np.array_equal(O.retrieval_mandatory(nt, spans, qb, qe, fp), _brute(nt, spans, qb, qe, fp))
@@ -74,6 +80,7 @@ def test_library_matches_oracle():
             nt[-1] = rng.integers(1, 129)
         total = int(nt.sum())
         spans = [tuple(sorted(rng.integers(-10, total + 10, 2))) for _ in range(rng.integers(0, 5))]
+        spans = None if not spans and rng.random() < 0.5 else spans
         qb, qe, fp = int(rng.integers(-2, total + 2)), int(rng.integers(-1, total + 2)), int(rng.integers(-2, total + 3))
         want = O.retrieval_mandatory(nt, spans, qb, qe, fp)
         assert np.array_equal(api.retrieval_mandatory(nt, spans, qb, qe, fp), want)
