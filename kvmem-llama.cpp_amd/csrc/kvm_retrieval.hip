@@ -288,12 +288,15 @@ struct score_lanes {
 
 template <int D>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
-    const score_args &a = sl.lane[blockIdx.z];
+    // one copy of the lane's arguments: its scalar loads are issued together
+    // ahead of the first branch, not one round trip per field
+    const score_args a = sl.lane[blockIdx.z];
+    asm volatile("" ::"s"(a.q_sum), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
     const uint32_t tile = blockIdx.x, il = blockIdx.y;
     if (tile >= a.n_tiles_used || il >= a.n_layer) return;
     __shared__ __align__(16) score_wg_lds<D, 4> L;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const uint32_t g = a.n_head / a.H, qc = a.q_count[il];
+    const uint32_t g = a.g, qc = a.q_count[il];
     score_regs r;
     if ((uint32_t)w < a.H) score_tile_load<D>(a, il, tile, (uint32_t)w, g, r);
     if (qc == 0) return;                 // a layer without queries: skipped by the reduction
@@ -439,7 +442,7 @@ void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes,
         const uint32_t used = r.p->n_blocks ? kvm_cdiv(r.p->n_blocks, KVM_MEANK_TILE) : 0u;
         out[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, (double *)tl.lane[i].layer_score,
                             r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
-                            r.q->n_head, ix->n_head_kv, used};
+                            r.q->n_head, ix->n_head_kv, used, r.q->n_head / ix->n_head_kv};
     }
 }
 

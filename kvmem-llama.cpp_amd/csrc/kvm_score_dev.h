@@ -28,6 +28,7 @@ struct score_args {
     double *layer_score;    // [n_layer][cap]
     uint32_t n_blocks, cap, n_tiles, n_layer, n_head, H;
     uint32_t n_tiles_used;  // tiles holding the first n_blocks blocks
+    uint32_t g;             // query heads per kv head, n_head / H
 };
 
 // Device-coherent 64-bit store / load of a layer contribution written and read
@@ -101,7 +102,7 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
                                                    float *cos_h) {
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
     const uint32_t l = threadIdx.x & 63u;
-    const float invq = kvm_fdiv(1.0f, (float)(qc * (g > 1u ? g : 1u)));
+    const float invq = kvm_recip_or0((float)(qc * (g > 1u ? g : 1u)));   // = 1.0f / x, IEEE
     if (l < NL) {
         float qv[4];
 #pragma unroll
@@ -120,7 +121,7 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
             kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]), kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
 #pragma unroll
         for (uint32_t bi = 0; bi < TW; ++bi) {
-            const float inv = r.mt[bi] ? kvm_fdiv(1.0f, (float)r.mt[bi]) : 0.0f;
+            const float inv = kvm_recip_or0((float)r.mt[bi]);
             const uint32_t keep = r.mt[bi] ? 0xffffffffu : 0u;
             const uint32_t hi = bi >= 4u ? 1u : 0u, e = bi & 3u;
             float k4[4];
@@ -137,13 +138,17 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
     // wave complete in order; the fence keeps the compiler from moving them)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    // ---- chains: lane c < 17 sums row c (lanes past 16 repeat row 16, unused),
-    // reading one 16-dim chunk ahead
+    // ---- chains: lane c < 17 sums row c (lanes past 16 repeat row 16, unused).
+    // The adds of one chain are dependent, so the chain runs at the VALU's
+    // dependent-issue rate only if its operands are in registers ahead of it:
+    // LOOK 16-dim chunks are in flight (the LDS latency is longer than one
+    // chunk's 16 adds).
     const float *row = L.p[l < 17u ? l : 16u];
     float chain = 0.0f;
     constexpr int CH = 4;                // float4 per 16-dim chunk
-    constexpr int NC = D / (4 * CH);     // chunks (even)
-    kvm_f32x4 b0[CH], b1[CH];
+    constexpr int NC = D / (4 * CH);     // chunks
+    constexpr int LOOK = 3;              // chunks in flight (12 LDS reads: under lgkmcnt's 15)
+    kvm_f32x4 buf[LOOK][CH];
     auto ld = [&](kvm_f32x4 (&x)[CH], int c) {
 #pragma unroll
         for (int j = 0; j < CH; ++j) x[j] = *(const kvm_f32x4 *)&row[4 * (CH * c + j)];
@@ -154,17 +159,14 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
 #pragma unroll
             for (int e = 0; e < 4; ++e) chain = kvm_fadd(chain, x[j][e]);
     };
-    ld(b0, 0);
-#pragma unroll 1
-    for (int c = 0; c < NC; c += 2) {
-        ld(b1, c + 1);
+#pragma unroll
+    for (int c = 0; c < LOOK; ++c) ld(buf[c], c);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
         __builtin_amdgcn_sched_barrier(0);
-        add(b0);
+        add(buf[c % LOOK]);
         __builtin_amdgcn_sched_barrier(0);
-        if (c + 2 < NC) ld(b0, c + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        add(b1);
-        __builtin_amdgcn_sched_barrier(0);
+        if (c + LOOK < NC) ld(buf[c % LOOK], c + LOOK);
     }
     // ---- cosines of blocks 0-7 (every lane takes part in the shuffles)
     const float nk = __shfl(chain, (int)((l & 7u) + 8u), 64);

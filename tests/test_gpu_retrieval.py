@@ -104,6 +104,24 @@ def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
     assert np.array_equal(res["to_base"], to_base) and res["total"] == total and res["status"] == 0
 
 
+def test_score_bit_exact_where_every_term_matters(kvm_state):
+    """The closed-form pin's inputs (norms near 1e-6 so the epsilon and invq
+    count, g = 3, three layers with query counts 5, 0, 2, a block without K in
+    one layer): the GPU scores equal the oracle's bit for bit."""
+    from scoring_cases import tiny_norm_case
+    n_head, H, D = 6, 2, 128
+    q, qc, k_sum, mt = tiny_norm_case(41, n_head=n_head, H=H, d=D)
+    n_layer, n_blocks = mt.shape
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 3, H, D)
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D)
+    qa.q_sum.copy_(dev(q))
+    qa.q_count.copy_(dev(qc.astype(np.int32)))
+    sel = api.score_topk(kvm_state, ix, qa, n_blocks, dev(np.full(n_blocks, 128, np.int32)), 4, sink_blocks=1)
+    sel.result()
+    want = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
+    assert np.array_equal(host(sel.scores)[:n_blocks].view(np.uint64), want.view(np.uint64))
+
+
 def test_score_topk_lanes_match_single_lane(kvm_state):
     """Four lanes of different sizes (multi-lane decode) in one launch sequence:
     every lane's scores, ids, layout and stage plan equal the oracle's and a

@@ -273,3 +273,44 @@ def test_score_missing_blocks_and_layers():
     assert np.all(s[[0, 1, 2, 5, 6, 7]] != 0.0)
     qc[:] = 0
     assert np.all(O.score_retrieval(q, qc, ks, mt, 24, 4, 256, present=present) == 0.0)
+
+
+# ------------------------------------------ scoring pinned by the closed form
+def test_score_closed_form_where_every_term_matters():
+    """Norms near 1e-6 (the epsilon weighs like them), g = 3, three layers
+    with query counts 5, 0 and 2, token counts 1..128 and a block without K in
+    one layer: the oracle equals the float64 closed form within 2e-5, and each
+    plausible mistake (invq without g, the epsilon inside the square root or
+    missing or in the numerator, interleaved query heads, a layer average
+    weighted by q_count or counting the layer without queries) moves some
+    score by more than 50 times that."""
+    from scoring_cases import VARIANTS, score_f64, tiny_norm_case
+    n_head, H, d = 6, 2, 128
+    q, qc, ks, mt = tiny_norm_case(41, n_head=n_head, H=H, d=d)
+    got = O.score_retrieval(q, qc, ks, mt, n_head, H, d)
+    want = score_f64(q, qc, ks, mt, n_head, H, d)
+    tol = 2e-5
+    assert np.max(np.abs(got - want)) < tol, np.max(np.abs(got - want))
+    assert np.ptp(want) > 0.1                          # the cosines are not all alike
+    for v in VARIANTS:
+        wrong = score_f64(q, qc, ks, mt, n_head, H, d, variant=v)
+        assert np.max(np.abs(wrong - want)) > 50 * tol, v
+    # a block whose mean-K is missing in one layer still averages that layer's zero
+    only = score_f64(q, qc[:1], ks[:1], mt[:1], n_head, H, d)
+    assert abs(got[3] - only[3] / 2) < tol            # layers 0 and 2 count, layer 2 gives 0 for block 3
+
+
+def test_score_closed_form_on_ordinary_magnitudes_with_unequal_counts():
+    """The same closed form at the scale of real activations (norms ~1..100,
+    where the epsilon is negligible), four layers with query counts 1, 7, 0, 3."""
+    from scoring_cases import score_f64
+    rng = np.random.default_rng(42)
+    n_head, H, d, nb, nl = 8, 2, 64, 9, 4
+    ks = (rng.standard_normal((nl, nb, H * d)) * 40).astype(np.float32)
+    mt = rng.integers(1, 129, (nl, nb)).astype(np.uint32)
+    q = (rng.standard_normal((nl, n_head * d)) * 3).astype(np.float32)
+    qc = np.array([1, 7, 0, 3], np.uint32)
+    got = O.score_retrieval(q, qc, ks, mt, n_head, H, d)
+    assert np.max(np.abs(got - score_f64(q, qc, ks, mt, n_head, H, d))) < 1e-5
+    for v in ("interleaved_heads", "all_layers"):
+        assert np.max(np.abs(score_f64(q, qc, ks, mt, n_head, H, d, variant=v) - got)) > 1e-3, v
