@@ -554,6 +554,18 @@ int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, c
 int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_retrieval_lane *ret,
                                            const kvm_history *const *hist, const kvm_lane *lanes, uint32_t n_lanes,
                                            const kvm_rope_params *rope, int q_type, uint32_t n_head, float scale);
+/* The same step from caller scores (set_retrieval_scores, kvmem_store.cpp:242-248,
+ * then pick_topk_blocks as in kvm_select_topk): one launch, in which the
+ * selector workgroup picks the blocks from scores[n_blocks] while the
+ * attention workgroups attend, staging and attending again when the plan
+ * stages anything; the results of kvm_select_topk then kvm_stagein_fa_decode.
+ * Falls back to those two calls where the one launch does not fit, as
+ * kvm_score_topk_stagein_fa_decode does. */
+int kvm_select_topk_stagein_fa_decode(kvm_state *st, const double *scores, const kvm_select_params *p,
+                                      const kvm_window *w, const kvm_selection *sel, const kvm_history *h,
+                                      const kvm_rope_params *rope, const void *q, int q_type,
+                                      const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head, float scale,
+                                      float *out);
 
 /* kvm_fa_decode without any allocation, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses

@@ -1217,21 +1217,23 @@ static const void *select_kernel_for(uint32_t D, uint32_t max_rows) {
                     : (pk ? select_kernel<128, 2, true>() : select_kernel<128, 2, false>());
 }
 
-extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_retrieval_lane *ret,
-                                                      const kvm_history *const *hist, const kvm_lane *lanes,
-                                                      uint32_t n_lanes, const kvm_rope_params *rope, int q_type,
-                                                      uint32_t n_head, float scale) {
-    if (!st) return KVM_EINVAL;
-    if (!ret || !hist || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: no lanes");
-    if (n_lanes > KVM_MAX_LANES)
-        return kvm_fail(st, KVM_ERANGE, "score_topk_stagein_fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
+// The decode step's selecting launch over prepared top-k arguments (tl: from
+// the scoring grid's layer contributions, or from caller scores); ret_score:
+// the retrieval lanes to score first (a launch of the scoring grid ahead of
+// it), or NULL when the scores are the caller's.  A step the selecting launch
+// does not take runs as separate launches with the same results.
+static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, const topk_lanes &tl,
+                            const kvm_window *const *wins, const kvm_selection *const *sels,
+                            const uint32_t *n_blocks, const kvm_history *const *hist, const kvm_lane *lanes,
+                            uint32_t n_lanes, const kvm_rope_params *rope, int q_type, uint32_t n_head, float scale,
+                            const char *what) {
     kvm_stagein_lane sg[KVM_MAX_LANES];
     for (uint32_t i = 0; i < n_lanes; ++i) {
-        const kvm_window *w = ret[i].w;
-        if (!w || !lanes[i].w) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: lane %u: null window", i);
+        const kvm_window *w = wins[i];
+        if (!w || !lanes[i].w) return kvm_fail(st, KVM_EINVAL, "%s: lane %u: null window", what, i);
         if (w->k != lanes[i].w->k || w->v != lanes[i].w->v || w->cell_pos != lanes[i].w->cell_pos)
-            return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: lane %u selects for another window than it attends", i);
-        sg[i] = kvm_stagein_lane{hist[i], w, ret[i].out};
+            return kvm_fail(st, KVM_EINVAL, "%s: lane %u selects for another window than it attends", what, i);
+        sg[i] = kvm_stagein_lane{hist[i], w, sels[i]};
     }
     // every argument is checked before the first launch
     stage_lanes stl;
@@ -1239,18 +1241,15 @@ extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_r
     size_t lds = 0;
     int rc = kvm_stage_prepare(st, sg, n_lanes, rope, &stl, &max_items, &lds);
     if (rc) return rc;
-    topk_lanes tl;
-    rc = kvm_retrieval_prepare(st, ret, n_lanes, &tl);
-    if (rc) return rc;
     // the selecting launch takes lanes that all have query rows, at most
     // KVM_SEL_MAXB blocks each and q8_0 windows; other steps take the
-    // three-launch path (scoring, top-k, stage-in + attention)
+    // separate launches (scoring, top-k, stage-in + attention)
     bool fuse = lanes[0].w->k_type == KVM_TYPE_Q8_0;
     uint32_t max_rows = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_window *w = lanes[i].w;
         const uint32_t r = w->n_head_kv && n_head % w->n_head_kv == 0 ? lanes[i].n_tokens * (n_head / w->n_head_kv) : 0u;
-        fuse = fuse && r > 0 && ret[i].p->n_blocks <= KVM_SEL_MAXB;
+        fuse = fuse && r > 0 && n_blocks[i] <= KVM_SEL_MAXB;
         max_rows = r > max_rows ? r : max_rows;
     }
     size_t lds_sel = lds * KVM_FA_STAGE_IT / 64;           // kvm_stage_prepare sizes 64-token items
@@ -1282,15 +1281,19 @@ extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_r
     if (!fuse) {
         rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp);
         if (rc) return rc;
-        if (fp.rows && !fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk_stagein_fa_decode: q8_0 windows only");
-        rc = kvm_retrieval_score(st, ret, n_lanes, tl);
-        if (rc) return rc;
+        if (fp.rows && !fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "%s: q8_0 windows only", what);
+        if (ret_score) {
+            rc = kvm_retrieval_score(st, ret_score, n_lanes, tl);
+            if (rc) return rc;
+        }
         rc = kvm_topk_launch(st, tl, n_lanes);
         if (rc) return rc;
         return kvm_stagein_fa_decode_lanes(st, sg, lanes, n_lanes, rope, q_type, n_head, scale);
     }
-    rc = kvm_retrieval_score(st, ret, n_lanes, tl);
-    if (rc) return rc;
+    if (ret_score) {
+        rc = kvm_retrieval_score(st, ret_score, n_lanes, tl);
+        if (rc) return rc;
+    }
     fa_select_args sa{};
     sa.a = fp.a;
     for (uint32_t i = 0; i < n_lanes; ++i) {
@@ -1300,6 +1303,43 @@ extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_r
     void *kargs[] = {&sa};
     KVM_HIP(st, hipLaunchKernel(fn, dim3(fp.a.n_splits + 1, fp.a.H, n_lanes), dim3(512), kargs, lds_sel, st->stream));
     return KVM_OK;
+}
+
+extern "C" int kvm_score_topk_stagein_fa_decode_lanes(kvm_state *st, const kvm_retrieval_lane *ret,
+                                                      const kvm_history *const *hist, const kvm_lane *lanes,
+                                                      uint32_t n_lanes, const kvm_rope_params *rope, int q_type,
+                                                      uint32_t n_head, float scale) {
+    if (!st) return KVM_EINVAL;
+    if (!ret || !hist || !lanes || n_lanes == 0) return kvm_fail(st, KVM_EINVAL, "score_topk_stagein_fa_decode: no lanes");
+    if (n_lanes > KVM_MAX_LANES)
+        return kvm_fail(st, KVM_ERANGE, "score_topk_stagein_fa_decode: %u lanes > %d", n_lanes, KVM_MAX_LANES);
+    const kvm_window *wins[KVM_MAX_LANES];
+    const kvm_selection *sels[KVM_MAX_LANES];
+    uint32_t nb[KVM_MAX_LANES];
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        wins[i] = ret[i].w;
+        sels[i] = ret[i].out;
+        nb[i] = ret[i].p ? ret[i].p->n_blocks : 0u;
+    }
+    topk_lanes tl;
+    int rc = kvm_retrieval_prepare(st, ret, n_lanes, &tl);
+    if (rc) return rc;
+    return select_fa_launch(st, ret, tl, wins, sels, nb, hist, lanes, n_lanes, rope, q_type, n_head, scale,
+                            "score_topk_stagein_fa_decode");
+}
+
+extern "C" int kvm_select_topk_stagein_fa_decode(kvm_state *st, const double *scores, const kvm_select_params *p,
+                                                 const kvm_window *w, const kvm_selection *sel, const kvm_history *h,
+                                                 const kvm_rope_params *rope, const void *q, int q_type,
+                                                 const int32_t *q_pos, uint32_t n_tokens, uint32_t n_head,
+                                                 float scale, float *out) {
+    if (!st) return KVM_EINVAL;
+    topk_lanes tl{};
+    int rc = kvm_select_prepare(st, scores, p, w, sel, &tl.lane[0]);
+    if (rc) return rc;
+    const kvm_lane lane{w, q, q_pos, out, n_tokens};
+    return select_fa_launch(st, nullptr, tl, &w, &sel, &p->n_blocks, &h, &lane, 1, rope, q_type, n_head, scale,
+                            "select_topk_stagein_fa_decode");
 }
 
 extern "C" int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *qa,

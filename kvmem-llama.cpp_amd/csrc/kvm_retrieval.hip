@@ -367,15 +367,20 @@ static int check_select(kvm_state *st, const kvm_select_params *p, const kvm_sel
     return KVM_OK;
 }
 
-extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_select_params *p,
-                               const kvm_window *w, const kvm_selection *out) {
+int kvm_select_prepare(kvm_state *st, const double *scores, const kvm_select_params *p, const kvm_window *w,
+                       const kvm_selection *out, topk_args *ta) {
     if (!st) return KVM_EINVAL;
     int rc = check_select(st, p, out);
     if (rc) return rc;
     if (p->n_blocks && !scores) return kvm_fail(st, KVM_EINVAL, "select_topk: null scores");
     KVM_HIP(st, hipSetDevice(st->device));
+    return make_topk(st, scores, nullptr, nullptr, nullptr, p, w, out, ta);
+}
+
+extern "C" int kvm_select_topk(kvm_state *st, const double *scores, const kvm_select_params *p,
+                               const kvm_window *w, const kvm_selection *out) {
     topk_lanes tl{};
-    rc = make_topk(st, scores, nullptr, nullptr, nullptr, p, w, out, &tl.lane[0]);
+    const int rc = kvm_select_prepare(st, scores, p, w, out, &tl.lane[0]);
     if (rc) return rc;
     return kvm_topk_launch(st, tl, 1);
 }

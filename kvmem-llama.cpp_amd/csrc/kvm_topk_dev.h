@@ -591,3 +591,7 @@ int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t
 void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes, const topk_lanes &tl,
                               score_args *out);
 int kvm_topk_launch(kvm_state *st, const topk_lanes &tl, uint32_t n_lanes);
+// Checks a selection from caller scores (kvm_select_topk) and fills its top-k
+// arguments; nothing is launched.
+int kvm_select_prepare(kvm_state *st, const double *scores, const kvm_select_params *p, const kvm_window *w,
+                       const kvm_selection *out, topk_args *ta);

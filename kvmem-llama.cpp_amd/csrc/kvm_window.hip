@@ -457,19 +457,45 @@ struct kvm_copy_op {
     uint64_t nbytes;
 };
 
-__global__ void k_copy_ops(const kvm_copy_op *ops, int n) {
-    const int i = blockIdx.x;
+// The host cuts every op into chunks of at most KVM_COPY_CHUNK bytes at
+// multiples of KVM_COPY_CHUNK from the op's start (so a chunk's source and
+// destination keep the op's alignment to each other); one wave copies one
+// chunk, four per workgroup.  Where source and destination agree modulo 16,
+// the wave moves the bytes up to the destination's next 16-byte boundary one
+// per lane, the body in 16-byte loads (four in flight per lane before their
+// stores) and the last bytes one per lane; otherwise byte by byte.
+#define KVM_COPY_CHUNK 16384u
+__global__ void __launch_bounds__(256) k_copy_ops(const kvm_copy_op *ops, uint32_t n) {
+    const uint32_t i = blockIdx.x * 4u + (threadIdx.x >> 6), l = threadIdx.x & 63u;
     if (i >= n) return;
     const kvm_copy_op op = ops[i];
-    if (!op.src || !op.dst || op.nbytes == 0) return;
-    const uintptr_t a = (uintptr_t)op.src | (uintptr_t)op.dst;
-    if ((a & 15u) == 0 && (op.nbytes & 15u) == 0) {
-        const uint4 *s = (const uint4 *)op.src;
-        uint4 *d = (uint4 *)op.dst;
-        for (uint64_t j = threadIdx.x; j < op.nbytes / 16; j += blockDim.x) d[j] = s[j];
+    const uint8_t *s = op.src;
+    uint8_t *d = op.dst;
+    uint64_t nb = op.nbytes;
+    if ((((uintptr_t)s ^ (uintptr_t)d) & 15u) != 0) {
+        for (uint64_t j = l; j < nb; j += 64) d[j] = s[j];
         return;
     }
-    for (uint64_t j = threadIdx.x; j < op.nbytes; j += blockDim.x) op.dst[j] = op.src[j];
+    const uint64_t head = (16u - ((uintptr_t)d & 15u)) & 15u;
+    const uint64_t hn = head < nb ? head : nb;
+    if (l < hn) d[l] = s[l];
+    s += hn;
+    d += hn;
+    nb -= hn;
+    const uint64_t nv = nb / 16;
+    const uint4 *s4 = (const uint4 *)s;
+    uint4 *d4 = (uint4 *)d;
+    uint64_t j = l;
+    for (; j + 192 < nv; j += 256) {
+        const uint4 a = s4[j], b = s4[j + 64], c = s4[j + 128], e = s4[j + 192];
+        d4[j] = a;
+        d4[j + 64] = b;
+        d4[j + 128] = c;
+        d4[j + 192] = e;
+    }
+    for (; j < nv; j += 64) d4[j] = s4[j];
+    const uint64_t t = nv * 16 + l;
+    if (t < nb) d[t] = s[t];
 }
 
 extern "C" int kvm_d2d_batched(kvm_state *st, const void *const *src, void *const *dst,
@@ -477,12 +503,22 @@ extern "C" int kvm_d2d_batched(kvm_state *st, const void *const *src, void *cons
     if (!st || n < 0 || (n > 0 && (!src || !dst || !nbytes))) return kvm_fail(st, KVM_EINVAL, "d2d_batched: args");
     if (n == 0) return KVM_OK;
     if (n > 65535) return kvm_fail(st, KVM_ERANGE, "d2d_batched: %d ops > 65535", n);
+    std::vector<kvm_copy_op> ops;
+    for (int i = 0; i < n; ++i) {
+        if (nbytes[i] && (!src[i] || !dst[i])) return kvm_fail(st, KVM_EINVAL, "d2d_batched: op %d: null pointer", i);
+        for (uint64_t off = 0; off < nbytes[i]; off += KVM_COPY_CHUNK) {
+            const uint64_t left = nbytes[i] - off;
+            ops.push_back({(const uint8_t *)src[i] + off, (uint8_t *)dst[i] + off,
+                           left < KVM_COPY_CHUNK ? left : (uint64_t)KVM_COPY_CHUNK});
+        }
+    }
+    if (ops.empty()) return KVM_OK;
+    if (ops.size() > (1u << 26)) return kvm_fail(st, KVM_ERANGE, "d2d_batched: %zu chunks", ops.size());
     KVM_HIP(st, hipSetDevice(st->device));
-    std::vector<kvm_copy_op> ops((size_t)n);
-    for (int i = 0; i < n; ++i) ops[i] = {(const uint8_t *)src[i], (uint8_t *)dst[i], (uint64_t)nbytes[i]};
     void *d = kvm_upload_desc(st, ops.data(), ops.size() * sizeof(kvm_copy_op));
     if (!d) return kvm_fail(st, KVM_ENOMEM, "d2d_batched: descriptor upload");
-    hipLaunchKernelGGL(k_copy_ops, dim3(n), dim3(256), 0, st->stream, (const kvm_copy_op *)d, n);
+    const uint32_t nc = (uint32_t)ops.size();
+    hipLaunchKernelGGL(k_copy_ops, dim3(kvm_cdiv(nc, 4)), dim3(256), 0, st->stream, (const kvm_copy_op *)d, nc);
     KVM_LAUNCH_CHECK(st, "d2d_batched");
     return KVM_OK;
 }

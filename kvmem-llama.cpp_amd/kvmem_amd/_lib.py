@@ -173,6 +173,9 @@ SIGNATURES = {
                                         C.c_int, _P, _u32, _u32, _f, _P]),
     "kvm_stagein_fa_decode_lanes": (C.c_int, [_P, C.POINTER(StageinLane), C.POINTER(Lane), _u32,
                                               C.POINTER(RopeParams), C.c_int, _u32, _f]),
+    "kvm_select_topk_stagein_fa_decode": (C.c_int, [_P, _P, C.POINTER(SelectParams), _PW, C.POINTER(Selection),
+                                                    C.POINTER(History), C.POINTER(RopeParams), _P, C.c_int, _P,
+                                                    _u32, _u32, _f, _P]),
     "kvm_score_topk_stagein_fa_decode": (C.c_int, [_P, C.POINTER(MeanKIndex), C.POINTER(QueryAcc),
                                                    C.POINTER(SelectParams), _PW, C.POINTER(Selection),
                                                    C.POINTER(History), C.POINTER(RopeParams), _P, C.c_int, _P,

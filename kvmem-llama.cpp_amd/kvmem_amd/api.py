@@ -622,6 +622,22 @@ def prepare_decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sin
                     (p, r, index, query, window, sel, n_tokens, history, q, q_pos, out, mandatory))
 
 
+def prepare_select_decode_step(st, scores, n_tokens, budget_blocks, sink_blocks, recent_blocks, window, sel,
+                               history, q, q_pos, n_head, scale, out, n_rot, freq_base, freq_scale=1.0,
+                               hadamard_nrot=-1, mandatory=None):
+    """kvm_select_topk_stagein_fa_decode: the decode step from caller scores
+    (device float64 [n_blocks]) in one launch."""
+    p = L.SelectParams(scores.numel(), budget_blocks, sink_blocks, recent_blocks,
+                       None if mandatory is None else mandatory.data_ptr(),
+                       0 if mandatory is None else mandatory.numel(), n_tokens.data_ptr())
+    r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
+    qt = L.T_BF16 if q.dtype == torch.bfloat16 else L.T_F32
+    return Prepared(st, st.lib.kvm_select_topk_stagein_fa_decode,
+                    (st.h, _ptr(scores), C.byref(p), C.byref(window.c), C.byref(sel.c), C.byref(history.c),
+                     C.byref(r), _ptr(q), qt, _ptr(q_pos), q.shape[0], n_head, float(scale), _ptr(out)),
+                    (p, r, scores, window, sel, n_tokens, history, q, q_pos, out, mandatory))
+
+
 def decode_step(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks, window, sel,
                 history, q, q_pos, n_head, scale, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1, out=None,
                 mandatory=None):

@@ -62,3 +62,32 @@ def test_d2d_batched(kvm_state):
     assert np.array_equal(bh[50000:54096], ah[:4096])
     assert np.array_equal(bh[7:40], ah[100:133])
     assert np.array_equal(bh[60000:61024], ah[4096:5120])
+
+
+def test_d2d_batched_alignments_and_sizes(kvm_state):
+    """kvm_d2d_batched (kvmem_d2d_batched, llama-kvmem-stagein.cu:236-261) over
+    every alignment of source and destination modulo 16, sizes from 0 to past
+    several 16 KiB chunks, and a block-sized move (128 rows of 1,088 bytes);
+    bytes outside the destinations stay untouched."""
+    import ctypes as C
+    rng = np.random.default_rng(52)
+    a = torch.from_numpy(rng.integers(0, 256, 1 << 21, dtype=np.uint8)).cuda()
+    b = torch.zeros(1 << 21, dtype=torch.uint8, device="cuda")
+    ops, pos = [], 0
+    sizes = [0, 1, 15, 16, 17, 63, 64, 1000, 16383, 16384, 16385, 50001, 128 * 1088]
+    for k in range(48):
+        n = sizes[k % len(sizes)]
+        so, do = int(rng.integers(0, 1 << 20)), pos + (k * 7) % 16
+        ops.append((so, do, n))
+        pos = do + n + 64
+    assert pos < b.numel()
+    srcs = (C.c_void_p * len(ops))(*[a.data_ptr() + so for so, _, _ in ops])
+    dsts = (C.c_void_p * len(ops))(*[b.data_ptr() + do for _, do, _ in ops])
+    ns = (C.c_size_t * len(ops))(*[n for _, _, n in ops])
+    kvm_state.check(kvm_state.lib.kvm_d2d_batched(kvm_state.h, srcs, dsts, ns, len(ops)))
+    torch.cuda.synchronize()
+    ah, bh = host(a), host(b)
+    want = np.zeros_like(bh)
+    for so, do, n in ops:
+        want[do:do + n] = ah[so:so + n]
+    assert np.array_equal(bh, want)

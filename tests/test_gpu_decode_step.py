@@ -133,6 +133,35 @@ def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, spl
     check_attention(host(ln["out"]), ref)
 
 
+def test_select_step_from_caller_scores_matches_separate_calls(kvm_state, monkeypatch):
+    """kvm_select_topk_stagein_fa_decode (caller scores, one launch) against
+    kvm_select_topk + kvm_stagein_fa_decode on a second window, over steps
+    whose scores change (plans restage and move blocks within a shadowed
+    window) and one whose scores repeat (an empty plan): selections, windows
+    and outputs equal (both attention paths take 32 splits)."""
+    monkeypatch.setenv("KVM_FA_SPLITS", "32")
+    st = kvm_state
+    ln = _lane(st, 0x5E1, 40, 12, 16)
+    rng = ln["rng"]
+    scores = None
+    for step in range(5):
+        if step != 3:
+            scores = dev(rng.standard_normal(ln["n_blocks"]))
+        ln["q"] = dev(rng.standard_normal((ln["n_tok_q"], H * G, D)).astype(np.float32)).to(torch.bfloat16)
+        ln["out"] = torch.empty((ln["n_tok_q"], H * G, D), dtype=torch.float32, device="cuda")
+        a, b = ln["a"], ln["b"]
+        api.prepare_select_decode_step(st, scores, ln["nt"], ln["budget"], 1, 0, a["window"], a["sel"],
+                                       a["history"], ln["q"], ln["q_pos"], H * G, D ** -0.5, ln["out"], 64, 1e7)()
+        api.select_topk(st, scores, ln["nt"], ln["budget"], 1, 0, None, b["window"], b["sel"])
+        ref = api.stagein_fa_decode(st, b["history"], b["sel"], b["window"], ln["q"], ln["q_pos"], H * G,
+                                    D ** -0.5, 64, 1e7)
+        torch.cuda.synchronize()
+        _compare(ln, ref, True, step)
+        if step == 3:
+            assert len(a["sel"].result()["stage_slots"]) == 0
+    assert st.status() == 0
+
+
 def test_decode_step_steady_state(kvm_state, monkeypatch):
     """The same query accumulator twice: the second step's plan is empty (the
     attention workgroups keep their first pass), its selection and window equal
