@@ -284,7 +284,8 @@ __device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args
     __syncthreads();
     const uint32_t e = s_e, G = a.H * cols, x = blockIdx.y * cols + blockIdx.x;
     stage_plan<D, 512, KVM_FA_STAGE_IT>(sg, s_rows, n_ent, x, G, e + 1, false);
-    if (!lane_barrier<512>(sg.sync, sg.status, sg.spin, e + 2, x, G, true) && threadIdx.x == 0) atomicOr(&sg.info[3], 16u);
+    if (!lane_barrier<512>(sg.sync, sg.status, sg.spin, e + 2, x, G, true, true) && threadIdx.x == 0)
+        atomicOr(&sg.info[3], 16u);
 }
 
 // A selecting launch: workgroup (n_splits, 0) of each lane runs the lane's

@@ -209,6 +209,23 @@ typedef _Float16 kvm_f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t kvm_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t kvm_u32x2 __attribute__((ext_vector_type(2)));
 
+// Bulk data handed between workgroups of one launch, which may sit on
+// different XCDs, each with its own L2: 16-byte stores written through past
+// the writer's L2 and 16-byte loads that miss the reader's L2 (the agent-scope
+// cache policy, sc1), so the flag that orders them needs no write-back or
+// invalidation of whole caches (as the split partials' 4-byte agent-scope
+// accesses).  Offsets from the base are below 2 GiB.
+#define KVM_CPOL_SC1 16
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kvm_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ kvm_u32x4 kvm_ld16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, KVM_CPOL_SC1);
+}
+__device__ __forceinline__ void kvm_st16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off, kvm_u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, KVM_CPOL_SC1);
+}
+
 __device__ inline float kvm_h2f(uint16_t h) {
     _Float16 v;
     __builtin_memcpy(&v, &h, 2);

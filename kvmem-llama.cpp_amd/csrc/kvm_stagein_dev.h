@@ -197,24 +197,69 @@ struct stage_args {
     uint32_t spin;                   // polls of a barrier wait before it gives up (0: at once)
 };
 
-// dst[i] = src[i] for i = tid, tid + nth, ... < n (16-byte units, n >= 1, the
+// dst[i] = src[i] for 16-byte units i = tid, tid + nth, ... < n (n >= 1, the
 // ranges disjoint): eight loads in flight before their stores (a load-store
 // pair per step would wait for each load in turn); loads past n re-read n - 1.
-__device__ inline void copy16(uint4 *__restrict__ dst, const uint4 *__restrict__ src, uint32_t n, uint32_t tid,
-                              uint32_t nth) {
+// The loads (LD_DEV) or the stores (ST_DEV) device-coherent (kvm_ld16_dev /
+// kvm_st16_dev): the move staging is written before a lane barrier and read
+// after it by other workgroups.
+template <bool LD_DEV, bool ST_DEV>
+__device__ inline void copy16_dev(uint8_t *dst, const uint8_t *src, uint32_t n, uint32_t tid, uint32_t nth) {
     constexpr uint32_t B = 8;
+    const __amdgpu_buffer_rsrc_t rs = kvm_rsrc(src), rd = kvm_rsrc(dst);
     for (uint32_t i0 = tid; i0 < n; i0 += B * nth) {
-        uint4 r[B];
+        kvm_u32x4 r[B];
 #pragma unroll
         for (uint32_t j = 0; j < B; ++j) {
-            const uint32_t i = i0 + j * nth;
-            r[j] = src[i < n ? i : n - 1];
+            const uint32_t i = i0 + j * nth, ic = i < n ? i : n - 1;
+            r[j] = LD_DEV ? kvm_ld16_dev(rs, 16u * ic) : *(const kvm_u32x4 *)(src + 16u * ic);
         }
 #pragma unroll
         for (uint32_t j = 0; j < B; ++j) {
             const uint32_t i = i0 + j * nth;
-            if (i < n) dst[i] = r[j];
+            if (i < n) {
+                if (ST_DEV) kvm_st16_dev(rd, 16u * i, r[j]);
+                else *(kvm_u32x4 *)(dst + 16u * i) = r[j];
+            }
         }
+    }
+}
+
+// The LDS fill of a moved block's item: nk 16-byte units of K rows from the
+// move staging (device-coherent loads) and nt units of (cos, sin) rows, the
+// first TB per thread held in registers while the K rows stream.
+__device__ inline void stage_fill_moved(uint8_t *dk, const uint8_t *__restrict__ sk, uint32_t nk, uint8_t *dt,
+                                        const uint8_t *__restrict__ stab, uint32_t nt, uint32_t tid, uint32_t nth) {
+    constexpr uint32_t B = 8, TB = 4;
+    kvm_u32x4 tr[TB];
+    if (nt) {
+#pragma unroll
+        for (uint32_t j = 0; j < TB; ++j) {
+            const uint32_t i = tid + j * nth, ic = i < nt ? i : nt - 1;
+            tr[j] = *(const kvm_u32x4 *)(stab + 16u * ic);
+        }
+    }
+    const __amdgpu_buffer_rsrc_t rs = kvm_rsrc(sk);
+    for (uint32_t i0 = tid; i0 < nk; i0 += B * nth) {
+        kvm_u32x4 r[B];
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth, ic = i < nk ? i : nk - 1;
+            r[j] = kvm_ld16_dev(rs, 16u * ic);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < B; ++j) {
+            const uint32_t i = i0 + j * nth;
+            if (i < nk) *(kvm_u32x4 *)(dk + 16u * i) = r[j];
+        }
+    }
+    if (nt) {
+#pragma unroll
+        for (uint32_t j = 0; j < TB; ++j) {
+            const uint32_t i = tid + j * nth;
+            if (i < nt) *(kvm_u32x4 *)(dt + 16u * i) = tr[j];
+        }
+        for (uint32_t i = tid + TB * nth; i < nt; i += nth) *(kvm_u32x4 *)(dt + 16u * i) = *(const kvm_u32x4 *)(stab + 16u * i);
     }
 }
 
@@ -260,12 +305,12 @@ __device__ inline void stage_gather_entry(const stage_args &a, uint32_t si, uint
     if (src < 0) return;
     const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
     uint8_t *dk = a.moves + (uint64_t)si * a.bt * (rowK + rowV);
-    copy16((uint4 *)dk, (const uint4 *)(a.k_shadow + (uint64_t)src * a.bt * rowK), a.bt * rowK / 16, tid, nth);
+    copy16_dev<false, true>(dk, a.k_shadow + (uint64_t)src * a.bt * rowK, a.bt * rowK / 16, tid, nth);
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
-    uint4 *dv = (uint4 *)(dk + (uint64_t)a.bt * rowK);
+    uint8_t *dv = dk + (uint64_t)a.bt * rowK;
     for (uint32_t h = 0; h < a.H; ++h)     // a slot's tiles of one head are consecutive
-        copy16(dv + (uint64_t)h * tps * per, (const uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile),
-               tps * per, tid, nth);
+        copy16_dev<false, true>(dv + (uint64_t)h * tps * vtile, a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile,
+                                tps * per, tid, nth);
 }
 
 
@@ -316,7 +361,11 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint32_t nh = a.rc.n_half, ntab = count * nh * 8;
     const uint8_t *gt = (const uint8_t *)(a.rc.tab + (uint64_t)(base + (int32_t)t0) * nh);
     const bool al16 = (((uintptr_t)gk | (uintptr_t)gv | rowK | rowV) & 15u) == 0;
-    if (al16) {
+    if (src >= 0) {
+        // rows gathered by other workgroups before the lane's barrier (the
+        // staging and the table are 16-byte aligned: rowK is a multiple of 16)
+        stage_fill_moved(lk, gk, nk / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
+    } else if (al16) {
         stage_fill(lk, gk, nk / 16, lv, gv, nv / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
     } else {
         stage_fill(lk, gk, 0, lv, gv, 0, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
@@ -362,10 +411,10 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         // skips V, its bytes come with this copy)
         if (c0 == 0) {
             const uint32_t per = vtile / 16;
-            const uint4 *mv = (const uint4 *)(gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile);
+            const uint8_t *mv = gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile;
             for (uint32_t h = 0; h < a.H; ++h)
-                copy16((uint4 *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile), mv + (uint64_t)h * (a.bt / 64) * per,
-                       per, tid, NTH);
+                copy16_dev<true, false>(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile, mv + (uint64_t)h * (a.bt / 64) * vtile,
+                                        per, tid, NTH);
         }
     } else {
         // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
@@ -448,18 +497,22 @@ __device__ inline uint32_t stage_entries(const stage_args &a) {
 // take values e + 1, e + 2, ...; workgroup 0 stores the last one as the epoch
 // (`last`) once every workgroup has arrived there, so no flag of an earlier
 // launch (at most e) passes for one of this launch, also when the launch is
-// replayed from a captured graph.  The writes before the barrier are written
-// back from the writer's L2 before its arrival (release) and the caches are
-// invalidated after the go flag (acquire).  False: the wait timed out.
+// replayed from a captured graph.  Every thread's writes before the barrier
+// are acknowledged before the arrival; with `fences` they are also written
+// back from the writer's L2 (release) and the caches are invalidated after the
+// go flag (acquire, by one wave: the invalidation covers the CU's and the XCD's
+// caches for every wave after the workgroup barrier).  Without `fences` the
+// data crossing the barrier must be written and read device-coherently
+// (kvm_st16_dev / kvm_ld16_dev).  False: the wait timed out.
 template <int NTH>
 __device__ bool lane_barrier(uint32_t *sync, uint32_t *status, uint32_t spin, uint32_t v, uint32_t x, uint32_t G,
-                             bool last) {
+                             bool last, bool fences) {
     __shared__ uint32_t s_ok;
     const uint32_t tid = threadIdx.x;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        __threadfence();
+        if (fences) __threadfence();
         sync_store(sync + 64 + x, v);
     }
     uint32_t ok = 1;
@@ -476,10 +529,13 @@ __device__ bool lane_barrier(uint32_t *sync, uint32_t *status, uint32_t spin, ui
         ok = sync_wait(sync + 1, v, spin) && sync_load(sync + 2) != v;
         s_ok = ok;
     }
+    if (fences && tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();
     if (x != 0) ok = s_ok;
     if (!ok && tid == 0) atomicOr(status, (uint32_t)KVM_WAIT_STAGE);
-    __threadfence();
     return ok != 0;
 }
 
@@ -513,7 +569,7 @@ __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent,
         for (uint32_t si = threadIdx.x; si < n_ent; si += NTH) any |= a.stage_src[si] >= 0 ? 1u : 0u;
         if (__syncthreads_or(any)) {
             for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
-            ok = lane_barrier<NTH>(a.sync, a.status, a.spin, v, x, G, last);
+            ok = lane_barrier<NTH>(a.sync, a.status, a.spin, v, x, G, last, false);
         }
     }
     for (uint32_t item = x; item < n_items; item += G) {
