@@ -275,15 +275,19 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
 // lane's G = H * cols stages its share of the items (after the gather of the
 // blocks that move within the window, behind the plan's first barrier), then
 // every workgroup waits at a second barrier for the whole plan.
-template <int D>
 // In a selecting launch (cols = n_splits + 1) the selector column stages too.
+// FAST: the stage-in's device-coherent move staging, split gather and 16-lane
+// K rows (stage_plan), which the selecting launch leaves out: with its
+// attention state live around the staging they raise its registers to the
+// limit and its steady-state time, though it never runs them there.
+template <int D, bool FAST>
 __device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent, uint32_t cols) {
     extern __shared__ __align__(16) uint8_t s_rows[];     // the staged launch's dynamic LDS
     __shared__ uint32_t s_e;
     if (threadIdx.x == 0) s_e = sync_load(sg.sync);
     __syncthreads();
     const uint32_t e = s_e, G = a.H * cols, x = blockIdx.y * cols + blockIdx.x;
-    stage_plan<D, 512, KVM_FA_STAGE_IT>(sg, s_rows, n_ent, x, G, e + 1, false);
+    stage_plan<D, 512, KVM_FA_STAGE_IT, FAST>(sg, s_rows, n_ent, x, G, e + 1, false);
     if (!lane_barrier<512>(sg.sync, sg.status, sg.spin, e + 2, x, G, true, true) && threadIdx.x == 0)
         atomicOr(&sg.info[3], 16u);
 }
@@ -419,7 +423,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             const uint32_t n = fa_await_plan(a, h, ep_c + 1);
             if (n) {
                 __threadfence();             // acquire: the selection's stores
-                fa_stage_lane<D>(a, stg[blockIdx.z], n, a.n_splits + 1);
+                fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n, a.n_splits + 1);
             }
             __syncthreads();
             if (tid == 0)
@@ -433,7 +437,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     if (R == 0) {
         if constexpr (STAGE && !SELECT) {
             const uint32_t n_ent = stage_entries(stg[blockIdx.z]);
-            if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent, a.n_splits);
+            if (n_ent) fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n_ent, a.n_splits);
         }
         return;
     }
@@ -479,7 +483,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (tid == 0) s_epoch = ep + 1;
     if constexpr (STAGE && !SELECT) {
-        if (n_ent) fa_stage_lane<D>(a, stg[blockIdx.z], n_ent, a.n_splits);
+        if (n_ent) fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n_ent, a.n_splits);
     }
     // SELECT, after the first pass over the window (both roles, at the same
     // barrier): true when the lane's plan staged anything, so the pass is redone
@@ -491,7 +495,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             const uint32_t n = fa_await_plan(a, h, ep + 1);
             if (!n) return false;
             __threadfence();                 // acquire: the selection's stores
-            fa_stage_lane<D>(a, stg[blockIdx.z], n, a.n_splits + 1);
+            fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n, a.n_splits + 1);
             return true;
         }
     };

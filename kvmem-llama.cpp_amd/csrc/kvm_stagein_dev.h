@@ -10,6 +10,8 @@
 #pragma once
 #include "kvm_internal.h"
 
+#include <type_traits>
+
 struct rope_ctx {
     const float2 *tab;     // [n_pos][n_half] (cos, sin)
     uint32_t n_half;       // n_rot / 2
@@ -168,6 +170,152 @@ __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, 
     stage_k_rows<D, 1>(s1, k1, c1, t1, l1, rc);
 }
 
+// The same K rows with LG = D / 16 lanes per (token, head) row, 64 / LG rows
+// per wave.  Lane l of a row's group holds the 16 consecutive dims 16 m ..
+// 16 m + 15, where the bits of m (dim bits 4 and up) are the lane's
+// coordinates c4, c5, ... in a basis of lane patterns that one DPP move
+// exchanges within the group: dim bit 4 <-> lane xor 1 and bit 5 <-> xor 2
+// (quad permutes), bit 6 <-> xor 8 (the 16-lane row rotated by 8; D = 128:
+// xor 7, the half-row mirror), bit 7 <-> xor 15 (the row mirror).  Two dims
+// that differ in one bit >= 4 then sit in lanes one DPP move apart, so the
+// Walsh-Hadamard stages above 8 and the RoPE pairs (n_half a power of two
+// >= 16) exchange values without an LDS round trip; dim bits 0-3 stay in the
+// lane's registers.  The arithmetic is stage_k_rows' (the same IEEE
+// operations in the same order, the same sign carried through the lane
+// stages), so the bytes are the same.
+template <int D>
+__device__ __forceinline__ uint32_t k16_m(uint32_t l) {
+    const uint32_t top = (l >> 2) & 1u;
+    if constexpr (D == 256) {
+        const uint32_t lp = l ^ (top * 15u);
+        return (lp & 1u) | (lp & 2u) | (((lp >> 3) & 1u) << 2) | (top << 3);
+    } else {
+        const uint32_t lp = l ^ (top * 7u);
+        return (lp & 1u) | (lp & 2u) | (top << 2);
+    }
+}
+template <int D, int BIT>
+__device__ __forceinline__ float k16_swap(float v) {
+    static_assert(BIT >= 4 && BIT <= (D == 256 ? 7 : 6), "dim bit held across lanes");
+    constexpr int ctrl = BIT == 4 ? 0xB1 : BIT == 5 ? 0x4E : BIT == 6 ? (D == 256 ? 0x128 : 0x141) : 0x140;
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+// Whether stage_k_row16 serves this RoPE width (n_half a power of two of
+// 16 .. D / 2); others take stage_k_rows.
+template <int D>
+__host__ __device__ inline bool k16_ok(uint32_t n_half) {
+    return n_half >= 16 && n_half <= (uint32_t)D / 2 && (n_half & (n_half - 1)) == 0;
+}
+// One row per lane group: src = the row's NB q8_0 blocks (34 B each, 2-byte
+// aligned), requantised into K tile kt at cell c; cs = the (cos, sin) row of
+// its window position; l = the lane within the group; live false: computed,
+// not written.  Every lane of the wave takes part (the DPP moves).
+template <int D>
+__device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, uint32_t c, const float2 *cs, bool live,
+                                              uint32_t l, const rope_ctx &rc) {
+    const uint32_t m = k16_m<D>(l), b = m >> 1, d0 = 16u * m;
+    float x[16];
+    {
+        const uint8_t *blk = src + b * 34u;
+        const float dsc = kvm_h2f(*(const uint16_t *)blk);
+        const uint16_t *q = (const uint16_t *)(blk + 2u + 16u * (m & 1u));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w = q[i];
+            x[2 * i] = kvm_fmul((float)(int8_t)(uint8_t)w, dsc);
+            x[2 * i + 1] = kvm_fmul((float)(int8_t)(uint8_t)(w >> 8), dsc);
+        }
+    }
+    // NeoX RoPE: dims i and i + n_half (one dim bit, log2 n_half >= 4, apart)
+    const uint32_t nh = rc.n_half;
+    {
+        float y[16];
+        switch (nh) {
+        case 16:
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[i] = k16_swap<D, 4>(x[i]);
+            break;
+        case 32:
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[i] = k16_swap<D, 5>(x[i]);
+            break;
+        case 64:
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[i] = k16_swap<D, 6>(x[i]);
+            break;
+        default:
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[i] = k16_swap<D, D == 256 ? 7 : 6>(x[i]);
+            break;
+        }
+        // x0' = x0 c - x1 s below n_half, x1' = x0 s + x1 c above, as
+        // RN(RN(x c) + RN(y s')) with s' = -s below; lanes past 2 n_half keep x
+        const bool lo = d0 < nh, act = d0 < 2u * nh;
+        const float2 *t = cs + (act ? (d0 & (nh - 1u)) : 0u);
+        const uint32_t sm = lo ? 0x80000000u : 0u;
+        float2 tv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tv[i] = t[act ? i : 0];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float v = kvm_fadd(kvm_fmul(x[i], tv[i].x), kvm_fmul(y[i], __uint_as_float(__float_as_uint(tv[i].y) ^ sm)));
+            x[i] = act ? v : x[i];
+        }
+    }
+    // normalised Walsh-Hadamard over nrot-wide chunks: pre-scale, butterflies
+    // h = 1, 2, 4, 8 in the lane, then one DPP exchange per dim bit 4 .. log2
+    // nrot - 1 with the lane's sign carried as in stage_k_rows
+    uint32_t xs = 0;
+    if (rc.nrot > 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
+#pragma unroll
+        for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (!(i & h)) {
+                    const float a = x[i], bb = x[i + h];
+                    x[i] = kvm_fadd(a, bb);
+                    x[i + h] = kvm_fsub(a, bb);
+                }
+        auto stage = [&](auto bit_c) {
+            constexpr int BIT = decltype(bit_c)::value;
+            const uint32_t ck = (m >> (BIT - 4)) & 1u;
+            const float sg = ck ? -1.0f : 1.0f;
+            xs ^= ck;
+            float o[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[i] = k16_swap<D, BIT>(x[i]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = __builtin_fmaf(o[i], sg, x[i]);
+        };
+        if (rc.nrot > 16) stage(std::integral_constant<int, 4>{});
+        if (rc.nrot > 32) stage(std::integral_constant<int, 5>{});
+        if (rc.nrot > 64) stage(std::integral_constant<int, 6>{});
+        if constexpr (D == 256)
+            if (rc.nrot > 128) stage(std::integral_constant<int, 7>{});
+    }
+    // q8_0 requantisation: a 32-dim block is the lane and its dim bit 4 partner
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = fmaxf(amax, k16_swap<D, 4>(amax));
+    const float d = kvm_div127(amax);
+    const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ (xs << 31));
+    uint32_t qw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        qw[k] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qw[k] |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[4 * k + i], id)) << (8 * i);
+    }
+    if (!live) return;
+    // two 8-byte runs of the tile (dims 16m .. +7 and 16m + 8 .. +15)
+    *(kvm_u32x2 *)(kt + kvm_kq_off(D, c, d0)) = kvm_u32x2{qw[0], qw[1]};
+    *(kvm_u32x2 *)(kt + kvm_kq_off(D, c, d0 + 8u)) = kvm_u32x2{qw[2], qw[3]};
+    if ((m & 1u) == 0) *(uint16_t *)(kt + kvm_kd_off(D, c, b)) = kvm_f2h(d);
+}
+
 // ---------------------------------------------------------------------------
 // Selection-driven stage-in: workgroup = (staged slot, 64-cell tile of it).
 // ---------------------------------------------------------------------------
@@ -293,31 +441,65 @@ __device__ inline void stage_fill(uint8_t *d0, const uint8_t *__restrict__ s0, u
 __host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 34; }
 __host__ __device__ inline uint32_t stage_row_v(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 18; }
 
-// Gather of a plan entry whose block moves within the window (stage_src[si] =
-// src >= 0) into its staging region, by threads tid, tid + nth, ...: the bt raw
-// K rows from the shadow of slot src, then the slot's V tiles, [head][tile of
-// the slot].  Slots start on tile boundaries (block_tokens % 64 == 0), so a V
-// tile's bytes do not depend on where the slot lies and move as they are.
-// Only full blocks move (the top-k stages partly filled ones from the host).
+// One entry's gather (the same copies) by one workgroup with ordinary stores,
+// for a launch whose gather barrier writes back and invalidates the caches.
 template <int D>
 __device__ inline void stage_gather_entry(const stage_args &a, uint32_t si, uint32_t tid, uint32_t nth) {
     const int32_t src = a.stage_src[si];
     if (src < 0) return;
     const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
     uint8_t *dk = a.moves + (uint64_t)si * a.bt * (rowK + rowV);
-    copy16_dev<false, true>(dk, a.k_shadow + (uint64_t)src * a.bt * rowK, a.bt * rowK / 16, tid, nth);
+    copy16_dev<false, false>(dk, a.k_shadow + (uint64_t)src * a.bt * rowK, a.bt * rowK / 16, tid, nth);
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
     uint8_t *dv = dk + (uint64_t)a.bt * rowK;
     for (uint32_t h = 0; h < a.H; ++h)     // a slot's tiles of one head are consecutive
-        copy16_dev<false, true>(dv + (uint64_t)h * tps * vtile, a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile,
-                                tps * per, tid, nth);
+        copy16_dev<false, false>(dv + (uint64_t)h * tps * vtile,
+                                 a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile, tps * per, tid, nth);
 }
 
+// Gather of the plan entries whose blocks move within the window (stage_src[si]
+// = src >= 0) into their staging regions: entry si's bt raw K rows from the
+// shadow of slot src, then the slot's V tiles, [head][tile of the slot].
+// Slots start on tile boundaries (block_tokens % 64 == 0), so a V tile's bytes
+// do not depend on where the slot lies and move as they are.  Only full blocks
+// move (the top-k stages partly filled ones from the host).  The n_ent
+// entries' staging regions are one run of 16-byte units, split evenly over the
+// lane's G workgroups: workgroup x copies units [U x / G, U (x+1) / G),
+// skipping the entries that do not move, each piece one contiguous copy (K
+// rows of one entry, or one head's tiles).
+template <int D>
+__device__ inline void stage_gather_split(const stage_args &a, uint32_t n_ent, uint32_t x, uint32_t G, uint32_t tid,
+                                          uint32_t nth) {
+    const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
+    const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
+    const uint64_t KU = (uint64_t)a.bt * rowK / 16, HU = (uint64_t)tps * per, EU = KU + a.H * HU;
+    const uint64_t U = (uint64_t)n_ent * EU, u0 = U * x / G, u1 = U * (x + 1) / G;
+    for (uint64_t si = u0 / EU; si < n_ent && si * EU < u1; ++si) {
+        const int32_t src = a.stage_src[si];
+        if (src < 0) continue;
+        const uint64_t e0 = si * EU;
+        const uint64_t lo = (u0 > e0 ? u0 : e0) - e0, hi = (u1 < e0 + EU ? u1 : e0 + EU) - e0;
+        uint8_t *dk = a.moves + si * a.bt * (rowK + rowV);
+        if (lo < KU) {
+            const uint64_t k1 = hi < KU ? hi : KU;
+            copy16_dev<false, true>(dk + 16 * lo, a.k_shadow + (uint64_t)src * a.bt * rowK + 16 * lo, (uint32_t)(k1 - lo),
+                                    tid, nth);
+        }
+        for (uint32_t h = 0; h < a.H; ++h) {           // a slot's tiles of one head are consecutive
+            const uint64_t h0 = KU + h * HU, h1 = h0 + HU;
+            const uint64_t c0 = lo > h0 ? lo : h0, c1 = hi < h1 ? hi : h1;
+            if (c0 >= c1) continue;
+            copy16_dev<false, true>(dk + (uint64_t)a.bt * rowK + (uint64_t)h * tps * vtile + 16 * (c0 - h0),
+                                    a.wv + ((uint64_t)h * a.n_tiles + (uint64_t)src * tps) * vtile + 16 * (c0 - h0),
+                                    (uint32_t)(c1 - c0), tid, nth);
+        }
+    }
+}
 
 // One (plan entry, IT-token run) item, staged by a workgroup of NTH threads
 // through the LDS rows buffer s_rows (IT * n_head_kv * (D/32) * 52 bytes).  An
 // item of 32 tokens fills one key half (ks) of a 64-cell window tile.
-template <int D, int NTH, int IT = 64>
+template <int D, int NTH, int IT = 64, bool FAST = true>
 __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt) {
     static_assert(IT == 64 || IT == 32, "stage-in item size");
     constexpr uint32_t NB = D / 32;
@@ -361,7 +543,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint32_t nh = a.rc.n_half, ntab = count * nh * 8;
     const uint8_t *gt = (const uint8_t *)(a.rc.tab + (uint64_t)(base + (int32_t)t0) * nh);
     const bool al16 = (((uintptr_t)gk | (uintptr_t)gv | rowK | rowV) & 15u) == 0;
-    if (src >= 0) {
+    if (FAST && src >= 0) {
         // rows gathered by other workgroups before the lane's barrier (the
         // staging and the table are 16-byte aligned: rowK is a multiple of 16)
         stage_fill_moved(lk, gk, nk / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
@@ -383,9 +565,21 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     }
 
     const uint32_t tile = (slot * a.bt + t0) / 64, c0 = t0 % 64;   // c0: the item's first cell in the tile
-    // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), nrow = count * a.H;
     constexpr uint32_t W = NTH / 64, NR = 4;
+    uint8_t *const ktile = a.wk + (uint64_t)tile * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
+    if (FAST && k16_ok<D>(nh)) {
+        // K rows: a wave takes RW rows (cell j, head h) at a time, one per lane group
+        constexpr uint32_t LG = D / 16, RW = 64 / LG;
+        const uint32_t lane = tid & 63u, grp = lane / LG, l = lane % LG;
+        for (uint32_t r0 = wave * RW; r0 < nrow; r0 += W * RW) {
+            const uint32_t r = r0 + grp, rr = r < nrow ? r : r0;     // past the rows: recompute r0, unwritten
+            const uint32_t j = rr / a.H, h = rr % a.H;
+            stage_k_row16<D>(lk + j * rowK + h * NB * 34, ktile + (uint64_t)h * a.n_tiles * kvm_ktile_bytes(KVM_TYPE_Q8_0, D),
+                             c0 + j, lt + j * nh, r < nrow, l, a.rc);
+        }
+    } else
+    // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time
     for (uint32_t r0 = wave; r0 < nrow; r0 += NR * W) {
         const uint8_t *src[NR];
         uint8_t *kt[NR];
@@ -413,7 +607,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
             const uint32_t per = vtile / 16;
             const uint8_t *mv = gv + (uint64_t)a.bt * rowK + (uint64_t)(t0 / 64) * vtile;
             for (uint32_t h = 0; h < a.H; ++h)
-                copy16_dev<true, false>(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile, mv + (uint64_t)h * (a.bt / 64) * vtile,
+                copy16_dev<FAST, false>(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile, mv + (uint64_t)h * (a.bt / 64) * vtile,
                                         per, tid, NTH);
         }
     } else {
@@ -559,7 +753,7 @@ __device__ void stage_void_item(const stage_args &a, uint32_t si, uint32_t tt) {
 // within the window, then items x, x + G, ... of IT tokens.  `last`: the
 // gather barrier is the launch's last on these sync words.  No barrier
 // follows the items.
-template <int D, int NTH, int IT>
+template <int D, int NTH, int IT, bool FAST = true>
 __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent, uint32_t x, uint32_t G,
                            uint32_t v, bool last) {
     const uint32_t tps = a.bt / IT, n_items = n_ent * tps;
@@ -568,12 +762,16 @@ __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent,
         uint32_t any = 0;
         for (uint32_t si = threadIdx.x; si < n_ent; si += NTH) any |= a.stage_src[si] >= 0 ? 1u : 0u;
         if (__syncthreads_or(any)) {
-            for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
-            ok = lane_barrier<NTH>(a.sync, a.status, a.spin, v, x, G, last, false);
+            if (FAST) {
+                stage_gather_split<D>(a, n_ent, x, G, threadIdx.x, NTH);
+            } else {
+                for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
+            }
+            ok = lane_barrier<NTH>(a.sync, a.status, a.spin, v, x, G, last, !FAST);
         }
     }
     for (uint32_t item = x; item < n_items; item += G) {
-        if (ok) stagein_item<D, NTH, IT>(a, s_rows, item / tps, item % tps);
+        if (ok) stagein_item<D, NTH, IT, FAST>(a, s_rows, item / tps, item % tps);
         else stage_void_item<IT>(a, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }

@@ -20,9 +20,13 @@ def _history(seed, n_tokens, H=4, D=256):
     return api.History(kr, vr), kr, vr
 
 
-@pytest.mark.parametrize("n_rot,hadamard,freq_base", [(64, -1, 1e7), (64, 0, 1e7), (128, 128, 1e4)])
-def test_stagein_selection_bytes(kvm_state, n_rot, hadamard, freq_base):
-    H, D, bt = 4, 256, 128
+@pytest.mark.parametrize("D,n_rot,hadamard,freq_base", [
+    (256, 64, -1, 1e7), (256, 64, 0, 1e7), (256, 128, 128, 1e4), (256, 32, -1, 1e4), (256, 256, 256, 1e4),
+    (128, 64, -1, 1e7), (128, 128, 128, 1e4), (128, 32, 0, 1e7),
+    # RoPE pairs not one dim bit >= 4 apart (n_half 12, 8): the one-row-per-wave path
+    (256, 24, -1, 1e7), (256, 16, 64, 1e7)])
+def test_stagein_selection_bytes(kvm_state, D, n_rot, hadamard, freq_base):
+    H, bt = 4, 128
     n_blocks = 40
     n_hist = n_blocks * bt - 50                     # last block is partial (78 tokens)
     hist, kr, vr = _history(n_rot + hadamard, n_hist, H, D)
@@ -35,7 +39,7 @@ def test_stagein_selection_bytes(kvm_state, n_rot, hadamard, freq_base):
     api.stagein_selection(kvm_state, hist, w, sel, n_rot, freq_base, 1.0, hadamard)
     res = sel.result()
     assert res["status"] == 0 and len(res["ids"]) == 12 and list(res["stage_slots"]) == list(range(12))
-    nrot = 256 if hadamard == -1 else hadamard
+    nrot = D if hadamard == -1 else hadamard
     theta = O.rope_theta(freq_base, 1.0, n_rot)
     ek, ev = w.export_rows(0, 12 * bt)
     ek, ev = host(ek), host(ev)
