@@ -373,11 +373,14 @@ __device__ inline void copy16_dev(uint8_t *dst, const uint8_t *src, uint32_t n, 
     }
 }
 
-// The LDS fill of a moved block's item: nk 16-byte units of K rows from the
-// move staging (device-coherent loads) and nt units of (cos, sin) rows, the
-// first TB per thread held in registers while the K rows stream.
-__device__ inline void stage_fill_moved(uint8_t *dk, const uint8_t *__restrict__ sk, uint32_t nk, uint8_t *dt,
-                                        const uint8_t *__restrict__ stab, uint32_t nt, uint32_t tid, uint32_t nth) {
+// The LDS fill of an item whose rows were gathered into the staging region
+// sb by other workgroups before the lane's barrier (device-coherent loads): nk
+// 16-byte units of K rows from sb + koff to dk, then nv units of V rows from
+// sb + voff to dv, and nt units of (cos, sin) rows, the first TB per thread
+// held in registers while the rows stream.
+__device__ inline void stage_fill_dev(uint8_t *dk, uint8_t *dv, const uint8_t *sb, uint32_t koff, uint32_t nk,
+                                      uint32_t voff, uint32_t nv, uint8_t *dt, const uint8_t *__restrict__ stab,
+                                      uint32_t nt, uint32_t tid, uint32_t nth) {
     constexpr uint32_t B = 8, TB = 4;
     kvm_u32x4 tr[TB];
     if (nt) {
@@ -387,18 +390,19 @@ __device__ inline void stage_fill_moved(uint8_t *dk, const uint8_t *__restrict__
             tr[j] = *(const kvm_u32x4 *)(stab + 16u * ic);
         }
     }
-    const __amdgpu_buffer_rsrc_t rs = kvm_rsrc(sk);
-    for (uint32_t i0 = tid; i0 < nk; i0 += B * nth) {
+    const __amdgpu_buffer_rsrc_t rs = kvm_rsrc(sb);
+    const uint32_t n = nk + nv;
+    for (uint32_t i0 = tid; i0 < n; i0 += B * nth) {
         kvm_u32x4 r[B];
 #pragma unroll
         for (uint32_t j = 0; j < B; ++j) {
-            const uint32_t i = i0 + j * nth, ic = i < nk ? i : nk - 1;
-            r[j] = kvm_ld16_dev(rs, 16u * ic);
+            const uint32_t i = i0 + j * nth, ic = i < n ? i : n - 1;
+            r[j] = kvm_ld16_dev(rs, ic < nk ? koff + 16u * ic : voff + 16u * (ic - nk));
         }
 #pragma unroll
         for (uint32_t j = 0; j < B; ++j) {
             const uint32_t i = i0 + j * nth;
-            if (i < nk) *(kvm_u32x4 *)(dk + 16u * i) = r[j];
+            if (i < n) *(kvm_u32x4 *)(i < nk ? dk + 16u * i : dv + 16u * (i - nk)) = r[j];
         }
     }
     if (nt) {
@@ -440,6 +444,15 @@ __device__ inline void stage_fill(uint8_t *d0, const uint8_t *__restrict__ s0, u
 // Row bytes of the history / shadow: q8_0 K and q4_0 V, all kv heads.
 __host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 34; }
 __host__ __device__ inline uint32_t stage_row_v(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 18; }
+// Whether a plan that moves blocks also gathers its host entries' rows into
+// the staging (16-byte units: rows and history 16-byte aligned), so that every
+// item reads HBM after the barrier and a block's rows cross the host link
+// spread over all of the lane's workgroups instead of one per item.
+template <int D>
+__device__ inline bool stage_host_via(const stage_args &a) {
+    return a.moves && ((stage_row_k(a, D) | stage_row_v(a, D)) & 15u) == 0 &&
+           (((uintptr_t)a.hk | (uintptr_t)a.hv) & 15u) == 0;
+}
 
 // One entry's gather (the same copies) by one workgroup with ordinary stores,
 // for a launch whose gather barrier writes back and invalidates the caches.
@@ -462,24 +475,40 @@ __device__ inline void stage_gather_entry(const stage_args &a, uint32_t si, uint
 // shadow of slot src, then the slot's V tiles, [head][tile of the slot].
 // Slots start on tile boundaries (block_tokens % 64 == 0), so a V tile's bytes
 // do not depend on where the slot lies and move as they are.  Only full blocks
-// move (the top-k stages partly filled ones from the host).  The n_ent
+// move (the top-k stages partly filled ones from the host).  With host_via
+// (stage_host_via) an entry staged from the host gathers its rows too: its
+// K rows, then its V rows (row format), the block's tokens only.  The n_ent
 // entries' staging regions are one run of 16-byte units, split evenly over the
-// lane's G workgroups: workgroup x copies units [U x / G, U (x+1) / G),
-// skipping the entries that do not move, each piece one contiguous copy (K
-// rows of one entry, or one head's tiles).
+// lane's G workgroups: workgroup x copies units [U x / G, U (x+1) / G), each
+// piece one contiguous copy (K rows of one entry, one head's tiles, or an
+// entry's V rows).
 template <int D>
 __device__ inline void stage_gather_split(const stage_args &a, uint32_t n_ent, uint32_t x, uint32_t G, uint32_t tid,
-                                          uint32_t nth) {
+                                          uint32_t nth, bool host_via) {
     const uint32_t rowK = stage_row_k(a, D), rowV = stage_row_v(a, D);
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D), tps = a.bt / 64, per = vtile / 16;
     const uint64_t KU = (uint64_t)a.bt * rowK / 16, HU = (uint64_t)tps * per, EU = KU + a.H * HU;
     const uint64_t U = (uint64_t)n_ent * EU, u0 = U * x / G, u1 = U * (x + 1) / G;
     for (uint64_t si = u0 / EU; si < n_ent && si * EU < u1; ++si) {
         const int32_t src = a.stage_src[si];
-        if (src < 0) continue;
         const uint64_t e0 = si * EU;
         const uint64_t lo = (u0 > e0 ? u0 : e0) - e0, hi = (u1 < e0 + EU ? u1 : e0 + EU) - e0;
         uint8_t *dk = a.moves + si * a.bt * (rowK + rowV);
+        if (src < 0) {
+            if (!host_via) continue;
+            const uint64_t first = (uint64_t)a.ids[a.stage_slots[si]] * a.bt;
+            if (first >= a.h_tokens) continue;                 // not staged (stagein_item reports it)
+            const uint64_t nt = a.h_tokens - first < a.bt ? a.h_tokens - first : a.bt;
+            const uint64_t k1 = nt * rowK / 16, v1 = KU + nt * rowV / 16;
+            if (lo < k1)
+                copy16_dev<false, true>(dk + 16 * lo, a.hk + first * rowK + 16 * lo, (uint32_t)((hi < k1 ? hi : k1) - lo),
+                                        tid, nth);
+            const uint64_t c0 = lo > KU ? lo : KU, c1 = hi < v1 ? hi : v1;
+            if (c0 < c1)
+                copy16_dev<false, true>(dk + (uint64_t)a.bt * rowK + 16 * (c0 - KU), a.hv + first * rowV + 16 * (c0 - KU),
+                                        (uint32_t)(c1 - c0), tid, nth);
+            continue;
+        }
         if (lo < KU) {
             const uint64_t k1 = hi < KU ? hi : KU;
             copy16_dev<false, true>(dk + 16 * lo, a.k_shadow + (uint64_t)src * a.bt * rowK + 16 * lo, (uint32_t)(k1 - lo),
@@ -500,7 +529,8 @@ __device__ inline void stage_gather_split(const stage_args &a, uint32_t n_ent, u
 // through the LDS rows buffer s_rows (IT * n_head_kv * (D/32) * 52 bytes).  An
 // item of 32 tokens fills one key half (ks) of a 64-cell window tile.
 template <int D, int NTH, int IT = 64, bool FAST = true>
-__device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt) {
+__device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt,
+                                             bool host_via = false) {
     static_assert(IT == 64 || IT == 32, "stage-in item size");
     constexpr uint32_t NB = D / 32;
     const uint32_t slot = a.stage_slots[si];
@@ -546,7 +576,12 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     if (FAST && src >= 0) {
         // rows gathered by other workgroups before the lane's barrier (the
         // staging and the table are 16-byte aligned: rowK is a multiple of 16)
-        stage_fill_moved(lk, gk, nk / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
+        stage_fill_dev(lk, lv, mk, t0 * rowK, nk / 16, 0, 0, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
+    } else if (FAST && host_via) {
+        // a host entry's rows, gathered into its staging region: K rows, then V rows
+        const uint8_t *hb = a.moves + (uint64_t)si * a.bt * (rowK + rowV);
+        stage_fill_dev(lk, lv, hb, t0 * rowK, nk / 16, a.bt * rowK + t0 * rowV, nv / 16, (uint8_t *)lt, gt, ntab / 16,
+                       tid, NTH);
     } else if (al16) {
         stage_fill(lk, gk, nk / 16, lv, gv, nv / 16, (uint8_t *)lt, gt, ntab / 16, tid, NTH);
     } else {
@@ -611,25 +646,36 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
                                         per, tid, NTH);
         }
     } else {
-        // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per step
+        // V nibbles: destination-driven, one 32-bit word (8 keys of one dim) per
+        // step; the 8 byte reads of a word are unconditional (keys past the
+        // item's rows read row 0 and are zeroed), so they are all in flight
+        // together, and two words per thread per round
         constexpr uint32_t NKS = IT / 32;    // key halves of the tile this item fills
-        for (uint32_t wi = tid; wi < a.H * D * 4 * NKS; wi += NTH) {
-            const uint32_t h = wi / (D * 4 * NKS), r = wi % (D * 4 * NKS);
+        constexpr uint32_t NW = (uint32_t)D * 4 * NKS;   // words per head
+        auto word_at = [&](uint32_t wi) {
+            const uint32_t h = wi / NW, r = wi % NW;
             const uint32_t X = r / NKS, ks = NKS == 2 ? (r & 1u) : c0 / 32;
             const uint32_t dd = (X >> 6) * 16 + (X & 15u), gg = (X & 63u) >> 4;
             const uint32_t b = dd / 32, e = dd % 32;
-            uint32_t word = 0;
+            const uint32_t byte = 2 + (e & 15u), shift = e < 16 ? 0u : 4u;
+            uint32_t nb8[8];
 #pragma unroll
             for (uint32_t j = 0; j < 8; ++j) {
                 const uint32_t cj = 32 * ks + 8 * gg + j - c0;    // key within the item
-                uint32_t nib = 0;
-                if (cj < count) {
-                    const uint8_t *blk = lv + cj * rowV + h * NB * 18 + b * 18;
-                    nib = e < 16 ? (blk[2 + e] & 15u) : (uint32_t)(blk[2 + e - 16] >> 4);
-                }
+                nb8[j] = lv[(cj < count ? cj : 0u) * rowV + h * NB * 18 + b * 18 + byte];
+            }
+            uint32_t word = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                const uint32_t cj = 32 * ks + 8 * gg + j - c0;
+                const uint32_t nib = cj < count ? (nb8[j] >> shift) & 15u : 0u;
                 word |= nib << kvm_vq_nib_shift(j);
             }
             *(uint32_t *)(a.wv + ((uint64_t)h * a.n_tiles + tile) * vtile + kvm_vq_word(dd, gg, ks)) = word;
+        };
+        for (uint32_t wi = tid; wi < a.H * NW; wi += 2 * NTH) {
+            word_at(wi);
+            if (wi + NTH < a.H * NW) word_at(wi + NTH);
         }
         for (uint32_t si2 = tid; si2 < a.H * IT * NB; si2 += NTH) {
             const uint32_t h = si2 / (IT * NB), cj = (si2 / NB) % IT, b = si2 % NB;
@@ -757,13 +803,14 @@ template <int D, int NTH, int IT, bool FAST = true>
 __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent, uint32_t x, uint32_t G,
                            uint32_t v, bool last) {
     const uint32_t tps = a.bt / IT, n_items = n_ent * tps;
-    bool ok = true;
+    bool ok = true, host_via = false;
     if (a.moves) {
         uint32_t any = 0;
         for (uint32_t si = threadIdx.x; si < n_ent; si += NTH) any |= a.stage_src[si] >= 0 ? 1u : 0u;
         if (__syncthreads_or(any)) {
             if (FAST) {
-                stage_gather_split<D>(a, n_ent, x, G, threadIdx.x, NTH);
+                host_via = stage_host_via<D>(a);
+                stage_gather_split<D>(a, n_ent, x, G, threadIdx.x, NTH, host_via);
             } else {
                 for (uint32_t si = x; si < n_ent; si += G) stage_gather_entry<D>(a, si, threadIdx.x, NTH);
             }
@@ -771,7 +818,7 @@ __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent,
         }
     }
     for (uint32_t item = x; item < n_items; item += G) {
-        if (ok) stagein_item<D, NTH, IT, FAST>(a, s_rows, item / tps, item % tps);
+        if (ok) stagein_item<D, NTH, IT, FAST>(a, s_rows, item / tps, item % tps, host_via);
         else stage_void_item<IT>(a, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }
