@@ -503,9 +503,12 @@ def run_churn(args, st, api, L, torch, np):
     queries select exactly those two sets.  Timed with a window that keeps a K
     shadow (moved blocks re-based from HBM, one block read from the host) and
     with one that does not (127 blocks restaged over PCIe), against the same
-    step with an unchanging query; the step as three launches (value) and as
-    two (kvm_score_topk_stagein_fa_decode: a changed plan is staged after a
-    pass of the attention over the window as it was, which then runs again)."""
+    step with an unchanging query; the step as three launches (value:
+    kvm_score_topk, then kvm_stagein_fa_decode, whose attention workgroups
+    stage the plan), as four (kvm_score_topk_stagein, whose stage-in kernel
+    runs two workgroups per CU, then kvm_fa_decode) and as two
+    (kvm_score_topk_stagein_fa_decode: a changed plan is staged after a pass of
+    the attention over the window as it was, which then runs again)."""
     dev = torch.device("cuda", 0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0xC0FFEE06)
@@ -544,6 +547,16 @@ def run_churn(args, st, api, L, torch, np):
         calls = [(api.prepare_score_topk(st, ix, qa, n_blocks, n_tokens, nsel, 1, 0, w, sel),
                   api.prepare_stagein_fa_decode(st, hist, sel, w, q, q_pos, N_HEAD, D ** -0.5, out, N_ROT, FREQ_BASE))
                  for qa in qas]
+        # the step as four launches: kvm_score_topk_stagein (scoring, top-k, the
+        # stage-in kernel at two workgroups per CU), then kvm_fa_decode
+        calls4 = [(api.prepare_score_topk_stagein(st, ix, qa, n_blocks, n_tokens, nsel, 1, 0, w, sel, hist, N_ROT,
+                                                  FREQ_BASE),
+                   api.prepare_fa_decode(st, w, q, q_pos, N_HEAD, D ** -0.5, out)) for qa in qas]
+
+        def churn4(i):
+            r, f = calls4[i % 2]
+            r()
+            f()
 
         def churn(i):
             r, f = calls[i % 2]
@@ -567,7 +580,7 @@ def run_churn(args, st, api, L, torch, np):
                                            args.warmup)
         churn(0)
         steady_ms, _ = time_steps(torch, steady, lambda i: None, args.steps, args.warmup)
-        churn_ms, _ = time_steps(torch, churn, lambda i: None, args.steps, args.warmup)
+        churn_ms, churn4_ms = time_steps(torch, churn, churn4, args.steps, args.warmup)
         r = sel.result()
         last = sb if (args.steps - 1) % 2 == 1 else sa            # the timed loop's last call
         assert np.array_equal(r["ids"], last) and r["status"] == 0, r["status"]
@@ -580,11 +593,12 @@ def run_churn(args, st, api, L, torch, np):
         ka, va = w.export_rows(0, RETRIEVED)
         kb, vb = wf.export_rows(0, RETRIEVED)
         assert torch.equal(ka, kb) and torch.equal(va, vb), "churned window differs from a fresh stage-in"
-        res[shadow] = dict(churn_us=churn_ms * 1e3, steady_us=steady_ms * 1e3, moved=moved,
+        res[shadow] = dict(churn_us=churn_ms * 1e3, churn4_us=churn4_ms * 1e3, steady_us=steady_ms * 1e3, moved=moved,
                            host_blocks=len(r["stage_slots"]) - moved, churn2_us=churn2_ms * 1e3,
                            steady2_us=steady2_ms * 1e3)
-        log("shadow=%s: steady %.2f us, churn %.2f us per step" % (shadow, steady_ms * 1e3, churn_ms * 1e3))
-        del w, sel, calls, steps2, wf, sf
+        log("shadow=%s: steady %.2f us, churn %.2f us (four launches %.2f) per step"
+            % (shadow, steady_ms * 1e3, churn_ms * 1e3, churn4_ms * 1e3))
+        del w, sel, calls, calls4, steps2, wf, sf
         torch.cuda.synchronize()
     a, b = res[True], res[False]
     # least HBM traffic of the shadow restage: a moved block's raw K read from the
@@ -602,12 +616,14 @@ def run_churn(args, st, api, L, torch, np):
                                "the second-oldest and the newest block: 127 slots restaged per step, 126 of them "
                                "blocks already in the window that move one slot",
                    "history_tokens": HIST_TOKENS, "window_cells": WINDOW},
-        "shadow": {"churn_us": round(a["churn_us"], 2), "steady_us": round(a["steady_us"], 2),
+        "shadow": {"churn_us": round(a["churn_us"], 2), "four_launch_churn_us": round(a["churn4_us"], 2),
+                   "steady_us": round(a["steady_us"], 2),
                    "restage_us": round(a["churn_us"] - a["steady_us"], 2), "moved_blocks": a["moved"],
                    "host_blocks": a["host_blocks"], "hbm_bytes_min": hbm_min,
                    "h2d_bytes": a["host_blocks"] * BT * (K_ROW + V_ROW),
                    "two_launch_churn_us": round(a["churn2_us"], 2), "two_launch_steady_us": round(a["steady2_us"], 2)},
-        "host_restage": {"churn_us": round(b["churn_us"], 2), "steady_us": round(b["steady_us"], 2),
+        "host_restage": {"churn_us": round(b["churn_us"], 2), "four_launch_churn_us": round(b["churn4_us"], 2),
+                         "steady_us": round(b["steady_us"], 2),
                          "restage_us": round(b["churn_us"] - b["steady_us"], 2), "host_blocks": b["host_blocks"],
                          "h2d_bytes": b["host_blocks"] * BT * (K_ROW + V_ROW),
                          "two_launch_churn_us": round(b["churn2_us"], 2),

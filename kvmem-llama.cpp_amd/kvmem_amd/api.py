@@ -499,7 +499,8 @@ def prepare_score_topk_lanes(st, lanes):
 
 def prepare_score_topk_stagein(st, index, query, n_blocks, n_tokens, budget_blocks, sink_blocks, recent_blocks,
                                window, sel, history, n_rot, freq_base, freq_scale=1.0, hadamard_nrot=-1):
-    """Retrieval whose top-k workgroup stages its own plan (kvm_score_topk_stagein)."""
+    """kvm_score_topk_stagein: the scoring grid, the top-k and the stage-in of
+    its plan (three launches, every argument checked before the first)."""
     p = L.SelectParams(n_blocks, budget_blocks, sink_blocks, recent_blocks, None, 0, n_tokens.data_ptr())
     r = L.RopeParams(n_rot, freq_base, freq_scale, hadamard_nrot)
     return Prepared(st, st.lib.kvm_score_topk_stagein,
