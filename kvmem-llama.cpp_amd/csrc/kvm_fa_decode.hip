@@ -1073,7 +1073,7 @@ static int fa_prepare(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, in
     }
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_type == KVM_TYPE_BF16;
-    const bool quant = w0->k_type == KVM_TYPE_Q8_0;
+    const bool quant = kvm_k_quant(w0->k_type);
     fp->D = D;
     fp->quant = quant;
     // workspace: the split partials, O then (m, l); with the caller's scratch,
@@ -1249,7 +1249,7 @@ static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, 
     // the selecting launch takes lanes that all have query rows, at most
     // KVM_SEL_MAXB blocks each and q8_0 windows; other steps take the
     // separate launches (scoring, top-k, stage-in + attention)
-    bool fuse = lanes[0].w->k_type == KVM_TYPE_Q8_0;
+    bool fuse = kvm_k_quant(lanes[0].w->k_type);
     uint32_t max_rows = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_window *w = lanes[i].w;

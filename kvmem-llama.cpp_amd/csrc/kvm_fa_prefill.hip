@@ -600,7 +600,7 @@ extern "C" int kvm_fa_prefill(kvm_state *st, const kvm_window *w, const void *q,
     sa.vh = (_Float16 *)(ws + up256(kv_bytes));
     sa.info = (int32_t *)(ws + 2 * up256(kv_bytes));
     sa.n_tiles = n_tiles;
-    sa.k_q8 = w->k_type == KVM_TYPE_Q8_0;
+    sa.k_q8 = kvm_k_quant(w->k_type);
     sa.v_q4 = w->v_type == KVM_TYPE_Q4_0;
     a.kh = sa.kh;
     a.vh = sa.vh;

@@ -155,8 +155,12 @@ int kvm_rope_table(kvm_state *st, const float *theta, uint32_t n_half, uint32_t 
 // f16 K tile: [sub 4][kstep D/32][lane 64][8 halves] = key 16*sub+m, dims 32ks+8g..+7
 // f16 V tile: halves ((d/16)*64 + 16g + d%16)*16 + 8ks + j (same key order as q4_0)
 // ---------------------------------------------------------------------------
+// A quantised K window (q8_0, or q4_0 held as q8_0: the nibble minus 8 as an
+// int8 quant under the block's fp16 scale, so the attention reads one tile
+// format and computes ggml's q4_0 x q8_0 integer dot exactly).
+__host__ __device__ inline bool kvm_k_quant(int ktype) { return ktype == KVM_TYPE_Q8_0 || ktype == KVM_TYPE_Q4_0; }
 __host__ __device__ inline uint32_t kvm_ktile_bytes(int ktype, uint32_t D) {
-    return ktype == KVM_TYPE_Q8_0 ? 64u * D + 64u * (D / 32u) * 2u : 64u * D * 2u;
+    return kvm_k_quant(ktype) ? 64u * D + 64u * (D / 32u) * 2u : 64u * D * 2u;
 }
 __host__ __device__ inline uint32_t kvm_vtile_bytes(int vtype, uint32_t D) {
     return vtype == KVM_TYPE_Q4_0 ? D * 32u + (D / 32u) * 64u * 2u : 64u * D * 2u;

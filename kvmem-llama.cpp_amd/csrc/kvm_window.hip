@@ -12,13 +12,13 @@ extern "C" int kvm_window_check(const kvm_window *w) {
     if (w->n_cells == 0 || w->n_cells % KVM_TILE_CELLS) return KVM_EINVAL;
     if (w->head_dim != 128 && w->head_dim != 256) return KVM_EUNSUPPORTED;
     if (w->n_head_kv == 0 || w->block_tokens == 0 || w->n_cells % w->block_tokens) return KVM_EINVAL;
-    const bool q = w->k_type == KVM_TYPE_Q8_0 && w->v_type == KVM_TYPE_Q4_0;
+    const bool q = kvm_k_quant(w->k_type) && w->v_type == KVM_TYPE_Q4_0;
     const bool h = w->k_type == KVM_TYPE_F16 && w->v_type == KVM_TYPE_F16;
     if (!q && !h) return KVM_EUNSUPPORTED;
     if (!w->k || !w->v || !w->cell_pos) return KVM_EINVAL;
     // a shadow comes with its row counts and the slot map, and holds q8_0 rows
     if (!w->k_shadow != !w->shadow_rows) return KVM_EINVAL;
-    if (w->k_shadow && (!q || !w->slot_block || !w->slot_base)) return KVM_EINVAL;
+    if (w->k_shadow && (w->k_type != KVM_TYPE_Q8_0 || !q || !w->slot_block || !w->slot_base)) return KVM_EINVAL;
     return KVM_OK;
 }
 
@@ -111,6 +111,31 @@ __global__ void k_import_k_q8(win_geo g, uint32_t cell0, uint32_t n, const uint8
         uint8_t *q = dst + kvm_kq_off(g.D, c, 32 * b + 8 * gg);
 #pragma unroll
         for (int j = 0; j < 8; ++j) q[j] = src[2 + 8 * gg + j];
+    }
+    uint8_t *sd = dst + kvm_kd_off(g.D, c, b);
+    sd[0] = src[0];
+    sd[1] = src[1];
+    if (b == 0 && h == 0) void_shadow(g, cell);
+}
+
+// q4_0 K rows into the q8_0 tile format: quant j = nibble - 8 (low nibbles
+// are dims 0-15 of the block, high nibbles 16-31), the fp16 scale as it is
+__global__ void k_import_k_q4(win_geo g, uint32_t cell0, uint32_t n, const uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    const uint8_t *src = rows + ((uint64_t)t * g.H + h) * NB * 18 + (uint64_t)b * 18;
+    uint8_t *dst = g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile;
+#pragma unroll
+    for (uint32_t gg = 0; gg < 4; ++gg) {
+        uint8_t *q = dst + kvm_kq_off(g.D, c, 32 * b + 8 * gg);
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t e = 8 * gg + j, nib = e < 16 ? src[2 + e] & 15u : (uint32_t)src[2 + e - 16] >> 4;
+            q[j] = (uint8_t)(int8_t)((int)nib - 8);
+        }
     }
     uint8_t *sd = dst + kvm_kd_off(g.D, c, b);
     sd[0] = src[0];
@@ -226,6 +251,10 @@ extern "C" int kvm_window_import_rows(kvm_state *st, const kvm_window *w, uint32
             const uint64_t nt = (uint64_t)n * g.H * NB;
             hipLaunchKernelGGL(k_import_k_q8, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
                                (const uint8_t *)k_rows);
+        } else if (w->k_type == KVM_TYPE_Q4_0) {
+            const uint64_t nt = (uint64_t)n * g.H * NB;
+            hipLaunchKernelGGL(k_import_k_q4, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (const uint8_t *)k_rows);
         } else {
             const uint64_t nt = (uint64_t)n * g.H * g.D;
             hipLaunchKernelGGL(k_import_k_f16, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
@@ -277,6 +306,28 @@ __global__ void k_export_k_q8(win_geo g, uint32_t cell0, uint32_t n, uint8_t *ro
     }
 }
 
+// the q8_0-format tile of a q4_0 K window back to q4_0 rows (quant + 8)
+__global__ void k_export_k_q4(win_geo g, uint32_t cell0, uint32_t n, uint8_t *rows) {
+    const uint32_t NB = g.D / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)n * g.H * NB) return;
+    const uint32_t b = i % NB, h = (i / NB) % g.H, t = (uint32_t)(i / ((uint64_t)NB * g.H));
+    const uint32_t cell = cell0 + t, tile = cell / 64, c = cell % 64;
+    uint8_t *dst = rows + ((uint64_t)t * g.H + h) * NB * 18 + (uint64_t)b * 18;
+    const uint8_t *src = g.k + ((uint64_t)h * g.n_tiles + tile) * g.ktile;
+    const uint8_t *sd = src + kvm_kd_off(g.D, c, b);
+    dst[0] = sd[0];
+    dst[1] = sd[1];
+    const uint8_t *lo = src + kvm_kq_off(g.D, c, 32 * b), *lo2 = src + kvm_kq_off(g.D, c, 32 * b + 8);
+    const uint8_t *hi = src + kvm_kq_off(g.D, c, 32 * b + 16), *hi2 = src + kvm_kq_off(g.D, c, 32 * b + 24);
+#pragma unroll
+    for (uint32_t e = 0; e < 16; ++e) {
+        const uint32_t n0 = (uint32_t)((int)(int8_t)(e < 8 ? lo[e] : lo2[e - 8]) + 8) & 15u;
+        const uint32_t n1 = (uint32_t)((int)(int8_t)(e < 8 ? hi[e] : hi2[e - 8]) + 8) & 15u;
+        dst[2 + e] = (uint8_t)(n0 | (n1 << 4));
+    }
+}
+
 __global__ void k_export_v_q4(win_geo g, uint32_t cell0, uint32_t n, uint8_t *rows) {
     const uint32_t NB = g.D / 32;
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -321,10 +372,13 @@ extern "C" int kvm_window_export_rows(kvm_state *st, const kvm_window *w, uint32
     KVM_HIP(st, hipSetDevice(st->device));
     const win_geo g = geo_of(w);
     const uint32_t NB = g.D / 32;
-    if (w->k_type == KVM_TYPE_Q8_0) {
+    if (kvm_k_quant(w->k_type)) {
         const uint64_t nt = (uint64_t)n * g.H * NB;
-        if (k_rows)
+        if (k_rows && w->k_type == KVM_TYPE_Q8_0)
             hipLaunchKernelGGL(k_export_k_q8, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
+                               (uint8_t *)k_rows);
+        if (k_rows && w->k_type == KVM_TYPE_Q4_0)
+            hipLaunchKernelGGL(k_export_k_q4, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
                                (uint8_t *)k_rows);
         if (v_rows)
             hipLaunchKernelGGL(k_export_v_q4, dim3(kvm_cdiv(nt, 256)), dim3(256), 0, st->stream, g, cell0, n,
@@ -553,7 +607,9 @@ extern "C" int kvm_slot_free(kvm_slot_pool *p, int32_t slot) {
 
 // Bytes per layer of one slot: block_tokens K rows, then block_tokens V rows.
 static uint64_t slot_span(const kvm_window *w, uint64_t *kspan) {
-    const uint64_t krow = (uint64_t)w->n_head_kv * (w->k_type == KVM_TYPE_Q8_0 ? w->head_dim / 32 * 34 : w->head_dim * 2);
+    const uint64_t krow = (uint64_t)w->n_head_kv * (w->k_type == KVM_TYPE_Q8_0   ? w->head_dim / 32 * 34
+                                                     : w->k_type == KVM_TYPE_Q4_0 ? w->head_dim / 32 * 18
+                                                                                  : w->head_dim * 2);
     const uint64_t vrow = (uint64_t)w->n_head_kv * (w->v_type == KVM_TYPE_Q4_0 ? w->head_dim / 32 * 18 : w->head_dim * 2);
     *kspan = w->block_tokens * krow;
     return *kspan + w->block_tokens * vrow;

@@ -480,7 +480,7 @@ int oracle_fa_ggml(int k_type, int v_type, const float *q, const void *k, const 
                    const int32_t *cell_pos, const int32_t *q_pos, int n_tokens, int n_head,
                    int n_head_kv, int head_dim, int n_cells, float scale, float *out,
                    int n_threads) {
-    if (k_type != ORACLE_T_F16 && k_type != ORACLE_T_Q8_0) return -1;
+    if (k_type != ORACLE_T_F16 && k_type != ORACLE_T_Q8_0 && k_type != ORACLE_T_Q4_0) return -1;
     if (v_type != ORACLE_T_F16 && v_type != ORACLE_T_Q4_0 && v_type != ORACLE_T_Q8_0) return -1;
     if (n_head_kv <= 0 || n_head % n_head_kv) return -1;
     const int g = n_head / n_head_kv;
@@ -503,7 +503,7 @@ int oracle_fa_ggml(int k_type, int v_type, const float *q, const void *k, const 
         for (int r = 0; r < n_rows; ++r) {
             const int t = r / n_head, h = r % n_head, hk = h / g;
             const float *pq = q + (size_t)r * head_dim;
-            if (k_type == ORACLE_T_Q8_0) oracle_quant_q8_0(pq, qq, head_dim);
+            if (k_type != ORACLE_T_F16) oracle_quant_q8_0(pq, qq, head_dim);   /* the vec_dot type of q8_0 and q4_0 */
             else for (int d = 0; d < head_dim; ++d) put_f16(qq + 2 * d, oracle_f32_to_f16(pq[d]));
             float S = 0.0f, M = -INFINITY;
             memset(vkq, 0, sizeof(float) * (size_t)head_dim);
@@ -521,6 +521,22 @@ int oracle_fa_ggml(int k_type, int v_type, const float *q, const void *k, const 
                             sumi += (int)(int8_t)xb[2 + j] * (int)(int8_t)yb[2 + j];
                         sumf += (float)sumi * (oracle_f16_to_f32(get_f16(xb)) *
                                                oracle_f16_to_f32(get_f16(yb)));
+                    }
+                    s = sumf;
+                } else if (k_type == ORACLE_T_Q4_0) {
+                    /* ggml's vec_dot_q4_0_q8_0: low nibbles (minus 8) against
+                     * query quants 0-15, high nibbles against 16-31, then
+                     * sumi * d_k * d_q left to right */
+                    float sumf = 0.0f;
+                    for (int b = 0; b < head_dim / 32; ++b) {
+                        const uint8_t *xb = kr + b * 18, *yb = qq + b * 34;
+                        int sumi0 = 0, sumi1 = 0;
+                        for (int j = 0; j < 16; ++j) {
+                            sumi0 += ((int)(xb[2 + j] & 15) - 8) * (int)(int8_t)yb[2 + j];
+                            sumi1 += ((int)(xb[2 + j] >> 4) - 8) * (int)(int8_t)yb[2 + j + 16];
+                        }
+                        sumf += (float)(sumi0 + sumi1) * oracle_f16_to_f32(get_f16(xb)) *
+                                oracle_f16_to_f32(get_f16(yb));
                     }
                     s = sumf;
                 } else {

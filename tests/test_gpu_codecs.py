@@ -30,7 +30,8 @@ def test_quantize_rows_bit_exact(kvm_state, ty):
 
 
 @pytest.mark.parametrize("kt,vt,d", [(L.T_Q8_0, L.T_Q4_0, 256), (L.T_Q8_0, L.T_Q4_0, 128),
-                                     (L.T_F16, L.T_F16, 128)])
+                                     (L.T_F16, L.T_F16, 128), (L.T_Q4_0, L.T_Q4_0, 256),
+                                     (L.T_Q4_0, L.T_Q4_0, 128)])
 def test_window_import_export_round_trip(kvm_state, kt, vt, d):
     rng = np.random.default_rng(d + kt)
     H, n_cells = 4, 512

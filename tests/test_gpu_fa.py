@@ -30,6 +30,8 @@ CASES = [
     (2048, 2, 4, 128, 1, L.T_F16, L.T_F16, 1.0),        # fp16 cache, head_dim 128
     (2048, 2, 4, 128, 3, L.T_Q8_0, L.T_Q4_0, 3.0),      # peaked softmax
     (1024, 4, 8, 256, 4, L.T_F16, L.T_F16, 2.0),        # 32 rows per kv head
+    (4096, 4, 6, 256, 4, L.T_Q4_0, L.T_Q4_0, 1.0),      # q4_0 K cache (held as q8_0 quants)
+    (2048, 2, 4, 128, 1, L.T_Q4_0, L.T_Q4_0, 3.0),
 ]
 
 
@@ -50,7 +52,7 @@ def test_fa_decode_parity(kvm_state, case, qdt):
     scale = 1.0 / np.sqrt(D)
     out = host(api.fa_decode(kvm_state, w, qd, dev(qp), H * G, scale))
     ref = O.fa_ggml(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
-    if kt == L.T_Q8_0:
+    if kt in (L.T_Q8_0, L.T_Q4_0):
         check_attention(out, ref)
         f64 = O.fa_f64(kt, vt, q, kr, vr, cp, qp, H * G, H, D, scale)
         assert np.abs(out - f64).max() <= 3e-2 * np.abs(f64).max()      # Q -> q8_0 as in ggml
@@ -171,8 +173,8 @@ def _prefill_check(out, q, kr, vr, cp, pos, H, G, D, kt, vt, scale):
     ref16 = O.fa_f64(L.T_F16, L.T_F16, qh, _f16_rows(kt, kr, n, H, D), _f16_rows(vt, vr, n, H, D), cp, pos,
                      H * G, H, D, scale)
     err = check_attention(out, ref16)
-    if kt == L.T_Q8_0:
-        # ggml-CPU rounds Q to q8_0 for a q8_0 K: a coarser computation of the same op
+    if kt in (L.T_Q8_0, L.T_Q4_0):
+        # ggml-CPU rounds Q to q8_0 for a q8_0 or q4_0 K: a coarser computation of the same op
         ref = O.fa_ggml(kt, vt, q, kr, vr, cp, pos, H * G, H, D, scale)
         assert np.abs(out - ref).max() <= 3e-2 * np.abs(ref).max()
     return err
@@ -198,6 +200,7 @@ PREFILL_CASES = [
     (1024, 2, 4, 128, 64, L.T_F16, L.T_F16, 0, None, 1, "f32"),
     (4096, 4, 6, 256, 30, L.T_Q8_0, L.T_Q4_0, 7, (1024, 2048), 3, "f32"),   # whole empty tiles
     (2048, 1, 8, 256, 20, L.T_Q8_0, L.T_Q4_0, 0, None, 8, "bf16"),
+    (2048, 4, 6, 256, 48, L.T_Q4_0, L.T_Q4_0, 40, None, None, "bf16"),
 ]
 
 

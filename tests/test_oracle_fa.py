@@ -85,3 +85,43 @@ def test_ggml_semantics_vs_textbook_f16():
     f = O.fa_f64(O.T_F16, O.T_F16, qh, kr, vr, None, qp, 8, 2, 128, 128 ** -0.5)
     # ggml accumulates V*p in an fp16 vector: error at the fp16 level of the accumulator
     assert np.abs(g - f).max() < 2e-3
+
+
+def _q4_as_q8(rows4, n_per_row):
+    """q4_0 rows -> the q8_0 rows of the same values (quant = nibble - 8, same scale)."""
+    nb = n_per_row // 32
+    r4 = rows4.reshape(rows4.shape[0], nb, 18)
+    out = np.zeros((rows4.shape[0], nb, 34), np.uint8)
+    out[:, :, :2] = r4[:, :, :2]
+    lo = (r4[:, :, 2:] & 15).astype(np.int16) - 8
+    hi = (r4[:, :, 2:] >> 4).astype(np.int16) - 8
+    out[:, :, 2:18] = lo.astype(np.int8).view(np.uint8)
+    out[:, :, 18:34] = hi.astype(np.int8).view(np.uint8)
+    return out.reshape(rows4.shape[0], -1)
+
+
+def test_q4_0_keys_are_q8_0_keys_of_the_same_values():
+    """A q4_0 K cache (ggml's vec_dot_q4_0_q8_0: low nibbles against query quants
+    0-15, high nibbles against 16-31, minus 8) attends exactly as the q8_0 cache
+    holding the same values, up to the order of the two scale products
+    (sumi * d_k * d_q against sumi * (d_k * d_q)); a swapped nibble half or a
+    missing -8 would move every score.  Against the float64 anchor (unquantised
+    Q) the gap is the query's q8_0 rounding, as for a q8_0 cache."""
+    n_cells, d, H, n_head = 200, 128, 2, 6
+    q, k4, vr = _case(9, n_cells, 3, n_head, H, d, O.T_Q4_0, O.T_Q4_0)
+    k8 = _q4_as_q8(k4, H * d)
+    assert np.array_equal(_deq(O.T_Q4_0, k4, H * d), _deq(O.T_Q8_0, k8, H * d))
+    cp = np.arange(n_cells, dtype=np.int32)
+    qp = np.array([60, 150, 199], np.int32)
+    a = O.fa_ggml(O.T_Q4_0, O.T_Q4_0, q, k4, vr, cp, qp, n_head, H, d, d ** -0.5)
+    b = O.fa_ggml(O.T_Q8_0, O.T_Q4_0, q, k8, vr, cp, qp, n_head, H, d, d ** -0.5)
+    np.testing.assert_allclose(a, b, rtol=0, atol=2e-6)
+    ref = O.fa_f64(O.T_Q4_0, O.T_Q4_0, q, k4, vr, cp, qp, n_head, H, d, d ** -0.5)
+    ref8 = O.fa_f64(O.T_Q8_0, O.T_Q4_0, q, k8, vr, cp, qp, n_head, H, d, d ** -0.5)
+    assert np.max(np.abs(ref - ref8)) < 1e-12
+    assert np.max(np.abs(a - ref)) / np.max(np.abs(ref)) < 2e-2
+    # the wrong nibble order is far outside that
+    k4s = k4.reshape(n_cells, -1, 18).copy()
+    k4s[:, :, 2:] = ((k4s[:, :, 2:] & 15) << 4) | (k4s[:, :, 2:] >> 4)
+    c = O.fa_ggml(O.T_Q4_0, O.T_Q4_0, q, k4s.reshape(n_cells, -1), vr, cp, qp, n_head, H, d, d ** -0.5)
+    assert np.max(np.abs(c - a)) > 1e-2
