@@ -1249,7 +1249,9 @@ static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, 
     // the selecting launch takes lanes that all have query rows, at most
     // KVM_SEL_MAXB blocks each and q8_0 windows; other steps take the
     // separate launches (scoring, top-k, stage-in + attention)
-    bool fuse = kvm_k_quant(lanes[0].w->k_type);
+    // (a q4_0 K window takes the separate launches: the selecting launch's
+    // staging is the one-row-per-wave form, q8_0 only)
+    bool fuse = lanes[0].w->k_type == KVM_TYPE_Q8_0;
     uint32_t max_rows = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_window *w = lanes[i].w;

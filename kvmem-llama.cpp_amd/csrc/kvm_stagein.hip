@@ -43,7 +43,7 @@ static int rope_ctx_for(kvm_state *st, const float *theta, uint32_t n_half, int3
 
 static int hadamard_width(const kvm_window *w, int32_t req) {
     if (req >= 0) return req;
-    if (w->k_type != KVM_TYPE_Q8_0 || w->head_dim < 64 || w->head_dim % 64) return 0;
+    if (!kvm_k_quant(w->k_type) || w->head_dim < 64 || w->head_dim % 64) return 0;   // attn_rot_on
     int nrot = 64;                               // kvmem_hadamard_nrot_k, llama-kvmem-quant.h:30-36
     do { nrot *= 2; } while (w->head_dim % nrot == 0);
     return nrot / 2;
@@ -59,7 +59,7 @@ static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window
     if (!h || !w || !sel) return kvm_fail(st, KVM_EINVAL, "stagein: null argument");
     int rc = kvm_window_check(w);
     if (rc) return kvm_fail(st, rc, "stagein: bad window");
-    if (w->k_type != KVM_TYPE_Q8_0) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: re-RoPE stage-in needs q8_0 K");
+    if (!kvm_k_quant(w->k_type)) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: re-RoPE stage-in needs q8_0 or q4_0 K");
     if (w->block_tokens % 64) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: block_tokens %u not a multiple of 64", w->block_tokens);
     if (!w->slot_block || !w->slot_base) return kvm_fail(st, KVM_EINVAL, "stagein: window without slot map");
     if (!h->k_raw || !h->v || !sel->ids || !sel->to_base || !sel->stage_slots || !sel->info)
@@ -91,6 +91,7 @@ static int stage_lane_args(kvm_state *st, const kvm_history *h, const kvm_window
     a->stage_src = w->k_shadow ? sel->stage_src : nullptr;
     a->moves = nullptr;
     a->sync = nullptr;
+    a->k_q4 = w->k_type == KVM_TYPE_Q4_0 ? 1u : 0u;
     const uint32_t max_slots = sel->cap < a->n_slots ? sel->cap : a->n_slots;
     *max_items = max_slots * (w->block_tokens / 64);
     return KVM_OK;
@@ -129,6 +130,12 @@ int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_l
         return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: n_rot %u (needs a multiple of 8 <= head_dim)", rope->n_rot);
     const int nrot = hadamard_width(w0, rope->hadamard_nrot);
     if (!hadamard_ok(nrot, w0->head_dim)) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: hadamard width %d", nrot);
+    // q4_0 K rows are staged by the 16-lane K rows only (RoPE pairs one dim bit >= 4 apart)
+    for (uint32_t i = 0; i < n_lanes; ++i)
+        if (lanes[i].w->k_type == KVM_TYPE_Q4_0 &&
+            !(w0->head_dim == 256 ? k16_ok<256>(rope->n_rot / 2) : k16_ok<128>(rope->n_rot / 2)))
+            return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: q4_0 K needs n_rot / 2 a power of two >= 16 (n_rot %u)",
+                            rope->n_rot);
     KVM_HIP(st, hipSetDevice(st->device));
     const std::vector<float> theta = kvm_rope_theta(rope->freq_base, rope->freq_scale, rope->n_rot);
     rope_ctx rc0;

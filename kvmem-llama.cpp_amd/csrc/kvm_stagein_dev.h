@@ -207,15 +207,17 @@ __host__ __device__ inline bool k16_ok(uint32_t n_half) {
     return n_half >= 16 && n_half <= (uint32_t)D / 2 && (n_half & (n_half - 1)) == 0;
 }
 // One row per lane group: src = the row's NB q8_0 blocks (34 B each, 2-byte
-// aligned), requantised into K tile kt at cell c; cs = the (cos, sin) row of
-// its window position; l = the lane within the group; live false: computed,
-// not written.  Every lane of the wave takes part (the DPP moves).
+// aligned; q4: q4_0 blocks of 18 B, requantised to q4_0 with quant_q4_0's
+// arithmetic, llama-kvmem-stagein.cu:201-234, and held as q8_0 tile quants,
+// the nibble minus 8), requantised into K tile kt at cell c; cs = the (cos,
+// sin) row of its window position; l = the lane within the group; live false:
+// computed, not written.  Every lane of the wave takes part (the DPP moves).
 template <int D>
 __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, uint32_t c, const float2 *cs, bool live,
-                                              uint32_t l, const rope_ctx &rc) {
+                                              uint32_t l, const rope_ctx &rc, bool q4 = false) {
     const uint32_t m = k16_m<D>(l), b = m >> 1, d0 = 16u * m;
     float x[16];
-    {
+    if (!q4) {
         const uint8_t *blk = src + b * 34u;
         const float dsc = kvm_h2f(*(const uint16_t *)blk);
         const uint16_t *q = (const uint16_t *)(blk + 2u + 16u * (m & 1u));
@@ -224,6 +226,18 @@ __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, u
             const uint32_t w = q[i];
             x[2 * i] = kvm_fmul((float)(int8_t)(uint8_t)w, dsc);
             x[2 * i + 1] = kvm_fmul((float)(int8_t)(uint8_t)(w >> 8), dsc);
+        }
+    } else {
+        // dims 0-15 of a block are the low nibbles of its 16 bytes, 16-31 the high
+        const uint8_t *blk = src + b * 18u;
+        const float dsc = kvm_h2f(*(const uint16_t *)blk);
+        const uint16_t *q = (const uint16_t *)(blk + 2u);
+        const uint32_t sh = 4u * (m & 1u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w = q[i];
+            x[2 * i] = kvm_fmul((float)((int)((w >> sh) & 15u) - 8), dsc);
+            x[2 * i + 1] = kvm_fmul((float)((int)((w >> (8u + sh)) & 15u) - 8), dsc);
         }
     }
     // NeoX RoPE: dims i and i + n_half (one dim bit, log2 n_half >= 4, apart)
@@ -295,19 +309,51 @@ __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, u
         if constexpr (D == 256)
             if (rc.nrot > 128) stage(std::integral_constant<int, 7>{});
     }
-    // q8_0 requantisation: a 32-dim block is the lane and its dim bit 4 partner
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = fmaxf(amax, k16_swap<D, 4>(amax));
-    const float d = kvm_div127(amax);
-    const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ (xs << 31));
+    // requantisation: a 32-dim block is the lane and its dim bit 4 partner
     uint32_t qw[4];
+    float d;
+    if (!q4) {
+        float amax = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        qw[k] = 0;
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        amax = fmaxf(amax, k16_swap<D, 4>(amax));
+        d = kvm_div127(amax);
+        const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ (xs << 31));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qw[k] |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[4 * k + i], id)) << (8 * i);
+        for (int k = 0; k < 4; ++k) {
+            qw[k] = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qw[k] |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[4 * k + i], id)) << (8 * i);
+        }
+    } else {
+        // quant_q4_0: vmax = the first value of largest magnitude in dim order
+        // (the lane with dims 0-15 of the block comes first), with its true
+        // sign (the lane's registers carry xs); d = vmax / -8 (vmax * -0.125
+        // exactly), id = d ? 1/d : 0, quant = min(15, (int)(x id + 8.5)) - 8
+        float am = 0.0f, vm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float a = fabsf(x[i]);
+            if (am < a) { am = a; vm = x[i]; }
+        }
+        vm = __uint_as_float(__float_as_uint(vm) ^ (xs << 31));
+        const float am_p = k16_swap<D, 4>(am), vm_p = k16_swap<D, 4>(vm);
+        const bool first = (m & 1u) == 0u;
+        const float am_f = first ? am : am_p, vm_f = first ? vm : vm_p;
+        const float am_s = first ? am_p : am, vm_s = first ? vm_p : vm;
+        const float vmax = am_f < am_s ? vm_s : vm_f;
+        d = kvm_fmul(vmax, -0.125f);
+        const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ (xs << 31));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            qw[k] = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                int xi = (int)kvm_fadd(kvm_fmul(x[4 * k + i], id), 8.5f);
+                xi = xi > 15 ? 15 : xi;
+                qw[k] |= (uint32_t)(uint8_t)(int8_t)(xi - 8) << (8 * i);
+            }
+        }
     }
     if (!live) return;
     // two 8-byte runs of the tile (dims 16m .. +7 and 16m + 8 .. +15)
@@ -343,6 +389,7 @@ struct stage_args {
     uint32_t *sync;                  // the lane's barrier words (kvm_state::stage_sync)
     uint32_t *status;                // the state's sticky wait status (KVM_WAIT_STAGE when a barrier gives up)
     uint32_t spin;                   // polls of a barrier wait before it gives up (0: at once)
+    uint32_t k_q4;                   // q4_0 K: history rows of 18-byte blocks, requantised to q4_0
 };
 
 // dst[i] = src[i] for 16-byte units i = tid, tid + nth, ... < n (n >= 1, the
@@ -441,8 +488,9 @@ __device__ inline void stage_fill(uint8_t *d0, const uint8_t *__restrict__ s0, u
     }
 }
 
-// Row bytes of the history / shadow: q8_0 K and q4_0 V, all kv heads.
-__host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 34; }
+// Row bytes of the history / shadow: q8_0 (or q4_0) K and q4_0 V, all kv heads.
+__host__ __device__ inline uint32_t stage_kblk(const stage_args &a) { return a.k_q4 ? 18u : 34u; }
+__host__ __device__ inline uint32_t stage_row_k(const stage_args &a, uint32_t D) { return a.H * (D / 32) * stage_kblk(a); }
 __host__ __device__ inline uint32_t stage_row_v(const stage_args &a, uint32_t D) { return a.H * (D / 32) * 18; }
 // Whether a plan that moves blocks also gathers its host entries' rows into
 // the staging (16-byte units: rows and history 16-byte aligned), so that every
@@ -558,7 +606,7 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
     const uint32_t t0 = tt * IT;
     const uint32_t count = nt > t0 ? (nt - t0 < IT ? nt - t0 : IT) : 0;
     const uint64_t htok0 = first + t0;
-    const uint32_t rowK = a.H * NB * 34, rowV = a.H * NB * 18;
+    const uint32_t kb = stage_kblk(a), rowK = a.H * NB * kb, rowV = a.H * NB * 18;
     // LDS: the item's K rows, V rows, and the (cos, sin) rows of its positions
     uint8_t *lk = s_rows, *lv = s_rows + IT * rowK;
     float2 *lt = (float2 *)(s_rows + IT * (rowK + rowV));
@@ -610,8 +658,8 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         for (uint32_t r0 = wave * RW; r0 < nrow; r0 += W * RW) {
             const uint32_t r = r0 + grp, rr = r < nrow ? r : r0;     // past the rows: recompute r0, unwritten
             const uint32_t j = rr / a.H, h = rr % a.H;
-            stage_k_row16<D>(lk + j * rowK + h * NB * 34, ktile + (uint64_t)h * a.n_tiles * kvm_ktile_bytes(KVM_TYPE_Q8_0, D),
-                             c0 + j, lt + j * nh, r < nrow, l, a.rc);
+            stage_k_row16<D>(lk + j * rowK + h * NB * kb, ktile + (uint64_t)h * a.n_tiles * kvm_ktile_bytes(KVM_TYPE_Q8_0, D),
+                             c0 + j, lt + j * nh, r < nrow, l, a.rc, a.k_q4 != 0);
         }
     } else
     // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time

@@ -230,15 +230,22 @@ int oracle_attn_rot_on(int type, int head_dim) {
     return quantized && head_dim >= 64 && head_dim % 64 == 0;
 }
 
-void oracle_stagein_k(const uint8_t *packed, uint8_t *out, int64_t nt, int n_head,
-                      int head_dim, int n_rot, int nrot, int32_t pos0, const float *theta) {
+void oracle_stagein_k_type(int k_type, const uint8_t *packed, uint8_t *out, int64_t nt, int n_head,
+                           int head_dim, int n_rot, int nrot, int32_t pos0, const float *theta) {
     const int64_t n_embd = (int64_t)n_head * head_dim;
     float *f = (float *)malloc(sizeof(float) * (size_t)(nt * n_embd));
-    oracle_dequant_q8_0(packed, f, nt * n_embd);
+    if (k_type == ORACLE_T_Q4_0) oracle_dequant_q4_0(packed, f, nt * n_embd);
+    else oracle_dequant_q8_0(packed, f, nt * n_embd);
     oracle_rope_neox(f, nt, n_head, head_dim, n_rot, pos0, theta);
     if (nrot > 0) oracle_fwht(f, nt * (n_embd / nrot), nrot);
-    oracle_quant_q8_0(f, out, nt * n_embd);
+    if (k_type == ORACLE_T_Q4_0) oracle_quant_q4_0(f, out, nt * n_embd);
+    else oracle_quant_q8_0(f, out, nt * n_embd);
     free(f);
+}
+
+void oracle_stagein_k(const uint8_t *packed, uint8_t *out, int64_t nt, int n_head,
+                      int head_dim, int n_rot, int nrot, int32_t pos0, const float *theta) {
+    oracle_stagein_k_type(ORACLE_T_Q8_0, packed, out, nt, n_head, head_dim, n_rot, nrot, pos0, theta);
 }
 
 /* ------------------------------------------------------------------------- */

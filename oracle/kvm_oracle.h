@@ -66,6 +66,10 @@ int  oracle_attn_rot_on(int type, int head_dim);       /* llama-kvmem-quant.h:22
  * packed: q8_0 rows [nt][n_head*head_dim]; out: same format.  nrot == 0 skips FWHT. */
 void oracle_stagein_k(const uint8_t *packed, uint8_t *out, int64_t nt, int n_head,
                       int head_dim, int n_rot, int nrot, int32_t pos0, const float *theta);
+/* The same chain for a q4_0 K cache (k_type ORACLE_T_Q4_0): dequant_q4_0 ->
+ * RoPE -> FWHT -> quant_q4_0 (llama-kvmem-stagein.cu:145-158, 201-234, 731-786). */
+void oracle_stagein_k_type(int k_type, const uint8_t *packed, uint8_t *out, int64_t nt, int n_head,
+                           int head_dim, int n_rot, int nrot, int32_t pos0, const float *theta);
 
 /* ---- mean-K index: kvmem/src/host/raw_kv_store.cpp:215-234, 987-1006 ------ */
 /* Ordered fp32 accumulation of `take` token rows starting at in-block offset off. */

@@ -45,6 +45,7 @@ def lib():
             "oracle_hadamard_nrot_k": (C.c_int, [C.c_int]),
             "oracle_attn_rot_on": (C.c_int, [C.c_int, C.c_int]),
             "oracle_stagein_k": (None, [P, P, i64, C.c_int, C.c_int, C.c_int, C.c_int, i32, P]),
+            "oracle_stagein_k_type": (None, [C.c_int, P, P, i64, C.c_int, C.c_int, C.c_int, C.c_int, i32, P]),
             "oracle_meank_add": (None, [P, P, P, u32, u32, C.c_int]),
             "oracle_meank_normalize": (None, [P, u32, P, C.c_int]),
             "oracle_score_retrieval": (None, [C.c_int] * 5 + [P, P, P, P, P, P, C.c_int]),
@@ -129,11 +130,15 @@ def fwht(x, n):
     return x
 
 
-def stagein_k(packed, nt, n_head, head_dim, n_rot, nrot, pos0, theta):
+def stagein_k(packed, nt, n_head, head_dim, n_rot, nrot, pos0, theta, k_type=None):
+    """Stage-in of raw K rows (q8_0, or q4_0 with k_type=T_Q4_0) at window position pos0."""
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     out = np.empty_like(packed)
-    lib().oracle_stagein_k(_p(packed), _p(out), nt, n_head, head_dim, n_rot, nrot, pos0,
-                           _p(np.ascontiguousarray(theta, np.float32)))
+    th = _p(np.ascontiguousarray(theta, np.float32))
+    if k_type is None or k_type == T_Q8_0:
+        lib().oracle_stagein_k(_p(packed), _p(out), nt, n_head, head_dim, n_rot, nrot, pos0, th)
+    else:
+        lib().oracle_stagein_k_type(k_type, _p(packed), _p(out), nt, n_head, head_dim, n_rot, nrot, pos0, th)
     return out
 
 

@@ -418,3 +418,42 @@ def test_decode_step_four_lanes_full_windows(kvm_state):
     ref = O.fa_ggml(O.T_Q8_0, O.T_Q4_0, lanes[0]["q"].float().cpu().numpy(), host(ek), host(ev),
                     host(w.cell_pos)[:budget * BT], host(lanes[0]["q_pos"]), H * G, H, D, D ** -0.5)
     check_attention(host(lanes[0]["out"]), ref)
+
+
+def test_decode_step_q4_0_k_window(kvm_state):
+    """The whole step over a q4_0 K cache (history rows and window in q4_0):
+    kvm_score_topk_stagein_fa_decode takes the separate launches for it; the
+    staged blocks equal the oracle's q4_0 stage-in and the output the ggml
+    attention over the window it leaves (a q4_0 K cache: Q quantised to q8_0,
+    vec_dot_q4_0_q8_0)."""
+    st = kvm_state
+    rng = np.random.default_rng(0x44)
+    n_blocks, budget = 24, 8
+    n_hist = n_blocks * BT
+    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q4_0, L.T_Q4_0)
+    ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
+    ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
+    qa = api.QueryAcc(st, 1, H * G, D)
+    qa.reset()
+    qa.add(0, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
+    nt = dev(np.full(n_blocks, BT, np.int32))
+    w = api.KVWindow(st, budget * BT, H, D, BT, L.T_Q4_0, L.T_Q4_0)
+    sel = api.SelectionBuffers(st, n_blocks, budget)
+    q = dev(rng.standard_normal((4, H * G, D)).astype(np.float32)).to(torch.bfloat16)
+    q_pos = dev(np.arange(budget * BT - 4, budget * BT, dtype=np.int32))
+    out = api.decode_step(st, ix, qa, n_blocks, nt, budget, 1, 0, w, sel, api.History(kr, vr), q, q_pos, H * G,
+                          D ** -0.5, 64, 1e7)
+    st.sync()
+    res = sel.result()
+    assert res["status"] == 0 and len(res["ids"]) == budget
+    theta = O.rope_theta(1e7, 1.0, 64)
+    ek, ev = w.export_rows(0, budget * BT)
+    ek, ev = host(ek), host(ev)
+    for k in (0, 3, budget - 1):
+        bid, base = int(res["ids"][k]), int(res["to_base"][k])
+        want = O.stagein_k(kr[bid * BT:(bid + 1) * BT].reshape(-1), BT, H, D, 64, 256, base, theta,
+                           k_type=O.T_Q4_0).reshape(BT, -1)
+        assert np.array_equal(ek[k * BT:(k + 1) * BT], want), k
+    ref = O.fa_ggml(O.T_Q4_0, O.T_Q4_0, q.float().cpu().numpy(), ek, ev, host(w.cell_pos), host(q_pos), H * G, H, D,
+                    D ** -0.5)
+    check_attention(host(out), ref)

@@ -127,3 +127,30 @@ def test_stagein_inverts_up_to_quantisation():
     back = np.stack([O.rope_neox(y[t:t + 1], n_head, d, n_rot, -(pos0 + t), theta)[0] for t in range(nt)])
     ref = O.dequant(O.T_Q8_0, packed, x.size).reshape(nt, n_head, d)
     assert np.abs(back - ref).max() < 0.05
+
+
+def test_stagein_q4_0_identity_and_inverse():
+    """The q4_0 K chain (dequant_q4_0 -> RoPE -> FWHT -> quant_q4_0): one token
+    at position 0 with the Hadamard step off gives back q4_0 blocks whose
+    largest-magnitude quant is -8 (nibble 0) unchanged, since quant_q4_0 of
+    their dequantised values reproduces them; and dequant, inverse Hadamard
+    and RoPE at -pos recover the raw K within the two q4_0 roundings."""
+    rng = np.random.default_rng(16)
+    blocks = np.zeros((32, 18), np.uint8)
+    nib = rng.integers(1, 16, (32, 32))                 # quants -7 .. 7 ...
+    nib[:, 5] = 0                                      # ... and one -8 (vmax = -8 d)
+    blocks[:, :2] = rng.uniform(0.01, 1, 32).astype(np.float16).view(np.uint8).reshape(32, 2)
+    blocks[:, 2:] = (nib[:, :16] | (nib[:, 16:] << 4)).astype(np.uint8)
+    packed = blocks.reshape(-1)                        # 1 token x 4 heads x 256 dims
+    theta = O.rope_theta(1e7, 1.0, 64)
+    assert np.array_equal(O.stagein_k(packed, 1, 4, 256, 64, 0, 0, theta, k_type=O.T_Q4_0), packed)
+    nt, n_head, d, n_rot, pos0 = 4, 4, 256, 64, 3000
+    x = rng.standard_normal((nt, n_head * d)).astype(np.float32)
+    p4 = O.quant(O.T_Q4_0, x.reshape(-1))
+    staged = O.stagein_k(p4, nt, n_head, d, n_rot, 256, pos0, theta, k_type=O.T_Q4_0)
+    f = O.dequant(O.T_Q4_0, p4, x.size)
+    assert np.array_equal(staged, O.quant(O.T_Q4_0, O.fwht(O.rope_neox(f, n_head, d, n_rot, pos0, theta), 256)))
+    y = O.fwht(O.dequant(O.T_Q4_0, staged, x.size), 256).reshape(nt, n_head, d)
+    back = np.stack([O.rope_neox(y[t:t + 1], n_head, d, n_rot, -(pos0 + t), theta)[0] for t in range(nt)])
+    ref = f.reshape(nt, n_head, d)
+    assert np.abs(back - ref).max() < 0.6 and np.abs(back - ref).mean() < 0.15
