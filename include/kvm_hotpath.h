@@ -303,12 +303,12 @@ int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uint32_t il, u
  * device-to-host copy, llama-kvmem-stagein.cu:879-969): the window cells
  * [cell0, cell0+n) give their V rows (cache format, unchanged) and the view
  * tokens tok0 .. tok0+n-1 of their captured pre-RoPE K give the history's
- * unrotated K rows, quantised to q8_0 with ggml's formula (the rows the
- * re-RoPE stage-in reads back); both are gathered on the device and copied to
- * k_raw_rows / v_rows (host: the history rows of the tokens' positions).
- * When ix is given the same K rows are added to its layer il at pos0
- * (write_layer_mean_k).  q8_0 K windows; the copies are done when the state's
- * stream reaches this point (kvm_state_sync).  With w->pending_rows, a slot
+ * unrotated K rows, quantised to the window's K type (q8_0 or q4_0) with
+ * ggml's formula (the rows the re-RoPE stage-in reads back); both are gathered
+ * on the device and copied to k_raw_rows / v_rows (host: the history rows of
+ * the tokens' positions).  When ix is given the same K rows are added to its
+ * layer il at pos0 (write_layer_mean_k).  q8_0 or q4_0 K windows; the copies
+ * are done when the state's stream reaches this point (kvm_state_sync).  With w->pending_rows, a slot
  * whose recorded end the cells reach is clear again. */
 int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                       const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,

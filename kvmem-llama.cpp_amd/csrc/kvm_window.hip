@@ -703,13 +703,32 @@ __global__ void k_quant_view_q8(view_args v, uint32_t tok0, uint32_t n, uint32_t
     for (int j = 0; j < 32; ++j) o[2 + j] = (uint8_t)q[j];
 }
 
+// the same for a q4_0 K cache (quant_q4_0's arithmetic)
+__global__ void k_quant_view_q4(view_args v, uint32_t tok0, uint32_t n, uint32_t n_embd, uint8_t *dst) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;     // 32-value block
+    const uint32_t nb = n_embd / 32;
+    if (i >= (uint64_t)n * nb) return;
+    const uint32_t t = (uint32_t)(i / nb), b = (uint32_t)(i % nb);
+    float x[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) x[j] = view_load(v, tok0 + t, 32 * b + j);
+    uint16_t d;
+    uint8_t q[16];
+    kvm_quant_block_q4_0(x, &d, q);
+    uint8_t *o = dst + i * 18;
+    o[0] = (uint8_t)d;
+    o[1] = (uint8_t)(d >> 8);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[2 + j] = q[j];
+}
+
 extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t cell0, uint32_t n,
                                  const kvm_view *k_prerope, uint32_t tok0, void *k_raw_rows, void *v_rows,
                                  const kvm_meank_index *ix, uint32_t il, uint32_t pos0) {
     if (!st) return KVM_EINVAL;
     int rc = kvm_window_check(w);
     if (rc) return kvm_fail(st, rc, "harvest: bad window");
-    if (w->k_type != KVM_TYPE_Q8_0) return kvm_fail(st, KVM_EUNSUPPORTED, "harvest: q8_0 K history only");
+    if (!kvm_k_quant(w->k_type)) return kvm_fail(st, KVM_EUNSUPPORTED, "harvest: q8_0 or q4_0 K history only");
     if ((uint64_t)cell0 + n > w->n_cells) return kvm_fail(st, KVM_ERANGE, "harvest: cells past the window");
     const uint32_t n_embd = w->n_head_kv * w->head_dim;
     rc = view_check(st, k_prerope, n_embd, "harvest");
@@ -717,7 +736,8 @@ extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t ce
     if ((uint64_t)tok0 + n > (uint64_t)k_prerope->ne2) return kvm_fail(st, KVM_ERANGE, "harvest: tokens past the view");
     if (!k_raw_rows || !v_rows) return kvm_fail(st, KVM_EINVAL, "harvest: null history rows");
     if (n == 0) return KVM_OK;
-    const uint64_t krow = (uint64_t)n_embd / 32 * 34;
+    const bool q4 = w->k_type == KVM_TYPE_Q4_0;
+    const uint64_t krow = (uint64_t)n_embd / 32 * (q4 ? 18 : 34);
     const uint64_t vrow = w->v_type == KVM_TYPE_Q4_0 ? (uint64_t)n_embd / 32 * 18 : (uint64_t)n_embd * 2;
     const uint64_t kb = n * krow, vb = n * vrow;
     uint8_t *stage = (uint8_t *)kvm_workspace(st, kb + vb);
@@ -725,8 +745,12 @@ extern "C" int kvm_harvest_block(kvm_state *st, const kvm_window *w, uint32_t ce
     KVM_HIP(st, hipSetDevice(st->device));
     // the gather: K rows quantised from the view, V rows out of the tiles
     const uint64_t nblk = (uint64_t)n * (n_embd / 32);
-    hipLaunchKernelGGL(k_quant_view_q8, dim3(kvm_cdiv(nblk, 256)), dim3(256), 0, st->stream, view_of(k_prerope),
-                       tok0, n, n_embd, stage);
+    if (q4)
+        hipLaunchKernelGGL(k_quant_view_q4, dim3(kvm_cdiv(nblk, 256)), dim3(256), 0, st->stream, view_of(k_prerope),
+                           tok0, n, n_embd, stage);
+    else
+        hipLaunchKernelGGL(k_quant_view_q8, dim3(kvm_cdiv(nblk, 256)), dim3(256), 0, st->stream, view_of(k_prerope),
+                           tok0, n, n_embd, stage);
     KVM_LAUNCH_CHECK(st, "harvest");
     rc = kvm_window_export_rows(st, w, cell0, n, nullptr, stage + kb);
     if (rc) return rc;

@@ -47,24 +47,25 @@ def test_slot_copies_round_trip(kvm_state, kt, vt, H, D):
         api.slot_copy_to_host(kvm_state, ws, 8)
 
 
-def test_harvest_then_restage(kvm_state):
+@pytest.mark.parametrize("kt", [L.T_Q8_0, L.T_Q4_0])
+def test_harvest_then_restage(kvm_state, kt):
     """Generated tokens occupy slot 5 of the window (window positions 640..767,
     original positions 4*128.. of the history); the harvest writes their
-    q8_0-quantised captured pre-RoPE K and their window V rows as history
+    captured pre-RoPE K quantised to the cache's K type (q8_0 or q4_0) and their window V rows as history
     block 4 and adds the K to the mean-K index; a reselect that drops the block
     reuses the slot, and a later one that picks it again stages it back from the
     history exactly as the oracle stages the harvested rows."""
     rng = np.random.default_rng(32)
     H, D, bt, n_hist_blocks = 4, 256, 128, 8
     n_hist = n_hist_blocks * bt
-    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    kr, vr = rand_rows(rng, n_hist, H, D, kt, L.T_Q4_0)
     k_hist = np.zeros_like(kr)
     v_hist = np.zeros_like(vr)
     k_hist[:4 * bt], v_hist[:4 * bt] = kr[:4 * bt], vr[:4 * bt]     # blocks 4.. are not harvested yet
     hist = api.History(k_hist, v_hist)
-    w = api.KVWindow(kvm_state, 6 * bt, H, D, bt)
+    w = api.KVWindow(kvm_state, 6 * bt, H, D, bt, kt, L.T_Q4_0)
     # generated block: rotated K rows in the cache (any bytes), V rows, positions
-    gk, gv = rand_rows(rng, bt, H, D, L.T_Q8_0, L.T_Q4_0)
+    gk, gv = rand_rows(rng, bt, H, D, kt, L.T_Q4_0)
     w.import_rows(5 * bt, dev(gk), dev(gv), dev(np.arange(5 * bt, 6 * bt, dtype=np.int32)))
     cap = torch.from_numpy(rng.standard_normal((bt + 3, H, D)).astype(np.float32)).to(torch.bfloat16).cuda()
     cap = cap.permute(1, 0, 2).contiguous().permute(1, 0, 2)          # the captured view, heads-major storage
@@ -72,7 +73,7 @@ def test_harvest_then_restage(kvm_state):
     api.harvest_block(kvm_state, w, 5 * bt, bt, cap, 3, hist.kbuf.u8[4 * bt * w.k_row_bytes():].reshape(-1)[:bt * w.k_row_bytes()],
                       hist.vbuf.u8[4 * bt * w.v_row_bytes():].reshape(-1)[:bt * w.v_row_bytes()], ix, 0, 4 * bt)
     k32 = cap[3:].float().cpu().numpy().reshape(bt, -1)
-    want_k = O.quant(O.T_Q8_0, k32.reshape(-1)).reshape(bt, -1)
+    want_k = O.quant(kt, k32.reshape(-1)).reshape(bt, -1)
     got_k = hist.kbuf.u8.reshape(n_hist, -1)[4 * bt:5 * bt]
     assert np.array_equal(got_k, want_k)
     assert np.array_equal(hist.vbuf.u8.reshape(n_hist, -1)[4 * bt:5 * bt], gv)
@@ -92,7 +93,8 @@ def test_harvest_then_restage(kvm_state):
     assert list(r["ids"]) == [0, 1, 2, 4] and r["status"] == 0
     theta = O.rope_theta(1e7, 1.0, 64)
     ek, ev = w.export_rows(3 * bt, bt)
-    assert np.array_equal(host(ek).reshape(-1), O.stagein_k(want_k.reshape(-1), bt, H, D, 64, 256, 3 * bt, theta))
+    assert np.array_equal(host(ek).reshape(-1), O.stagein_k(want_k.reshape(-1), bt, H, D, 64, 256, 3 * bt, theta,
+                                                          k_type=kt))
     assert np.array_equal(host(ev), gv)
 
 
