@@ -116,7 +116,9 @@ typedef struct kvm_window {
     uint32_t n_head_kv;
     uint32_t head_dim;      /* 128 or 256 */
     uint32_t block_tokens;  /* cells per slot (llama_kvmem_params.block_tokens) */
-    int32_t k_type;         /* KVM_TYPE_Q8_0 (with v_type Q4_0) or KVM_TYPE_F16 (with F16) */
+    int32_t k_type;         /* KVM_TYPE_Q8_0 or KVM_TYPE_Q4_0 (with v_type Q4_0), or KVM_TYPE_F16
+                             * (with F16); a q4_0 K window holds its rows as q8_0 tile quants
+                             * (the nibble minus 8), so its K bytes are q8_0's */
     int32_t v_type;
     void *k;                /* device, kvm_window_k_bytes() */
     void *v;                /* device, kvm_window_v_bytes() */
@@ -442,7 +444,10 @@ typedef struct kvm_history {
  * Entries with sel->stage_src[i] >= 0 (a window with a shadow) take their raw K
  * rows from the shadow of that slot and their V from that slot's tiles, all
  * gathered before any slot is written, so the window ends byte-equal to a
- * stage-in of the whole plan from the host. */
+ * stage-in of the whole plan from the host.  A q4_0 K window (no shadow) has
+ * q4_0 raw K rows in its history, requantised to q4_0 (quant_q4_0,
+ * llama-kvmem-stagein.cu:201-234); its rope->n_rot / 2 must be a power of two
+ * of at least 16 (else KVM_EUNSUPPORTED). */
 int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
                           const kvm_selection *sel, const kvm_rope_params *rope);
 
@@ -518,7 +523,7 @@ int kvm_fa_decode_lanes(kvm_state *st, const kvm_lane *lanes, uint32_t n_lanes, 
  * loop's steady state) the step's stage-in launch disappears.  The reference
  * stages in the memory module (write_block_to_gpu + kvmem_stagein_flush,
  * llama-memory-kvmem.cpp:4000-4071) before the graph's flash attention runs
- * (ggml_cuda_flash_attn_ext, ggml-cuda/fattn.cu:457).  q8_0 / q4_0 windows;
+ * (ggml_cuda_flash_attn_ext, ggml-cuda/fattn.cu:457).  q8_0 or q4_0 K / q4_0 V windows;
  * in the lanes form stage[i].w must be lanes[i].w's window. */
 int kvm_stagein_fa_decode(kvm_state *st, const kvm_history *h, const kvm_selection *sel,
                           const kvm_rope_params *rope, const kvm_window *w, const void *q, int q_type,
@@ -539,11 +544,13 @@ int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, co
  * and then runs the graph's flash attention (ggml-cuda/fattn.cu:457), one
  * after the other.  Steps with more than 4,096 blocks in a lane or a lane
  * without query tokens run as three launches (kvm_score_topk, then
- * kvm_stagein_fa_decode) with the same results; a window that is not
- * q8_0 / q4_0 is refused (KVM_EUNSUPPORTED), as kvm_stagein_fa_decode refuses
- * it.  A step whose plan stages anything pays for the attention's first pass:
- * where a plan change is expected (the first retrieval after a new query) the
- * three-launch calls are faster.  In the lanes form ret[i].w must be
+ * kvm_stagein_fa_decode) with the same results, and so do q4_0 K windows; a
+ * window that is not q8_0 or q4_0 K / q4_0 V is refused (KVM_EUNSUPPORTED), as
+ * kvm_stagein_fa_decode refuses it.  A step whose plan stages anything pays for
+ * the attention's first pass: where a plan change is expected (the first
+ * retrieval after a new query) the separate calls are faster, and for a plan
+ * that moves most of the window kvm_score_topk_stagein then kvm_fa_decode is
+ * the fastest (the stage-in kernel runs two workgroups per CU).  In the lanes form ret[i].w must be
  * lanes[i].w's window and hist[i] is lane i's history; every argument is
  * checked before the first launch. */
 int kvm_score_topk_stagein_fa_decode(kvm_state *st, const kvm_meank_index *ix, const kvm_query_acc *qa,
