@@ -92,7 +92,8 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HI
     qsum_kv = means.sum(1).view(H_KV, D)
     qrows = qsum_kv.repeat_interleave(G, 0).reshape(1, N_HEAD * D).repeat(mtp, 1)
     qrows = qrows + 0.1 * torch.randn(qrows.shape, generator=gen, device=dev)
-    qa = api.QueryAcc(st, 1, N_HEAD, D)
+    # the accumulator carries the scorer's query terms, kept current by add
+    qa = api.QueryAcc(st, 1, N_HEAD, D, n_head_kv=H_KV)
     qa.reset()
     qa.add(0, qrows)
     n_tokens = torch.full((n_blocks,), BT, dtype=torch.int32, device=dev)
@@ -526,10 +527,11 @@ def run_churn(args, st, api, L, torch, np):
     ix.present[:n_blocks] = 1
     qas = []
     for dim in (0, 1):
-        qa = api.QueryAcc(st, 1, N_HEAD, D)
+        qa = api.QueryAcc(st, 1, N_HEAD, D, n_head_kv=H_KV)
         qa.q_sum.zero_()
         qa.q_sum[0, dim] = 1.0
         qa.q_count.fill_(1)
+        qa.refresh()
         qas.append(qa)
     n_tokens = torch.full((n_blocks,), BT, dtype=torch.int32, device=dev)
     ng = WINDOW - RETRIEVED

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 4
+#define KVM_ABI_VERSION 5
 
 enum kvm_status {
     KVM_OK = 0,
@@ -226,6 +226,21 @@ typedef struct kvm_query_acc {
     uint32_t head_dim;
     float *q_sum;           /* device [n_layer][n_head * head_dim] */
     uint32_t *q_count;      /* device [n_layer] */
+    /* Optional: the query terms of score_retrieval, formed once per change of
+     * the sums instead of once per block tile by the scorer.  With q_vec !=
+     * NULL, for kv head h of n_head_kv (group g = n_head / n_head_kv):
+     *   q_vec[il][h][d] = (q_sum rows h*g .. h*g+g-1 of layer il added in row
+     *                      order) * (1 / (q_count[il] * g))
+     *   q_norm[il][h]   = the sum over d, in dim order, of q_vec[il][h][d]^2
+     * (fp32, each operation one IEEE rounding: the reference's qv and nq,
+     * llama-memory-kvmem.cpp:4167-4185).  kvm_query_reset, _add and _add_view
+     * keep them current; a caller that writes q_sum or q_count itself calls
+     * kvm_query_refresh before the next scoring.  The scorers then read them
+     * (n_head_kv must equal the mean-K index's); NULL: the scorer forms them
+     * itself. */
+    uint32_t n_head_kv;
+    float *q_vec;           /* device [n_layer][n_head_kv * head_dim] or NULL */
+    float *q_norm;          /* device [n_layer][n_head_kv] or NULL */
 } kvm_query_acc;
 
 /* A captured graph output as the attn-qk-capture hook sees it (patches/
@@ -253,6 +268,10 @@ int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const fl
  * q_count[il] += the rows added. */
 int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const kvm_view *q,
                        const uint8_t *keep);
+/* Forms q_vec / q_norm of every layer from q_sum / q_count (no counterpart in
+ * the reference, which forms them inside score_retrieval): for callers that
+ * write the sums directly.  KVM_OK without work when q_vec is NULL. */
+int kvm_query_refresh(kvm_state *st, const kvm_query_acc *acc);
 
 /* Mean-K index: per (layer, block) the ordered fp32 sum of pre-RoPE K rows and
  * its token count (RawKvStore k_sum / mean_tokens, raw_kv_store.cpp:215-234). */

@@ -51,16 +51,87 @@ __global__ void k_zero_u32(uint32_t *p, uint64_t n) {
     if (i < n) p[i] = 0u;
 }
 
+// The query terms of score_retrieval (llama-memory-kvmem.cpp:4167-4185) for
+// one (layer, kv head) per workgroup of 64 threads: lane l forms qv of dims l,
+// l + 64, ... (the group's rows added in row order from 0.0f, times 1 / (q_count
+// g)), then lane 0 sums qv^2 over the dims in order from LDS.  The same
+// operations as the scorer's own formation, so the scores do not change.
+template <int D>
+__global__ void __launch_bounds__(64) k_query_terms(const float *q_sum, const uint32_t *q_count, float *q_vec,
+                                                    float *q_norm, uint32_t il0, uint32_t n_head, uint32_t H) {
+    const uint32_t il = il0 + blockIdx.x, h = blockIdx.y, l = threadIdx.x, g = n_head / H;
+    __shared__ float s_sq[D];
+    const uint32_t qc = q_count[il];
+    const float invq = kvm_recip_or0((float)(qc * (g > 1u ? g : 1u)));
+    const float *qrow = q_sum + ((uint64_t)il * n_head + (uint64_t)h * g) * D;
+    float *out = q_vec + ((uint64_t)il * H + h) * D;
+    for (uint32_t d = l; d < (uint32_t)D; d += 64u) {
+        float qh = 0.0f;
+        for (uint32_t gi = 0; gi < g; ++gi) qh = kvm_fadd(qh, qrow[(uint64_t)gi * D + d]);
+        const float qv = kvm_fmul(qh, invq);
+        out[d] = qv;
+        s_sq[d] = kvm_fmul(qv, qv);
+    }
+    __syncthreads();
+    if (l == 0) {
+        float nq = 0.0f;
+        for (uint32_t d = 0; d < (uint32_t)D; ++d) nq = kvm_fadd(nq, s_sq[d]);
+        q_norm[(uint64_t)il * H + h] = nq;
+    }
+}
+
+// An accumulator that carries the query terms: their buffers and grouping.
+static int query_terms_check(kvm_state *st, const kvm_query_acc *acc, const char *who) {
+    if (!acc->q_vec) return KVM_OK;
+    if (!acc->q_norm || acc->n_head_kv == 0 || acc->n_head % acc->n_head_kv)
+        return kvm_fail(st, KVM_EINVAL, "%s: q_vec needs q_norm and n_head_kv dividing n_head (%u / %u)", who,
+                        acc->n_head, acc->n_head_kv);
+    if (acc->head_dim != 128 && acc->head_dim != 256)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "%s: query terms at head_dim %u", who, acc->head_dim);
+    return KVM_OK;
+}
+
+// Forms the terms of layers [il0, il0 + n) on the state's stream.
+static int query_terms_launch(kvm_state *st, const kvm_query_acc *acc, uint32_t il0, uint32_t n) {
+    if (!acc->q_vec || n == 0) return KVM_OK;
+    const dim3 grid(n, acc->n_head_kv);
+    if (acc->head_dim == 256)
+        hipLaunchKernelGGL(k_query_terms<256>, grid, dim3(64), 0, st->stream, acc->q_sum, acc->q_count, acc->q_vec,
+                           acc->q_norm, il0, acc->n_head, acc->n_head_kv);
+    else
+        hipLaunchKernelGGL(k_query_terms<128>, grid, dim3(64), 0, st->stream, acc->q_sum, acc->q_count, acc->q_vec,
+                           acc->q_norm, il0, acc->n_head, acc->n_head_kv);
+    KVM_LAUNCH_CHECK(st, "query_terms");
+    return KVM_OK;
+}
+
 extern "C" int kvm_query_reset(kvm_state *st, const kvm_query_acc *acc) {
     if (!st || !acc || !acc->q_sum || !acc->q_count) return kvm_fail(st, KVM_EINVAL, "query_reset: args");
+    int rc = query_terms_check(st, acc, "query_reset");
+    if (rc) return rc;
     KVM_HIP(st, hipSetDevice(st->device));
     const uint64_t n = (uint64_t)acc->n_layer * acc->n_head * acc->head_dim;
     if (n) hipLaunchKernelGGL(k_zero_f32, dim3(kvm_cdiv(n, 256)), dim3(256), 0, st->stream, acc->q_sum, n);
     if (acc->n_layer)
         hipLaunchKernelGGL(k_zero_u32, dim3(kvm_cdiv(acc->n_layer, 256)), dim3(256), 0, st->stream,
                            acc->q_count, (uint64_t)acc->n_layer);
+    if (acc->q_vec) {
+        // the terms of an empty accumulator: qv = 0 * (1 / 0 -> 0), nq = 0
+        const uint64_t nv = (uint64_t)acc->n_layer * acc->n_head_kv * acc->head_dim;
+        const uint64_t nn = (uint64_t)acc->n_layer * acc->n_head_kv;
+        if (nv) hipLaunchKernelGGL(k_zero_f32, dim3(kvm_cdiv(nv, 256)), dim3(256), 0, st->stream, acc->q_vec, nv);
+        if (nn) hipLaunchKernelGGL(k_zero_f32, dim3(kvm_cdiv(nn, 256)), dim3(256), 0, st->stream, acc->q_norm, nn);
+    }
     KVM_LAUNCH_CHECK(st, "query_reset");
     return KVM_OK;
+}
+
+extern "C" int kvm_query_refresh(kvm_state *st, const kvm_query_acc *acc) {
+    if (!st || !acc || !acc->q_sum || !acc->q_count) return kvm_fail(st, KVM_EINVAL, "query_refresh: args");
+    int rc = query_terms_check(st, acc, "query_refresh");
+    if (rc) return rc;
+    KVM_HIP(st, hipSetDevice(st->device));
+    return query_terms_launch(st, acc, 0, acc->n_layer);
 }
 
 extern "C" int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint32_t il, const kvm_view *q,
@@ -68,9 +139,12 @@ extern "C" int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint3
     if (!st || !acc || !acc->q_sum || !acc->q_count) return kvm_fail(st, KVM_EINVAL, "query_add: args");
     if (il >= acc->n_layer) return kvm_fail(st, KVM_ERANGE, "query_add: layer %u >= %u", il, acc->n_layer);
     const uint32_t n_embd = acc->n_head * acc->head_dim;
-    int rc = view_check(st, q, n_embd, "query_add");
+    int rc = query_terms_check(st, acc, "query_add");
+    if (rc) return rc;
+    rc = view_check(st, q, n_embd, "query_add");
     if (rc) return rc;
     KVM_HIP(st, hipSetDevice(st->device));
+    bool added = false;
     for (uint64_t t0 = 0; t0 < (uint64_t)q->ne2; t0 += KVM_QVIEW_ROWS) {
         qview_args a{};
         a.v = view_of(q);
@@ -87,8 +161,9 @@ extern "C" int kvm_query_add_view(kvm_state *st, const kvm_query_acc *acc, uint3
         if (a.n_kept == 0) continue;
         hipLaunchKernelGGL(k_query_add, dim3(kvm_cdiv(n_embd, 256)), dim3(256), 0, st->stream, a);
         KVM_LAUNCH_CHECK(st, "query_add");
+        added = true;
     }
-    return KVM_OK;
+    return added ? query_terms_launch(st, acc, il, 1) : KVM_OK;
 }
 
 extern "C" int kvm_query_add(kvm_state *st, const kvm_query_acc *acc, uint32_t il,
@@ -286,23 +361,24 @@ struct score_lanes {
     score_args lane[KVM_RET_LANES];
 };
 
-template <int D>
+template <int D, bool QV>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     // one copy of the lane's arguments: its scalar loads are issued together
     // ahead of the first branch, not one round trip per field
     const score_args a = sl.lane[blockIdx.z];
-    asm volatile("" ::"s"(a.q_sum), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
+    if constexpr (QV) asm volatile("" ::"s"(a.q_vec), "s"(a.q_norm), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
+    else asm volatile("" ::"s"(a.q_sum), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
     const uint32_t tile = blockIdx.x, il = blockIdx.y;
     if (tile >= a.n_tiles_used || il >= a.n_layer) return;
     __shared__ __align__(16) score_wg_lds<D, 4> L;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t g = a.g, qc = a.q_count[il];
     score_regs r;
-    if ((uint32_t)w < a.H) score_tile_load<D>(a, il, tile, (uint32_t)w, g, r);
+    if ((uint32_t)w < a.H) score_tile_load<D, QV>(a, il, tile, (uint32_t)w, g, r);
     if (qc == 0) return;                 // a layer without queries: skipped by the reduction
     for (uint32_t hh = (uint32_t)w; hh < a.H; hh += 4u) {
-        if (hh != (uint32_t)w) score_tile_load<D>(a, il, tile, hh, g, r);
-        score_tile_compute<D>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
+        if (hh != (uint32_t)w) score_tile_load<D, QV>(a, il, tile, hh, g, r);
+        score_tile_compute<D, QV>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
     }
     __syncthreads();
     if (w == 0) score_tile_store(a, il, tile, L.cos);
@@ -401,6 +477,9 @@ static int check_score(kvm_state *st, const kvm_retrieval_lane &r, uint32_t i) {
         q->n_head / ix->n_head_kv > KVM_SCORE_GMAX)
         return kvm_fail(st, KVM_EUNSUPPORTED, "score_topk: n_head %u / n_head_kv %u (at most %d kv heads, groups of at most %d)",
                         q->n_head, ix->n_head_kv, KVM_SCORE_HMAX, KVM_SCORE_GMAX);
+    if (q->q_vec && (!q->q_norm || q->n_head_kv != ix->n_head_kv))
+        return kvm_fail(st, KVM_EINVAL, "score_topk: lane %u: query terms for %u kv heads, index has %u", i,
+                        q->n_head_kv, ix->n_head_kv);
     return KVM_OK;
 }
 
@@ -447,7 +526,7 @@ void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes,
         const uint32_t used = r.p->n_blocks ? kvm_cdiv(r.p->n_blocks, KVM_MEANK_TILE) : 0u;
         out[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, (double *)tl.lane[i].layer_score,
                             r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
-                            r.q->n_head, ix->n_head_kv, used, r.q->n_head / ix->n_head_kv};
+                            r.q->n_head, ix->n_head_kv, used, r.q->n_head / ix->n_head_kv, r.q->q_vec, r.q->q_norm};
     }
 }
 
@@ -460,10 +539,18 @@ int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t
         max_layer = sl.lane[i].n_layer > max_layer ? sl.lane[i].n_layer : max_layer;
     }
     if (max_tiles == 0) return KVM_OK;
+    // the accumulators' formed query terms when every lane has them
+    bool qv = true;
+    for (uint32_t i = 0; i < n_lanes; ++i) qv = qv && sl.lane[i].q_vec;
     KVM_HIP(st, hipSetDevice(st->device));
     const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
-    if (lanes[0].ix->head_dim == 256) hipLaunchKernelGGL(k_score<256>, grid, block, 0, st->stream, sl);
-    else hipLaunchKernelGGL(k_score<128>, grid, block, 0, st->stream, sl);
+    if (lanes[0].ix->head_dim == 256) {
+        if (qv) hipLaunchKernelGGL((k_score<256, true>), grid, block, 0, st->stream, sl);
+        else hipLaunchKernelGGL((k_score<256, false>), grid, block, 0, st->stream, sl);
+    } else {
+        if (qv) hipLaunchKernelGGL((k_score<128, true>), grid, block, 0, st->stream, sl);
+        else hipLaunchKernelGGL((k_score<128, false>), grid, block, 0, st->stream, sl);
+    }
     KVM_LAUNCH_CHECK(st, "score");
     return KVM_OK;
 }

@@ -29,6 +29,8 @@ struct score_args {
     uint32_t n_blocks, cap, n_tiles, n_layer, n_head, H;
     uint32_t n_tiles_used;  // tiles holding the first n_blocks blocks
     uint32_t g;             // query heads per kv head, n_head / H
+    const float *q_vec;     // [n_layer][H][D]: qv formed with the sums, or null
+    const float *q_norm;    // [n_layer][H]: nq beside it
 };
 
 // Device-coherent 64-bit store / load of a layer contribution written and read
@@ -63,13 +65,15 @@ struct score_wg_lds {
 // l < D/4 holds dims 4l..4l+3 of the tile's 8 blocks (8 x 16 B of the slab:
 // blocks 0-3 then 4-7 of each dim) and of the group's first 8 query rows
 // (clamped: a load under a branch would be waited for at the branch's join),
-// and the 8 token counts.  Issued early, they overlap other round trips.
+// or with QV of the head's qv row and its nq, and the 8 token counts.  Issued
+// early, they overlap other round trips.
 struct score_regs {
     kvm_f32x4 kv[8];
     kvm_f32x4 qg[8];
     uint32_t mt[KVM_MEANK_TILE];
+    float nq;
 };
-template <int D>
+template <int D, bool QV>
 __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il, uint32_t tile, uint32_t h, uint32_t g,
                                                 score_regs &r) {
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
@@ -78,9 +82,14 @@ __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il
     const kvm_f32x4 *slab = (const kvm_f32x4 *)(a.k_sum + (((uint64_t)il * a.n_tiles + tile) * HD + (uint64_t)h * D) * TW);
 #pragma unroll
     for (int j = 0; j < 8; ++j) r.kv[j] = slab[lc * 8u + j];
-    const float *qrow = a.q_sum + ((uint64_t)il * a.n_head + (uint64_t)h * g) * D + 4u * lc;
+    if constexpr (QV) {
+        r.qg[0] = *(const kvm_f32x4 *)(a.q_vec + ((uint64_t)il * a.H + h) * D + 4u * lc);
+        r.nq = a.q_norm[(uint64_t)il * a.H + h];
+    } else {
+        const float *qrow = a.q_sum + ((uint64_t)il * a.n_head + (uint64_t)h * g) * D + 4u * lc;
 #pragma unroll
-    for (uint32_t gi = 0; gi < 8; ++gi) r.qg[gi] = *(const kvm_f32x4 *)(qrow + (uint64_t)(gi < g ? gi : 0u) * D);
+        for (uint32_t gi = 0; gi < 8; ++gi) r.qg[gi] = *(const kvm_f32x4 *)(qrow + (uint64_t)(gi < g ? gi : 0u) * D);
+    }
 #pragma unroll
     for (uint32_t bi = 0; bi < TW; ++bi) {
         const uint32_t b = tile * TW + bi;
@@ -95,30 +104,37 @@ __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il
 // the wave's LDS rows (read back by the same wave only); lane c < 17 then sums
 // row c over d in order (the reference's dot, nk and nq chains: the product
 // of each step is the same float, and the additions the same sequence), and
-// lanes 0-7 form the cosines into cos_h[0..7].  qc = q_count[il] > 0.
-template <int D>
+// lanes 0-7 form the cosines into cos_h[0..7].  qc = q_count[il] > 0.  With
+// QV, qv and nq come formed (the same operations, done once per change of the
+// query sums): 16 product rows, 16 chains.
+template <int D, bool QV>
 __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t il, uint32_t h, uint32_t qc,
                                                    uint32_t g, const score_regs &r, score_wave_lds<D> &L,
                                                    float *cos_h) {
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
     const uint32_t l = threadIdx.x & 63u;
-    const float invq = kvm_recip_or0((float)(qc * (g > 1u ? g : 1u)));   // = 1.0f / x, IEEE
     if (l < NL) {
         float qv[4];
+        if constexpr (QV) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float qh = 0.0f;
+            for (int e = 0; e < 4; ++e) qv[e] = r.qg[0][e];
+        } else {
+            const float invq = kvm_recip_or0((float)(qc * (g > 1u ? g : 1u)));   // = 1.0f / x, IEEE
 #pragma unroll
-            for (uint32_t gi = 0; gi < 8; ++gi)
-                if (gi < g) qh = kvm_fadd(qh, r.qg[gi][e]);
-            if (g > 8u) {                                    // groups above 8 (rare)
-                const float *qrow = a.q_sum + ((uint64_t)il * a.n_head + (uint64_t)h * g) * D + 4u * l;
-                for (uint32_t gi = 8; gi < g; ++gi) qh = kvm_fadd(qh, qrow[(uint64_t)gi * D + e]);
+            for (int e = 0; e < 4; ++e) {
+                float qh = 0.0f;
+#pragma unroll
+                for (uint32_t gi = 0; gi < 8; ++gi)
+                    if (gi < g) qh = kvm_fadd(qh, r.qg[gi][e]);
+                if (g > 8u) {                                // groups above 8 (rare)
+                    const float *qrow = a.q_sum + ((uint64_t)il * a.n_head + (uint64_t)h * g) * D + 4u * l;
+                    for (uint32_t gi = 8; gi < g; ++gi) qh = kvm_fadd(qh, qrow[(uint64_t)gi * D + e]);
+                }
+                qv[e] = kvm_fmul(qh, invq);
             }
-            qv[e] = kvm_fmul(qh, invq);
+            *(kvm_f32x4 *)&L.p[16][4u * l] = kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]),
+                                                       kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
         }
-        *(kvm_f32x4 *)&L.p[16][4u * l] =
-            kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]), kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
 #pragma unroll
         for (uint32_t bi = 0; bi < TW; ++bi) {
             const float inv = kvm_recip_or0((float)r.mt[bi]);
@@ -138,7 +154,8 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
     // wave complete in order; the fence keeps the compiler from moving them)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    // ---- chains: lane c < 17 sums row c (lanes past 16 repeat row 16, unused).
+    // ---- chains: lane c < 17 sums row c (lanes past 16 repeat row 16, unused;
+    // with QV row 16 is not written and its chain not used).
     // The adds of one chain are dependent, so the chain runs at the VALU's
     // dependent-issue rate only if its operands are in registers ahead of it:
     // LOOK 16-dim chunks are in flight (the LDS latency is longer than one
@@ -170,7 +187,7 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
     }
     // ---- cosines of blocks 0-7 (every lane takes part in the shuffles)
     const float nk = __shfl(chain, (int)((l & 7u) + 8u), 64);
-    const float nq = __shfl(chain, 16, 64);
+    const float nq = QV ? r.nq : __shfl(chain, 16, 64);
     if (l < TW) {
         const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(nq), kvm_fsqrt(nk)), 1e-6f);
         cos_h[l] = kvm_fdiv(chain, den);

@@ -38,7 +38,8 @@ class Window(C.Structure):
 
 class QueryAcc(C.Structure):
     _fields_ = [("n_layer", C.c_uint32), ("n_head", C.c_uint32), ("head_dim", C.c_uint32),
-                ("q_sum", C.c_void_p), ("q_count", C.c_void_p)]
+                ("q_sum", C.c_void_p), ("q_count", C.c_void_p), ("n_head_kv", C.c_uint32),
+                ("q_vec", C.c_void_p), ("q_norm", C.c_void_p)]
 
 
 class MeanKIndex(C.Structure):
@@ -141,6 +142,7 @@ SIGNATURES = {
     "kvm_quantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_dequantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_query_reset": (C.c_int, [_P, C.POINTER(QueryAcc)]),
+    "kvm_query_refresh": (C.c_int, [_P, C.POINTER(QueryAcc)]),
     "kvm_query_add": (C.c_int, [_P, C.POINTER(QueryAcc), _u32, _P, _u32]),
     "kvm_meank_k_sum_floats": (_sz, [C.POINTER(MeanKIndex)]),
     "kvm_meank_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32, _P]),

@@ -244,15 +244,29 @@ class MeanKIndex:
 
 
 class QueryAcc:
-    def __init__(self, st, n_layer, n_head, head_dim):
+    """q_sum_ / q_count_ on the device.  With n_head_kv, the accumulator also
+    carries the scorer's query terms (q_vec = the group sums times 1 / (q_count
+    g), q_norm = their squared norm), which reset / add / add_view keep
+    current; after writing q_sum or q_count directly, call refresh()."""
+
+    def __init__(self, st, n_layer, n_head, head_dim, n_head_kv=0):
         dev = torch.device("cuda", st.device)
         self.st = st
         self.q_sum = torch.zeros((n_layer, n_head * head_dim), dtype=torch.float32, device=dev)
         self.q_count = torch.zeros((n_layer,), dtype=torch.int32, device=dev)
-        self.c = L.QueryAcc(n_layer, n_head, head_dim, self.q_sum.data_ptr(), self.q_count.data_ptr())
+        self.q_vec = self.q_norm = None
+        if n_head_kv:
+            self.q_vec = torch.zeros((n_layer, n_head_kv, head_dim), dtype=torch.float32, device=dev)
+            self.q_norm = torch.zeros((n_layer, n_head_kv), dtype=torch.float32, device=dev)
+        self.c = L.QueryAcc(n_layer, n_head, head_dim, self.q_sum.data_ptr(), self.q_count.data_ptr(), n_head_kv,
+                            self.q_vec.data_ptr() if n_head_kv else None,
+                            self.q_norm.data_ptr() if n_head_kv else None)
 
     def reset(self):
         self.st.check(self.st.lib.kvm_query_reset(self.st.h, C.byref(self.c)))
+
+    def refresh(self):
+        self.st.check(self.st.lib.kvm_query_refresh(self.st.h, C.byref(self.c)))
 
     def add(self, il, q_rows):
         q_rows = q_rows.contiguous()

@@ -138,9 +138,13 @@ static int decode_step_on_caller_stream(void) {
     CHECK_HIP(hipMalloc((void **)&ix.mean_tokens, sizeof(uint32_t) * S_BLOCKS));
     CHECK_HIP(hipMemsetAsync(ix.k_sum, 0, sizeof(float) * kvm_meank_k_sum_floats(&ix), stream));
     CHECK_HIP(hipMemsetAsync(ix.mean_tokens, 0, sizeof(uint32_t) * S_BLOCKS, stream));
-    kvm_query_acc qa = {1, NQ, D, NULL, NULL};
+    /* the accumulator carries the scorer's query terms (kept current by
+       reset and add) */
+    kvm_query_acc qa = {1, NQ, D, NULL, NULL, H, NULL, NULL};
     CHECK_HIP(hipMalloc((void **)&qa.q_sum, sizeof(float) * QEMBD));
     CHECK_HIP(hipMalloc((void **)&qa.q_count, sizeof(uint32_t)));
+    CHECK_HIP(hipMalloc((void **)&qa.q_vec, sizeof(float) * EMBD));
+    CHECK_HIP(hipMalloc((void **)&qa.q_norm, sizeof(float) * H));
     CHECK_KVM(kvm_meank_add(st, &ix, 0, 0, S_HIST, d_kf));
     CHECK_KVM(kvm_query_reset(st, &qa));
     CHECK_KVM(kvm_query_add(st, &qa, 0, d_qrows, NTOK));

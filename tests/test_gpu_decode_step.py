@@ -22,13 +22,13 @@ H, G, D, BT = 4, 6, 256, 128
 K_ROW, V_ROW = H * D // 32 * 34, H * D // 32 * 18
 
 
-def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4):
+def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4, terms=False):
     rng = np.random.default_rng(seed)
     n_hist = n_blocks * BT - 40                         # the last block partly filled
     kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
     ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
     ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
-    qa = api.QueryAcc(st, 1, H * G, D)
+    qa = api.QueryAcc(st, 1, H * G, D, n_head_kv=H if terms else 0)
     qa.reset()
     qa.add(0, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
     nt = dev(np.array([min(BT, n_hist - b * BT) for b in range(n_blocks)], np.int32))
@@ -83,24 +83,28 @@ def _compare(ln, ref, bit_equal, tag):
     return int((ra["stage_src"] >= 0).sum())
 
 
-@pytest.mark.parametrize("n_lanes,splits", [(1, None), (1, 32), (3, None)])
-def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, splits):
+@pytest.mark.parametrize("n_lanes,splits,terms", [(1, None, False), (1, 32, True), (3, None, True)])
+def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, splits, terms):
     """Queries drift over six steps, so plans restage and move blocks within
     windows that carry a K shadow (the host rows of the full blocks a window
     holds are poisoned while its step runs: a moved block must come from the
     shadow).  splits: both attention paths take that many key splits, so the
     outputs are bit-equal (the same code over the same bytes); otherwise the
     step's launch takes one split fewer per head than kvm_fa_decode (the
-    selectors' column) and the outputs agree within the attention tolerance."""
+    selectors' column) and the outputs agree within the attention tolerance.
+    terms: the query accumulators carry the scorer's query terms, refreshed
+    after each drift of the sums."""
     if splits:
         monkeypatch.setenv("KVM_FA_SPLITS", str(splits))
     st = kvm_state
-    lanes = [_lane(st, 0x5D00 + i, 40 + 6 * i, 12, 16) for i in range(n_lanes)]
+    lanes = [_lane(st, 0x5D00 + i, 40 + 6 * i, 12, 16, terms=terms) for i in range(n_lanes)]
     moved = staged = 0
     for step in range(6):
         for ln in lanes:
             if step:
                 ln["qa"].q_sum.add_(dev((ln["rng"].standard_normal((1, H * G * D)) * 0.6).astype(np.float32)))
+                if terms:
+                    ln["qa"].refresh()
             ln["q"] = dev(ln["rng"].standard_normal((ln["n_tok_q"], H * G, D)).astype(np.float32)).to(torch.bfloat16)
             ln["out"] = torch.empty((ln["n_tok_q"], H * G, D), dtype=torch.float32, device="cuda")
         nts = [host(ln["nt"]) for ln in lanes]

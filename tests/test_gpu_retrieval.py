@@ -83,12 +83,17 @@ def _case(seed, n_blocks, n_layer=1, n_head=24, H=4, D=256, planted=16):
                                                        # blocks at 4 kv heads take 16-block workgroups
                                                        (700, 2, 8, 8, 128), (260, 1, 32, 16, 128),
                                                        (500, 1, 12, 3, 128), (333, 1, 3, 1, 256)])
-def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
+@pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
+def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D, terms):
+    """terms: the accumulator carries the query terms (formed by
+    kvm_query_refresh after the direct writes) and the scorer reads them."""
     q, qc, k_sum, mt, planted = _case(n_blocks + n_layer, n_blocks, n_layer, n_head, H, D)
     ix = _build_index(kvm_state, k_sum, mt, n_blocks + 5, H, D)
-    qa = api.QueryAcc(kvm_state, n_layer, n_head, D)
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms else 0)
     qa.q_sum.copy_(dev(q))
     qa.q_count.copy_(dev(qc.astype(np.int32)))
+    if terms:
+        qa.refresh()
     n_tokens = np.full(n_blocks, 128, np.int32)
     n_tokens[-1] = 77
     budget = 128 if n_blocks > 128 else 32
@@ -104,22 +109,70 @@ def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D):
     assert np.array_equal(res["to_base"], to_base) and res["total"] == total and res["status"] == 0
 
 
-def test_score_bit_exact_where_every_term_matters(kvm_state):
+@pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
+def test_score_bit_exact_where_every_term_matters(kvm_state, terms):
     """The closed-form pin's inputs (norms near 1e-6 so the epsilon and invq
     count, g = 3, three layers with query counts 5, 0, 2, a block without K in
-    one layer): the GPU scores equal the oracle's bit for bit."""
+    one layer): the GPU scores equal the oracle's bit for bit, with the query
+    terms formed by the scorer or carried by the accumulator."""
     from scoring_cases import tiny_norm_case
     n_head, H, D = 6, 2, 128
     q, qc, k_sum, mt = tiny_norm_case(41, n_head=n_head, H=H, d=D)
     n_layer, n_blocks = mt.shape
     ix = _build_index(kvm_state, k_sum, mt, n_blocks + 3, H, D)
-    qa = api.QueryAcc(kvm_state, n_layer, n_head, D)
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms else 0)
     qa.q_sum.copy_(dev(q))
     qa.q_count.copy_(dev(qc.astype(np.int32)))
+    if terms:
+        qa.refresh()
     sel = api.score_topk(kvm_state, ix, qa, n_blocks, dev(np.full(n_blocks, 128, np.int32)), 4, sink_blocks=1)
     sel.result()
     want = O.score_retrieval(q, qc, k_sum, mt, n_head, H, D)
     assert np.array_equal(host(sel.scores)[:n_blocks].view(np.uint64), want.view(np.uint64))
+
+
+def test_query_terms_follow_reset_and_adds(kvm_state):
+    """The accumulator's query terms are kept current by reset, add and
+    add_view (no refresh): after each, the scores equal the oracle's on the
+    accumulated sums bit for bit, and equal those of an accumulator without
+    terms.  An index with another kv-head count is refused."""
+    n_blocks, n_layer, n_head, H, D = 300, 2, 12, 3, 128
+    q, _, k_sum, mt, _ = _case(77, n_blocks, n_layer, n_head, H, D)
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H)
+    plain = api.QueryAcc(kvm_state, n_layer, n_head, D)
+    rng = np.random.default_rng(5)
+    n_tokens = dev(np.full(n_blocks, 128, np.int32))
+
+    def check():
+        a = api.score_topk(kvm_state, ix, qa, n_blocks, n_tokens, 32, sink_blocks=1)
+        b = api.score_topk(kvm_state, ix, plain, n_blocks, n_tokens, 32, sink_blocks=1)
+        qs, qc = host(plain.q_sum), host(plain.q_count).astype(np.uint32)
+        want = O.score_retrieval(qs, qc, k_sum, mt, n_head, H, D)
+        got = host(a.scores)[:n_blocks]
+        assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+        assert np.array_equal(got.view(np.uint64), host(b.scores)[:n_blocks].view(np.uint64))
+
+    for acc in (qa, plain):
+        acc.reset()
+    rows = (q[0] + rng.standard_normal((3, n_head * D)) * 0.2).astype(np.float32)
+    for acc in (qa, plain):
+        acc.add(0, dev(rows))
+    check()                                   # layer 1 has no queries yet
+    rows1 = torch.from_numpy((q[1] + rng.standard_normal((5, n_head * D)) * 0.2).astype(np.float32))
+    view = dev(rows1.numpy()).view(5, n_head, D).to(torch.bfloat16)
+    keep = np.array([1, 0, 1, 1, 0], np.uint8)
+    for acc in (qa, plain):
+        acc.add_view(1, view, keep)
+    check()
+    for acc in (qa, plain):
+        acc.reset()
+        acc.add(1, dev(rows[:1]))
+    check()
+    assert not host(qa.q_vec)[0].any() and not host(qa.q_norm)[0].any()
+    wrong = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=1)
+    with pytest.raises(RuntimeError):
+        api.score_topk(kvm_state, ix, wrong, n_blocks, n_tokens, 32, sink_blocks=1)
 
 
 def test_score_topk_lanes_match_single_lane(kvm_state):
