@@ -34,6 +34,7 @@ struct kvm_stage_item {          // one queued enqueue_k / enqueue_v
 //   KVM_FA_SYNC_EPOCH + lane*64+h  the (lane, head)'s epoch
 //   KVM_FA_SYNC_PLAN, 64-bit [lane*64+h]  the plan a selecting launch published
 #define KVM_MAX_LANES 8
+#define KVM_LDS_PER_CU 163840u     // LDS bytes of one CU (gfx950)
 #define KVM_FA_MAX_HEADS 64
 #define KVM_MAX_SPLITS 512
 #define KVM_FA_SYNC_STATUS (KVM_MAX_LANES * KVM_FA_MAX_HEADS * KVM_MAX_SPLITS)

@@ -361,7 +361,7 @@ struct score_lanes {
     score_args lane[KVM_RET_LANES];
 };
 
-template <int D, bool QV>
+template <int D, bool QV, bool OTF>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     // one copy of the lane's arguments: its scalar loads are issued together
     // ahead of the first branch, not one round trip per field
@@ -370,7 +370,7 @@ __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     else asm volatile("" ::"s"(a.q_sum), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
     const uint32_t tile = blockIdx.x, il = blockIdx.y;
     if (tile >= a.n_tiles_used || il >= a.n_layer) return;
-    __shared__ __align__(16) score_wg_lds<D, 4> L;
+    __shared__ __align__(16) score_wg_lds<D, 4, OTF> L;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t g = a.g, qc = a.q_count[il];
     score_regs r;
@@ -378,7 +378,7 @@ __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     if (qc == 0) return;                 // a layer without queries: skipped by the reduction
     for (uint32_t hh = (uint32_t)w; hh < a.H; hh += 4u) {
         if (hh != (uint32_t)w) score_tile_load<D, QV>(a, il, tile, hh, g, r);
-        score_tile_compute<D, QV>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
+        score_tile_compute<D, QV, OTF>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
     }
     __syncthreads();
     if (w == 0) score_tile_store(a, il, tile, L.cos);
@@ -544,12 +544,20 @@ int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t
     for (uint32_t i = 0; i < n_lanes; ++i) qv = qv && sl.lane[i].q_vec;
     KVM_HIP(st, hipSetDevice(st->device));
     const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
-    if (lanes[0].ix->head_dim == 256) {
-        if (qv) hipLaunchKernelGGL((k_score<256, true>), grid, block, 0, st->stream, sl);
-        else hipLaunchKernelGGL((k_score<256, false>), grid, block, 0, st->stream, sl);
+    // product rows in LDS (the shorter chains) while the grid fits the CUs at
+    // once with them; past that the chains form their products (half the LDS,
+    // twice the workgroups per CU)
+    const uint64_t n_wg = (uint64_t)max_tiles * max_layer * n_lanes;
+    const bool wide = lanes[0].ix->head_dim == 256;
+    const size_t lds_rows = wide ? sizeof(score_wg_lds<256, 4, false>) : sizeof(score_wg_lds<128, 4, false>);
+    const bool otf = n_wg > (uint64_t)st->n_cu * (KVM_LDS_PER_CU / lds_rows);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, st->stream, sl); };
+    if (wide) {
+        if (qv) otf ? go(k_score<256, true, true>) : go(k_score<256, true, false>);
+        else otf ? go(k_score<256, false, true>) : go(k_score<256, false, false>);
     } else {
-        if (qv) hipLaunchKernelGGL((k_score<128, true>), grid, block, 0, st->stream, sl);
-        else hipLaunchKernelGGL((k_score<128, false>), grid, block, 0, st->stream, sl);
+        if (qv) otf ? go(k_score<128, true, true>) : go(k_score<128, true, false>);
+        else otf ? go(k_score<128, false, true>) : go(k_score<128, false, false>);
     }
     KVM_LAUNCH_CHECK(st, "score");
     return KVM_OK;

@@ -44,19 +44,25 @@ __device__ __forceinline__ double kvm_ld_f64_dev(const double *p) {
         (long long)__hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-// LDS of one wave's (tile, head) pass: the 17 product rows of D floats each
-// (dot products of blocks 0-7, their kh squares, qv squares), padded against
-// bank conflicts.
+// LDS of one wave's (tile, head) pass, rows of D floats padded against bank
+// conflicts: the 17 product rows (dot products of blocks 0-7, their kh
+// squares, qv squares), or with OTF (products formed on the fly by the
+// chains, about half the LDS) qv and the kh of blocks 0-7.
 #define KVM_SCORE_ROWS 17
-template <int D>
+template <int D, bool OTF>
 struct score_wave_lds {
     float p[KVM_SCORE_ROWS][D + 4];
 };
+template <int D>
+struct score_wave_lds<D, true> {
+    float qv[D + 4];
+    float kh[KVM_MEANK_TILE][D + 4];
+};
 // The scoring workgroup's LDS: one region per scoring wave, the cosines of
 // every head and the count of heads done.
-template <int D, int NW>
+template <int D, int NW, bool OTF>
 struct score_wg_lds {
-    score_wave_lds<D> w[NW];
+    score_wave_lds<D, OTF> w[NW];
     float cos[KVM_SCORE_HMAX][KVM_MEANK_TILE];
     uint32_t heads_done;
 };
@@ -101,15 +107,16 @@ __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il
 // barrier (the other waves of its workgroup may be in a barrier sequence of
 // their own): every lane forms qv and kh of its 4 dims and the products
 // qv kh (8 blocks), kh kh (8 blocks) and qv qv, each one IEEE rounding, into
-// the wave's LDS rows (read back by the same wave only); lane c < 17 then sums
-// row c over d in order (the reference's dot, nk and nq chains: the product
-// of each step is the same float, and the additions the same sequence), and
-// lanes 0-7 form the cosines into cos_h[0..7].  qc = q_count[il] > 0.  With
-// QV, qv and nq come formed (the same operations, done once per change of the
-// query sums): 16 product rows, 16 chains.
-template <int D, bool QV>
+// the wave's LDS rows (read back by the same wave only); lane c < 17 then runs
+// chain c over d in order (the reference's dot of block c, nk of block c - 8,
+// nq: the product of each step is the same float, and the additions the same
+// sequence), and lanes 0-7 form the cosines into cos_h[0..7].  With OTF the
+// lanes store qv and kh instead and each chain forms its products as it goes
+// (the same floats).  qc = q_count[il] > 0.  With QV, qv and nq come formed
+// (the same operations, done once per change of the query sums): 16 chains.
+template <int D, bool QV, bool OTF>
 __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t il, uint32_t h, uint32_t qc,
-                                                   uint32_t g, const score_regs &r, score_wave_lds<D> &L,
+                                                   uint32_t g, const score_regs &r, score_wave_lds<D, OTF> &L,
                                                    float *cos_h) {
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
     const uint32_t l = threadIdx.x & 63u;
@@ -132,9 +139,11 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
                 }
                 qv[e] = kvm_fmul(qh, invq);
             }
-            *(kvm_f32x4 *)&L.p[16][4u * l] = kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]),
-                                                       kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
+            if constexpr (!OTF)
+                *(kvm_f32x4 *)&L.p[16][4u * l] = kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]),
+                                                           kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
         }
+        if constexpr (OTF) *(kvm_f32x4 *)&L.qv[4u * l] = kvm_f32x4{qv[0], qv[1], qv[2], qv[3]};
 #pragma unroll
         for (uint32_t bi = 0; bi < TW; ++bi) {
             const float inv = kvm_recip_or0((float)r.mt[bi]);
@@ -144,46 +153,82 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
 #pragma unroll
             for (int dd = 0; dd < 4; ++dd)
                 k4[dd] = __uint_as_float(__float_as_uint(kvm_fmul(r.kv[2 * dd + hi][e], inv)) & keep);
-            *(kvm_f32x4 *)&L.p[bi][4u * l] = kvm_f32x4{kvm_fmul(qv[0], k4[0]), kvm_fmul(qv[1], k4[1]),
-                                                       kvm_fmul(qv[2], k4[2]), kvm_fmul(qv[3], k4[3])};
-            *(kvm_f32x4 *)&L.p[8 + bi][4u * l] = kvm_f32x4{kvm_fmul(k4[0], k4[0]), kvm_fmul(k4[1], k4[1]),
-                                                           kvm_fmul(k4[2], k4[2]), kvm_fmul(k4[3], k4[3])};
+            if constexpr (OTF) {
+                *(kvm_f32x4 *)&L.kh[bi][4u * l] = kvm_f32x4{k4[0], k4[1], k4[2], k4[3]};
+            } else {
+                *(kvm_f32x4 *)&L.p[bi][4u * l] = kvm_f32x4{kvm_fmul(qv[0], k4[0]), kvm_fmul(qv[1], k4[1]),
+                                                           kvm_fmul(qv[2], k4[2]), kvm_fmul(qv[3], k4[3])};
+                *(kvm_f32x4 *)&L.p[8 + bi][4u * l] = kvm_f32x4{kvm_fmul(k4[0], k4[0]), kvm_fmul(k4[1], k4[1]),
+                                                               kvm_fmul(k4[2], k4[2]), kvm_fmul(k4[3], k4[3])};
+            }
         }
     }
     // the wave's LDS writes are done before its reads (LDS operations of one
     // wave complete in order; the fence keeps the compiler from moving them)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    // ---- chains: lane c < 17 sums row c (lanes past 16 repeat row 16, unused;
-    // with QV row 16 is not written and its chain not used).
-    // The adds of one chain are dependent, so the chain runs at the VALU's
-    // dependent-issue rate only if its operands are in registers ahead of it:
-    // LOOK 16-dim chunks are in flight (the LDS latency is longer than one
-    // chunk's 16 adds).
-    const float *row = L.p[l < 17u ? l : 16u];
+    // ---- chains: lane c < 17 runs chain c (lanes past 16 repeat chain 16,
+    // unused; with QV chain 16 is not used).  The adds of one chain are
+    // dependent, so the chain runs at the VALU's dependent-issue rate only if
+    // its operands are in registers ahead of it: LOOK chunks of 16 dims (of
+    // both factors, 8 dims, with OTF) are in flight, the LDS latency being
+    // longer than one chunk's adds.
     float chain = 0.0f;
-    constexpr int CH = 4;                // float4 per 16-dim chunk
-    constexpr int NC = D / (4 * CH);     // chunks
-    constexpr int LOOK = 3;              // chunks in flight (12 LDS reads: under lgkmcnt's 15)
-    kvm_f32x4 buf[LOOK][CH];
-    auto ld = [&](kvm_f32x4 (&x)[CH], int c) {
+    const uint32_t c = l < 17u ? l : 16u;
+    if constexpr (!OTF) {
+        const float *row = L.p[c];
+        constexpr int CH = 4;                // float4 per 16-dim chunk
+        constexpr int NC = D / (4 * CH);     // chunks
+        constexpr int LOOK = 3;              // chunks in flight (12 LDS reads: under lgkmcnt's 15)
+        kvm_f32x4 buf[LOOK][CH];
+        auto ld = [&](kvm_f32x4 (&x)[CH], int k) {
 #pragma unroll
-        for (int j = 0; j < CH; ++j) x[j] = *(const kvm_f32x4 *)&row[4 * (CH * c + j)];
-    };
-    auto add = [&](const kvm_f32x4 (&x)[CH]) {
+            for (int j = 0; j < CH; ++j) x[j] = *(const kvm_f32x4 *)&row[4 * (CH * k + j)];
+        };
+        auto add = [&](const kvm_f32x4 (&x)[CH]) {
 #pragma unroll
-        for (int j = 0; j < CH; ++j)
+            for (int j = 0; j < CH; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) chain = kvm_fadd(chain, x[j][e]);
-    };
+                for (int e = 0; e < 4; ++e) chain = kvm_fadd(chain, x[j][e]);
+        };
 #pragma unroll
-    for (int c = 0; c < LOOK; ++c) ld(buf[c], c);
+        for (int k = 0; k < LOOK; ++k) ld(buf[k], k);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        __builtin_amdgcn_sched_barrier(0);
-        add(buf[c % LOOK]);
-        __builtin_amdgcn_sched_barrier(0);
-        if (c + LOOK < NC) ld(buf[c % LOOK], c + LOOK);
+        for (int k = 0; k < NC; ++k) {
+            __builtin_amdgcn_sched_barrier(0);
+            add(buf[k % LOOK]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + LOOK < NC) ld(buf[k % LOOK], k + LOOK);
+        }
+    } else {
+        const float *fa = c < 8u || c == 16u ? L.qv : L.kh[c - 8u];
+        const float *fb = c < 8u ? L.kh[c] : (c < 16u ? L.kh[c - 8u] : L.qv);
+        constexpr int CH = 2;                // float4 per 8-dim chunk
+        constexpr int NC = D / (4 * CH);     // chunks
+        constexpr int LOOK = 3;              // chunks in flight (12 LDS reads)
+        kvm_f32x4 bufa[LOOK][CH], bufb[LOOK][CH];
+        auto ld = [&](kvm_f32x4 (&x)[CH], kvm_f32x4 (&y)[CH], int k) {
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                x[j] = *(const kvm_f32x4 *)&fa[4 * (CH * k + j)];
+                y[j] = *(const kvm_f32x4 *)&fb[4 * (CH * k + j)];
+            }
+        };
+        auto add = [&](const kvm_f32x4 (&x)[CH], const kvm_f32x4 (&y)[CH]) {
+#pragma unroll
+            for (int j = 0; j < CH; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) chain = kvm_fadd(chain, kvm_fmul(x[j][e], y[j][e]));
+        };
+#pragma unroll
+        for (int k = 0; k < LOOK; ++k) ld(bufa[k], bufb[k], k);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+            __builtin_amdgcn_sched_barrier(0);
+            add(bufa[k % LOOK], bufb[k % LOOK]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + LOOK < NC) ld(bufa[k % LOOK], bufb[k % LOOK], k + LOOK);
+        }
     }
     // ---- cosines of blocks 0-7 (every lane takes part in the shuffles)
     const float nk = __shfl(chain, (int)((l & 7u) + 8u), 64);

@@ -175,18 +175,23 @@ def test_query_terms_follow_reset_and_adds(kvm_state):
         api.score_topk(kvm_state, ix, wrong, n_blocks, n_tokens, 32, sink_blocks=1)
 
 
-def test_score_topk_lanes_match_single_lane(kvm_state):
+@pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
+def test_score_topk_lanes_match_single_lane(kvm_state, terms):
     """Four lanes of different sizes (multi-lane decode) in one launch sequence:
     every lane's scores, ids, layout and stage plan equal the oracle's and a
-    single-lane call's."""
+    single-lane call's.  The four-lane grid (1,024 workgroups) takes the
+    scorer whose chains form their products, a single lane the one with
+    product rows in LDS."""
     H, n_head, D = 4, 24, 256
     lanes, single, cases = [], [], []
     for i, n_blocks in enumerate((512, 1024, 1536, 2048)):
         q, qc, k_sum, mt, planted = _case(200 + i, n_blocks, 1, n_head, H, D)
         ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
-        qa = api.QueryAcc(kvm_state, 1, n_head, D)
+        qa = api.QueryAcc(kvm_state, 1, n_head, D, n_head_kv=H if terms else 0)
         qa.q_sum.copy_(dev(q))
         qa.q_count.copy_(dev(qc.astype(np.int32)))
+        if terms:
+            qa.refresh()
         n_tokens = dev(np.full(n_blocks, 128, np.int32))
         w = api.KVWindow(kvm_state, 128 * 128, H, D, 128)
         sel = api.SelectionBuffers(kvm_state, n_blocks, 128)
