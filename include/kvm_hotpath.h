@@ -126,15 +126,15 @@ typedef struct kvm_window {
     uint32_t *slot_block;   /* device [n_slots]: block id held by the slot, 0xffffffff = none */
     int32_t *slot_base;     /* device [n_slots]: position the slot's first cell is baked at */
     /* Optional HBM shadow of the staged blocks' raw K (both NULL = none).  A
-     * stage-in writes every staged cell's unrotated q8_0 K row (the history's
-     * bytes) here and the slot's staged row count into shadow_rows; a later
+     * stage-in writes every staged cell's unrotated K row (the history's q8_0
+     * or q4_0 bytes) here and the slot's staged row count into shadow_rows; a later
      * plan that moves a full block to another slot or base re-rotates it from
      * the shadow and moves its V within HBM instead of reading the host
      * history again (the reference reloads such blocks from the host, or moves
      * them with kvmem_d2d_batched without re-rotation,
      * llama-memory-kvmem.cpp:1958-2285).  Importing rows into a slot's cells
      * and kvm_slot_copy_from_host void that slot's shadow (shadow_rows = 0). */
-    void *k_shadow;         /* device [n_cells][n_head_kv * row(head_dim)] of q8_0 */
+    void *k_shadow;         /* device [n_cells][n_head_kv * row(head_dim)] of the K type */
     uint32_t *shadow_rows;  /* device [n_slots]: rows of the slot the shadow holds */
     /* Optional (NULL = not tracked): per slot the end, in rows from the slot's
      * first cell, of the rows imported into its cells (generated tokens,
@@ -152,7 +152,7 @@ typedef struct kvm_window {
 
 size_t kvm_window_k_bytes(const kvm_window *w);
 size_t kvm_window_v_bytes(const kvm_window *w);
-/* Bytes of the optional K shadow (q8_0 windows; 0 otherwise). */
+/* Bytes of the optional K shadow (q8_0 and q4_0 K windows; 0 otherwise). */
 size_t kvm_window_shadow_bytes(const kvm_window *w);
 /* Checks geometry; KVM_OK when the window is usable. */
 int kvm_window_check(const kvm_window *w);
@@ -463,8 +463,8 @@ typedef struct kvm_history {
  * Entries with sel->stage_src[i] >= 0 (a window with a shadow) take their raw K
  * rows from the shadow of that slot and their V from that slot's tiles, all
  * gathered before any slot is written, so the window ends byte-equal to a
- * stage-in of the whole plan from the host.  A q4_0 K window (no shadow) has
- * q4_0 raw K rows in its history, requantised to q4_0 (quant_q4_0,
+ * stage-in of the whole plan from the host.  A q4_0 K window has
+ * q4_0 raw K rows in its history (and shadow), requantised to q4_0 (quant_q4_0,
  * llama-kvmem-stagein.cu:201-234); its rope->n_rot / 2 must be a power of two
  * of at least 16 (else KVM_EUNSUPPORTED). */
 int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,

@@ -16,15 +16,16 @@ extern "C" int kvm_window_check(const kvm_window *w) {
     const bool h = w->k_type == KVM_TYPE_F16 && w->v_type == KVM_TYPE_F16;
     if (!q && !h) return KVM_EUNSUPPORTED;
     if (!w->k || !w->v || !w->cell_pos) return KVM_EINVAL;
-    // a shadow comes with its row counts and the slot map, and holds q8_0 rows
+    // a shadow comes with its row counts and the slot map, and holds the
+    // history's q8_0 or q4_0 K rows
     if (!w->k_shadow != !w->shadow_rows) return KVM_EINVAL;
-    if (w->k_shadow && (w->k_type != KVM_TYPE_Q8_0 || !q || !w->slot_block || !w->slot_base)) return KVM_EINVAL;
+    if (w->k_shadow && (!q || !w->slot_block || !w->slot_base)) return KVM_EINVAL;
     return KVM_OK;
 }
 
 extern "C" size_t kvm_window_shadow_bytes(const kvm_window *w) {
-    if (!w || w->k_type != KVM_TYPE_Q8_0) return 0;
-    return (size_t)w->n_cells * w->n_head_kv * (w->head_dim / 32) * 34;
+    if (!w || !kvm_k_quant(w->k_type)) return 0;
+    return (size_t)w->n_cells * w->n_head_kv * (w->head_dim / 32) * (w->k_type == KVM_TYPE_Q4_0 ? 18u : 34u);
 }
 
 extern "C" size_t kvm_window_k_bytes(const kvm_window *w) {

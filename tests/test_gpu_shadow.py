@@ -1,7 +1,7 @@
 """Re-basing resident blocks from the window's HBM shadow.
 
-A window with a K shadow keeps the raw (unrotated) q8_0 K rows of every staged
-cell.  When a new plan moves a full block that the window already holds to
+A window with a K shadow keeps the raw (unrotated) q8_0 or q4_0 K rows of every
+staged cell.  When a new plan moves a full block that the window already holds to
 another slot (its window position changes), the stage-in re-rotates it from
 that shadow and moves its V tiles within HBM; only blocks new to the window are
 read from the host history.  Before each plan the tests poison the host rows of
@@ -20,29 +20,33 @@ from kvmem_amd import api, _lib as L
 pytestmark = pytest.mark.gpu
 
 H, D, BT = 4, 256, 128
-K_ROW, V_ROW = H * D // 32 * 34, H * D // 32 * 18
+V_ROW = H * D // 32 * 18
 
 
-def _histories(seed, n_tok):
+def _k_row(kt):
+    return H * D // 32 * (18 if kt == L.T_Q4_0 else 34)
+
+
+def _histories(seed, n_tok, kt=L.T_Q8_0):
     rng = np.random.default_rng(seed)
-    kr, vr = rand_rows(rng, n_tok, H, D, L.T_Q8_0, L.T_Q4_0)
+    kr, vr = rand_rows(rng, n_tok, H, D, kt, L.T_Q4_0)
     return api.History(kr, vr), api.History(kr, vr), kr, vr, rng
 
 
 def _poison(hist, blocks, rng):
     """Overwrite the host K and V rows of `blocks` (full blocks) with random bytes."""
     torch.cuda.synchronize()
-    k = hist.kbuf.u8.reshape(hist.n_tokens, K_ROW)
+    k = hist.kbuf.u8.reshape(hist.n_tokens, -1)
     v = hist.vbuf.u8.reshape(hist.n_tokens, V_ROW)
     for b in blocks:
-        k[b * BT:(b + 1) * BT] = rng.integers(0, 256, (BT, K_ROW), dtype=np.uint8)
+        k[b * BT:(b + 1) * BT] = rng.integers(0, 256, (BT, k.shape[1]), dtype=np.uint8)
         v[b * BT:(b + 1) * BT] = rng.integers(0, 256, (BT, V_ROW), dtype=np.uint8)
 
 
 def _restore(hist, blocks, kr, vr):
     """Put the clean rows of `blocks` back once the stage-in has run."""
     torch.cuda.synchronize()
-    k = hist.kbuf.u8.reshape(hist.n_tokens, K_ROW)
+    k = hist.kbuf.u8.reshape(hist.n_tokens, -1)
     v = hist.vbuf.u8.reshape(hist.n_tokens, V_ROW)
     for b in blocks:
         k[b * BT:(b + 1) * BT] = kr[b * BT:(b + 1) * BT]
@@ -65,7 +69,7 @@ def _same_window(wa, wb, n_used):
 
 def _check_shadow(w, kr, res, nt):
     """The shadow holds each occupied slot's raw K rows and their count."""
-    sh = host(w.k_shadow).reshape(w.n_cells, K_ROW)
+    sh = host(w.k_shadow).reshape(w.n_cells, _k_row(w.k_type))
     rows = host(w.shadow_rows)
     for k, b in enumerate(res["ids"]):
         n = int(nt[b])
@@ -73,16 +77,17 @@ def _check_shadow(w, kr, res, nt):
         assert np.array_equal(sh[k * BT:k * BT + n], kr[b * BT:b * BT + n]), (k, b)
 
 
-def _fresh(st, hist, s, nt, budget, slots):
-    w = api.KVWindow(st, slots * BT, H, D, BT)
+def _fresh(st, hist, s, nt, budget, slots, kt=L.T_Q8_0):
+    w = api.KVWindow(st, slots * BT, H, D, BT, kt, L.T_Q4_0)
     sel = api.select_topk(st, dev(s), dev(nt), budget, 1, 0, None, window=w)
     api.stagein_selection(st, hist, w, sel, 64, 1e7)
     return w, sel.result()
 
 
-def test_moved_blocks_restage_from_shadow(kvm_state):
+@pytest.mark.parametrize("kt", [L.T_Q8_0, L.T_Q4_0], ids=["q8_0", "q4_0"])
+def test_moved_blocks_restage_from_shadow(kvm_state, kt):
     """select_topk + stagein_selection (the gather launch, then the stage-in
-    launch).  Plan 1 stages 12 of 40 blocks (the last, partly filled block
+    launch), over q8_0 and q4_0 K caches.  Plan 1 stages 12 of 40 blocks (the last, partly filled block
     among them).  Plan 2 drops an early block and adds a later one, so the
     blocks between shift down a slot; plan 3 adds an early block and drops a
     late one, so blocks shift up.  Moved full blocks name their old slot in
@@ -91,10 +96,10 @@ def test_moved_blocks_restage_from_shadow(kvm_state):
     st = kvm_state
     n_blocks, budget, slots = 40, 12, 16
     n_tok = n_blocks * BT - 30
-    hp, hc, kr, vr, rng = _histories(0x5AD0, n_tok)
+    hp, hc, kr, vr, rng = _histories(0x5AD0, n_tok, kt)
     nt = np.array([min(BT, n_tok - b * BT) for b in range(n_blocks)], np.int32)
-    w = api.KVWindow(st, slots * BT, H, D, BT, shadow=True)
-    assert w.k_shadow.numel() == slots * BT * K_ROW
+    w = api.KVWindow(st, slots * BT, H, D, BT, kt, L.T_Q4_0, shadow=True)
+    assert w.k_shadow.numel() == slots * BT * _k_row(kt)
     s = rng.standard_normal(n_blocks)
     s[n_blocks - 1] = 10.0
     prev = None
@@ -115,7 +120,7 @@ def test_moved_blocks_restage_from_shadow(kvm_state):
         _restore(hp, held, kr, vr)
         res = sel.result()
         assert res["status"] == 0
-        ref_w, ref = _fresh(st, hc, s, nt, budget, slots)
+        ref_w, ref = _fresh(st, hc, s, nt, budget, slots, kt)
         assert np.array_equal(res["ids"], ref["ids"]) and np.array_equal(res["to_base"], ref["to_base"])
         _same_window(w, ref_w, budget * BT)
         _check_shadow(w, kr, res, nt)
@@ -140,7 +145,8 @@ def test_moved_blocks_restage_from_shadow(kvm_state):
     k = budget // 2
     b, base = int(res["ids"][k]), int(res["to_base"][k])
     ek, ev = w.export_rows(k * BT, BT)
-    want = O.stagein_k(kr[b * BT:(b + 1) * BT].reshape(-1), BT, H, D, 64, 256, base, O.rope_theta(1e7, 1.0, 64))
+    want = O.stagein_k(kr[b * BT:(b + 1) * BT].reshape(-1), BT, H, D, 64, 256, base, O.rope_theta(1e7, 1.0, 64),
+                       k_type=kt)
     assert np.array_equal(host(ek).reshape(-1), want) and np.array_equal(host(ev), vr[b * BT:(b + 1) * BT])
 
 
@@ -241,7 +247,8 @@ def test_import_voids_the_slot_shadow(kvm_state):
 
 
 def test_shadow_geometry_is_checked(kvm_state):
-    """A shadow needs its row counts (and the other way round) and q8_0 K."""
+    """A shadow needs its row counts (and the other way round) and a q8_0 or
+    q4_0 K cache; a q4_0 shadow holds 18-byte blocks."""
     w = api.KVWindow(kvm_state, 256, H, D, BT, shadow=True)
     lib = kvm_state.lib
     import ctypes as C
@@ -253,24 +260,27 @@ def test_shadow_geometry_is_checked(kvm_state):
     assert lib.kvm_window_check(C.byref(c)) == L.KVM_EINVAL
     wf = api.KVWindow(kvm_state, 256, H, 128, BT, L.T_F16, L.T_F16)
     assert lib.kvm_window_shadow_bytes(C.byref(wf.c)) == 0
+    w4 = api.KVWindow(kvm_state, 256, H, D, BT, L.T_Q4_0, L.T_Q4_0, shadow=True)
+    assert w4.k_shadow.numel() == 256 * H * (D // 32) * 18
     with pytest.raises(L.KvmError):
         api.KVWindow(kvm_state, 256, H, 128, BT, L.T_F16, L.T_F16, shadow=True)
 
 
-def test_churn_over_a_128_block_window(kvm_state):
+@pytest.mark.parametrize("kt", [L.T_Q8_0, L.T_Q4_0], ids=["q8_0", "q4_0"])
+def test_churn_over_a_128_block_window(kvm_state, kt):
     """The decode workload's window shape: 128 blocks of 128 tokens from a
-    512-block history.  Each step drops the second-earliest block and adds one
+    512-block history (q8_0 or q4_0 K).  Each step drops the second-earliest block and adds one
     past the last, or the reverse, so 126 blocks move a slot (504 staging items,
     the stage-in's gather barrier over its full grid); the window equals a fresh
     stage-in of the plan from the clean history."""
     st = kvm_state
     n_blocks, nsel = 512, 128
-    hp, hc, kr, vr, rng = _histories(0x5B00, n_blocks * BT)
+    hp, hc, kr, vr, rng = _histories(0x5B00, n_blocks * BT, kt)
     nt = np.full(n_blocks, BT, np.int32)
     sa = np.concatenate([[0], np.sort(rng.choice(np.arange(1, n_blocks - 1), nsel - 1, replace=False))])
     late = next(b for b in range(n_blocks - 1, 0, -1) if b not in set(sa))
     sb = np.sort(np.concatenate([np.setdiff1d(sa, [sa[1]]), [late]]))
-    w = api.KVWindow(st, nsel * BT, H, D, BT, shadow=True)
+    w = api.KVWindow(st, nsel * BT, H, D, BT, kt, L.T_Q4_0, shadow=True)
     for step, chosen in enumerate((sa, sb, sa, sb)):
         s = np.zeros(n_blocks)
         s[chosen] = 1.0
@@ -283,5 +293,5 @@ def test_churn_over_a_128_block_window(kvm_state):
         assert res["status"] == 0 and np.array_equal(res["ids"], chosen), step
         n_moved = int((res["stage_src"] >= 0).sum())
         assert (len(res["stage_slots"]), n_moved) == ((nsel, 0) if step == 0 else (nsel - 1, nsel - 2)), step
-        ref_w, _ = _fresh(st, hc, s, nt, nsel, nsel)
+        ref_w, _ = _fresh(st, hc, s, nt, nsel, nsel, kt)
         _same_window(w, ref_w, nsel * BT)
