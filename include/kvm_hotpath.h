@@ -465,8 +465,7 @@ typedef struct kvm_history {
  * gathered before any slot is written, so the window ends byte-equal to a
  * stage-in of the whole plan from the host.  A q4_0 K window has
  * q4_0 raw K rows in its history (and shadow), requantised to q4_0 (quant_q4_0,
- * llama-kvmem-stagein.cu:201-234); its rope->n_rot / 2 must be a power of two
- * of at least 16 (else KVM_EUNSUPPORTED). */
+ * llama-kvmem-stagein.cu:201-234). */
 int kvm_stagein_selection(kvm_state *st, const kvm_history *h, const kvm_window *w,
                           const kvm_selection *sel, const kvm_rope_params *rope);
 
@@ -563,7 +562,7 @@ int kvm_stagein_fa_decode_lanes(kvm_state *st, const kvm_stagein_lane *stage, co
  * and then runs the graph's flash attention (ggml-cuda/fattn.cu:457), one
  * after the other.  Steps with more than 4,096 blocks in a lane or a lane
  * without query tokens run as three launches (kvm_score_topk, then
- * kvm_stagein_fa_decode) with the same results, and so do q4_0 K windows; a
+ * kvm_stagein_fa_decode) with the same results; a
  * window that is not q8_0 or q4_0 K / q4_0 V is refused (KVM_EUNSUPPORTED), as
  * kvm_stagein_fa_decode refuses it.  A step whose plan stages anything pays for
  * the attention's first pass: where a plan change is expected (the first

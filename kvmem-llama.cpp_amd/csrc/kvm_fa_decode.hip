@@ -280,14 +280,14 @@ __device__ __forceinline__ void fa_merge(const fa_args &a, const fa_lane &ln, ui
 // K rows (stage_plan), which the selecting launch leaves out: with its
 // attention state live around the staging they raise its registers to the
 // limit and its steady-state time, though it never runs them there.
-template <int D, bool FAST>
+template <int D, bool FAST, int KQ = KVM_KQ_ANY>
 __device__ __forceinline__ void fa_stage_lane(const fa_args &a, const stage_args &sg, uint32_t n_ent, uint32_t cols) {
     extern __shared__ __align__(16) uint8_t s_rows[];     // the staged launch's dynamic LDS
     __shared__ uint32_t s_e;
     if (threadIdx.x == 0) s_e = sync_load(sg.sync);
     __syncthreads();
     const uint32_t e = s_e, G = a.H * cols, x = blockIdx.y * cols + blockIdx.x;
-    stage_plan<D, 512, KVM_FA_STAGE_IT, FAST>(sg, s_rows, n_ent, x, G, e + 1, false);
+    stage_plan<D, 512, KVM_FA_STAGE_IT, FAST, KQ>(sg, s_rows, n_ent, x, G, e + 1, false);
     if (!lane_barrier<512>(sg.sync, sg.status, sg.spin, e + 2, x, G, true, true) && threadIdx.x == 0)
         atomicOr(&sg.info[3], 16u);
 }
@@ -359,7 +359,7 @@ __device__ __forceinline__ uint32_t fa_await_plan(const fa_args &a, uint32_t h, 
 // (with STAGE): the plans come from the launch's selectors; the attention
 // workgroups attend over the window as it is, then wait for the lane's plan,
 // and only when it stages anything stage it and attend again.
-template <int D, int NRT, bool QUANT, bool PK, bool STAGE, bool SELECT>
+template <int D, int NRT, bool QUANT, bool PK, bool STAGE, bool SELECT, int KQ = KVM_KQ_ANY>
 __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_args *stg, const topk_args *sel) {
     static_assert(!SELECT || STAGE, "a selecting launch stages its plans");
     constexpr int NB = D / 32;          // 32-dim blocks per row
@@ -423,7 +423,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             const uint32_t n = fa_await_plan(a, h, ep_c + 1);
             if (n) {
                 __threadfence();             // acquire: the selection's stores
-                fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n, a.n_splits + 1);
+                fa_stage_lane<D, !SELECT, KQ>(a, stg[blockIdx.z], n, a.n_splits + 1);
             }
             __syncthreads();
             if (tid == 0)
@@ -437,7 +437,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     if (R == 0) {
         if constexpr (STAGE && !SELECT) {
             const uint32_t n_ent = stage_entries(stg[blockIdx.z]);
-            if (n_ent) fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n_ent, a.n_splits);
+            if (n_ent) fa_stage_lane<D, !SELECT, KQ>(a, stg[blockIdx.z], n_ent, a.n_splits);
         }
         return;
     }
@@ -483,7 +483,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (tid == 0) s_epoch = ep + 1;
     if constexpr (STAGE && !SELECT) {
-        if (n_ent) fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n_ent, a.n_splits);
+        if (n_ent) fa_stage_lane<D, !SELECT, KQ>(a, stg[blockIdx.z], n_ent, a.n_splits);
     }
     // SELECT, after the first pass over the window (both roles, at the same
     // barrier): true when the lane's plan staged anything, so the pass is redone
@@ -495,7 +495,7 @@ __device__ __forceinline__ void fa_decode_body(const fa_args &a, const stage_arg
             const uint32_t n = fa_await_plan(a, h, ep + 1);
             if (!n) return false;
             __threadfence();                 // acquire: the selection's stores
-            fa_stage_lane<D, !SELECT>(a, stg[blockIdx.z], n, a.n_splits + 1);
+            fa_stage_lane<D, !SELECT, KQ>(a, stg[blockIdx.z], n, a.n_splits + 1);
             return true;
         }
     };
@@ -976,9 +976,11 @@ struct fa_select_args {
     topk_args sel[KVM_MAX_LANES];
 };
 static_assert(sizeof(fa_select_args) <= 4096, "kernel argument segment");
-template <int D, int NRT, bool PK>
+// KQ: the windows' K type (KVM_KQ_Q8 or KVM_KQ_Q4), fixed so the staging
+// code of the other type adds nothing to the registers.
+template <int D, int NRT, bool PK, int KQ>
 __global__ void __launch_bounds__(512) k_fa_decode_select(fa_select_args sa) {
-    fa_decode_body<D, NRT, true, PK, true, true>(sa.a, sa.stage, sa.sel);
+    fa_decode_body<D, NRT, true, PK, true, true, KQ>(sa.a, sa.stage, sa.sel);
 }
 
 static uint32_t choose_splits(uint32_t n_cu, uint32_t n_lanes, uint32_t H, uint32_t n_tiles) {
@@ -1211,15 +1213,18 @@ extern "C" int kvm_stagein_fa_decode(kvm_state *st, const kvm_history *h, const 
 // by its attention workgroups, which then attend again.
 // ---------------------------------------------------------------------------
 template <int D, int NRT, bool PK>
-static const void *select_kernel() { return (const void *)k_fa_decode_select<D, NRT, PK>; }
+static const void *select_kernel(bool q4) {
+    return q4 ? (const void *)k_fa_decode_select<D, NRT, PK, KVM_KQ_Q4>
+              : (const void *)k_fa_decode_select<D, NRT, PK, KVM_KQ_Q8>;
+}
 
-static const void *select_kernel_for(uint32_t D, uint32_t max_rows) {
+static const void *select_kernel_for(uint32_t D, uint32_t max_rows, bool q4) {
     const int NRT = max_rows <= 16 ? 1 : 2;
     const bool pk = max_rows - 16u * (NRT - 1) <= 8u;
-    if (D == 256) return NRT == 1 ? (pk ? select_kernel<256, 1, true>() : select_kernel<256, 1, false>())
-                                  : (pk ? select_kernel<256, 2, true>() : select_kernel<256, 2, false>());
-    return NRT == 1 ? (pk ? select_kernel<128, 1, true>() : select_kernel<128, 1, false>())
-                    : (pk ? select_kernel<128, 2, true>() : select_kernel<128, 2, false>());
+    if (D == 256) return NRT == 1 ? (pk ? select_kernel<256, 1, true>(q4) : select_kernel<256, 1, false>(q4))
+                                  : (pk ? select_kernel<256, 2, true>(q4) : select_kernel<256, 2, false>(q4));
+    return NRT == 1 ? (pk ? select_kernel<128, 1, true>(q4) : select_kernel<128, 1, false>(q4))
+                    : (pk ? select_kernel<128, 2, true>(q4) : select_kernel<128, 2, false>(q4));
 }
 
 // The decode step's selecting launch over prepared top-k arguments (tl: from
@@ -1247,16 +1252,14 @@ static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, 
     int rc = kvm_stage_prepare(st, sg, n_lanes, rope, &stl, &max_items, &lds);
     if (rc) return rc;
     // the selecting launch takes lanes that all have query rows, at most
-    // KVM_SEL_MAXB blocks each and q8_0 windows; other steps take the
-    // separate launches (scoring, top-k, stage-in + attention)
-    // (a q4_0 K window takes the separate launches: the selecting launch's
-    // staging is the one-row-per-wave form, q8_0 only)
-    bool fuse = lanes[0].w->k_type == KVM_TYPE_Q8_0;
+    // KVM_SEL_MAXB blocks each and quantised (q8_0 or q4_0 K) windows; other
+    // steps take the separate launches (scoring, top-k, stage-in + attention)
+    bool fuse = kvm_k_quant(lanes[0].w->k_type);
     uint32_t max_rows = 0;
     for (uint32_t i = 0; i < n_lanes; ++i) {
         const kvm_window *w = lanes[i].w;
         const uint32_t r = w->n_head_kv && n_head % w->n_head_kv == 0 ? lanes[i].n_tokens * (n_head / w->n_head_kv) : 0u;
-        fuse = fuse && r > 0 && n_blocks[i] <= KVM_SEL_MAXB;
+        fuse = fuse && r > 0 && n_blocks[i] <= KVM_SEL_MAXB && w->k_type == lanes[0].w->k_type;
         max_rows = r > max_rows ? r : max_rows;
     }
     size_t lds_sel = lds * KVM_FA_STAGE_IT / 64;           // kvm_stage_prepare sizes 64-token items
@@ -1264,7 +1267,7 @@ static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, 
     const void *fn = nullptr;
     fa_plan fp;
     if (fuse) {
-        fn = select_kernel_for(lanes[0].w->head_dim, max_rows);
+        fn = select_kernel_for(lanes[0].w->head_dim, max_rows, lanes[0].w->k_type == KVM_TYPE_Q4_0);
         KVM_HIP(st, hipSetDevice(st->device));
         int occ = 0;
         rc = kvm_resident_blocks(st, fn, 512, lds_sel, &occ);
@@ -1288,7 +1291,7 @@ static int select_fa_launch(kvm_state *st, const kvm_retrieval_lane *ret_score, 
     if (!fuse) {
         rc = fa_prepare(st, lanes, n_lanes, q_type, n_head, scale, nullptr, 0, &fp);
         if (rc) return rc;
-        if (fp.rows && !fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "%s: q8_0 windows only", what);
+        if (fp.rows && !fp.quant) return kvm_fail(st, KVM_EUNSUPPORTED, "%s: q8_0 or q4_0 K windows only", what);
         if (ret_score) {
             rc = kvm_retrieval_score(st, ret_score, n_lanes, tl);
             if (rc) return rc;

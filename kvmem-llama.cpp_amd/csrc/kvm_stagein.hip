@@ -130,12 +130,6 @@ int kvm_stage_prepare(kvm_state *st, const kvm_stagein_lane *lanes, uint32_t n_l
         return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: n_rot %u (needs a multiple of 8 <= head_dim)", rope->n_rot);
     const int nrot = hadamard_width(w0, rope->hadamard_nrot);
     if (!hadamard_ok(nrot, w0->head_dim)) return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: hadamard width %d", nrot);
-    // q4_0 K rows are staged by the 16-lane K rows only (RoPE pairs one dim bit >= 4 apart)
-    for (uint32_t i = 0; i < n_lanes; ++i)
-        if (lanes[i].w->k_type == KVM_TYPE_Q4_0 &&
-            !(w0->head_dim == 256 ? k16_ok<256>(rope->n_rot / 2) : k16_ok<128>(rope->n_rot / 2)))
-            return kvm_fail(st, KVM_EUNSUPPORTED, "stagein: q4_0 K needs n_rot / 2 a power of two >= 16 (n_rot %u)",
-                            rope->n_rot);
     KVM_HIP(st, hipSetDevice(st->device));
     const std::vector<float> theta = kvm_rope_theta(rope->freq_base, rope->freq_scale, rope->n_rot);
     rope_ctx rc0;

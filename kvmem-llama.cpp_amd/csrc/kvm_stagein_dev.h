@@ -21,14 +21,22 @@ struct rope_ctx {
 };
 
 // NR (token, head) rows of D dims, interleaved so that their dependent shuffle
-// chains overlap: row r's src = NB q8_0 blocks (34 B each) readable by every
-// lane, requantised into K tile kt[r] at cell c[r] (0..63); cs[r] = the (cos,
-// sin) row of its window position, [n_half] (global memory or LDS).  Rows with
-// live[r] false are computed on their (valid) inputs but not written.
-template <int D, int NR>
+// chains overlap: row r's src = NB q8_0 blocks (34 B each; q4: q4_0 blocks of
+// 18 B, requantised with quant_q4_0's arithmetic, llama-kvmem-stagein.cu:201-234,
+// and held as q8_0 tile quants, the nibble minus 8) readable by every lane,
+// requantised into K tile kt[r] at cell c[r] (0..63); cs[r] = the (cos, sin)
+// row of its window position, [n_half] (global memory or LDS).  Rows with
+// live[r] false are computed on their (valid) inputs but not written.  KQ:
+// KVM_KQ_Q8 / KVM_KQ_Q4 fix the K type at compile time (the other's code left
+// out), KVM_KQ_ANY takes it from q4_arg.
+#define KVM_KQ_Q8 0
+#define KVM_KQ_Q4 1
+#define KVM_KQ_ANY 2
+template <int D, int NR, int KQ = KVM_KQ_ANY>
 __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *const (&kt)[NR],
                                     const uint32_t (&c)[NR], const float2 *const (&cs_pos)[NR],
-                                    const bool (&live)[NR], const rope_ctx &rc) {
+                                    const bool (&live)[NR], const rope_ctx &rc, bool q4_arg = false) {
+    const bool q4 = KQ == KVM_KQ_ANY ? q4_arg : KQ == KVM_KQ_Q4;
     constexpr int DPL = D / 64;
     const int L = threadIdx.x & 63;
     const int d0 = DPL * L;
@@ -36,10 +44,20 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
     float x[NR][DPL];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const uint8_t *blk = src[r] + b * 34;
-        const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+        if (!q4) {
+            const uint8_t *blk = src[r] + b * 34;
+            const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) x[r][i] = kvm_fmul((float)(int8_t)blk[2 + e + i], dsc);
+            for (int i = 0; i < DPL; ++i) x[r][i] = kvm_fmul((float)(int8_t)blk[2 + e + i], dsc);
+        } else {
+            // dims 0-15 of a block are the low nibbles of its 16 bytes, 16-31 the
+            // high ones (a lane's DPL dims sit in one half)
+            const uint8_t *blk = src[r] + b * 18;
+            const float dsc = kvm_h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+            const int sh = e >= 16 ? 4 : 0, j0 = e & 15;
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) x[r][i] = kvm_fmul((float)((int)((blk[2 + j0 + i] >> sh) & 15) - 8), dsc);
+        }
     }
 
     // NeoX RoPE: dims i and i + n_half rotate together for i < n_half.
@@ -125,28 +143,67 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
     // 1/d (|x| is unaffected, and x * -id is -x * id exactly)
     const uint32_t xs = rc.nrot > DPL && (__popc((uint32_t)L & (uint32_t)(rc.nrot / DPL - 1)) & 1) ? 0x80000000u : 0u;
 
-    // q8_0 requantisation of each 32-dim block (32/DPL lanes per block)
+    // q8_0 requantisation of each 32-dim block (32/DPL lanes per block); q4:
+    // quant_q4_0's, vmax = the first value of largest magnitude in dim order
+    // (lanes in dim order, the lower lanes' value kept on a tie) with its true
+    // sign, d = vmax / -8 (vmax * -0.125 exactly), id = d ? 1/d : 0, quant =
+    // min(15, (int)(x id + 8.5)) - 8
     const uint32_t lq = kvm_kq_off(D, 0, d0);
-    float amax[NR];
+    float amax[NR], vmax[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
         amax[r] = 0.0f;
+        vmax[r] = 0.0f;
+        if (!q4) {
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) amax[r] = fmaxf(amax[r], fabsf(x[r][i]));
+            for (int i = 0; i < DPL; ++i) amax[r] = fmaxf(amax[r], fabsf(x[r][i]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < DPL; ++i) {
+                const float av = fabsf(x[r][i]);
+                if (amax[r] < av) {
+                    amax[r] = av;
+                    vmax[r] = x[r][i];
+                }
+            }
+            vmax[r] = __uint_as_float(__float_as_uint(vmax[r]) ^ xs);
+        }
     }
 #pragma unroll
     for (int o = 1; o < 32 / DPL; o <<= 1)
 #pragma unroll
-        for (int r = 0; r < NR; ++r) amax[r] = fmaxf(amax[r], __shfl_xor(amax[r], o, 64));
+        for (int r = 0; r < NR; ++r) {
+            const float ap = __shfl_xor(amax[r], o, 64);
+            if (!q4) {
+                amax[r] = fmaxf(amax[r], ap);
+            } else {
+                const float vp = __shfl_xor(vmax[r], o, 64);
+                const bool lower = (L & o) == 0;                 // this lane's dims come first
+                const float a_f = lower ? amax[r] : ap, v_f = lower ? vmax[r] : vp;
+                const float a_s = lower ? ap : amax[r], v_s = lower ? vp : vmax[r];
+                const bool take_s = a_f < a_s;
+                amax[r] = take_s ? a_s : a_f;
+                vmax[r] = take_s ? v_s : v_f;
+            }
+        }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const float d = kvm_div127(amax[r]);
+        const float d = q4 ? kvm_fmul(vmax[r], -0.125f) : kvm_div127(amax[r]);
         const float id = __uint_as_float(__float_as_uint(kvm_recip_or0(d)) ^ xs);
         // the lane's DPL quants are consecutive in the tile (8-byte runs of one
         // block and lane group): one store of DPL bytes, aligned to DPL
         uint32_t qw = 0;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) qw |= (uint32_t)(uint8_t)kvm_round_away(kvm_fmul(x[r][i], id)) << (8 * i);
+        for (int i = 0; i < DPL; ++i) {
+            int qi;
+            if (!q4) {
+                qi = kvm_round_away(kvm_fmul(x[r][i], id));
+            } else {
+                qi = (int)kvm_fadd(kvm_fmul(x[r][i], id), 8.5f);
+                qi = (qi > 15 ? 15 : qi) - 8;
+            }
+            qw |= (uint32_t)(uint8_t)(int8_t)qi << (8 * i);
+        }
         if (!live[r]) continue;
         // tile offsets split into the row's cell part and the lane's dim part
         uint8_t *row = kt[r] + kvm_kq_off(D, c[r], 0);
@@ -576,7 +633,7 @@ __device__ inline void stage_gather_split(const stage_args &a, uint32_t n_ent, u
 // One (plan entry, IT-token run) item, staged by a workgroup of NTH threads
 // through the LDS rows buffer s_rows (IT * n_head_kv * (D/32) * 52 bytes).  An
 // item of 32 tokens fills one key half (ks) of a 64-cell window tile.
-template <int D, int NTH, int IT = 64, bool FAST = true>
+template <int D, int NTH, int IT = 64, bool FAST = true, int KQ = KVM_KQ_ANY>
 __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_rows, uint32_t si, uint32_t tt,
                                              bool host_via = false) {
     static_assert(IT == 64 || IT == 32, "stage-in item size");
@@ -673,13 +730,13 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         for (uint32_t k = 0; k < NR; ++k) {
             const uint32_t r = r0 + k * W < nrow ? r0 + k * W : r0;    // past the rows: recompute r0, unwritten
             const uint32_t j = r / a.H, h = r % a.H;
-            src[k] = lk + j * rowK + h * NB * 34;
+            src[k] = lk + j * rowK + h * NB * kb;
             kt[k] = a.wk + ((uint64_t)h * a.n_tiles + tile) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
             cc[k] = c0 + j;
             cs[k] = lt + j * nh;
             live[k] = r0 + k * W < nrow;
         }
-        stage_k_rows<D, NR>(src, kt, cc, cs, live, a.rc);
+        stage_k_rows<D, NR, KQ>(src, kt, cc, cs, live, a.rc, a.k_q4 != 0);
     }
     const uint32_t vtile = kvm_vtile_bytes(KVM_TYPE_Q4_0, D);
     if (src >= 0) {
@@ -847,7 +904,7 @@ __device__ void stage_void_item(const stage_args &a, uint32_t si, uint32_t tt) {
 // within the window, then items x, x + G, ... of IT tokens.  `last`: the
 // gather barrier is the launch's last on these sync words.  No barrier
 // follows the items.
-template <int D, int NTH, int IT, bool FAST = true>
+template <int D, int NTH, int IT, bool FAST = true, int KQ = KVM_KQ_ANY>
 __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent, uint32_t x, uint32_t G,
                            uint32_t v, bool last) {
     const uint32_t tps = a.bt / IT, n_items = n_ent * tps;
@@ -866,7 +923,7 @@ __device__ void stage_plan(const stage_args &a, uint8_t *s_rows, uint32_t n_ent,
         }
     }
     for (uint32_t item = x; item < n_items; item += G) {
-        if (ok) stagein_item<D, NTH, IT, FAST>(a, s_rows, item / tps, item % tps, host_via);
+        if (ok) stagein_item<D, NTH, IT, FAST, KQ>(a, s_rows, item / tps, item % tps, host_via);
         else stage_void_item<IT>(a, item / tps, item % tps);
         __syncthreads();                 // LDS rows of this item read before the next overwrites them
     }

@@ -22,19 +22,19 @@ H, G, D, BT = 4, 6, 256, 128
 K_ROW, V_ROW = H * D // 32 * 34, H * D // 32 * 18
 
 
-def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4, terms=False):
+def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4, terms=False, kt=L.T_Q8_0):
     rng = np.random.default_rng(seed)
     n_hist = n_blocks * BT - 40                         # the last block partly filled
-    kr, vr = rand_rows(rng, n_hist, H, D, L.T_Q8_0, L.T_Q4_0)
+    kr, vr = rand_rows(rng, n_hist, H, D, kt, L.T_Q4_0)
     ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
     ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
     qa = api.QueryAcc(st, 1, H * G, D, n_head_kv=H if terms else 0)
     qa.reset()
     qa.add(0, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
     nt = dev(np.array([min(BT, n_hist - b * BT) for b in range(n_blocks)], np.int32))
-    mk = lambda sh: dict(window=api.KVWindow(st, slots * BT, H, D, BT, shadow=sh),
+    mk = lambda sh: dict(window=api.KVWindow(st, slots * BT, H, D, BT, kt, L.T_Q4_0, shadow=sh),
                          sel=api.SelectionBuffers(st, n_blocks, budget), history=api.History(kr, vr))
-    return dict(rng=rng, kr=kr, vr=vr, ix=ix, qa=qa, nt=nt, n_blocks=n_blocks, budget=budget, n_hist=n_hist,
+    return dict(rng=rng, kr=kr, vr=vr, kt=kt, ix=ix, qa=qa, nt=nt, n_blocks=n_blocks, budget=budget, n_hist=n_hist,
                 q_pos=dev(np.arange(budget * BT - max(n_tok_q, 1), budget * BT, dtype=np.int32)), n_tok_q=n_tok_q,
                 a=mk(True), b=mk(False))
 
@@ -52,7 +52,7 @@ def _resident_full(w, nt_host):
 
 def _set_rows(hist, blocks, rows_k, rows_v):
     torch.cuda.synchronize()
-    k = hist.kbuf.u8.reshape(hist.n_tokens, K_ROW)
+    k = hist.kbuf.u8.reshape(hist.n_tokens, -1)
     v = hist.vbuf.u8.reshape(hist.n_tokens, V_ROW)
     for b in blocks:
         k[b * BT:(b + 1) * BT] = rows_k(b)
@@ -83,8 +83,10 @@ def _compare(ln, ref, bit_equal, tag):
     return int((ra["stage_src"] >= 0).sum())
 
 
-@pytest.mark.parametrize("n_lanes,splits,terms", [(1, None, False), (1, 32, True), (3, None, True)])
-def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, splits, terms):
+@pytest.mark.parametrize("n_lanes,splits,terms,kt", [(1, None, False, L.T_Q8_0), (1, 32, True, L.T_Q8_0),
+                                                    (3, None, True, L.T_Q8_0), (1, 32, True, L.T_Q4_0)],
+                         ids=["q8_0", "q8_0-32-splits-terms", "q8_0-3-lanes-terms", "q4_0-32-splits-terms"])
+def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, splits, terms, kt):
     """Queries drift over six steps, so plans restage and move blocks within
     windows that carry a K shadow (the host rows of the full blocks a window
     holds are poisoned while its step runs: a moved block must come from the
@@ -93,11 +95,13 @@ def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, spl
     step's launch takes one split fewer per head than kvm_fa_decode (the
     selectors' column) and the outputs agree within the attention tolerance.
     terms: the query accumulators carry the scorer's query terms, refreshed
-    after each drift of the sums."""
+    after each drift of the sums.  kt: the K cache type (q4_0: the selecting
+    launch stages the q4_0 rows with the one-row-per-wave requantiser, the
+    separate calls with the 16-lane one)."""
     if splits:
         monkeypatch.setenv("KVM_FA_SPLITS", str(splits))
     st = kvm_state
-    lanes = [_lane(st, 0x5D00 + i, 40 + 6 * i, 12, 16, terms=terms) for i in range(n_lanes)]
+    lanes = [_lane(st, 0x5D00 + i, 40 + 6 * i, 12, 16, terms=terms, kt=kt) for i in range(n_lanes)]
     moved = staged = 0
     for step in range(6):
         for ln in lanes:
@@ -110,7 +114,7 @@ def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, spl
         nts = [host(ln["nt"]) for ln in lanes]
         held = [_resident_full(ln["a"]["window"], nt) for ln, nt in zip(lanes, nts)]
         for ln, hb in zip(lanes, held):
-            _set_rows(ln["a"]["history"], hb, lambda b, r=ln["rng"]: r.integers(0, 256, (BT, K_ROW), dtype=np.uint8),
+            _set_rows(ln["a"]["history"], hb, lambda b, r=ln["rng"], kw=ln["kr"].shape[1]: r.integers(0, 256, (BT, kw), dtype=np.uint8),
                       lambda b, r=ln["rng"]: r.integers(0, 256, (BT, V_ROW), dtype=np.uint8))
         if n_lanes == 1:
             d = _step_dict(lanes[0])
@@ -132,7 +136,7 @@ def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, spl
     ln = lanes[0]
     w = ln["b"]["window"]
     ek, ev = w.export_rows(0, w.n_cells)
-    ref = O.fa_ggml(O.T_Q8_0, O.T_Q4_0, ln["q"].float().cpu().numpy(), host(ek), host(ev), host(w.cell_pos),
+    ref = O.fa_ggml(kt, O.T_Q4_0, ln["q"].float().cpu().numpy(), host(ek), host(ev), host(w.cell_pos),
                     host(ln["q_pos"]), H * G, H, D, D ** -0.5)
     check_attention(host(ln["out"]), ref)
 
@@ -426,8 +430,9 @@ def test_decode_step_four_lanes_full_windows(kvm_state):
 
 def test_decode_step_q4_0_k_window(kvm_state):
     """The whole step over a q4_0 K cache (history rows and window in q4_0):
-    kvm_score_topk_stagein_fa_decode takes the separate launches for it; the
-    staged blocks equal the oracle's q4_0 stage-in and the output the ggml
+    kvm_score_topk_stagein_fa_decode runs it as the two-launch step (the
+    selecting launch stages the q4_0 rows); the staged blocks equal the
+    oracle's q4_0 stage-in and the output the ggml
     attention over the window it leaves (a q4_0 K cache: Q quantised to q8_0,
     vec_dot_q4_0_q8_0)."""
     st = kvm_state

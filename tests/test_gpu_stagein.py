@@ -367,12 +367,15 @@ def test_score_topk_stagein_lanes_matches_two_calls(kvm_state):
             assert len(r["stage_slots"]) == (budget if step == 0 else 0)
 
 
-@pytest.mark.parametrize("D,n_rot,hadamard", [(256, 64, -1), (256, 128, 0), (128, 32, -1)])
+@pytest.mark.parametrize("D,n_rot,hadamard", [(256, 64, -1), (256, 128, 0), (128, 32, -1), (256, 24, -1),
+                                              (128, 16, 64)])
 def test_stagein_selection_bytes_q4_0_k(kvm_state, D, n_rot, hadamard):
     """A q4_0 K cache: the history's raw K rows are q4_0 and the stage-in
     requantises to q4_0 (quant_q4_0, llama-kvmem-stagein.cu:201-234, in the
     chain of :731-786); the window holds them as q8_0 tile quants and exports
-    the q4_0 rows the oracle's chain produces, byte for byte."""
+    the q4_0 rows the oracle's chain produces, byte for byte.  RoPE pairs 12 or
+    8 dims apart (n_rot 24, 16) take the one-row-per-wave requantiser, the
+    others the 16-lane one."""
     H, bt, n_blocks = 4, 128, 30
     n_hist = n_blocks * bt - 70
     rng = np.random.default_rng(D + n_rot)
@@ -398,14 +401,3 @@ def test_stagein_selection_bytes_q4_0_k(kvm_state, D, n_rot, hadamard):
         assert np.array_equal(ev[k * bt:k * bt + n], vr[bid * bt:bid * bt + n])
 
 
-def test_stagein_q4_0_k_refuses_other_rope_widths(kvm_state):
-    """q4_0 K rows are staged for RoPE widths whose pairs are a power of two
-    of 16 or more dims apart; others are refused before anything runs."""
-    H, D, bt = 4, 256, 128
-    rng = np.random.default_rng(3)
-    kr, vr = rand_rows(rng, 4 * bt, H, D, L.T_Q4_0, L.T_Q4_0)
-    w = api.KVWindow(kvm_state, 4 * bt, H, D, bt, L.T_Q4_0, L.T_Q4_0)
-    sel = api.select_topk(kvm_state, dev(np.arange(4.0)), dev(np.full(4, bt, np.int32)), 4, 1, 0, None, window=w)
-    with pytest.raises(L.KvmError) as e:
-        api.stagein_selection(kvm_state, api.History(kr, vr), w, sel, 24, 1e7)
-    assert e.value.code == L.KVM_EUNSUPPORTED
