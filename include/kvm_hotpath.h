@@ -499,7 +499,9 @@ int kvm_score_topk_stagein_lanes(kvm_state *st, const kvm_retrieval_lane *lanes,
  * (src/adapter/llama-kvmem-stagein.h:36-46).  `dst` is (window, first cell)
  * instead of a raw cache pointer; packed rows are copied into the state's
  * pinned slab, so the host buffer is free on return (stagein.h:23).  flush
- * runs one fused launch over all queued items. */
+ * runs one fused launch over all queued items.  `type` is the window's K type,
+ * q8_0 or q4_0 (kvmem_stagein_quant_ok, llama-kvmem-stagein.cu:481-483); q4_0
+ * rows are requantised with quant_q4_0's arithmetic (:201-234). */
 int kvm_stagein_enqueue_k(kvm_state *st, int type, const void *packed, size_t nbytes,
                           const kvm_window *w, uint32_t cell0, int64_t nt, int64_t n_embd,
                           int nrot, int n_head, int n_embd_head, int n_rot_rope, int32_t pos0,

@@ -212,6 +212,7 @@ struct kitem_desc {
     int32_t pos0;
     int32_t nrot;       // Hadamard width of this item, 0 = off
     float hscale;       // 1 / sqrtf(nrot), per item: items of different widths may share a flush
+    uint32_t q4;        // the rows are q4_0 (a q4_0 K window), else q8_0
 };
 
 template <int D>
@@ -226,8 +227,9 @@ __global__ void __launch_bounds__(256) k_stagein_items(const kitem_desc *items, 
     rc.hscale = it.hscale;
     const uint32_t cell = it.cell0 + t;
     uint8_t *kt = it.wk + ((uint64_t)h * it.n_tiles + cell / 64) * kvm_ktile_bytes(KVM_TYPE_Q8_0, D);
-    stage_k_row<D>(it.src + (uint64_t)t * it.H * NB * 34 + h * NB * 34, kt, cell % 64,
-                   rc.tab + (uint64_t)(it.pos0 + (int32_t)t) * rc.n_half, rc);
+    const uint32_t kb = it.q4 ? 18u : 34u;
+    stage_k_row<D>(it.src + (uint64_t)t * it.H * NB * kb + h * NB * kb, kt, cell % 64,
+                   rc.tab + (uint64_t)(it.pos0 + (int32_t)t) * rc.n_half, rc, it.q4 != 0);
     if ((threadIdx.x & 63) == 0 && h == 0) it.cell_pos[cell] = it.pos0 + (int32_t)t;
 }
 
@@ -267,11 +269,14 @@ extern "C" int kvm_stagein_enqueue_k(kvm_state *st, int type, const void *packed
     if (!st || !packed || !w) return kvm_fail(st, KVM_EINVAL, "enqueue_k: null argument");
     int rc = kvm_window_check(w);
     if (rc) return kvm_fail(st, rc, "enqueue_k: bad window");
-    if (type != KVM_TYPE_Q8_0 || w->k_type != KVM_TYPE_Q8_0) return kvm_fail(st, KVM_EUNSUPPORTED, "enqueue_k: q8_0 only");
+    if (!kvm_k_quant(type) || type != w->k_type)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "enqueue_k: rows of type %d into a window of K type %d (q8_0 or q4_0)", type,
+                        w->k_type);
     if ((int64_t)n_head * n_embd_head != n_embd || (uint32_t)n_head != w->n_head_kv || (uint32_t)n_embd_head != w->head_dim)
         return kvm_fail(st, KVM_EINVAL, "enqueue_k: n_embd %lld != %d x %d or window shape", (long long)n_embd, n_head, n_embd_head);
     if (nt <= 0 || (uint64_t)cell0 + (uint64_t)nt > w->n_cells) return kvm_fail(st, KVM_ERANGE, "enqueue_k: cells past window");
-    if ((size_t)nt * (size_t)(n_embd / 32 * 34) != nbytes) return kvm_fail(st, KVM_EINVAL, "enqueue_k: nbytes %zu mismatch", nbytes);
+    const size_t kb = type == KVM_TYPE_Q4_0 ? 18u : 34u;
+    if ((size_t)nt * (size_t)(n_embd / 32 * kb) != nbytes) return kvm_fail(st, KVM_EINVAL, "enqueue_k: nbytes %zu mismatch", nbytes);
     if (n_rot_rope < 8 || n_rot_rope % 8 || n_rot_rope > n_embd_head || n_theta != n_rot_rope / 2 || !theta)
         return kvm_fail(st, KVM_EUNSUPPORTED, "enqueue_k: n_rot %d / n_theta %d", n_rot_rope, n_theta);
     if (!hadamard_ok(nrot, w->head_dim)) return kvm_fail(st, KVM_EUNSUPPORTED, "enqueue_k: hadamard width %d", nrot);
@@ -350,6 +355,7 @@ extern "C" int kvm_stagein_flush(kvm_state *st) {
             d.nrot = it.nrot;
             // the reference computes the scale on the host (llama-kvmem-stagein.cu:594)
             d.hscale = it.nrot > 0 ? 1.0f / sqrtf((float)it.nrot) : 1.0f;
+            d.q4 = it.w.k_type == KVM_TYPE_Q4_0 ? 1u : 0u;
             ds.push_back(d);
             max_rows = std::max(max_rows, it.nt * it.w.n_head_kv);
             max_pos = std::max(max_pos, (uint32_t)std::max(0, it.pos0) + it.nt);

@@ -215,16 +215,16 @@ __device__ inline void stage_k_rows(const uint8_t *const (&src)[NR], uint8_t *co
     }
 }
 
-// One row (stage_k_rows of one).
+// One row (stage_k_rows of one; q4: src holds q4_0 blocks).
 template <int D>
 __device__ inline void stage_k_row(const uint8_t *src, uint8_t *kt, uint32_t c, const float2 *cs_pos,
-                                   const rope_ctx &rc) {
+                                   const rope_ctx &rc, bool q4 = false) {
     const uint8_t *const s1[1] = {src};
     uint8_t *const k1[1] = {kt};
     const uint32_t c1[1] = {c};
     const float2 *const t1[1] = {cs_pos};
     const bool l1[1] = {true};
-    stage_k_rows<D, 1>(s1, k1, c1, t1, l1, rc);
+    stage_k_rows<D, 1>(s1, k1, c1, t1, l1, rc, q4);
 }
 
 // The same K rows with LG = D / 16 lanes per (token, head) row, 64 / LG rows

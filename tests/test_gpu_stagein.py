@@ -160,12 +160,15 @@ def test_stagein_lanes_match_single_lane(kvm_state):
         api.stagein_selection_lanes(kvm_state, [lanes[0], (lanes[0][0], w128, sel128)], 64, 1e7)
 
 
-def test_enqueue_flush_api(kvm_state):
-    """Reference-shaped item API (llama-kvmem-stagein.h:36-46) at arbitrary cells."""
+@pytest.mark.parametrize("kt", [L.T_Q8_0, L.T_Q4_0], ids=["q8_0", "q4_0"])
+def test_enqueue_flush_api(kvm_state, kt):
+    """Reference-shaped item API (llama-kvmem-stagein.h:36-46) at arbitrary
+    cells, q8_0 and q4_0 K rows; rows of another type than the window's are
+    refused."""
     H, D = 4, 256
     rng = np.random.default_rng(10)
-    w = api.KVWindow(kvm_state, 512, H, D, 128)
-    kr, vr = rand_rows(rng, 100, H, D, L.T_Q8_0, L.T_Q4_0)
+    w = api.KVWindow(kvm_state, 512, H, D, 128, kt, L.T_Q4_0)
+    kr, vr = rand_rows(rng, 100, H, D, kt, L.T_Q4_0)
     theta = O.rope_theta(1e7, 1.0, 64)
     lib = kvm_state.lib
     items = [(0, 30, 500), (30, 70, 7)]             # (row0, n, pos0)
@@ -173,17 +176,21 @@ def test_enqueue_flush_api(kvm_state):
     for (r0, n, pos0), c0 in zip(items, cells):
         kb = np.ascontiguousarray(kr[r0:r0 + n])
         vb = np.ascontiguousarray(vr[r0:r0 + n])
-        kvm_state.check(lib.kvm_stagein_enqueue_k(kvm_state.h, L.T_Q8_0, kb.ctypes.data_as(C.c_void_p), kb.nbytes,
+        kvm_state.check(lib.kvm_stagein_enqueue_k(kvm_state.h, kt, kb.ctypes.data_as(C.c_void_p), kb.nbytes,
                                                   C.byref(w.c), c0, n, H * D, 256, H, D, 64, pos0,
                                                   theta.ctypes.data_as(C.c_void_p), 32))
         kvm_state.check(lib.kvm_stagein_enqueue_v(kvm_state.h, vb.ctypes.data_as(C.c_void_p), vb.nbytes,
                                                   C.byref(w.c), c0, n))
+    other = L.T_Q4_0 if kt == L.T_Q8_0 else L.T_Q8_0
+    kb = np.ascontiguousarray(kr[:4])
+    assert lib.kvm_stagein_enqueue_k(kvm_state.h, other, kb.ctypes.data_as(C.c_void_p), kb.nbytes, C.byref(w.c), 0, 4,
+                                     H * D, 256, H, D, 64, 0, theta.ctypes.data_as(C.c_void_p), 32) == L.KVM_EUNSUPPORTED
     kvm_state.check(lib.kvm_stagein_flush(kvm_state.h))
     ek, ev = w.export_rows(0, 512)
     ek, ev = host(ek), host(ev)
     cp = host(w.cell_pos)
     for (r0, n, pos0), c0 in zip(items, cells):
-        want = O.stagein_k(kr[r0:r0 + n].reshape(-1), n, H, D, 64, 256, pos0, theta).reshape(n, -1)
+        want = O.stagein_k(kr[r0:r0 + n].reshape(-1), n, H, D, 64, 256, pos0, theta, k_type=kt).reshape(n, -1)
         assert np.array_equal(ek[c0:c0 + n], want)
         assert np.array_equal(ev[c0:c0 + n], vr[r0:r0 + n])
         assert np.array_equal(cp[c0:c0 + n], np.arange(pos0, pos0 + n))
