@@ -104,10 +104,12 @@ def build_workload(st, api, L, torch, np, n_rep, seed=0xC0FFEE02, hist_tokens=HI
     gpos = torch.arange(RETRIEVED, WINDOW, dtype=torch.int32, device=dev)
     reps = []
     for r in range(n_rep):
-        ix = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT)
+        # the index carries the blocks' score term nk (formed after the copies)
+        ix = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT, norms=True)
         ix.k_sum.copy_(ix0.k_sum)
         ix.mean_tokens.copy_(ix0.mean_tokens)
         ix.present.copy_(ix0.present)
+        ix.refresh()
         w = api.KVWindow(st, WINDOW, H_KV, D, BT)
         sel = api.SelectionBuffers(st, n_blocks, RETRIEVED // BT)
         api.score_topk(st, ix, qa, n_blocks, n_tokens, RETRIEVED // BT, 1, 0, None, w, sel)
@@ -521,10 +523,11 @@ def run_churn(args, st, api, L, torch, np):
     sums = torch.zeros((1, n_blocks, H_KV * D), device=dev)
     sums[0, torch.from_numpy(sa).to(dev), 0] = float(BT)
     sums[0, torch.from_numpy(sb).to(dev), 1] = float(BT)
-    ix = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT)
+    ix = api.MeanKIndex(st, 1, n_blocks, H_KV, D, BT, norms=True)
     ix.set_block_sums(sums)
     ix.mean_tokens[:, :n_blocks] = BT
     ix.present[:n_blocks] = 1
+    ix.refresh()
     qas = []
     for dim in (0, 1):
         qa = api.QueryAcc(st, 1, N_HEAD, D, n_head_kv=H_KV)

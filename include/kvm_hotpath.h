@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KVM_ABI_VERSION 5
+#define KVM_ABI_VERSION 6
 
 enum kvm_status {
     KVM_OK = 0,
@@ -289,10 +289,25 @@ typedef struct kvm_meank_index {
     uint8_t *present;       /* device [n_blocks] (RawKvStore::has_block), or NULL = all */
     float *acc;             /* device [n_layer][n_head_kv * head_dim]: the decode running sum
                              * (kvmem_meank_*, llama-kvmem-stagein.h:58-66), or NULL */
+    /* Optional: the block term of score_retrieval that no query changes, formed
+     * once per change of a block's sum instead of once per scoring.  With
+     * k_norm != NULL, k_norm[il][h][b] = the sum over d, in dim order, of
+     * kh[d]^2 with kh = k_sum * (1 / mean_tokens) of kv head h (0 for a block
+     * without tokens): the reference's nk (llama-memory-kvmem.cpp:4176-4183),
+     * each operation one IEEE rounding.  kvm_meank_add(_view),
+     * kvm_meank_acc_flush and kvm_harvest_block keep it current for the blocks
+     * they change; a caller that writes k_sum or mean_tokens itself calls
+     * kvm_meank_refresh before the next scoring.  The scorers then read it. */
+    float *k_norm;          /* device [n_layer][n_head_kv][n_blocks] or NULL */
 } kvm_meank_index;
 
 /* Number of floats k_sum must hold for the index geometry in *ix. */
 size_t kvm_meank_k_sum_floats(const kvm_meank_index *ix);
+/* Forms k_norm of every layer and block from k_sum / mean_tokens (no
+ * counterpart in the reference, which forms nk inside score_retrieval): for
+ * callers that write the sums directly.  KVM_OK without work when k_norm is
+ * NULL. */
+int kvm_meank_refresh(kvm_state *st, const kvm_meank_index *ix);
 
 /* RawKvStore::write_layer_mean_k (raw_kv_store.cpp:685-705): add n token rows of
  * layer il starting at original position pos0.  k_rows: device fp32

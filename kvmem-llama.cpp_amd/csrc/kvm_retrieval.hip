@@ -228,10 +228,67 @@ static uint64_t meank_layer_floats(const kvm_meank_index *ix) {
     return (uint64_t)kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE) * KVM_MEANK_TILE * ix->n_head_kv * ix->head_dim;
 }
 
+// The index's block terms (k_norm) of blocks b0 .. b0 + gridDim.x - 1, kv head
+// blockIdx.y, layer il0 + blockIdx.z, one wave each: lane l forms kh of dims
+// l, l + 64, ... as the scorer does (k_sum * (1 / mean_tokens), 0 without
+// tokens), then lane 0 sums kh^2 over the dims in order from LDS.
+template <int D>
+__global__ void __launch_bounds__(64) k_meank_terms(const float *k_sum, const uint32_t *mean_tokens, float *k_norm,
+                                                    uint64_t layer_floats, uint32_t cap, uint32_t H, uint32_t il0,
+                                                    uint32_t b0) {
+    const uint32_t b = b0 + blockIdx.x, h = blockIdx.y, il = il0 + blockIdx.z, l = threadIdx.x, n_embd = H * D;
+    __shared__ float s_sq[D];
+    const uint32_t mt = mean_tokens[(uint64_t)il * cap + b];
+    const float inv = kvm_recip_or0((float)mt);
+    const uint32_t keep = mt ? 0xffffffffu : 0u;
+    const float *ks = k_sum + (uint64_t)il * layer_floats;
+    for (uint32_t d = l; d < (uint32_t)D; d += 64u) {
+        const float kh = __uint_as_float(__float_as_uint(kvm_fmul(ks[kvm_meank_off(n_embd, h * D + d, b)], inv)) & keep);
+        s_sq[d] = kvm_fmul(kh, kh);
+    }
+    __syncthreads();
+    if (l == 0) {
+        float nk = 0.0f;
+        for (uint32_t d = 0; d < (uint32_t)D; ++d) nk = kvm_fadd(nk, s_sq[d]);
+        k_norm[((uint64_t)il * H + h) * cap + b] = nk;
+    }
+}
+
+// Forms k_norm of layers [il0, il0 + n_lay) and blocks [b0, b1) on the state's stream.
+static int meank_terms_launch(kvm_state *st, const kvm_meank_index *ix, uint32_t il0, uint32_t n_lay, uint32_t b0,
+                              uint32_t b1) {
+    if (!ix->k_norm || n_lay == 0 || b1 <= b0) return KVM_OK;
+    const dim3 grid(b1 - b0, ix->n_head_kv, n_lay);
+    if (ix->head_dim == 256)
+        hipLaunchKernelGGL(k_meank_terms<256>, grid, dim3(64), 0, st->stream, ix->k_sum, ix->mean_tokens, ix->k_norm,
+                           meank_layer_floats(ix), ix->n_blocks, ix->n_head_kv, il0, b0);
+    else
+        hipLaunchKernelGGL(k_meank_terms<128>, grid, dim3(64), 0, st->stream, ix->k_sum, ix->mean_tokens, ix->k_norm,
+                           meank_layer_floats(ix), ix->n_blocks, ix->n_head_kv, il0, b0);
+    KVM_LAUNCH_CHECK(st, "meank_terms");
+    return KVM_OK;
+}
+
+static int meank_terms_check(kvm_state *st, const kvm_meank_index *ix, const char *what) {
+    if (ix->k_norm && ix->head_dim != 128 && ix->head_dim != 256)
+        return kvm_fail(st, KVM_EUNSUPPORTED, "%s: block terms at head_dim %u", what, ix->head_dim);
+    return KVM_OK;
+}
+
+extern "C" int kvm_meank_refresh(kvm_state *st, const kvm_meank_index *ix) {
+    if (!st || !ix || !ix->k_sum || !ix->mean_tokens) return kvm_fail(st, KVM_EINVAL, "meank_refresh: args");
+    int rc = meank_terms_check(st, ix, "meank_refresh");
+    if (rc) return rc;
+    KVM_HIP(st, hipSetDevice(st->device));
+    return meank_terms_launch(st, ix, 0, ix->n_layer, 0, ix->n_blocks);
+}
+
 // write_layer_mean_k from view tokens tok0 .. tok0+n-1 at positions pos0 ..
 static int meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0, const kvm_view *k,
                           uint32_t tok0, uint32_t n) {
     int rc = meank_check(st, ix, il, "meank_add");
+    if (rc) return rc;
+    rc = meank_terms_check(st, ix, "meank_add");
     if (rc) return rc;
     const uint32_t n_embd = ix->n_head_kv * ix->head_dim;
     rc = view_check(st, k, n_embd, "meank_add");
@@ -249,7 +306,7 @@ static int meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il,
                        ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present, ix->n_blocks, n_embd,
                        bt, pos0, n, view_of(k), tok0);
     KVM_LAUNCH_CHECK(st, "meank_add");
-    return KVM_OK;
+    return meank_terms_launch(st, ix, il, 1, pos0 / bt, (uint32_t)last + 1);
 }
 
 extern "C" int kvm_meank_add_view(kvm_state *st, const kvm_meank_index *ix, uint32_t il, uint32_t pos0,
@@ -331,6 +388,8 @@ extern "C" int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uin
     int rc = meank_check(st, ix, il, "meank_acc_flush");
     if (rc) return rc;
     if (!ix->acc) return kvm_fail(st, KVM_EINVAL, "meank_acc_flush: index without a running sum");
+    rc = meank_terms_check(st, ix, "meank_acc_flush");
+    if (rc) return rc;
     if (n == 0) return KVM_OK;
     const uint32_t bt = ix->block_tokens, bid = pos0 / bt, off = pos0 % bt;
     const uint32_t take = n < bt - off ? n : bt - off;
@@ -342,7 +401,7 @@ extern "C" int kvm_meank_acc_flush(kvm_state *st, const kvm_meank_index *ix, uin
                        ix->mean_tokens + (uint64_t)il * ix->n_blocks, ix->present,
                        ix->acc + (uint64_t)il * n_embd, n_embd, bid, off, take);
     KVM_LAUNCH_CHECK(st, "meank_acc_flush");
-    return KVM_OK;
+    return meank_terms_launch(st, ix, il, 1, bid, bid + 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -361,24 +420,25 @@ struct score_lanes {
     score_args lane[KVM_RET_LANES];
 };
 
-template <int D, bool QV, bool OTF>
+template <int D, bool QV, int LAY>
 __global__ void __launch_bounds__(256) k_score(score_lanes sl) {
     // one copy of the lane's arguments: its scalar loads are issued together
     // ahead of the first branch, not one round trip per field
     const score_args a = sl.lane[blockIdx.z];
     if constexpr (QV) asm volatile("" ::"s"(a.q_vec), "s"(a.q_norm), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
     else asm volatile("" ::"s"(a.q_sum), "s"(a.q_count), "s"(a.k_sum), "s"(a.mean_tokens));
+    if constexpr (LAY == KVM_SL_NK) asm volatile("" ::"s"(a.k_norm));
     const uint32_t tile = blockIdx.x, il = blockIdx.y;
     if (tile >= a.n_tiles_used || il >= a.n_layer) return;
-    __shared__ __align__(16) score_wg_lds<D, 4, OTF> L;
+    __shared__ __align__(16) score_wg_lds<D, 4, LAY> L;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const uint32_t g = a.g, qc = a.q_count[il];
     score_regs r;
-    if ((uint32_t)w < a.H) score_tile_load<D, QV>(a, il, tile, (uint32_t)w, g, r);
+    if ((uint32_t)w < a.H) score_tile_load<D, QV, LAY>(a, il, tile, (uint32_t)w, g, r);
     if (qc == 0) return;                 // a layer without queries: skipped by the reduction
     for (uint32_t hh = (uint32_t)w; hh < a.H; hh += 4u) {
-        if (hh != (uint32_t)w) score_tile_load<D, QV>(a, il, tile, hh, g, r);
-        score_tile_compute<D, QV, OTF>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
+        if (hh != (uint32_t)w) score_tile_load<D, QV, LAY>(a, il, tile, hh, g, r);
+        score_tile_compute<D, QV, LAY>(a, il, hh, qc, g, r, L.w[w], L.cos[hh]);
     }
     __syncthreads();
     if (w == 0) score_tile_store(a, il, tile, L.cos);
@@ -526,7 +586,8 @@ void kvm_retrieval_score_args(const kvm_retrieval_lane *lanes, uint32_t n_lanes,
         const uint32_t used = r.p->n_blocks ? kvm_cdiv(r.p->n_blocks, KVM_MEANK_TILE) : 0u;
         out[i] = score_args{r.q->q_sum, r.q->q_count, ix->k_sum, ix->mean_tokens, (double *)tl.lane[i].layer_score,
                             r.p->n_blocks, ix->n_blocks, kvm_cdiv(ix->n_blocks, KVM_MEANK_TILE), ix->n_layer,
-                            r.q->n_head, ix->n_head_kv, used, r.q->n_head / ix->n_head_kv, r.q->q_vec, r.q->q_norm};
+                            r.q->n_head, ix->n_head_kv, used, r.q->n_head / ix->n_head_kv, r.q->q_vec, r.q->q_norm,
+                            ix->k_norm};
     }
 }
 
@@ -539,9 +600,13 @@ int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t
         max_layer = sl.lane[i].n_layer > max_layer ? sl.lane[i].n_layer : max_layer;
     }
     if (max_tiles == 0) return KVM_OK;
-    // the accumulators' formed query terms when every lane has them
-    bool qv = true;
-    for (uint32_t i = 0; i < n_lanes; ++i) qv = qv && sl.lane[i].q_vec;
+    // the accumulators' formed query terms when every lane has them, the
+    // indexes' block terms likewise
+    bool qv = true, nk = true;
+    for (uint32_t i = 0; i < n_lanes; ++i) {
+        qv = qv && sl.lane[i].q_vec;
+        nk = nk && sl.lane[i].k_norm;
+    }
     KVM_HIP(st, hipSetDevice(st->device));
     const dim3 grid(max_tiles, max_layer, n_lanes), block(256);
     // product rows in LDS (the shorter chains) while the grid fits the CUs at
@@ -549,15 +614,22 @@ int kvm_retrieval_score(kvm_state *st, const kvm_retrieval_lane *lanes, uint32_t
     // twice the workgroups per CU)
     const uint64_t n_wg = (uint64_t)max_tiles * max_layer * n_lanes;
     const bool wide = lanes[0].ix->head_dim == 256;
-    const size_t lds_rows = wide ? sizeof(score_wg_lds<256, 4, false>) : sizeof(score_wg_lds<128, 4, false>);
-    const bool otf = n_wg > (uint64_t)st->n_cu * (KVM_LDS_PER_CU / lds_rows);
+    const size_t lds_rows = wide ? sizeof(score_wg_lds<256, 4, KVM_SL_ROWS>) : sizeof(score_wg_lds<128, 4, KVM_SL_ROWS>);
+    const int lay = nk ? KVM_SL_NK : n_wg > (uint64_t)st->n_cu * (KVM_LDS_PER_CU / lds_rows) ? KVM_SL_OTF : KVM_SL_ROWS;
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, st->stream, sl); };
+    auto pick = [&](auto d, auto q) {
+        constexpr int DD = decltype(d)::value;
+        constexpr bool QQ = decltype(q)::value;
+        if (lay == KVM_SL_NK) go(k_score<DD, QQ, KVM_SL_NK>);
+        else if (lay == KVM_SL_OTF) go(k_score<DD, QQ, KVM_SL_OTF>);
+        else go(k_score<DD, QQ, KVM_SL_ROWS>);
+    };
     if (wide) {
-        if (qv) otf ? go(k_score<256, true, true>) : go(k_score<256, true, false>);
-        else otf ? go(k_score<256, false, true>) : go(k_score<256, false, false>);
+        if (qv) pick(std::integral_constant<int, 256>{}, std::true_type{});
+        else pick(std::integral_constant<int, 256>{}, std::false_type{});
     } else {
-        if (qv) otf ? go(k_score<128, true, true>) : go(k_score<128, true, false>);
-        else otf ? go(k_score<128, false, true>) : go(k_score<128, false, false>);
+        if (qv) pick(std::integral_constant<int, 128>{}, std::true_type{});
+        else pick(std::integral_constant<int, 128>{}, std::false_type{});
     }
     KVM_LAUNCH_CHECK(st, "score");
     return KVM_OK;

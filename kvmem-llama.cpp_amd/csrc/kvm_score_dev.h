@@ -31,6 +31,7 @@ struct score_args {
     uint32_t g;             // query heads per kv head, n_head / H
     const float *q_vec;     // [n_layer][H][D]: qv formed with the sums, or null
     const float *q_norm;    // [n_layer][H]: nq beside it
+    const float *k_norm;    // [n_layer][H][cap]: the blocks' nk formed with the index, or null
 };
 
 // Device-coherent 64-bit store / load of a layer contribution written and read
@@ -45,24 +46,30 @@ __device__ __forceinline__ double kvm_ld_f64_dev(const double *p) {
 }
 
 // LDS of one wave's (tile, head) pass, rows of D floats padded against bank
-// conflicts: the 17 product rows (dot products of blocks 0-7, their kh
-// squares, qv squares), or with OTF (products formed on the fly by the
-// chains, about half the LDS) qv and the kh of blocks 0-7.
-#define KVM_SCORE_ROWS 17
-template <int D, bool OTF>
+// conflicts, by layout:
+//   KVM_SL_ROWS  the 17 product rows (dot products of blocks 0-7, their kh
+//                squares, qv squares);
+//   KVM_SL_OTF   qv and the kh of blocks 0-7, the chains forming their
+//                products on the fly (about half the LDS);
+//   KVM_SL_NK    the index carries the blocks' nk: 9 product rows (the dot
+//                products, qv squares).
+#define KVM_SL_ROWS 0
+#define KVM_SL_OTF 1
+#define KVM_SL_NK 2
+template <int D, int LAY>
 struct score_wave_lds {
-    float p[KVM_SCORE_ROWS][D + 4];
+    float p[LAY == KVM_SL_NK ? 9 : 17][D + 4];
 };
 template <int D>
-struct score_wave_lds<D, true> {
+struct score_wave_lds<D, KVM_SL_OTF> {
     float qv[D + 4];
     float kh[KVM_MEANK_TILE][D + 4];
 };
 // The scoring workgroup's LDS: one region per scoring wave, the cosines of
 // every head and the count of heads done.
-template <int D, int NW, bool OTF>
+template <int D, int NW, int LAY>
 struct score_wg_lds {
-    score_wave_lds<D, OTF> w[NW];
+    score_wave_lds<D, LAY> w[NW];
     float cos[KVM_SCORE_HMAX][KVM_MEANK_TILE];
     uint32_t heads_done;
 };
@@ -77,9 +84,9 @@ struct score_regs {
     kvm_f32x4 kv[8];
     kvm_f32x4 qg[8];
     uint32_t mt[KVM_MEANK_TILE];
-    float nq;
+    float nq, nk;
 };
-template <int D, bool QV>
+template <int D, bool QV, int LAY>
 __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il, uint32_t tile, uint32_t h, uint32_t g,
                                                 score_regs &r) {
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
@@ -101,6 +108,11 @@ __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il
         const uint32_t b = tile * TW + bi;
         r.mt[bi] = a.mean_tokens[(uint64_t)il * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
     }
+    if constexpr (LAY == KVM_SL_NK) {
+        // lane c < 8: nk of block 8 tile + c (clamped, as the counts)
+        const uint32_t b = tile * TW + (l & 7u);
+        r.nk = a.k_norm[((uint64_t)il * a.H + h) * a.cap + (b < a.n_blocks ? b : a.n_blocks - 1)];
+    }
 }
 
 // One wave scores the pass whose reads `r` holds, without any workgroup
@@ -110,14 +122,19 @@ __device__ __forceinline__ void score_tile_load(const score_args &a, uint32_t il
 // the wave's LDS rows (read back by the same wave only); lane c < 17 then runs
 // chain c over d in order (the reference's dot of block c, nk of block c - 8,
 // nq: the product of each step is the same float, and the additions the same
-// sequence), and lanes 0-7 form the cosines into cos_h[0..7].  With OTF the
-// lanes store qv and kh instead and each chain forms its products as it goes
-// (the same floats).  qc = q_count[il] > 0.  With QV, qv and nq come formed
-// (the same operations, done once per change of the query sums): 16 chains.
-template <int D, bool QV, bool OTF>
+// sequence), and lanes 0-7 form the cosines into cos_h[0..7].  LAY (the LDS
+// layouts above): KVM_SL_OTF stores qv and kh instead and each chain forms
+// its products as it goes (the same floats); KVM_SL_NK takes nk from the
+// index (formed once per change of a block's sum, the same operations), so
+// only the dot rows and qv squares are formed: chain 8 is nq.  qc =
+// q_count[il] > 0.  With QV, qv and nq come formed (the same operations, done
+// once per change of the query sums).
+template <int D, bool QV, int LAY>
 __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t il, uint32_t h, uint32_t qc,
-                                                   uint32_t g, const score_regs &r, score_wave_lds<D, OTF> &L,
+                                                   uint32_t g, const score_regs &r, score_wave_lds<D, LAY> &L,
                                                    float *cos_h) {
+    constexpr bool OTF = LAY == KVM_SL_OTF, NK = LAY == KVM_SL_NK;
+    constexpr uint32_t RQ = NK ? 8u : 16u;          // the row of the qv squares
     constexpr uint32_t TW = KVM_MEANK_TILE, NL = D / 4;
     const uint32_t l = threadIdx.x & 63u;
     if (l < NL) {
@@ -140,7 +157,7 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
                 qv[e] = kvm_fmul(qh, invq);
             }
             if constexpr (!OTF)
-                *(kvm_f32x4 *)&L.p[16][4u * l] = kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]),
+                *(kvm_f32x4 *)&L.p[RQ][4u * l] = kvm_f32x4{kvm_fmul(qv[0], qv[0]), kvm_fmul(qv[1], qv[1]),
                                                            kvm_fmul(qv[2], qv[2]), kvm_fmul(qv[3], qv[3])};
         }
         if constexpr (OTF) *(kvm_f32x4 *)&L.qv[4u * l] = kvm_f32x4{qv[0], qv[1], qv[2], qv[3]};
@@ -158,8 +175,9 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
             } else {
                 *(kvm_f32x4 *)&L.p[bi][4u * l] = kvm_f32x4{kvm_fmul(qv[0], k4[0]), kvm_fmul(qv[1], k4[1]),
                                                            kvm_fmul(qv[2], k4[2]), kvm_fmul(qv[3], k4[3])};
-                *(kvm_f32x4 *)&L.p[8 + bi][4u * l] = kvm_f32x4{kvm_fmul(k4[0], k4[0]), kvm_fmul(k4[1], k4[1]),
-                                                               kvm_fmul(k4[2], k4[2]), kvm_fmul(k4[3], k4[3])};
+                if constexpr (!NK)
+                    *(kvm_f32x4 *)&L.p[8 + bi][4u * l] = kvm_f32x4{kvm_fmul(k4[0], k4[0]), kvm_fmul(k4[1], k4[1]),
+                                                                   kvm_fmul(k4[2], k4[2]), kvm_fmul(k4[3], k4[3])};
             }
         }
     }
@@ -167,14 +185,14 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
     // wave complete in order; the fence keeps the compiler from moving them)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
-    // ---- chains: lane c < 17 runs chain c (lanes past 16 repeat chain 16,
-    // unused; with QV chain 16 is not used).  The adds of one chain are
+    // ---- chains: lane c <= RQ runs chain c (lanes past RQ repeat chain RQ,
+    // unused; with QV chain RQ is not used).  The adds of one chain are
     // dependent, so the chain runs at the VALU's dependent-issue rate only if
     // its operands are in registers ahead of it: LOOK chunks of 16 dims (of
     // both factors, 8 dims, with OTF) are in flight, the LDS latency being
     // longer than one chunk's adds.
     float chain = 0.0f;
-    const uint32_t c = l < 17u ? l : 16u;
+    const uint32_t c = l <= RQ ? l : RQ;
     if constexpr (!OTF) {
         const float *row = L.p[c];
         constexpr int CH = 4;                // float4 per 16-dim chunk
@@ -230,9 +248,13 @@ __device__ __forceinline__ void score_tile_compute(const score_args &a, uint32_t
             if (k + LOOK < NC) ld(bufa[k % LOOK], bufb[k % LOOK], k + LOOK);
         }
     }
+    // (the chain counts as live on every lane: where only lanes 0-7 use theirs,
+    // the compiler otherwise runs the chain under a narrowed exec mask and
+    // takes three times the registers)
+    asm volatile("" : "+v"(chain));
     // ---- cosines of blocks 0-7 (every lane takes part in the shuffles)
-    const float nk = __shfl(chain, (int)((l & 7u) + 8u), 64);
-    const float nq = QV ? r.nq : __shfl(chain, 16, 64);
+    const float nk = NK ? r.nk : __shfl(chain, (int)((l & 7u) + 8u), 64);
+    const float nq = QV ? r.nq : __shfl(chain, (int)RQ, 64);
     if (l < TW) {
         const float den = kvm_fadd(kvm_fmul(kvm_fsqrt(nq), kvm_fsqrt(nk)), 1e-6f);
         cos_h[l] = kvm_fdiv(chain, den);

@@ -45,7 +45,7 @@ class QueryAcc(C.Structure):
 class MeanKIndex(C.Structure):
     _fields_ = [("n_layer", C.c_uint32), ("n_blocks", C.c_uint32), ("n_head_kv", C.c_uint32),
                 ("head_dim", C.c_uint32), ("block_tokens", C.c_uint32), ("k_sum", C.c_void_p),
-                ("mean_tokens", C.c_void_p), ("present", C.c_void_p), ("acc", C.c_void_p)]
+                ("mean_tokens", C.c_void_p), ("present", C.c_void_p), ("acc", C.c_void_p), ("k_norm", C.c_void_p)]
 
 
 class View(C.Structure):
@@ -143,6 +143,7 @@ SIGNATURES = {
     "kvm_dequantize_rows": (C.c_int, [_P, C.c_int, _P, _P, _i64, _i64]),
     "kvm_query_reset": (C.c_int, [_P, C.POINTER(QueryAcc)]),
     "kvm_query_refresh": (C.c_int, [_P, C.POINTER(QueryAcc)]),
+    "kvm_meank_refresh": (C.c_int, [_P, C.POINTER(MeanKIndex)]),
     "kvm_query_add": (C.c_int, [_P, C.POINTER(QueryAcc), _u32, _P, _u32]),
     "kvm_meank_k_sum_floats": (_sz, [C.POINTER(MeanKIndex)]),
     "kvm_meank_add": (C.c_int, [_P, C.POINTER(MeanKIndex), _u32, _u32, _u32, _P]),

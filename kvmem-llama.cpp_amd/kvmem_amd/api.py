@@ -196,7 +196,10 @@ class MeanKIndex:
 
     TILE = 8
 
-    def __init__(self, st, n_layer, n_blocks, n_head_kv, head_dim, block_tokens=128):
+    def __init__(self, st, n_layer, n_blocks, n_head_kv, head_dim, block_tokens=128, norms=False):
+        """norms: the index also carries the blocks' score term nk (k_norm),
+        which add / acc_flush keep current; after writing k_sum or mean_tokens
+        directly, call refresh()."""
         dev = torch.device("cuda", st.device)
         self.st = st
         self.n_blocks = n_blocks
@@ -205,10 +208,14 @@ class MeanKIndex:
         self.mean_tokens = torch.zeros((n_layer, n_blocks), dtype=torch.int32, device=dev)
         self.present = torch.zeros((n_blocks,), dtype=torch.uint8, device=dev)
         self.acc = torch.zeros((n_layer, n_head_kv * head_dim), dtype=torch.float32, device=dev)
+        self.k_norm = torch.zeros((n_layer, n_head_kv, n_blocks), dtype=torch.float32, device=dev) if norms else None
         self.c = L.MeanKIndex(n_layer, n_blocks, n_head_kv, head_dim, block_tokens,
                               self.k_sum.data_ptr(), self.mean_tokens.data_ptr(), self.present.data_ptr(),
-                              self.acc.data_ptr())
+                              self.acc.data_ptr(), self.k_norm.data_ptr() if norms else None)
         assert self.k_sum.numel() == st.lib.kvm_meank_k_sum_floats(C.byref(self.c))
+
+    def refresh(self):
+        self.st.check(self.st.lib.kvm_meank_refresh(self.st.h, C.byref(self.c)))
 
     def block_sums(self):
         """K sums as [n_layer][n_blocks][n_head_kv*head_dim] (a copy)."""

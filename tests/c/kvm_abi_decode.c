@@ -138,6 +138,8 @@ static int decode_step_on_caller_stream(void) {
     CHECK_HIP(hipMalloc((void **)&ix.mean_tokens, sizeof(uint32_t) * S_BLOCKS));
     CHECK_HIP(hipMemsetAsync(ix.k_sum, 0, sizeof(float) * kvm_meank_k_sum_floats(&ix), stream));
     CHECK_HIP(hipMemsetAsync(ix.mean_tokens, 0, sizeof(uint32_t) * S_BLOCKS, stream));
+    /* the index carries the blocks' score terms, kept current by kvm_meank_add */
+    CHECK_HIP(hipMalloc((void **)&ix.k_norm, sizeof(float) * H * S_BLOCKS));
     /* the accumulator carries the scorer's query terms (kept current by
        reset and add) */
     kvm_query_acc qa = {1, NQ, D, NULL, NULL, H, NULL, NULL};

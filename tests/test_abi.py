@@ -34,7 +34,7 @@ def test_binding_covers_header():
 
 
 def test_abi_version_without_gpu():
-    assert L.load().kvm_abi_version() == 5
+    assert L.load().kvm_abi_version() == 6
 
 
 # ctypes mirror -> C typedef of include/kvm_hotpath.h

@@ -26,7 +26,7 @@ def _lane(st, seed, n_blocks, budget, slots, n_tok_q=4, terms=False, kt=L.T_Q8_0
     rng = np.random.default_rng(seed)
     n_hist = n_blocks * BT - 40                         # the last block partly filled
     kr, vr = rand_rows(rng, n_hist, H, D, kt, L.T_Q4_0)
-    ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT)
+    ix = api.MeanKIndex(st, 1, n_blocks, H, D, BT, norms=terms)
     ix.add(0, 0, dev(rng.standard_normal((n_hist, H * D)).astype(np.float32)))
     qa = api.QueryAcc(st, 1, H * G, D, n_head_kv=H if terms else 0)
     qa.reset()
@@ -95,7 +95,7 @@ def test_decode_step_matches_separate_calls(kvm_state, monkeypatch, n_lanes, spl
     step's launch takes one split fewer per head than kvm_fa_decode (the
     selectors' column) and the outputs agree within the attention tolerance.
     terms: the query accumulators carry the scorer's query terms, refreshed
-    after each drift of the sums.  kt: the K cache type (q4_0: the selecting
+    after each drift of the sums, and the indexes the blocks' terms.  kt: the K cache type (q4_0: the selecting
     launch stages the q4_0 rows with the one-row-per-wave requantiser, the
     separate calls with the 16-lane one)."""
     if splits:

@@ -49,12 +49,16 @@ def test_meank_add_bit_exact(kvm_state):
     assert list(host(ix.present)[:7]) == [1, 1, 1, 1, 1, 1, 0]
 
 
-def _build_index(st, k_sum, mt, n_blocks_cap, H, D, bt=128):
+def _build_index(st, k_sum, mt, n_blocks_cap, H, D, bt=128, norms=False):
+    """norms: the index carries the blocks' nk, formed by kvm_meank_refresh
+    after the direct writes."""
     L_, nb, e = k_sum.shape
-    ix = api.MeanKIndex(st, L_, n_blocks_cap, H, D, bt)
+    ix = api.MeanKIndex(st, L_, n_blocks_cap, H, D, bt, norms=norms)
     ix.set_block_sums(dev(np.ascontiguousarray(k_sum)))
     ix.mean_tokens[:, :nb] = dev(mt.astype(np.int32))
     ix.present[:nb] = 1
+    if norms:
+        ix.refresh()
     return ix
 
 
@@ -83,16 +87,17 @@ def _case(seed, n_blocks, n_layer=1, n_head=24, H=4, D=256, planted=16):
                                                        # blocks at 4 kv heads take 16-block workgroups
                                                        (700, 2, 8, 8, 128), (260, 1, 32, 16, 128),
                                                        (500, 1, 12, 3, 128), (333, 1, 3, 1, 256)])
-@pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
+@pytest.mark.parametrize("terms", ["none", "q", "qk"], ids=["q_sum", "q_terms", "q_k_terms"])
 def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D, terms):
-    """terms: the accumulator carries the query terms (formed by
-    kvm_query_refresh after the direct writes) and the scorer reads them."""
+    """terms: q, the accumulator carries the query terms (formed by
+    kvm_query_refresh after the direct writes) and the scorer reads them; qk,
+    the index carries the blocks' nk too (kvm_meank_refresh)."""
     q, qc, k_sum, mt, planted = _case(n_blocks + n_layer, n_blocks, n_layer, n_head, H, D)
-    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 5, H, D)
-    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms else 0)
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 5, H, D, norms=terms == "qk")
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms != "none" else 0)
     qa.q_sum.copy_(dev(q))
     qa.q_count.copy_(dev(qc.astype(np.int32)))
-    if terms:
+    if terms != "none":
         qa.refresh()
     n_tokens = np.full(n_blocks, 128, np.int32)
     n_tokens[-1] = 77
@@ -109,7 +114,7 @@ def test_score_topk_bit_exact(kvm_state, n_blocks, n_layer, n_head, H, D, terms)
     assert np.array_equal(res["to_base"], to_base) and res["total"] == total and res["status"] == 0
 
 
-@pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
+@pytest.mark.parametrize("terms", ["none", "q", "qk"], ids=["q_sum", "q_terms", "q_k_terms"])
 def test_score_bit_exact_where_every_term_matters(kvm_state, terms):
     """The closed-form pin's inputs (norms near 1e-6 so the epsilon and invq
     count, g = 3, three layers with query counts 5, 0, 2, a block without K in
@@ -119,11 +124,11 @@ def test_score_bit_exact_where_every_term_matters(kvm_state, terms):
     n_head, H, D = 6, 2, 128
     q, qc, k_sum, mt = tiny_norm_case(41, n_head=n_head, H=H, d=D)
     n_layer, n_blocks = mt.shape
-    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 3, H, D)
-    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms else 0)
+    ix = _build_index(kvm_state, k_sum, mt, n_blocks + 3, H, D, norms=terms == "qk")
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H if terms != "none" else 0)
     qa.q_sum.copy_(dev(q))
     qa.q_count.copy_(dev(qc.astype(np.int32)))
-    if terms:
+    if terms != "none":
         qa.refresh()
     sel = api.score_topk(kvm_state, ix, qa, n_blocks, dev(np.full(n_blocks, 128, np.int32)), 4, sink_blocks=1)
     sel.result()
@@ -175,18 +180,69 @@ def test_query_terms_follow_reset_and_adds(kvm_state):
         api.score_topk(kvm_state, ix, wrong, n_blocks, n_tokens, 32, sink_blocks=1)
 
 
+def test_index_terms_follow_adds_and_flushes(kvm_state):
+    """The index's block terms (nk) are kept current by kvm_meank_add (whole
+    and partial blocks), the decode running sum's flush and refresh: after
+    each, the scores equal the oracle's on the index's sums bit for bit, and
+    those of an index without the terms.  The query accumulator carries its
+    terms too."""
+    n_layer, n_head, H, D, bt = 2, 12, 3, 128, 128
+    n_blocks = 20
+    rng = np.random.default_rng(8)
+    ixs = [api.MeanKIndex(kvm_state, n_layer, n_blocks, H, D, bt, norms=nm) for nm in (True, False)]
+    qa = api.QueryAcc(kvm_state, n_layer, n_head, D, n_head_kv=H)
+    qa.reset()
+    for il in range(n_layer):
+        qa.add(il, dev(rng.standard_normal((3, n_head * D)).astype(np.float32)))
+    n_tokens = dev(np.full(n_blocks, bt, np.int32))
+
+    def check(n_used):
+        outs = [api.score_topk(kvm_state, ix, qa, n_used, n_tokens[:n_used].contiguous(), 4, sink_blocks=1)
+                for ix in ixs]
+        ks = host(ixs[1].block_sums())[:, :n_used]
+        mt = host(ixs[1].mean_tokens)[:, :n_used].astype(np.uint32)
+        want = O.score_retrieval(host(qa.q_sum), host(qa.q_count).astype(np.uint32), ks, mt, n_head, H, D)
+        got = host(outs[0].scores)[:n_used]
+        assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+        assert np.array_equal(got.view(np.uint64), host(outs[1].scores)[:n_used].view(np.uint64))
+
+    rows = (rng.standard_normal((n_layer, 9 * bt + 50, H * D)) * 3).astype(np.float32)
+    for il in range(n_layer):
+        for ix in ixs:
+            ix.add(il, 0, dev(rows[il, :5 * bt + 17]))          # 5 full blocks and part of a sixth
+    check(6)
+    for il in range(n_layer):
+        for ix in ixs:
+            ix.add(il, 5 * bt + 17, dev(rows[il, 5 * bt + 17:9 * bt + 50]))   # the sixth completed, up to 10
+    check(10)
+    # the decode running sum flushed into block 10
+    dec = dev(rng.standard_normal((40, H * D)).astype(np.float32))
+    for ix in ixs:
+        ix.acc_zero(1)
+        ix.acc_add(1, dec.view(40, H, D), 0, 40)
+        ix.acc_flush(1, 10 * bt, 40)
+    check(11)
+    # direct writes, then refresh
+    for ix in ixs:
+        ix.k_sum.mul_(0.5)
+        if ix.k_norm is not None:
+            ix.refresh()
+    check(11)
+
+
 @pytest.mark.parametrize("terms", [False, True], ids=["q_sum", "q_terms"])
 def test_score_topk_lanes_match_single_lane(kvm_state, terms):
     """Four lanes of different sizes (multi-lane decode) in one launch sequence:
     every lane's scores, ids, layout and stage plan equal the oracle's and a
-    single-lane call's.  The four-lane grid (1,024 workgroups) takes the
-    scorer whose chains form their products, a single lane the one with
-    product rows in LDS."""
+    single-lane call's.  Without the terms the four-lane grid (1,024
+    workgroups) takes the scorer whose chains form their products, a single
+    lane the one with product rows in LDS; with them (query and index terms)
+    both take the one with the 9 rows of dot products and qv squares."""
     H, n_head, D = 4, 24, 256
     lanes, single, cases = [], [], []
     for i, n_blocks in enumerate((512, 1024, 1536, 2048)):
         q, qc, k_sum, mt, planted = _case(200 + i, n_blocks, 1, n_head, H, D)
-        ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
+        ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D, norms=terms)
         qa = api.QueryAcc(kvm_state, 1, n_head, D, n_head_kv=H if terms else 0)
         qa.q_sum.copy_(dev(q))
         qa.q_count.copy_(dev(qc.astype(np.int32)))
@@ -213,18 +269,22 @@ def test_score_topk_lanes_match_single_lane(kvm_state, terms):
         assert set(planted) <= set(r["ids"])
 
 
-@pytest.mark.parametrize("H,n_head,D", [(2, 8, 128), (1, 3, 256)])
-def test_score_topk_lanes_wide_grids(kvm_state, H, n_head, D):
-    """Four lanes of 8192 blocks (the top-k maximum) at 2 or 1 kv heads: the
-    scoring grid then takes 4 or 8 tiles (32 or 64 blocks) per workgroup; every
-    lane's scores are bit-exact and its ids equal the oracle's."""
+@pytest.mark.parametrize("H,n_head,D,terms", [(2, 8, 128, False), (1, 3, 256, False), (2, 8, 128, True)])
+def test_score_topk_lanes_wide_grids(kvm_state, H, n_head, D, terms):
+    """Four lanes of 8192 blocks (the top-k maximum) at 2 or 1 kv heads: a
+    grid of 4,096 workgroups (8-block tiles), past what the CUs hold with
+    product rows in LDS, so the chains form their products; every lane's
+    scores are bit-exact and its ids equal the oracle's (terms: with the query
+    terms carried by the accumulators)."""
     n_blocks, lanes, cases = 8192, [], []
     for i in range(4):
         q, qc, k_sum, mt, _ = _case(300 + i, n_blocks, 1, n_head, H, D)
         ix = _build_index(kvm_state, k_sum, mt, n_blocks, H, D)
-        qa = api.QueryAcc(kvm_state, 1, n_head, D)
+        qa = api.QueryAcc(kvm_state, 1, n_head, D, n_head_kv=H if terms else 0)
         qa.q_sum.copy_(dev(q))
         qa.q_count.copy_(dev(qc.astype(np.int32)))
+        if terms:
+            qa.refresh()
         lanes.append(dict(index=ix, query=qa, n_blocks=n_blocks, n_tokens=dev(np.full(n_blocks, 128, np.int32)),
                           budget_blocks=128, sink_blocks=1, window=api.KVWindow(kvm_state, 128 * 128, H, D, 128),
                           sel=api.SelectionBuffers(kvm_state, n_blocks, 128)))
