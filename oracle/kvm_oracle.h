@@ -3,8 +3,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links this code:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it,
- * and only as the checker (or as the timed CPU baseline), never as the thing
- * being measured or shipped.
+ * and only to check results against (or as the timed CPU baseline), never as
+ * the thing being measured or shipped.
  *
  * Every function restates one piece of the reference's algorithm in plain C and
  * cites the reference file:line it follows (paths relative to the reference

@@ -2,7 +2,8 @@
 kvmem host library built into oracle/_ref/ (libkvmem_ref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.
+bench.py's cpu_baseline leg, to check results against or as the timed CPU
+baseline.
 """
 import ctypes as C
 import os

@@ -374,7 +374,7 @@ def test_decode_step_lane_without_blocks(kvm_state):
 
 
 def test_decode_step_four_lanes_full_windows(kvm_state):
-    """Config 5's shape through the two-launch step: four lanes with
+    """The four-lane decode shape through the two-launch step: four lanes with
     32,768-cell windows (24 q / 4 kv heads, head_dim 256, one bf16 token each)
     selecting 128 blocks from histories of 160-400 blocks; the same step as
     three launches on second windows gives the same selections and window

@@ -22,7 +22,7 @@ H_Q, H, D, BT = 8, 2, 128, 128
 N_TOK, BUDGET, GEN = 16384, 4096, 512
 
 
-def test_config1_end_to_end(kvm_state):
+def test_fp16_16k_history_end_to_end(kvm_state):
     st = kvm_state
     rng = np.random.default_rng(0xC0FFEE01)
     n_blocks = N_TOK // BT
