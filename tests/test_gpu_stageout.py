@@ -69,7 +69,7 @@ def test_harvest_then_restage(kvm_state, kt):
     w.import_rows(5 * bt, dev(gk), dev(gv), dev(np.arange(5 * bt, 6 * bt, dtype=np.int32)))
     cap = torch.from_numpy(rng.standard_normal((bt + 3, H, D)).astype(np.float32)).to(torch.bfloat16).cuda()
     cap = cap.permute(1, 0, 2).contiguous().permute(1, 0, 2)          # the captured view, heads-major storage
-    ix = api.MeanKIndex(kvm_state, 1, n_hist_blocks, H, D, bt)
+    ix = api.MeanKIndex(kvm_state, 1, n_hist_blocks, H, D, bt, norms=True)
     api.harvest_block(kvm_state, w, 5 * bt, bt, cap, 3, hist.kbuf.u8[4 * bt * w.k_row_bytes():].reshape(-1)[:bt * w.k_row_bytes()],
                       hist.vbuf.u8[4 * bt * w.v_row_bytes():].reshape(-1)[:bt * w.v_row_bytes()], ix, 0, 4 * bt)
     k32 = cap[3:].float().cpu().numpy().reshape(bt, -1)
@@ -80,6 +80,10 @@ def test_harvest_then_restage(kvm_state, kt):
     sums, mt = O.meank_sums(k32, bt)
     assert np.array_equal(host(ix.block_sums())[0][4].view(np.uint32), sums[0].view(np.uint32))
     assert int(host(ix.mean_tokens)[0][4]) == bt
+    # the harvest's add kept the block's nk current: a refresh leaves it bit-equal
+    kn = ix.k_norm.clone()
+    ix.refresh()
+    assert torch.equal(kn.view(torch.int32), ix.k_norm.view(torch.int32)) and bool((kn[0, :, 4] > 0).all())
     # the window's slot map: slots 0..3 hold blocks 0..3; block 4 leaves and comes back
     nt = dev(np.full(n_hist_blocks, bt, np.int32))
     s = np.zeros(n_hist_blocks)
