@@ -200,6 +200,43 @@ def test_decode_step_steady_state(kvm_state, monkeypatch):
     assert torch.equal(ln["out"], ref)
 
 
+@pytest.mark.parametrize("n_layer,splits", [(3, None), (14, 8)], ids=["3-layers", "14-layers-8-splits"])
+def test_decode_step_scores_every_layer(kvm_state, monkeypatch, n_layer, splits):
+    """Indexes and accumulators of several layers that carry their terms, one
+    layer without query rows (the top-k skips it, averaging the others in
+    layer order): over three steps whose last layer's query drifts, the step
+    equals the separate calls (scores bit for bit; outputs bit-equal under a
+    common split count)."""
+    if splits:
+        monkeypatch.setenv("KVM_FA_SPLITS", str(splits))
+    st = kvm_state
+    ln = _lane(st, 0x5D50 + n_layer, 40, 12, 16, terms=True)
+    rng = ln["rng"]
+    ix = api.MeanKIndex(st, n_layer, ln["n_blocks"], H, D, BT, norms=True)
+    for il in range(n_layer):
+        ix.add(il, 0, dev(rng.standard_normal((ln["n_hist"], H * D)).astype(np.float32)))
+    qa = api.QueryAcc(st, n_layer, H * G, D, n_head_kv=H)
+    qa.reset()
+    for il in range(n_layer):
+        if il != 1:
+            qa.add(il, dev(rng.standard_normal((4, H * G * D)).astype(np.float32)))
+    ln["ix"], ln["qa"] = ix, qa
+    for step in range(3):
+        if step:
+            qa.q_sum[2].add_(dev((rng.standard_normal(H * G * D) * 0.8).astype(np.float32)))
+            qa.refresh()
+        ln["q"] = dev(rng.standard_normal((4, H * G, D)).astype(np.float32)).to(torch.bfloat16)
+        ln["out"] = torch.empty((4, H * G, D), dtype=torch.float32, device="cuda")
+        d = _step_dict(ln)
+        api.decode_step(st, d["index"], d["query"], d["n_blocks"], d["n_tokens"], d["budget_blocks"], 1, 0,
+                        d["window"], d["sel"], d["history"], d["q"], d["q_pos"], H * G, D ** -0.5, 64, 1e7,
+                        out=d["out"])
+        ref = _reference_step(st, ln)
+        torch.cuda.synchronize()
+        _compare(ln, ref, splits is not None, step)
+    assert st.status() == 0
+
+
 def test_decode_step_three_launch_path(kvm_state):
     """A step with a lane that has no query token takes the three-launch path
     (kvm_score_topk + kvm_stagein_fa_decode) with the same results: the other
