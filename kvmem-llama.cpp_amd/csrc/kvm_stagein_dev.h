@@ -273,10 +273,15 @@ template <int D>
 __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, uint32_t c, const float2 *cs, bool live,
                                               uint32_t l, const rope_ctx &rc, bool q4 = false) {
     const uint32_t m = k16_m<D>(l), b = m >> 1, d0 = 16u * m;
+    // a power-of-two Hadamard pre-scale (a width that is a power of 4) rides
+    // on the block scale: every value it reaches before the butterflies is
+    // then scaled by it exactly (no product comes near the subnormals)
+    const bool hs2 = (__float_as_uint(rc.hscale) & 0x807fffffu) == 0u;
+    const float hs = hs2 ? rc.hscale : 1.0f;
     float x[16];
     if (!q4) {
         const uint8_t *blk = src + b * 34u;
-        const float dsc = kvm_h2f(*(const uint16_t *)blk);
+        const float dsc = kvm_fmul(kvm_h2f(*(const uint16_t *)blk), hs);
         const uint16_t *q = (const uint16_t *)(blk + 2u + 16u * (m & 1u));
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -287,7 +292,7 @@ __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, u
     } else {
         // dims 0-15 of a block are the low nibbles of its 16 bytes, 16-31 the high
         const uint8_t *blk = src + b * 18u;
-        const float dsc = kvm_h2f(*(const uint16_t *)blk);
+        const float dsc = kvm_fmul(kvm_h2f(*(const uint16_t *)blk), hs);
         const uint16_t *q = (const uint16_t *)(blk + 2u);
         const uint32_t sh = 4u * (m & 1u);
 #pragma unroll
@@ -338,8 +343,10 @@ __device__ __forceinline__ void stage_k_row16(const uint8_t *src, uint8_t *kt, u
     // nrot - 1 with the lane's sign carried as in stage_k_rows
     uint32_t xs = 0;
     if (rc.nrot > 0) {
+        if (!hs2) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
+            for (int i = 0; i < 16; ++i) x[i] = kvm_fmul(x[i], rc.hscale);
+        }
 #pragma unroll
         for (int h = 1; h < 16; h <<= 1)
 #pragma unroll
@@ -712,11 +719,27 @@ __device__ __forceinline__ void stagein_item(const stage_args &a, uint8_t *s_row
         // K rows: a wave takes RW rows (cell j, head h) at a time, one per lane group
         constexpr uint32_t LG = D / 16, RW = 64 / LG;
         const uint32_t lane = tid & 63u, grp = lane / LG, l = lane % LG;
+        // row r = (cell j, head h), advanced by W RW rows a step without a division
+        const uint32_t H = a.H, dj = W * RW / H, dh = W * RW % H;
+        uint32_t j = (wave * RW + grp) / H, h = (wave * RW + grp) % H;
+        uint32_t j0 = wave * RW / H, h0 = wave * RW % H;            // row r0
         for (uint32_t r0 = wave * RW; r0 < nrow; r0 += W * RW) {
-            const uint32_t r = r0 + grp, rr = r < nrow ? r : r0;     // past the rows: recompute r0, unwritten
-            const uint32_t j = rr / a.H, h = rr % a.H;
-            stage_k_row16<D>(lk + j * rowK + h * NB * kb, ktile + (uint64_t)h * a.n_tiles * kvm_ktile_bytes(KVM_TYPE_Q8_0, D),
-                             c0 + j, lt + j * nh, r < nrow, l, a.rc, a.k_q4 != 0);
+            const bool live = r0 + grp < nrow;                         // past the rows: recompute r0, unwritten
+            const uint32_t jj = live ? j : j0, hh = live ? h : h0;
+            stage_k_row16<D>(lk + jj * rowK + hh * NB * kb, ktile + (uint64_t)hh * a.n_tiles * kvm_ktile_bytes(KVM_TYPE_Q8_0, D),
+                             c0 + jj, lt + jj * nh, live, l, a.rc, a.k_q4 != 0);
+            j += dj;
+            h += dh;
+            if (h >= H) {
+                h -= H;
+                ++j;
+            }
+            j0 += dj;
+            h0 += dh;
+            if (h0 >= H) {
+                h0 -= H;
+                ++j0;
+            }
         }
     } else
     // K rows: wave w takes rows (cell j, head h) = r, r + NTH/64, ..., four at a time
