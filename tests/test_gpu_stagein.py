@@ -24,7 +24,9 @@ def _history(seed, n_tokens, H=4, D=256):
     (256, 64, -1, 1e7), (256, 64, 0, 1e7), (256, 128, 128, 1e4), (256, 32, -1, 1e4), (256, 256, 256, 1e4),
     (128, 64, -1, 1e7), (128, 128, 128, 1e4), (128, 32, 0, 1e7),
     # RoPE pairs not one dim bit >= 4 apart (n_half 12, 8): the one-row-per-wave path
-    (256, 24, -1, 1e7), (256, 16, 64, 1e7)])
+    (256, 24, -1, 1e7), (256, 16, 64, 1e7),
+    # 16-lane rows with a Hadamard width below the head (64: its pre-scale 1/8 rides on the block scale)
+    (256, 64, 64, 1e7)])
 def test_stagein_selection_bytes(kvm_state, D, n_rot, hadamard, freq_base):
     H, bt = 4, 128
     n_blocks = 40
@@ -375,7 +377,7 @@ def test_score_topk_stagein_lanes_matches_two_calls(kvm_state):
 
 
 @pytest.mark.parametrize("D,n_rot,hadamard", [(256, 64, -1), (256, 128, 0), (128, 32, -1), (256, 24, -1),
-                                              (128, 16, 64)])
+                                              (128, 16, 64), (256, 64, 128), (256, 64, 64)])
 def test_stagein_selection_bytes_q4_0_k(kvm_state, D, n_rot, hadamard):
     """A q4_0 K cache: the history's raw K rows are q4_0 and the stage-in
     requantises to q4_0 (quant_q4_0, llama-kvmem-stagein.cu:201-234, in the
